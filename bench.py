@@ -1,0 +1,211 @@
+#!/usr/bin/env python3
+"""MoE-layer benchmark on one MI355X.
+
+Workloads (hmoe.synth.CONFIGS):
+  C4     (default) INT8 Qwen3-30B-A3B-shape block, 4096-token prefill,
+         128 experts, top-8, Zipf(1.1)-skewed routing
+  C3-1, C3-4, C3-16   decode shapes (1/4/16 tokens)
+  C1, C2 FP32 64-expert blocks
+
+One step = one MoE-block call (route -> permute -> INT8-MFMA SwiGLU experts
+-> combine) over a batch already resident in HBM.  Prints ONE JSON line.
+
+Roofline: the dominant kernel's algorithmic work per launch divided by its
+average launch duration, measured with hipEvents recorded on the launch
+stream at the block's stage boundaries over the timed steps.
+  prefill (C4): gate/up GEMM, ops = 2*T*k*2*H*I, bound = INT8 MFMA (5.0 POP/s)
+  decode (C3):  gate/up GEMM, bytes = U*2*H*I (+ activations), bound = HBM 8 TB/s
+The CPU baseline is the oracle's restatement of the reference CPU path
+(single thread, reference loop order) timed on a bounded token sample.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "hypermoe-engine_amd"))
+
+PEAK_HBM_GBS = 8000.0
+PEAK_INT8_TOPS = 5000.0      # dense INT8 MFMA, TOP/s
+PEAK_FP32_TFLOPS = 157.3
+METRIC = "MoE-layer tokens/s (INT8, 128e top-8) + % of HBM / INT8-MFMA roofline"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="C4")
+    ap.add_argument("--limbs", type=int, default=2)
+    ap.add_argument("--cpu-sample", type=int, default=-1,
+                    help="tokens timed on the CPU baseline (-1: per-workload default, 0: skip)")
+    ap.add_argument("--quiet", action="store_true")
+    return ap.parse_args()
+
+
+def log(msg, quiet=False):
+    if not quiet:
+        print(msg, file=sys.stderr, flush=True)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: every box in this build has one MI355X and the "
+              "block runs on one GPU's share (see DESIGN.md for how it would shard). "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    from hmoe import capi, synth
+    from hmoe.block import DeviceExpertLayer, MoEBlock
+
+    cfg = synth.CONFIGS[args.workload]
+    T, H, E, I, k = cfg.tokens, cfg.hidden, cfg.experts, cfg.inter, cfg.top_k
+    q = args.quiet
+    log(f"[bench] workload {cfg.name}: T={T} H={H} E={E} I={I} k={k} int8={cfg.int8} "
+        f"skew={cfg.skew} limbs={args.limbs}", q)
+    t0 = time.time()
+    payload, scale, zp = synth.expert_layer(cfg.seed, 0, E, H, I, cfg.int8,
+                                            threads=min(16, os.cpu_count() or 1))
+    raw = synth.raw_hidden(cfg.seed, T, H)
+    w = synth.router_weights(cfg.seed, 0, H, E)
+    torch.cuda.set_device(0)
+    lib = capi.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    # hidden = RMSNorm(N(0,1)) on the device (bit-exact with the reference)
+    d_raw = torch.from_numpy(raw).cuda()
+    gamma = torch.ones(H, dtype=torch.float32, device="cuda")
+    d_h = torch.empty_like(d_raw)
+    capi.call("hm_rmsnorm", d_raw.data_ptr(), gamma.data_ptr(), d_h.data_ptr(), T, H, 1e-6, stream)
+    if cfg.skew:
+        bias = synth.zipf_bias(cfg.seed, E)
+        d_h[:, -1] = 1.0
+        w[-1, :] = bias
+    d_w = torch.from_numpy(w).cuda()
+    layer = DeviceExpertLayer(payload, scale, zp, H, I)
+    block = MoEBlock(layer, k, limbs_x=args.limbs, limbs_z=args.limbs)
+    torch.cuda.synchronize()
+    log(f"[bench] setup {time.time() - t0:.1f}s", q)
+
+    # events: per step HM_BLOCK_EVENTS stage marks + overall start/stop
+    def new_event():
+        h = C.c_void_p()
+        capi.call("hm_event_create", C.byref(h))
+        return h.value
+
+    stage_ev = [[new_event() for _ in range(capi.HM_BLOCK_EVENTS)] for _ in range(args.steps)]
+    ev_start, ev_stop = new_event(), new_event()
+
+    for _ in range(args.warmup):
+        block.launch(d_h, d_w)
+    torch.cuda.synchronize()
+    log(f"[bench] warmup {args.warmup} done", q)
+
+    torch.cuda.synchronize()
+    capi.call("hm_event_record", ev_start, stream)
+    for i in range(args.steps):
+        block.launch(d_h, d_w, events=stage_ev[i])
+    capi.call("hm_event_record", ev_stop, stream)
+    torch.cuda.synchronize()
+    ms = C.c_float()
+    capi.call("hm_event_elapsed_ms", C.byref(ms), ev_start, ev_stop)
+    total_ms = ms.value
+    ms_per_step = total_ms / args.steps
+    names = ["route", "permute", "quantize", "gate_up", "down", "combine"]
+    stage = {n: 0.0 for n in names}
+    for i in range(args.steps):
+        for j, n in enumerate(names):
+            capi.call("hm_event_elapsed_ms", C.byref(ms), stage_ev[i][j], stage_ev[i][j + 1])
+            stage[n] += ms.value / args.steps
+    log(f"[bench] timed {args.steps} steps: {ms_per_step:.4f} ms/step", q)
+
+    # one checked call: routing stats + parity of a token sample
+    res = block.execute_batch(d_h, d_w)
+    counts = res.counts
+    unique = int((counts > 0).sum())
+    h_host = d_h.cpu().numpy()
+    out = res.output.cpu().numpy()
+    tokens_per_s = T / (ms_per_step / 1e3)
+
+    if cfg.int8:
+        gu_ops = 2 * T * k * 2 * H * I
+        dn_ops = 2 * T * k * H * I
+        gu_bytes = unique * 2 * H * I + T * H * args.limbs + T * k * I * args.limbs
+    else:
+        gu_ops = 2 * T * k * 2 * H * I
+        dn_ops = 2 * T * k * H * I
+        gu_bytes = unique * 2 * H * I * 4 + T * H * 4 + T * k * I * 4
+    prefill = T >= 256
+    gu_s = stage["gate_up"] / 1e3
+    if prefill:
+        achieved = gu_ops / gu_s / 1e12
+        peak = PEAK_INT8_TOPS if cfg.int8 else PEAK_FP32_TFLOPS
+        roof = {"bound": "mfma", "kernel": "gateup_i8_mfma_kernel" if cfg.int8 else "gateup_f32_kernel",
+                "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
+                "frac": round(achieved / peak, 4), "traffic": None,
+                "work_per_launch": gu_ops, "launch_ms": round(stage["gate_up"], 5),
+                "hw_mfma_frac_with_limbs": round(achieved * (args.limbs if cfg.int8 else 1) / peak, 4)}
+    else:
+        achieved = gu_bytes / gu_s / 1e9
+        roof = {"bound": "hbm", "kernel": "gateup_i8_mfma_kernel" if cfg.int8 else "gateup_f32_kernel",
+                "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                "work_per_launch": gu_bytes, "launch_ms": round(stage["gate_up"], 5)}
+    layer_bytes = synth.algorithmic_bytes(cfg, unique)
+    layer_ops = synth.algorithmic_ops(cfg)
+    layer = {"hbm_frac": round(layer_bytes / (ms_per_step / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
+             "mfma_frac": round(layer_ops / (ms_per_step / 1e3) / 1e12 /
+                                (PEAK_INT8_TOPS if cfg.int8 else PEAK_FP32_TFLOPS), 4),
+             "algorithmic_bytes": layer_bytes, "algorithmic_ops": layer_ops}
+
+    cpu = None
+    sample = args.cpu_sample
+    if sample < 0:
+        sample = min(T, 160 if cfg.int8 else 32)
+    parity = None
+    if sample > 0:
+        sys.path.insert(0, str(REPO / "oracle"))
+        import hm_oracle as O
+        hs = np.ascontiguousarray(h_host[:sample])
+        t1 = time.time()
+        rout, rids, _ = O.moe_block(payload, scale, zp, hs, w, k, I)
+        dt = time.time() - t1
+        cpu = {"value": round(sample / dt, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
+               "sample": f"first {sample} of the {T} tokens of {cfg.name} (same weights and "
+                         f"router), oracle restatement of the reference CPU path "
+                         f"(MoERuntime CPU branch, single thread, -O3 -ffp-contract=off), "
+                         f"{dt:.1f}s on {os.cpu_count()} host cores"}
+        ids_ok = bool(np.array_equal(res.ids[:sample], rids))
+        d = np.abs(out[:sample].astype(np.float64) - rout)
+        parity = {"tokens_checked": sample, "ids_bitexact": ids_ok,
+                  "normwise_vs_reference": float(d.max() / max(np.abs(rout).max(), 1e-30)),
+                  "compare_1e-4": bool(np.all(d <= 1e-4 + 1e-4 * np.abs(rout)))}
+        log(f"[bench] cpu baseline {cpu['value']} tokens/s; parity {parity}", q)
+
+    line = {
+        "metric": METRIC, "value": round(tokens_per_s, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8" if cfg.int8 else "fp32", "data": "synthetic",
+        "config": {"workload": cfg.name, "tokens": T, "hidden": H, "experts": E,
+                   "intermediate": I, "top_k": k, "weights": "int8" if cfg.int8 else "fp32",
+                   "skewed_routing": cfg.skew, "limbs": args.limbs if cfg.int8 else None,
+                   "unique_experts": unique, "max_expert_rows": int(counts.max())},
+        "roofline": roof, "layer_roofline": layer,
+        "stages_ms": {n: round(v, 5) for n, v in stage.items()},
+        "cpu_baseline": cpu, "parity": parity,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,226 @@
+// hm_block.hip -- the fused MoE block entry (MoERuntime::executeBatch,
+// src/core/runtime/MoERuntime.cpp:58-349, with every expert device
+// resident) and the host-side INT8 packer.
+#include "hm_device.h"
+
+#include <limits.h>
+#include <math.h>
+
+int hm_launch_quantize_rows(const float* x, int64_t rows, int64_t n, int32_t limbs,
+                            int8_t* digits, float* scales, int32_t* dsum,
+                            hipStream_t stream);
+bool hm_use_mfma(const hm_layer* layer, int32_t lx, int32_t lz, bool force_generic);
+int hm_launch_gateup_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int8_t* xdig,
+                        const float* xscale, const int32_t* xdsum, int64_t tokens,
+                        const int32_t* counts, const int32_t* offsets,
+                        const int32_t* perm_tokens, int64_t R, int8_t* zdig, float* zscale,
+                        int32_t* zdsum, float* zf, bool force_generic, hipStream_t stream);
+int hm_launch_down_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int32_t* counts,
+                      const int32_t* offsets, int64_t R, const int8_t* zdig,
+                      const float* zscale, const int32_t* zdsum, float* y,
+                      bool force_generic, hipStream_t stream);
+int hm_launch_gateup_f32(const hm_layer* layer, const float* hidden, const int32_t* counts,
+                         const int32_t* offsets, const int32_t* perm_tokens, int64_t R,
+                         float* zf, hipStream_t stream);
+int hm_launch_down_f32(const hm_layer* layer, const int32_t* counts, const int32_t* offsets,
+                       int64_t R, const float* zf, float* y, hipStream_t stream);
+bool hm_mfma_shape_ok(int64_t H, int64_t I);
+
+namespace {
+
+constexpr size_t kAlign = 256;
+
+// Clears the workspace status word (a kernel, not a memset node, so the
+// sequence stays safe to capture in a HIP graph).
+__global__ void zero_status_kernel(int32_t* status) { *status = 0; }
+
+size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
+
+// Sequential carve of the workspace; every region 256-byte aligned.
+struct Carve {
+    char* base;
+    size_t used = 0;
+    explicit Carve(void* b) : base(static_cast<char*>(b)) {}
+    template <typename T>
+    T* take(size_t count) {
+        T* p = base ? reinterpret_cast<T*>(base + used) : nullptr;
+        used += align_up(count * sizeof(T));
+        return p;
+    }
+};
+
+struct BlockPlan {
+    void* route_ws;
+    uint32_t* ids;
+    float* scores;
+    int32_t* offsets;
+    int32_t* perm_tokens;
+    float* perm_weights;
+    int32_t* slots;
+    int8_t* xdig;
+    float* xscale;
+    int32_t* xdsum;
+    int8_t* zdig;
+    float* zscale;
+    int32_t* zdsum;
+    float* zf;
+    float* y;
+    int32_t* status;
+};
+
+bool layer_valid(const hm_layer* L) {
+    if (!L || !L->packed || L->experts <= 0 || L->hidden <= 0 || L->intermediate <= 0)
+        return false;
+    if (L->dtype == HM_DTYPE_INT8) return L->scale && L->zero_point;
+    return L->dtype == HM_DTYPE_FP32;
+}
+
+// Lays the workspace out; with base == nullptr only computes the size.
+size_t plan_block(const hm_layer* L, int64_t T, int32_t k, int32_t lx, int32_t lz,
+                  bool generic, void* base, BlockPlan* p) {
+    const int64_t H = L->hidden, I = L->intermediate, E = L->experts;
+    const int64_t P = T * k;
+    const int64_t nb = (I + 127) / 128;
+    Carve c(base);
+    BlockPlan q{};
+    q.route_ws = c.take<char>(hm_route_workspace_bytes(T, E));
+    q.ids = c.take<uint32_t>((size_t)P);
+    q.scores = c.take<float>((size_t)P);
+    q.offsets = c.take<int32_t>((size_t)E + 1);
+    q.perm_tokens = c.take<int32_t>((size_t)P);
+    q.perm_weights = c.take<float>((size_t)P);
+    q.slots = c.take<int32_t>((size_t)P);
+    q.status = c.take<int32_t>(1);
+    if (L->dtype == HM_DTYPE_INT8) {
+        q.xdig = c.take<int8_t>((size_t)lx * T * H);
+        q.xscale = c.take<float>((size_t)T);
+        q.xdsum = c.take<int32_t>((size_t)lx * T);
+        q.zdig = c.take<int8_t>((size_t)lz * P * I);
+        q.zscale = c.take<float>((size_t)P * nb);
+        q.zdsum = c.take<int32_t>((size_t)lz * P * nb);
+        q.zf = hm_use_mfma(L, lx, lz, generic) ? nullptr : c.take<float>((size_t)P * I);
+    } else {
+        q.zf = c.take<float>((size_t)P * I);
+    }
+    q.y = c.take<float>((size_t)P * H);
+    if (p) *p = q;
+    return c.used;
+}
+
+}  // namespace
+
+int32_t* hm_route_counts_ptr(void* route_ws, int64_t tokens, int64_t experts);
+
+extern "C" {
+
+size_t hm_moe_block_workspace_bytes(const hm_layer* layer, int64_t tokens, int32_t top_k,
+                                    int32_t limbs_x, int32_t limbs_z, uint32_t exec_flags) {
+    if (!layer_valid(layer) || tokens <= 0 || top_k <= 0) return 0;
+    const bool generic = (exec_flags & HM_EXEC_GENERIC) != 0;
+    return plan_block(layer, tokens, top_k, limbs_x, limbs_z, generic, nullptr, nullptr) + kAlign;
+}
+
+int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float* router_w,
+                         int64_t tokens, int32_t top_k, uint32_t route_flags,
+                         int32_t limbs_x, int32_t limbs_z, const hm_block_io* io,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+    HM_REQUIRE(layer_valid(layer) && hidden && router_w && io && io->out && workspace);
+    HM_REQUIRE(tokens > 0 && top_k > 0 && top_k <= layer->experts);
+    if (layer->dtype == HM_DTYPE_INT8) {
+        HM_REQUIRE(limbs_x >= 1 && limbs_x <= 3 && limbs_z >= 1 && limbs_z <= 3);
+        if (layer->hidden > 65536 || layer->intermediate > 65536) return HM_ERR_OVERFLOW;
+    }
+    if (tokens > INT_MAX / top_k) return HM_ERR_OVERFLOW;
+    const bool generic = (route_flags & HM_EXEC_GENERIC) != 0;
+    void* base = reinterpret_cast<void*>(
+        (reinterpret_cast<uintptr_t>(workspace) + kAlign - 1) & ~(uintptr_t)(kAlign - 1));
+    const size_t need = plan_block(layer, tokens, top_k, limbs_x, limbs_z, generic, nullptr, nullptr);
+    HM_REQUIRE(workspace_bytes >= need + (size_t)(static_cast<char*>(base) - static_cast<char*>(workspace)));
+    BlockPlan p;
+    plan_block(layer, tokens, top_k, limbs_x, limbs_z, generic, base, &p);
+    if (io->ids) p.ids = io->ids;
+    if (io->scores) p.scores = io->scores;
+    if (io->offsets) p.offsets = io->offsets;
+    if (io->perm_tokens) p.perm_tokens = io->perm_tokens;
+    if (io->perm_weights) p.perm_weights = io->perm_weights;
+    if (io->expert_out) p.y = io->expert_out;
+    int32_t* status = io->status ? io->status : p.status;
+    hipStream_t s = hm_stream(stream);
+    hipEvent_t ev[HM_BLOCK_EVENTS] = {};
+    if (io->events) {
+        for (int i = 0; i < HM_BLOCK_EVENTS; ++i) ev[i] = static_cast<hipEvent_t>(io->events[i]);
+    }
+    auto mark = [&](int i) -> int {
+        if (ev[i]) HM_HIP(hipEventRecord(ev[i], s));
+        return HM_OK;
+    };
+    int rc = mark(0);
+    if (rc) return rc;
+    if (!io->status) {
+        hipLaunchKernelGGL(zero_status_kernel, dim3(1), dim3(1), 0, s, status);
+        HM_LAUNCHED();
+    }
+    const int64_t E = layer->experts, H = layer->hidden;
+    const int64_t P = tokens * top_k;
+    rc = hm_router_topk(hidden, router_w, tokens, H, E, top_k, route_flags & 3u, p.ids,
+                        p.scores, nullptr, status, p.route_ws, stream);
+    if (rc || (rc = mark(1))) return rc;
+    rc = hm_permute(p.ids, p.scores, tokens, top_k, E, p.route_ws, nullptr, p.offsets,
+                    p.perm_tokens, p.perm_weights, p.slots, stream);
+    if (rc || (rc = mark(2))) return rc;
+    const int32_t* counts = hm_route_counts_ptr(p.route_ws, tokens, E);
+    if (layer->dtype == HM_DTYPE_INT8) {
+        rc = hm_launch_quantize_rows(hidden, tokens, H, limbs_x, p.xdig, p.xscale, p.xdsum, s);
+        if (rc || (rc = mark(3))) return rc;
+        rc = hm_launch_gateup_i8(layer, limbs_x, limbs_z, p.xdig, p.xscale, p.xdsum, tokens,
+                                 counts, p.offsets, p.perm_tokens, P, p.zdig, p.zscale,
+                                 p.zdsum, p.zf, generic, s);
+        if (rc || (rc = mark(4))) return rc;
+        rc = hm_launch_down_i8(layer, limbs_x, limbs_z, counts, p.offsets, P, p.zdig,
+                               p.zscale, p.zdsum, p.y, generic, s);
+    } else {
+        if ((rc = mark(3))) return rc;
+        rc = hm_launch_gateup_f32(layer, hidden, counts, p.offsets, p.perm_tokens, P, p.zf, s);
+        if (rc || (rc = mark(4))) return rc;
+        rc = hm_launch_down_f32(layer, counts, p.offsets, P, p.zf, p.y, s);
+    }
+    if (rc || (rc = mark(5))) return rc;
+    rc = hm_combine(p.y, p.ids, p.slots, p.scores, tokens, top_k, H, io->residual, io->out,
+                    stream);
+    if (rc || (rc = mark(6))) return rc;
+    if (io->counts) {
+        HM_HIP(hipMemcpyAsync(io->counts, counts, (size_t)E * sizeof(int32_t),
+                              hipMemcpyDeviceToDevice, s));
+    }
+    return HM_OK;
+}
+
+// Quantization.cpp:45-79 on the host: the reference's deterministic
+// per-projection affine packer (scale = max|w|/127, zp = 0, round half away
+// from zero, clamp to [-127, 127]).
+int hm_quantize_int8_host(const float* w, int64_t n, int8_t* q, float* scale,
+                          int32_t* zero_point, float* max_abs_error) {
+    HM_REQUIRE(w && q && scale && zero_point && n > 0);
+    float maximum = 0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+        if (!std::isfinite(w[i])) return HM_ERR_INVALID;
+        const float m = fabsf(w[i]);
+        if (m > maximum) maximum = m;
+    }
+    const float s = maximum == 0.0f ? 1.0f : maximum / 127.0f;
+    float err = 0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+        float r = roundf(w[i] / s);
+        r = r < -127.0f ? -127.0f : (r > 127.0f ? 127.0f : r);
+        q[i] = (int8_t)r;
+        const float rec = (float)(int32_t)q[i] * s;
+        const float d = fabsf(w[i] - rec);
+        if (d > err) err = d;
+    }
+    *scale = s;
+    *zero_point = 0;
+    if (max_abs_error) *max_abs_error = err;
+    return HM_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,112 @@
+// hm_device.h -- device helpers shared by the gfx950 kernels.
+//
+// Wave64 reductions, the device restatement of glibc 2.35 expf, and the
+// integer-limb fixed-point split used by the INT8 expert GEMMs.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cmath>
+
+#include "hm_moe.h"
+
+#define HM_WAVE 64
+
+// Error plumbing shared by all launchers (defined in hm_runtime.hip).
+void hm_record_hip_error(hipError_t e);
+#define HM_HIP(expr)                                   \
+    do {                                               \
+        hipError_t hm_e_ = (expr);                     \
+        if (hm_e_ != hipSuccess) {                     \
+            hm_record_hip_error(hm_e_);                \
+            return HM_ERR_RUNTIME;                     \
+        }                                              \
+    } while (0)
+#define HM_LAUNCHED() HM_HIP(hipGetLastError())
+#define HM_REQUIRE(cond) \
+    do { if (!(cond)) return HM_ERR_INVALID; } while (0)
+
+static inline hipStream_t hm_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+// ---------------------------------------------------------------------------
+// Wave64 reductions (all 64 lanes must be active).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float hm_wave_max_f32(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, HM_WAVE));
+    return v;
+}
+
+__device__ __forceinline__ double hm_wave_sum_f64(double v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, HM_WAVE);
+    return v;
+}
+
+__device__ __forceinline__ int hm_wave_sum_i32(int v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, HM_WAVE);
+    return v;
+}
+
+__device__ __forceinline__ unsigned long long hm_wave_max_u64(unsigned long long v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        unsigned long long o = __shfl_xor(v, m, HM_WAVE);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// glibc 2.35 expf restated for host and device (hm_expf.h); matches the host
+// libm expf on every float input (exhaustive check, tests/test_expf_parity.py).
+#include "hm_expf.h"
+
+// SiLU exactly as src/tensor/activation/Activation.cpp:44 computes it:
+// value / (1 + expf(-value)) in float.
+__device__ __forceinline__ float hm_silu(float v) {
+    return __fdiv_rn(v, __fadd_rn(1.0f, hm_expf(-v)));
+}
+
+// ---------------------------------------------------------------------------
+// Integer-limb fixed point (build-owned numeric format).
+//   range(L) = 127 * (256^L - 1) / 255
+//   inv = range / amax, s = amax / range (float divisions)
+//   n   = clamp(rint(x * inv), -range, range)
+//   n   = sum_l d_l 256^l with balanced digits d_l in [-128, 127]
+// ---------------------------------------------------------------------------
+__host__ __device__ __forceinline__ int hm_limb_range(int limbs) {
+    return limbs == 1 ? 127 : limbs == 2 ? 32639 : 8355711;
+}
+
+__device__ __forceinline__ int hm_fixed_point(float x, float inv, float range) {
+    float v = rintf(__fmul_rn(x, inv));
+    v = fminf(fmaxf(v, -range), range);
+    return (int)v;
+}
+
+// Digit l of n (l = 0 least significant).
+__device__ __forceinline__ int hm_digit(int n, int l) {
+    int d = 0;
+    for (int i = 0; i <= l; ++i) {
+        d = ((n + 128) & 255) - 128;
+        n = (n - d) / 256;
+    }
+    return d;
+}
+
+// c = (float)P_{L-1}; c = fmaf(c, 256, (float)P_l) for l = L-2 .. 0.
+__device__ __forceinline__ float hm_recombine(const int* p, int limbs) {
+    float c = (float)p[limbs - 1];
+    for (int l = limbs - 2; l >= 0; --l) c = __builtin_fmaf(c, 256.0f, (float)p[l]);
+    return c;
+}
+
+// Float total order key for top-k: larger score first, equal scores (with
+// -0 == +0) broken by the lower expert id; 0 is never a valid key.
+__device__ __forceinline__ unsigned long long hm_rank_key(float v, unsigned int id) {
+    unsigned int u = v == 0.0f ? 0u : __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (0xffffffffu - id);
+}

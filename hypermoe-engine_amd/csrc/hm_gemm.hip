@@ -1,0 +1,1046 @@
+// hm_gemm.hip -- expert GEMM kernels for gfx950.
+//
+// INT8 experts (W8A32 in the reference, CpuTensorBackend.cpp:173-186) run on
+// INT8 MFMA through the integer-limb format (hm_device.h): activations are
+// fixed point split into L balanced signed INT8 digit planes, one
+// v_mfma_i32_16x16x64_i8 per plane, exact int32 partials, recombined in the
+// epilogue.  The generic kernels compute the identical integers with scalar
+// loops; they serve shapes the MFMA tiles do not cover and pin the MFMA
+// kernels in tests (bit-for-bit).
+//
+// Packed expert layout (hm_pack_layer): expert e at e*3*H*I elements:
+//   gate^T [I x H] | up^T [I x H] | down^T [H x I]   (K contiguous per row)
+#include "hm_device.h"
+
+#include <limits.h>
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kZBlock = 128;       // columns of Z per fixed-point segment
+constexpr int kTileM = 64;         // rows per MFMA workgroup tile
+constexpr int kGateUpN = 128;      // columns per projection per gate/up tile
+constexpr int kDownN = 256;        // output columns per down tile
+constexpr int kStepK = 64;         // K per MFMA step
+constexpr int kLdsRow = kStepK + 16;  // padded LDS row (bytes)
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// Which expert and tile of that expert does workgroup `tile` own?  Tiles of
+// expert e are ceil(counts[e]/tile_m), experts in ascending id.  Returns
+// false when `tile` is past the last tile.  Executed by every thread (the
+// counts are tiny and cached).
+__device__ bool locate_tile(const int32_t* __restrict__ counts, int64_t experts,
+                            int tile_m, int64_t tile, int64_t* expert_out,
+                            int64_t* tile_in_expert) {
+    int64_t acc = 0;
+    for (int64_t e = 0; e < experts; ++e) {
+        const int64_t n = (counts[e] + tile_m - 1) / tile_m;
+        if (tile < acc + n) {
+            *expert_out = e;
+            *tile_in_expert = tile - acc;
+            return true;
+        }
+        acc += n;
+    }
+    return false;
+}
+
+// ---------------------------------------------------------------------------
+// Activation rows -> digit planes (one wave per row segment).
+// digits [L][rows][n] (row stride n), scales [rows], dsum [L][rows].
+// ---------------------------------------------------------------------------
+template <int L>
+__global__ __launch_bounds__(kBlock) void limb_quantize_rows_kernel(
+    const float* __restrict__ x, int64_t rows, int64_t n,
+    int8_t* __restrict__ digits, float* __restrict__ scales,
+    int32_t* __restrict__ dsum) {
+    const int lane = threadIdx.x & (HM_WAVE - 1);
+    const int64_t r = (int64_t)blockIdx.x * (kBlock / HM_WAVE) + threadIdx.x / HM_WAVE;
+    if (r >= rows) return;
+    const float* xr = x + r * n;
+    float amax = 0.0f;
+    for (int64_t k = lane; k < n; k += HM_WAVE) amax = fmaxf(amax, fabsf(xr[k]));
+    amax = hm_wave_max_f32(amax);
+    const float range = (float)hm_limb_range(L);
+    const float inv = amax > 0.0f ? __fdiv_rn(range, amax) : 0.0f;
+    int dl[L];
+#pragma unroll
+    for (int l = 0; l < L; ++l) dl[l] = 0;
+    for (int64_t k = lane; k < n; k += HM_WAVE) {
+        const int v = hm_fixed_point(xr[k], inv, range);
+#pragma unroll
+        for (int l = 0; l < L; ++l) {
+            const int d = hm_digit(v, l);
+            digits[((int64_t)l * rows + r) * n + k] = (int8_t)d;
+            dl[l] += d;
+        }
+    }
+#pragma unroll
+    for (int l = 0; l < L; ++l) {
+        const int s = hm_wave_sum_i32(dl[l]);
+        if (lane == 0 && dsum) dsum[(int64_t)l * rows + r] = s;
+    }
+    if (lane == 0) scales[r] = amax > 0.0f ? __fdiv_rn(amax, range) : 0.0f;
+}
+
+// Exact limb partials against a packed [cols x inner] INT8 matrix (test hook
+// and reference semantics for the MFMA kernels).
+__global__ void limb_partials_kernel(const int8_t* __restrict__ digits,
+                                     int64_t rows, int64_t inner, int32_t limbs,
+                                     const int8_t* __restrict__ qp, int32_t zp,
+                                     int64_t cols, int32_t* __restrict__ out) {
+    const int64_t idx = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    const int64_t total = (int64_t)limbs * rows * cols;
+    if (idx >= total) return;
+    const int64_t c = idx % cols;
+    const int64_t lr = idx / cols;  // l*rows + r
+    const int8_t* d = digits + lr * inner;
+    const int8_t* q = qp + c * inner;
+    int acc = 0;
+    for (int64_t k = 0; k < inner; ++k) acc += (int)d[k] * ((int)q[k] - zp);
+    out[idx] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// Generic INT8 expert path (any shape).  Same integers and float operation
+// sequence as the MFMA kernels.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int64_t group_of_row(const int32_t* __restrict__ offsets,
+                                                int64_t experts, int64_t row) {
+    int64_t lo = 0, hi = experts;  // find e with offsets[e] <= row < offsets[e+1]
+    while (hi - lo > 1) {
+        const int64_t mid = (lo + hi) / 2;
+        if (offsets[mid] <= row) lo = mid; else hi = mid;
+    }
+    return lo;
+}
+
+template <int L>
+__global__ void gateup_generic_kernel(
+    const int8_t* __restrict__ xdig, const float* __restrict__ xscale,
+    int64_t tokens, int64_t H, int64_t I, int64_t experts,
+    const int8_t* __restrict__ packed, const float* __restrict__ scale,
+    const int32_t* __restrict__ zp, const int32_t* __restrict__ offsets,
+    const int32_t* __restrict__ perm_tokens, int64_t R, float* __restrict__ zf) {
+    const int64_t idx = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (idx >= R * I) return;
+    const int64_t row = idx / I, col = idx % I;
+    const int64_t e = group_of_row(offsets, experts, row);
+    const int64_t t = perm_tokens[row];
+    const int8_t* qg = packed + e * 3 * H * I + col * H;
+    const int8_t* qu = qg + H * I;
+    const int zg = zp[e * 3 + 0], zu = zp[e * 3 + 1];
+    int pg[L], pu[L];
+#pragma unroll
+    for (int l = 0; l < L; ++l) {
+        const int8_t* d = xdig + ((int64_t)l * tokens + t) * H;
+        int ag = 0, au = 0;
+        for (int64_t k = 0; k < H; ++k) {
+            ag += (int)d[k] * ((int)qg[k] - zg);
+            au += (int)d[k] * ((int)qu[k] - zu);
+        }
+        pg[l] = ag;
+        pu[l] = au;
+    }
+    const float sx = xscale[t];
+    const float g = __fmul_rn(hm_recombine(pg, L), __fmul_rn(sx, scale[e * 3 + 0]));
+    const float u = __fmul_rn(hm_recombine(pu, L), __fmul_rn(sx, scale[e * 3 + 1]));
+    zf[idx] = __fmul_rn(hm_silu(g), u);
+}
+
+// Z [R x I] float -> digit planes per 128-column segment (one wave each).
+template <int L>
+__global__ __launch_bounds__(kBlock) void zquant_generic_kernel(
+    const float* __restrict__ zf, int64_t R, int64_t I, int8_t* __restrict__ zdig,
+    float* __restrict__ zscale, int32_t* __restrict__ zdsum) {
+    const int lane = threadIdx.x & (HM_WAVE - 1);
+    const int64_t nb = (I + kZBlock - 1) / kZBlock;
+    const int64_t seg = (int64_t)blockIdx.x * (kBlock / HM_WAVE) + threadIdx.x / HM_WAVE;
+    if (seg >= R * nb) return;
+    const int64_t row = seg / nb, b = seg % nb;
+    const int64_t k0 = b * kZBlock;
+    const int64_t kn = (I - k0) < kZBlock ? (I - k0) : kZBlock;
+    const float* zr = zf + row * I + k0;
+    float amax = 0.0f;
+    for (int64_t k = lane; k < kn; k += HM_WAVE) amax = fmaxf(amax, fabsf(zr[k]));
+    amax = hm_wave_max_f32(amax);
+    const float range = (float)hm_limb_range(L);
+    const float inv = amax > 0.0f ? __fdiv_rn(range, amax) : 0.0f;
+    int dl[L];
+#pragma unroll
+    for (int l = 0; l < L; ++l) dl[l] = 0;
+    for (int64_t k = lane; k < kn; k += HM_WAVE) {
+        const int v = hm_fixed_point(zr[k], inv, range);
+#pragma unroll
+        for (int l = 0; l < L; ++l) {
+            const int d = hm_digit(v, l);
+            zdig[((int64_t)l * R + row) * I + k0 + k] = (int8_t)d;
+            dl[l] += d;
+        }
+    }
+#pragma unroll
+    for (int l = 0; l < L; ++l) {
+        const int s = hm_wave_sum_i32(dl[l]);
+        if (lane == 0) zdsum[((int64_t)l * R + row) * nb + b] = s;
+    }
+    if (lane == 0) zscale[row * nb + b] = amax > 0.0f ? __fdiv_rn(amax, range) : 0.0f;
+}
+
+template <int L>
+__global__ void down_generic_kernel(
+    const int8_t* __restrict__ zdig, const float* __restrict__ zscale, int64_t R,
+    int64_t H, int64_t I, int64_t experts, const int8_t* __restrict__ packed,
+    const float* __restrict__ scale, const int32_t* __restrict__ zp,
+    const int32_t* __restrict__ offsets, float* __restrict__ y) {
+    const int64_t idx = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (idx >= R * H) return;
+    const int64_t row = idx / H, col = idx % H;
+    const int64_t e = group_of_row(offsets, experts, row);
+    const int8_t* qd = packed + e * 3 * H * I + 2 * H * I + col * I;
+    const int zd = zp[e * 3 + 2];
+    const float sd = scale[e * 3 + 2];
+    const int64_t nb = (I + kZBlock - 1) / kZBlock;
+    float acc = 0.0f;
+    for (int64_t b = 0; b < nb; ++b) {
+        const int64_t k0 = b * kZBlock;
+        const int64_t k1 = (k0 + kZBlock) < I ? (k0 + kZBlock) : I;
+        int p[L];
+#pragma unroll
+        for (int l = 0; l < L; ++l) {
+            const int8_t* d = zdig + ((int64_t)l * R + row) * I;
+            int a = 0;
+            for (int64_t k = k0; k < k1; ++k) a += (int)d[k] * ((int)qd[k] - zd);
+            p[l] = a;
+        }
+        const float alpha = __fmul_rn(zscale[row * nb + b], sd);
+        acc = __builtin_fmaf(hm_recombine(p, L), alpha, acc);
+    }
+    y[idx] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// MFMA gate/up kernel.  Workgroup tile: 64 grouped rows of one expert x 128
+// columns of gate and the same 128 columns of up.  Wave w owns columns
+// [32w, 32w+32) of both projections, so the G and U values of an output
+// element sit in the same lane.  A (activation digits, gathered through
+// perm_tokens) is staged in LDS; B fragments stream from HBM straight into
+// registers in MFMA layout (lane l: column l%16, 16 K bytes 16*(l/16)).
+// Epilogue: z = silu(g) * u, then the 128-column fixed-point segment of Z
+// for each row is quantised to digits (amax across the four waves via LDS).
+// ---------------------------------------------------------------------------
+template <int L>
+__global__ __launch_bounds__(kBlock) void gateup_i8_mfma_kernel(
+    const int8_t* __restrict__ xdig, const float* __restrict__ xscale,
+    const int32_t* __restrict__ xdsum, int64_t tokens, int64_t H, int64_t I,
+    int64_t experts, const int8_t* __restrict__ packed,
+    const float* __restrict__ scale, const int32_t* __restrict__ zp,
+    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
+    const int32_t* __restrict__ perm_tokens, int64_t R, int8_t* __restrict__ zdig,
+    float* __restrict__ zscale, int32_t* __restrict__ zdsum) {
+    __shared__ __attribute__((aligned(16))) int8_t lds_a[L][kTileM][kLdsRow];
+    __shared__ float red[kTileM][4];
+    __shared__ int red_i[L][kTileM][4];
+    __shared__ int32_t row_token[kTileM];
+    const int tid = threadIdx.x;
+    const int lane = tid & (HM_WAVE - 1);
+    const int wave = tid / HM_WAVE;
+    int64_t e, mt;
+    if (!locate_tile(counts, experts, kTileM, blockIdx.x, &e, &mt)) return;
+    const int64_t g0 = offsets[e] + mt * kTileM;
+    const int nrows = (int)min((int64_t)kTileM, (int64_t)counts[e] - mt * kTileM);
+    const int64_t n0 = (int64_t)blockIdx.y * kGateUpN;
+    if (tid < kTileM) row_token[tid] = tid < nrows ? perm_tokens[g0 + tid] : -1;
+    __syncthreads();
+    // A loader: thread -> (row = tid/4, 16-byte segment = tid%4)
+    const int a_row = tid >> 2, a_seg = tid & 3;
+    const int a_tok = row_token[a_row];
+    // B fragment base pointers: j = 0,1 gate; j = 2,3 up.
+    const int8_t* ebase = packed + e * 3 * H * I;
+    const int8_t* bptr[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t col = n0 + 32 * wave + 16 * (j & 1) + (lane & 15);
+        bptr[j] = ebase + (j >> 1) * H * I + col * H + 16 * (lane >> 4);
+    }
+    v4i acc[4][4][L];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int l = 0; l < L; ++l) acc[i][j][l] = v4i{0, 0, 0, 0};
+
+    for (int64_t k0 = 0; k0 < H; k0 += kStepK) {
+        v4i b[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const v4i*>(bptr[j] + k0);
+#pragma unroll
+        for (int l = 0; l < L; ++l) {
+            v4i v = v4i{0, 0, 0, 0};
+            if (a_tok >= 0) {
+                v = *reinterpret_cast<const v4i*>(
+                    xdig + ((int64_t)l * tokens + a_tok) * H + k0 + 16 * a_seg);
+            }
+            *reinterpret_cast<v4i*>(&lds_a[l][a_row][16 * a_seg]) = v;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int l = 0; l < L; ++l) {
+                const v4i a = *reinterpret_cast<const v4i*>(
+                    &lds_a[l][16 * i + (lane & 15)][16 * (lane >> 4)]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    acc[i][j][l] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[j], acc[i][j][l], 0, 0, 0);
+                }
+            }
+        }
+        __syncthreads();
+    }
+
+    // ---- epilogue -------------------------------------------------------
+    const float sg = scale[e * 3 + 0], su = scale[e * 3 + 1];
+    const int zg = zp[e * 3 + 0], zu = zp[e * 3 + 1];
+    float z[4][2][4];
+    float rmax[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int r = 16 * i + 4 * (lane >> 4) + q;
+            const int tok = row_token[r];
+            float m = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                float zv = 0.0f;
+                if (tok >= 0) {
+                    int pg[L], pu[L];
+#pragma unroll
+                    for (int l = 0; l < L; ++l) {
+                        const int ds = (zg | zu) ? xdsum[(int64_t)l * tokens + tok] : 0;
+                        pg[l] = acc[i][j][l][q] - zg * ds;
+                        pu[l] = acc[i][j + 2][l][q] - zu * ds;
+                    }
+                    const float sx = xscale[tok];
+                    const float g = __fmul_rn(hm_recombine(pg, L), __fmul_rn(sx, sg));
+                    const float u = __fmul_rn(hm_recombine(pu, L), __fmul_rn(sx, su));
+                    zv = __fmul_rn(hm_silu(g), u);
+                }
+                z[i][j][q] = zv;
+                m = fmaxf(m, fabsf(zv));
+            }
+            rmax[i][q] = m;
+        }
+    }
+    // row max across the 16 lanes of a row group, then across waves
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float m = rmax[i][q];
+#pragma unroll
+            for (int s = 1; s < 16; s <<= 1) m = fmaxf(m, __shfl_xor(m, s, HM_WAVE));
+            if ((lane & 15) == 0) red[16 * i + 4 * (lane >> 4) + q][wave] = m;
+        }
+    __syncthreads();
+    const float range = (float)hm_limb_range(L);
+    const int64_t nb = I / kZBlock;
+    const int64_t zb = n0 / kZBlock;
+    const int zd = zp[e * 3 + 2];
+    int dsum_part[4][4][L];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int r = 16 * i + 4 * (lane >> 4) + q;
+            const float amax = fmaxf(fmaxf(red[r][0], red[r][1]), fmaxf(red[r][2], red[r][3]));
+            const float inv = amax > 0.0f ? __fdiv_rn(range, amax) : 0.0f;
+#pragma unroll
+            for (int l = 0; l < L; ++l) dsum_part[i][q][l] = 0;
+            if (r < nrows) {
+                const int64_t grow = g0 + r;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int64_t col = n0 + 32 * wave + 16 * j + (lane & 15);
+                    const int v = hm_fixed_point(z[i][j][q], inv, range);
+#pragma unroll
+                    for (int l = 0; l < L; ++l) {
+                        const int d = hm_digit(v, l);
+                        zdig[((int64_t)l * R + grow) * I + col] = (int8_t)d;
+                        dsum_part[i][q][l] += d;
+                    }
+                }
+                if (wave == 0 && (lane & 15) == 0) {
+                    zscale[grow * nb + zb] = amax > 0.0f ? __fdiv_rn(amax, range) : 0.0f;
+                }
+            }
+        }
+    }
+    if (zd != 0) {  // digit sums per segment, needed only for a down zero point
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int l = 0; l < L; ++l) {
+                    int s = dsum_part[i][q][l];
+#pragma unroll
+                    for (int sh = 1; sh < 16; sh <<= 1) s += __shfl_xor(s, sh, HM_WAVE);
+                    if ((lane & 15) == 0) red_i[l][16 * i + 4 * (lane >> 4) + q][wave] = s;
+                }
+        __syncthreads();
+        if (tid < kTileM && tid < nrows) {
+#pragma unroll
+            for (int l = 0; l < L; ++l) {
+                zdsum[((int64_t)l * R + g0 + tid) * nb + zb] =
+                    red_i[l][tid][0] + red_i[l][tid][1] + red_i[l][tid][2] + red_i[l][tid][3];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA down kernel.  Workgroup tile: 64 contiguous grouped rows of one expert
+// x 256 output columns; wave w owns columns [64w, 64w+64).  K (= I) runs in
+// 64-wide MFMA steps; at the end of each 128-column Z segment the exact
+// int32 partials are recombined, scaled by that segment's s * scale_down and
+// accumulated in float with fmaf, segment by segment in ascending order.
+// ---------------------------------------------------------------------------
+template <int L>
+__global__ __launch_bounds__(kBlock) void down_i8_mfma_kernel(
+    const int8_t* __restrict__ zdig, const float* __restrict__ zscale,
+    const int32_t* __restrict__ zdsum, int64_t R, int64_t H, int64_t I,
+    int64_t experts, const int8_t* __restrict__ packed,
+    const float* __restrict__ scale, const int32_t* __restrict__ zp,
+    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
+    float* __restrict__ y) {
+    __shared__ __attribute__((aligned(16))) int8_t lds_a[L][kTileM][kLdsRow];
+    const int tid = threadIdx.x;
+    const int lane = tid & (HM_WAVE - 1);
+    const int wave = tid / HM_WAVE;
+    int64_t e, mt;
+    if (!locate_tile(counts, experts, kTileM, blockIdx.x, &e, &mt)) return;
+    const int64_t g0 = offsets[e] + mt * kTileM;
+    const int nrows = (int)min((int64_t)kTileM, (int64_t)counts[e] - mt * kTileM);
+    const int64_t n0 = (int64_t)blockIdx.y * kDownN;
+    const int a_row = tid >> 2, a_seg = tid & 3;
+    const int8_t* dbase = packed + e * 3 * H * I + 2 * H * I;
+    const int8_t* bptr[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t col = n0 + 64 * wave + 16 * j + (lane & 15);
+        bptr[j] = dbase + col * I + 16 * (lane >> 4);
+    }
+    const float sd = scale[e * 3 + 2];
+    const int zd = zp[e * 3 + 2];
+    const int64_t nb = I / kZBlock;
+    v4i acc[4][4][L];
+    float facc[4][4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int l = 0; l < L; ++l) acc[i][j][l] = v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) facc[i][j][q] = 0.0f;
+        }
+    for (int64_t k0 = 0; k0 < I; k0 += kStepK) {
+        v4i b[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const v4i*>(bptr[j] + k0);
+#pragma unroll
+        for (int l = 0; l < L; ++l) {
+            v4i v = v4i{0, 0, 0, 0};
+            if (a_row < nrows) {
+                v = *reinterpret_cast<const v4i*>(
+                    zdig + ((int64_t)l * R + g0 + a_row) * I + k0 + 16 * a_seg);
+            }
+            *reinterpret_cast<v4i*>(&lds_a[l][a_row][16 * a_seg]) = v;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int l = 0; l < L; ++l) {
+                const v4i a = *reinterpret_cast<const v4i*>(
+                    &lds_a[l][16 * i + (lane & 15)][16 * (lane >> 4)]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    acc[i][j][l] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[j], acc[i][j][l], 0, 0, 0);
+                }
+            }
+        }
+        __syncthreads();
+        if (((k0 + kStepK) % kZBlock) == 0) {  // end of a Z segment
+            const int64_t zb = (k0 + kStepK) / kZBlock - 1;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int r = 16 * i + 4 * (lane >> 4) + q;
+                    const int64_t grow = g0 + (r < nrows ? r : 0);
+                    const float alpha = __fmul_rn(zscale[grow * nb + zb], sd);
+                    int ds[L];
+#pragma unroll
+                    for (int l = 0; l < L; ++l) {
+                        ds[l] = zd ? zdsum[((int64_t)l * R + grow) * nb + zb] : 0;
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        int p[L];
+#pragma unroll
+                        for (int l = 0; l < L; ++l) {
+                            p[l] = acc[i][j][l][q] - zd * ds[l];
+                            acc[i][j][l][q] = 0;
+                        }
+                        facc[i][j][q] = __builtin_fmaf(hm_recombine(p, L), alpha, facc[i][j][q]);
+                    }
+                }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int r = 16 * i + 4 * (lane >> 4) + q;
+            if (r >= nrows) continue;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t col = n0 + 64 * wave + 16 * j + (lane & 15);
+                y[(g0 + r) * H + col] = facc[i][j][q];
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------
+// FP32 expert path (configs with FP32 weights).  Tiled FMA GEMMs, 64x64
+// output tiles, 4x4 outputs per thread, K staged through LDS in steps of 16.
+// ---------------------------------------------------------------------------
+constexpr int kF32Tile = 64;
+constexpr int kF32K = 16;
+
+__global__ __launch_bounds__(kBlock) void gateup_f32_kernel(
+    const float* __restrict__ x, int64_t H, int64_t I, int64_t experts,
+    const float* __restrict__ packed, const int32_t* __restrict__ counts,
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ perm_tokens,
+    float* __restrict__ zf) {
+    __shared__ float as[kF32K][kF32Tile + 1];
+    __shared__ float bg[kF32K][kF32Tile + 1];
+    __shared__ float bu[kF32K][kF32Tile + 1];
+    __shared__ int32_t row_token[kF32Tile];
+    const int tid = threadIdx.x;
+    int64_t e, mt;
+    if (!locate_tile(counts, experts, kF32Tile, blockIdx.x, &e, &mt)) return;
+    const int64_t g0 = offsets[e] + mt * kF32Tile;
+    const int nrows = (int)min((int64_t)kF32Tile, (int64_t)counts[e] - mt * kF32Tile);
+    const int64_t n0 = (int64_t)blockIdx.y * kF32Tile;
+    if (tid < kF32Tile) row_token[tid] = tid < nrows ? perm_tokens[g0 + tid] : -1;
+    __syncthreads();
+    const float* gbase = packed + e * 3 * H * I;
+    const float* ubase = gbase + H * I;
+    const int tr = tid / 16, tc = tid % 16;
+    float ag[4][4] = {}, au[4][4] = {};
+    for (int64_t k0 = 0; k0 < H; k0 += kF32K) {
+        for (int i = tid; i < kF32Tile * kF32K; i += kBlock) {
+            const int r = i / kF32K, kk = i % kF32K;
+            const int tok = row_token[r];
+            const int64_t k = k0 + kk;
+            as[kk][r] = (tok >= 0 && k < H) ? x[(int64_t)tok * H + k] : 0.0f;
+            const int64_t n = n0 + r;
+            const bool ok = n < I && k < H;
+            bg[kk][r] = ok ? gbase[n * H + k] : 0.0f;
+            bu[kk][r] = ok ? ubase[n * H + k] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kF32K; ++kk) {
+            float a[4], g[4], u[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a[i] = as[kk][tr + 16 * i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { g[j] = bg[kk][tc + 16 * j]; u[j] = bu[kk][tc + 16 * j]; }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    ag[i][j] = __builtin_fmaf(a[i], g[j], ag[i][j]);
+                    au[i][j] = __builtin_fmaf(a[i], u[j], au[i][j]);
+                }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = tr + 16 * i;
+        if (r >= nrows) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t n = n0 + tc + 16 * j;
+            if (n < I) zf[(g0 + r) * I + n] = __fmul_rn(hm_silu(ag[i][j]), au[i][j]);
+        }
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void down_f32_kernel(
+    const float* __restrict__ zf, int64_t H, int64_t I, int64_t experts,
+    const float* __restrict__ packed, const int32_t* __restrict__ counts,
+    const int32_t* __restrict__ offsets, float* __restrict__ y) {
+    __shared__ float as[kF32K][kF32Tile + 1];
+    __shared__ float bs[kF32K][kF32Tile + 1];
+    const int tid = threadIdx.x;
+    int64_t e, mt;
+    if (!locate_tile(counts, experts, kF32Tile, blockIdx.x, &e, &mt)) return;
+    const int64_t g0 = offsets[e] + mt * kF32Tile;
+    const int nrows = (int)min((int64_t)kF32Tile, (int64_t)counts[e] - mt * kF32Tile);
+    const int64_t n0 = (int64_t)blockIdx.y * kF32Tile;
+    const float* dbase = packed + e * 3 * H * I + 2 * H * I;
+    const int tr = tid / 16, tc = tid % 16;
+    float acc[4][4] = {};
+    for (int64_t k0 = 0; k0 < I; k0 += kF32K) {
+        for (int i = tid; i < kF32Tile * kF32K; i += kBlock) {
+            const int r = i / kF32K, kk = i % kF32K;
+            const int64_t k = k0 + kk;
+            as[kk][r] = (r < nrows && k < I) ? zf[(g0 + r) * I + k] : 0.0f;
+            const int64_t n = n0 + r;
+            bs[kk][r] = (n < H && k < I) ? dbase[n * I + k] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kF32K; ++kk) {
+            float a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a[i] = as[kk][tr + 16 * i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = bs[kk][tc + 16 * j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(a[i], b[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = tr + 16 * i;
+        if (r >= nrows) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t n = n0 + tc + 16 * j;
+            if (n < H) y[(g0 + r) * H + n] = acc[i][j];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Op-level GEMMs on the reference's [K x N] weight layout.
+// ---------------------------------------------------------------------------
+// Reference mode: one lane per output, K ascending, float multiply then add
+// with the dequantised weight float(q - zp) * scale: the reference loop
+// (CpuTensorBackend.cpp:173-186) operation for operation, hence bit-exact.
+__global__ void w8a32_reference_kernel(const float* __restrict__ x,
+                                       const int8_t* __restrict__ q, float scale,
+                                       int32_t zp, float* __restrict__ y,
+                                       int64_t rows, int64_t inner, int64_t cols) {
+    const int64_t idx = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (idx >= rows * cols) return;
+    const int64_t r = idx / cols, c = idx % cols;
+    float sum = 0.0f;
+    for (int64_t k = 0; k < inner; ++k) {
+        const float w = __fmul_rn((float)((int)q[k * cols + c] - zp), scale);
+        sum = __fadd_rn(sum, __fmul_rn(x[r * inner + k], w));
+    }
+    y[idx] = sum;
+}
+
+// Cooperative mode: bounded split-K.  Grid (ceil(N/64), M, P); partition p
+// covers the balanced K range [p*base + min(p, rem), ...); lane = column;
+// wave w accumulates k = begin + w, begin + w + 4, ... in order; the four
+// wave sums are added in fixed order ((w0 + w1) + w2) + w3.  P > 1 writes
+// partials that a second kernel adds in ascending p.  Deterministic.
+__global__ __launch_bounds__(kBlock) void w8a32_coop_kernel(
+    const float* __restrict__ x, const int8_t* __restrict__ q, float scale,
+    int32_t zp, float* __restrict__ out, int64_t rows, int64_t inner,
+    int64_t cols, int64_t parts) {
+    __shared__ float red[4][HM_WAVE];
+    const int lane = threadIdx.x & (HM_WAVE - 1);
+    const int wave = threadIdx.x / HM_WAVE;
+    const int64_t c = (int64_t)blockIdx.x * HM_WAVE + lane;
+    const int64_t r = blockIdx.y;
+    const int64_t p = blockIdx.z;
+    const int64_t base = inner / parts, rem = inner % parts;
+    const int64_t begin = p * base + (p < rem ? p : rem);
+    const int64_t end = begin + base + (p < rem ? 1 : 0);
+    float sum = 0.0f;
+    if (c < cols) {
+        for (int64_t k = begin + wave; k < end; k += 4) {
+            const float w = __fmul_rn((float)((int)q[k * cols + c] - zp), scale);
+            sum = __fadd_rn(sum, __fmul_rn(x[r * inner + k], w));
+        }
+    }
+    red[wave][lane] = sum;
+    __syncthreads();
+    if (wave == 0 && c < cols) {
+        const float s = __fadd_rn(__fadd_rn(__fadd_rn(red[0][lane], red[1][lane]), red[2][lane]),
+                                  red[3][lane]);
+        out[(p * rows + r) * cols + c] = s;
+    }
+}
+
+__global__ void reduce_parts_kernel(const float* __restrict__ parts_in, int64_t parts,
+                                    int64_t count, float* __restrict__ y) {
+    const int64_t idx = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (idx >= count) return;
+    float s = parts_in[idx];
+    for (int64_t p = 1; p < parts; ++p) s = __fadd_rn(s, parts_in[p * count + idx]);
+    y[idx] = s;
+}
+
+__global__ __launch_bounds__(kBlock) void matmul_f32_kernel(
+    const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ y,
+    int64_t rows, int64_t inner, int64_t cols) {
+    __shared__ float as[kF32K][kF32Tile + 1];
+    __shared__ float bs[kF32K][kF32Tile + 1];
+    const int tid = threadIdx.x;
+    const int64_t m0 = (int64_t)blockIdx.x * kF32Tile, n0 = (int64_t)blockIdx.y * kF32Tile;
+    const int tr = tid / 16, tc = tid % 16;
+    float acc[4][4] = {};
+    for (int64_t k0 = 0; k0 < inner; k0 += kF32K) {
+        for (int i = tid; i < kF32Tile * kF32K; i += kBlock) {
+            const int r = i / kF32K, kk = i % kF32K;
+            const int64_t k = k0 + kk;
+            as[kk][r] = (m0 + r < rows && k < inner) ? x[(m0 + r) * inner + k] : 0.0f;
+            const int kk2 = i / kF32Tile, cc = i % kF32Tile;
+            const int64_t k2 = k0 + kk2;
+            bs[kk2][cc] = (k2 < inner && n0 + cc < cols) ? w[k2 * cols + n0 + cc] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < kF32K; ++kk) {
+            float a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a[i] = as[kk][tr + 16 * i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = bs[kk][tc + 16 * j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_fmaf(a[i], b[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t r = m0 + tr + 16 * i, c = n0 + tc + 16 * j;
+            if (r < rows && c < cols) y[r * cols + c] = acc[i][j];
+        }
+}
+
+// [K x N] -> [N x K] transpose of one projection (32x32 LDS tiles).
+template <typename T>
+__global__ void transpose_kernel(const T* __restrict__ src, T* __restrict__ dst,
+                                 int64_t K, int64_t N) {
+    __shared__ T tile[32][33];
+    const int64_t k0 = (int64_t)blockIdx.y * 32, n0 = (int64_t)blockIdx.x * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
+    for (int i = ty; i < 32; i += 8) {
+        const int64_t k = k0 + i, n = n0 + tx;
+        if (k < K && n < N) tile[i][tx] = src[k * N + n];
+    }
+    __syncthreads();
+    for (int i = ty; i < 32; i += 8) {
+        const int64_t n = n0 + i, k = k0 + tx;
+        if (k < K && n < N) dst[n * K + k] = tile[tx][i];
+    }
+}
+
+}  // namespace
+
+// ===========================================================================
+// Launchers used by the block entry (hm_block.hip) and the C ABI.
+// ===========================================================================
+int hm_launch_quantize_rows(const float* x, int64_t rows, int64_t n, int32_t limbs,
+                            int8_t* digits, float* scales, int32_t* dsum,
+                            hipStream_t stream) {
+    if (rows == 0) return HM_OK;
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    switch (limbs) {
+    case 1: hipLaunchKernelGGL(limb_quantize_rows_kernel<1>, grid, dim3(kBlock), 0, stream, x, rows, n, digits, scales, dsum); break;
+    case 2: hipLaunchKernelGGL(limb_quantize_rows_kernel<2>, grid, dim3(kBlock), 0, stream, x, rows, n, digits, scales, dsum); break;
+    case 3: hipLaunchKernelGGL(limb_quantize_rows_kernel<3>, grid, dim3(kBlock), 0, stream, x, rows, n, digits, scales, dsum); break;
+    default: return HM_ERR_INVALID;
+    }
+    HM_LAUNCHED();
+    return HM_OK;
+}
+
+bool hm_mfma_shape_ok(int64_t H, int64_t I) {
+    return H % kDownN == 0 && H % kStepK == 0 && I % kGateUpN == 0 && I % kZBlock == 0;
+}
+
+int64_t hm_max_tiles(int64_t pairs, int64_t experts, int64_t tile_m) {
+    return (pairs < experts ? pairs : experts) + pairs / tile_m;
+}
+
+// INT8 expert GEMMs, in two launches (gate/up, then down) so callers can
+// record events between them.  xdig/xscale/xdsum come from
+// hm_launch_quantize_rows over all tokens; zf ([R x I] floats) is only used
+// by the generic path.
+bool hm_use_mfma(const hm_layer* layer, int32_t lx, int32_t lz, bool force_generic) {
+    return !force_generic && hm_mfma_shape_ok(layer->hidden, layer->intermediate) && lx == lz;
+}
+
+int hm_launch_gateup_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int8_t* xdig,
+                        const float* xscale, const int32_t* xdsum, int64_t tokens,
+                        const int32_t* counts, const int32_t* offsets,
+                        const int32_t* perm_tokens, int64_t R, int8_t* zdig, float* zscale,
+                        int32_t* zdsum, float* zf, bool force_generic, hipStream_t stream) {
+    const int64_t H = layer->hidden, I = layer->intermediate, E = layer->experts;
+    const int8_t* packed = static_cast<const int8_t*>(layer->packed);
+    if (R == 0) return HM_OK;
+    if (hm_use_mfma(layer, lx, lz, force_generic)) {
+        const dim3 g1((unsigned)hm_max_tiles(R, E, kTileM), (unsigned)(I / kGateUpN));
+#define HM_GU_MFMA(LV)                                                                   \
+        hipLaunchKernelGGL(gateup_i8_mfma_kernel<LV>, g1, dim3(kBlock), 0, stream, xdig,  \
+                           xscale, xdsum, tokens, H, I, E, packed, layer->scale,          \
+                           layer->zero_point, counts, offsets, perm_tokens, R, zdig,      \
+                           zscale, zdsum)
+        switch (lx) {
+        case 1: HM_GU_MFMA(1); break;
+        case 2: HM_GU_MFMA(2); break;
+        case 3: HM_GU_MFMA(3); break;
+        default: return HM_ERR_INVALID;
+        }
+#undef HM_GU_MFMA
+        HM_LAUNCHED();
+        return HM_OK;
+    }
+    const int64_t nb = (I + kZBlock - 1) / kZBlock;
+    const unsigned g_gu = (unsigned)((R * I + kBlock - 1) / kBlock);
+    const unsigned g_zq = (unsigned)((R * nb + 3) / 4);
+#define HM_GU(LV)                                                                       \
+    hipLaunchKernelGGL(gateup_generic_kernel<LV>, dim3(g_gu), dim3(kBlock), 0, stream,   \
+                       xdig, xscale, tokens, H, I, E, packed, layer->scale,              \
+                       layer->zero_point, offsets, perm_tokens, R, zf)
+#define HM_ZQ(LV)                                                                       \
+    hipLaunchKernelGGL(zquant_generic_kernel<LV>, dim3(g_zq), dim3(kBlock), 0, stream,   \
+                       zf, R, I, zdig, zscale, zdsum)
+    switch (lx) {
+    case 1: HM_GU(1); break;
+    case 2: HM_GU(2); break;
+    case 3: HM_GU(3); break;
+    default: return HM_ERR_INVALID;
+    }
+    HM_LAUNCHED();
+    switch (lz) {
+    case 1: HM_ZQ(1); break;
+    case 2: HM_ZQ(2); break;
+    case 3: HM_ZQ(3); break;
+    default: return HM_ERR_INVALID;
+    }
+#undef HM_GU
+#undef HM_ZQ
+    HM_LAUNCHED();
+    return HM_OK;
+}
+
+int hm_launch_down_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int32_t* counts,
+                      const int32_t* offsets, int64_t R, const int8_t* zdig,
+                      const float* zscale, const int32_t* zdsum, float* y,
+                      bool force_generic, hipStream_t stream) {
+    const int64_t H = layer->hidden, I = layer->intermediate, E = layer->experts;
+    const int8_t* packed = static_cast<const int8_t*>(layer->packed);
+    if (R == 0) return HM_OK;
+    if (hm_use_mfma(layer, lx, lz, force_generic)) {
+        const dim3 g2((unsigned)hm_max_tiles(R, E, kTileM), (unsigned)(H / kDownN));
+#define HM_DN_MFMA(LV)                                                                   \
+        hipLaunchKernelGGL(down_i8_mfma_kernel<LV>, g2, dim3(kBlock), 0, stream, zdig,    \
+                           zscale, zdsum, R, H, I, E, packed, layer->scale,               \
+                           layer->zero_point, counts, offsets, y)
+        switch (lz) {
+        case 1: HM_DN_MFMA(1); break;
+        case 2: HM_DN_MFMA(2); break;
+        case 3: HM_DN_MFMA(3); break;
+        default: return HM_ERR_INVALID;
+        }
+#undef HM_DN_MFMA
+        HM_LAUNCHED();
+        return HM_OK;
+    }
+    const unsigned g_dn = (unsigned)((R * H + kBlock - 1) / kBlock);
+#define HM_DN(LV)                                                                       \
+    hipLaunchKernelGGL(down_generic_kernel<LV>, dim3(g_dn), dim3(kBlock), 0, stream,     \
+                       zdig, zscale, R, H, I, E, packed, layer->scale, layer->zero_point,\
+                       offsets, y)
+    switch (lz) {
+    case 1: HM_DN(1); break;
+    case 2: HM_DN(2); break;
+    case 3: HM_DN(3); break;
+    default: return HM_ERR_INVALID;
+    }
+#undef HM_DN
+    HM_LAUNCHED();
+    return HM_OK;
+}
+
+int hm_launch_gateup_f32(const hm_layer* layer, const float* hidden, const int32_t* counts,
+                         const int32_t* offsets, const int32_t* perm_tokens, int64_t R,
+                         float* zf, hipStream_t stream) {
+    const int64_t H = layer->hidden, I = layer->intermediate, E = layer->experts;
+    if (R == 0) return HM_OK;
+    const dim3 g1((unsigned)hm_max_tiles(R, E, kF32Tile), (unsigned)((I + kF32Tile - 1) / kF32Tile));
+    hipLaunchKernelGGL(gateup_f32_kernel, g1, dim3(kBlock), 0, stream, hidden, H, I, E,
+                       static_cast<const float*>(layer->packed), counts, offsets, perm_tokens, zf);
+    HM_LAUNCHED();
+    return HM_OK;
+}
+
+int hm_launch_down_f32(const hm_layer* layer, const int32_t* counts, const int32_t* offsets,
+                       int64_t R, const float* zf, float* y, hipStream_t stream) {
+    const int64_t H = layer->hidden, I = layer->intermediate, E = layer->experts;
+    if (R == 0) return HM_OK;
+    const dim3 g2((unsigned)hm_max_tiles(R, E, kF32Tile), (unsigned)((H + kF32Tile - 1) / kF32Tile));
+    hipLaunchKernelGGL(down_f32_kernel, g2, dim3(kBlock), 0, stream, zf, H, I, E,
+                       static_cast<const float*>(layer->packed), counts, offsets, y);
+    HM_LAUNCHED();
+    return HM_OK;
+}
+
+extern "C" {
+
+int hm_limb_quantize_rows(const float* x, int64_t rows, int64_t inner, int32_t limbs,
+                          int8_t* digits, float* scales, void* stream) {
+    HM_REQUIRE(x && digits && scales && rows >= 0 && inner > 0);
+    HM_REQUIRE(limbs >= 1 && limbs <= 3);
+    return hm_launch_quantize_rows(x, rows, inner, limbs, digits, scales, nullptr,
+                                   hm_stream(stream));
+}
+
+int hm_limb_partials(const int8_t* digits, int64_t rows, int64_t inner, int32_t limbs,
+                     const int8_t* q_packed, int32_t zp, int64_t cols,
+                     int32_t* partials, void* stream) {
+    HM_REQUIRE(digits && q_packed && partials && rows >= 0 && inner > 0 && cols > 0);
+    HM_REQUIRE(limbs >= 1 && limbs <= 3 && zp >= -128 && zp <= 127);
+    if (inner > 65536) return HM_ERR_OVERFLOW;  // |partial| <= inner*128*255 < 2^31
+    const int64_t total = (int64_t)limbs * rows * cols;
+    if (total == 0) return HM_OK;
+    hipLaunchKernelGGL(limb_partials_kernel, dim3((unsigned)((total + kBlock - 1) / kBlock)),
+                       dim3(kBlock), 0, hm_stream(stream), digits, rows, inner, limbs,
+                       q_packed, zp, cols, partials);
+    HM_LAUNCHED();
+    return HM_OK;
+}
+
+int hm_plan_int8_gemm(int64_t rows, int64_t inner, int64_t cols, int32_t mode,
+                      hm_int8_gemm_plan* plan) {
+    HM_REQUIRE(plan && rows > 0 && inner > 0 && cols > 0);
+    HM_REQUIRE(mode >= 0 && mode <= 2);
+    // Int8GemmPlan.cpp:31-36: overflow guards on M*N, M*K, K*N
+    if (rows > INT64_MAX / cols || rows > INT64_MAX / inner || inner > INT64_MAX / cols)
+        return HM_ERR_OVERFLOW;
+    const int implementation = mode == 0 ? ((inner >= 256 && cols >= 64) ? 2 : 1) : mode;
+    plan->implementation = implementation;
+    if (implementation == 1) {
+        plan->partitions = 1;
+        plan->blocks = (rows * cols + kBlock - 1) / kBlock;
+        plan->scratch_elements = 0;
+    } else {
+        const int64_t p = (inner + 511) / 512;
+        plan->partitions = p < 8 ? p : 8;
+        const int64_t col_blocks = (cols + HM_WAVE - 1) / HM_WAVE;
+        if (rows > INT64_MAX / plan->partitions ||
+            rows * plan->partitions > INT64_MAX / col_blocks) return HM_ERR_OVERFLOW;
+        plan->blocks = rows * plan->partitions * col_blocks;
+        plan->scratch_elements = plan->partitions > 1 ? rows * cols * plan->partitions : 0;
+    }
+    if (plan->blocks > INT_MAX) return HM_ERR_OVERFLOW;
+    return HM_OK;
+}
+
+int hm_matmul_w8a32(const float* x, const int8_t* q, float scale, int32_t zp,
+                    float* y, int64_t rows, int64_t inner, int64_t cols, int32_t mode,
+                    float* scratch, size_t scratch_bytes, void* stream) {
+    // quantization::validateParameters (Quantization.cpp:24-35)
+    HM_REQUIRE(std::isfinite(scale) && scale > 0.0f && zp >= -128 && zp <= 127);
+    HM_REQUIRE(x && q && y);
+    HM_REQUIRE((const void*)x != (const void*)y && (const void*)q != (const void*)y);
+    hm_int8_gemm_plan plan;
+    const int rc = hm_plan_int8_gemm(rows, inner, cols, mode, &plan);
+    if (rc) return rc;
+    hipStream_t s = hm_stream(stream);
+    if (plan.implementation == 1) {
+        hipLaunchKernelGGL(w8a32_reference_kernel, dim3((unsigned)plan.blocks), dim3(kBlock),
+                           0, s, x, q, scale, zp, y, rows, inner, cols);
+        HM_LAUNCHED();
+        return HM_OK;
+    }
+    if (rows > 65535) return HM_ERR_UNSUPPORTED;
+    const dim3 grid((unsigned)((cols + HM_WAVE - 1) / HM_WAVE), (unsigned)rows,
+                    (unsigned)plan.partitions);
+    if (plan.partitions == 1) {
+        hipLaunchKernelGGL(w8a32_coop_kernel, grid, dim3(kBlock), 0, s, x, q, scale, zp, y,
+                           rows, inner, cols, plan.partitions);
+        HM_LAUNCHED();
+        return HM_OK;
+    }
+    HM_REQUIRE(scratch && scratch_bytes >= (size_t)plan.scratch_elements * sizeof(float));
+    hipLaunchKernelGGL(w8a32_coop_kernel, grid, dim3(kBlock), 0, s, x, q, scale, zp, scratch,
+                       rows, inner, cols, plan.partitions);
+    HM_LAUNCHED();
+    const int64_t count = rows * cols;
+    hipLaunchKernelGGL(reduce_parts_kernel, dim3((unsigned)((count + kBlock - 1) / kBlock)),
+                       dim3(kBlock), 0, s, scratch, plan.partitions, count, y);
+    HM_LAUNCHED();
+    return HM_OK;
+}
+
+int hm_matmul_f32(const float* x, const float* w, float* y, int64_t rows, int64_t inner,
+                  int64_t cols, void* stream) {
+    HM_REQUIRE(x && w && y && rows > 0 && inner > 0 && cols > 0);
+    HM_REQUIRE((const void*)x != (const void*)y && (const void*)w != (const void*)y);
+    const dim3 grid((unsigned)((rows + kF32Tile - 1) / kF32Tile),
+                    (unsigned)((cols + kF32Tile - 1) / kF32Tile));
+    hipLaunchKernelGGL(matmul_f32_kernel, grid, dim3(kBlock), 0, hm_stream(stream), x, w, y,
+                       rows, inner, cols);
+    HM_LAUNCHED();
+    return HM_OK;
+}
+
+size_t hm_packed_layer_bytes(int64_t experts, int64_t hidden, int64_t intermediate,
+                             int32_t dtype) {
+    if (experts <= 0 || hidden <= 0 || intermediate <= 0) return 0;
+    const size_t elem = dtype == HM_DTYPE_INT8 ? 1 : dtype == HM_DTYPE_FP32 ? 4 : 0;
+    return (size_t)experts * 3 * (size_t)hidden * (size_t)intermediate * elem;
+}
+
+int hm_pack_layer(const void* src, int64_t experts, int64_t hidden, int64_t intermediate,
+                  int32_t dtype, void* dst, void* stream) {
+    HM_REQUIRE(src && dst && src != dst && experts > 0 && hidden > 0 && intermediate > 0);
+    HM_REQUIRE(dtype == HM_DTYPE_INT8 || dtype == HM_DTYPE_FP32);
+    const int64_t H = hidden, I = intermediate;
+    hipStream_t s = hm_stream(stream);
+    for (int64_t e = 0; e < experts; ++e) {
+        for (int p = 0; p < 3; ++p) {
+            const int64_t K = p < 2 ? H : I, N = p < 2 ? I : H;
+            const int64_t off = e * 3 * H * I + p * H * I;
+            const dim3 grid((unsigned)((N + 31) / 32), (unsigned)((K + 31) / 32));
+            if (dtype == HM_DTYPE_INT8) {
+                hipLaunchKernelGGL(transpose_kernel<int8_t>, grid, dim3(kBlock), 0, s,
+                                   static_cast<const int8_t*>(src) + off,
+                                   static_cast<int8_t*>(dst) + off, K, N);
+            } else {
+                hipLaunchKernelGGL(transpose_kernel<float>, grid, dim3(kBlock), 0, s,
+                                   static_cast<const float*>(src) + off,
+                                   static_cast<float*>(dst) + off, K, N);
+            }
+            HM_LAUNCHED();
+        }
+    }
+    return HM_OK;
+}
+
+}  // extern "C"
