@@ -53,6 +53,7 @@ struct BlockPlan {
     void* route_ws;
     uint32_t* ids;
     float* scores;
+    int32_t* counts;
     int32_t* offsets;
     int32_t* perm_tokens;
     float* perm_weights;
@@ -86,6 +87,7 @@ size_t plan_block(const hm_layer* L, int64_t T, int32_t k, int32_t lx, int32_t l
     q.route_ws = c.take<char>(hm_route_workspace_bytes(T, E));
     q.ids = c.take<uint32_t>((size_t)P);
     q.scores = c.take<float>((size_t)P);
+    q.counts = c.take<int32_t>((size_t)E);
     q.offsets = c.take<int32_t>((size_t)E + 1);
     q.perm_tokens = c.take<int32_t>((size_t)P);
     q.perm_weights = c.take<float>((size_t)P);
@@ -109,7 +111,6 @@ size_t plan_block(const hm_layer* L, int64_t T, int32_t k, int32_t lx, int32_t l
 
 }  // namespace
 
-int32_t* hm_route_counts_ptr(void* route_ws, int64_t tokens, int64_t experts);
 
 extern "C" {
 
@@ -140,6 +141,7 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
     plan_block(layer, tokens, top_k, limbs_x, limbs_z, generic, base, &p);
     if (io->ids) p.ids = io->ids;
     if (io->scores) p.scores = io->scores;
+    if (io->counts) p.counts = io->counts;
     if (io->offsets) p.offsets = io->offsets;
     if (io->perm_tokens) p.perm_tokens = io->perm_tokens;
     if (io->perm_weights) p.perm_weights = io->perm_weights;
@@ -165,10 +167,10 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
     rc = hm_router_topk(hidden, router_w, tokens, H, E, top_k, route_flags & 3u, p.ids,
                         p.scores, nullptr, status, p.route_ws, stream);
     if (rc || (rc = mark(1))) return rc;
-    rc = hm_permute(p.ids, p.scores, tokens, top_k, E, p.route_ws, nullptr, p.offsets,
-                    p.perm_tokens, p.perm_weights, p.slots, stream);
+    rc = hm_permute(p.ids, p.scores, tokens, top_k, E, p.counts, p.offsets, p.perm_tokens,
+                    p.perm_weights, p.slots, stream);
     if (rc || (rc = mark(2))) return rc;
-    const int32_t* counts = hm_route_counts_ptr(p.route_ws, tokens, E);
+    const int32_t* counts = p.counts;
     if (layer->dtype == HM_DTYPE_INT8) {
         rc = hm_launch_quantize_rows(hidden, tokens, H, limbs_x, p.xdig, p.xscale, p.xdsum, s);
         if (rc || (rc = mark(3))) return rc;
@@ -188,10 +190,6 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
     rc = hm_combine(p.y, p.ids, p.slots, p.scores, tokens, top_k, H, io->residual, io->out,
                     stream);
     if (rc || (rc = mark(6))) return rc;
-    if (io->counts) {
-        HM_HIP(hipMemcpyAsync(io->counts, counts, (size_t)E * sizeof(int32_t),
-                              hipMemcpyDeviceToDevice, s));
-    }
     return HM_OK;
 }
 

@@ -103,6 +103,25 @@ __device__ __forceinline__ float hm_recombine(const int* p, int limbs) {
     return c;
 }
 
+// Grouped-GEMM tile lookup: tiles of expert e are ceil(counts[e]/tile_m),
+// experts in ascending id.  Which expert, and which tile of it, does linear
+// tile index `tile` name?  False when `tile` is past the last tile.
+__device__ __forceinline__ bool hm_locate_tile(const int32_t* __restrict__ counts,
+                                               int64_t experts, int tile_m, int64_t tile,
+                                               int64_t* expert_out, int64_t* tile_in_expert) {
+    int64_t acc = 0;
+    for (int64_t e = 0; e < experts; ++e) {
+        const int64_t n = (counts[e] + tile_m - 1) / tile_m;
+        if (tile < acc + n) {
+            *expert_out = e;
+            *tile_in_expert = tile - acc;
+            return true;
+        }
+        acc += n;
+    }
+    return false;
+}
+
 // Float total order key for top-k: larger score first, equal scores (with
 // -0 == +0) broken by the lower expert id; 0 is never a valid key.
 __device__ __forceinline__ unsigned long long hm_rank_key(float v, unsigned int id) {

@@ -18,33 +18,6 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kZBlock = 128;       // columns of Z per fixed-point segment
-constexpr int kTileM = 64;         // rows per MFMA workgroup tile
-constexpr int kGateUpN = 128;      // columns per projection per gate/up tile
-constexpr int kDownN = 256;        // output columns per down tile
-constexpr int kStepK = 64;         // K per MFMA step
-constexpr int kLdsRow = kStepK + 16;  // padded LDS row (bytes)
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-
-// Which expert and tile of that expert does workgroup `tile` own?  Tiles of
-// expert e are ceil(counts[e]/tile_m), experts in ascending id.  Returns
-// false when `tile` is past the last tile.  Executed by every thread (the
-// counts are tiny and cached).
-__device__ bool locate_tile(const int32_t* __restrict__ counts, int64_t experts,
-                            int tile_m, int64_t tile, int64_t* expert_out,
-                            int64_t* tile_in_expert) {
-    int64_t acc = 0;
-    for (int64_t e = 0; e < experts; ++e) {
-        const int64_t n = (counts[e] + tile_m - 1) / tile_m;
-        if (tile < acc + n) {
-            *expert_out = e;
-            *tile_in_expert = tile - acc;
-            return true;
-        }
-        acc += n;
-    }
-    return false;
-}
 
 // ---------------------------------------------------------------------------
 // Activation rows -> digit planes (one wave per row segment).
@@ -220,302 +193,6 @@ __global__ void down_generic_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// MFMA gate/up kernel.  Workgroup tile: 64 grouped rows of one expert x 128
-// columns of gate and the same 128 columns of up.  Wave w owns columns
-// [32w, 32w+32) of both projections, so the G and U values of an output
-// element sit in the same lane.  A (activation digits, gathered through
-// perm_tokens) is staged in LDS; B fragments stream from HBM straight into
-// registers in MFMA layout (lane l: column l%16, 16 K bytes 16*(l/16)).
-// Epilogue: z = silu(g) * u, then the 128-column fixed-point segment of Z
-// for each row is quantised to digits (amax across the four waves via LDS).
-// ---------------------------------------------------------------------------
-template <int L>
-__global__ __launch_bounds__(kBlock) void gateup_i8_mfma_kernel(
-    const int8_t* __restrict__ xdig, const float* __restrict__ xscale,
-    const int32_t* __restrict__ xdsum, int64_t tokens, int64_t H, int64_t I,
-    int64_t experts, const int8_t* __restrict__ packed,
-    const float* __restrict__ scale, const int32_t* __restrict__ zp,
-    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
-    const int32_t* __restrict__ perm_tokens, int64_t R, int8_t* __restrict__ zdig,
-    float* __restrict__ zscale, int32_t* __restrict__ zdsum) {
-    __shared__ __attribute__((aligned(16))) int8_t lds_a[L][kTileM][kLdsRow];
-    __shared__ float red[kTileM][4];
-    __shared__ int red_i[L][kTileM][4];
-    __shared__ int32_t row_token[kTileM];
-    const int tid = threadIdx.x;
-    const int lane = tid & (HM_WAVE - 1);
-    const int wave = tid / HM_WAVE;
-    int64_t e, mt;
-    if (!locate_tile(counts, experts, kTileM, blockIdx.x, &e, &mt)) return;
-    const int64_t g0 = offsets[e] + mt * kTileM;
-    const int nrows = (int)min((int64_t)kTileM, (int64_t)counts[e] - mt * kTileM);
-    const int64_t n0 = (int64_t)blockIdx.y * kGateUpN;
-    if (tid < kTileM) row_token[tid] = tid < nrows ? perm_tokens[g0 + tid] : -1;
-    __syncthreads();
-    // A loader: thread -> (row = tid/4, 16-byte segment = tid%4)
-    const int a_row = tid >> 2, a_seg = tid & 3;
-    const int a_tok = row_token[a_row];
-    // B fragment base pointers: j = 0,1 gate; j = 2,3 up.
-    const int8_t* ebase = packed + e * 3 * H * I;
-    const int8_t* bptr[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int64_t col = n0 + 32 * wave + 16 * (j & 1) + (lane & 15);
-        bptr[j] = ebase + (j >> 1) * H * I + col * H + 16 * (lane >> 4);
-    }
-    v4i acc[4][4][L];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int l = 0; l < L; ++l) acc[i][j][l] = v4i{0, 0, 0, 0};
-
-    for (int64_t k0 = 0; k0 < H; k0 += kStepK) {
-        v4i b[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const v4i*>(bptr[j] + k0);
-#pragma unroll
-        for (int l = 0; l < L; ++l) {
-            v4i v = v4i{0, 0, 0, 0};
-            if (a_tok >= 0) {
-                v = *reinterpret_cast<const v4i*>(
-                    xdig + ((int64_t)l * tokens + a_tok) * H + k0 + 16 * a_seg);
-            }
-            *reinterpret_cast<v4i*>(&lds_a[l][a_row][16 * a_seg]) = v;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-#pragma unroll
-            for (int l = 0; l < L; ++l) {
-                const v4i a = *reinterpret_cast<const v4i*>(
-                    &lds_a[l][16 * i + (lane & 15)][16 * (lane >> 4)]);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    acc[i][j][l] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[j], acc[i][j][l], 0, 0, 0);
-                }
-            }
-        }
-        __syncthreads();
-    }
-
-    // ---- epilogue -------------------------------------------------------
-    const float sg = scale[e * 3 + 0], su = scale[e * 3 + 1];
-    const int zg = zp[e * 3 + 0], zu = zp[e * 3 + 1];
-    float z[4][2][4];
-    float rmax[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int r = 16 * i + 4 * (lane >> 4) + q;
-            const int tok = row_token[r];
-            float m = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                float zv = 0.0f;
-                if (tok >= 0) {
-                    int pg[L], pu[L];
-#pragma unroll
-                    for (int l = 0; l < L; ++l) {
-                        const int ds = (zg | zu) ? xdsum[(int64_t)l * tokens + tok] : 0;
-                        pg[l] = acc[i][j][l][q] - zg * ds;
-                        pu[l] = acc[i][j + 2][l][q] - zu * ds;
-                    }
-                    const float sx = xscale[tok];
-                    const float g = __fmul_rn(hm_recombine(pg, L), __fmul_rn(sx, sg));
-                    const float u = __fmul_rn(hm_recombine(pu, L), __fmul_rn(sx, su));
-                    zv = __fmul_rn(hm_silu(g), u);
-                }
-                z[i][j][q] = zv;
-                m = fmaxf(m, fabsf(zv));
-            }
-            rmax[i][q] = m;
-        }
-    }
-    // row max across the 16 lanes of a row group, then across waves
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            float m = rmax[i][q];
-#pragma unroll
-            for (int s = 1; s < 16; s <<= 1) m = fmaxf(m, __shfl_xor(m, s, HM_WAVE));
-            if ((lane & 15) == 0) red[16 * i + 4 * (lane >> 4) + q][wave] = m;
-        }
-    __syncthreads();
-    const float range = (float)hm_limb_range(L);
-    const int64_t nb = I / kZBlock;
-    const int64_t zb = n0 / kZBlock;
-    const int zd = zp[e * 3 + 2];
-    int dsum_part[4][4][L];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int r = 16 * i + 4 * (lane >> 4) + q;
-            const float amax = fmaxf(fmaxf(red[r][0], red[r][1]), fmaxf(red[r][2], red[r][3]));
-            const float inv = amax > 0.0f ? __fdiv_rn(range, amax) : 0.0f;
-#pragma unroll
-            for (int l = 0; l < L; ++l) dsum_part[i][q][l] = 0;
-            if (r < nrows) {
-                const int64_t grow = g0 + r;
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const int64_t col = n0 + 32 * wave + 16 * j + (lane & 15);
-                    const int v = hm_fixed_point(z[i][j][q], inv, range);
-#pragma unroll
-                    for (int l = 0; l < L; ++l) {
-                        const int d = hm_digit(v, l);
-                        zdig[((int64_t)l * R + grow) * I + col] = (int8_t)d;
-                        dsum_part[i][q][l] += d;
-                    }
-                }
-                if (wave == 0 && (lane & 15) == 0) {
-                    zscale[grow * nb + zb] = amax > 0.0f ? __fdiv_rn(amax, range) : 0.0f;
-                }
-            }
-        }
-    }
-    if (zd != 0) {  // digit sums per segment, needed only for a down zero point
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-                for (int l = 0; l < L; ++l) {
-                    int s = dsum_part[i][q][l];
-#pragma unroll
-                    for (int sh = 1; sh < 16; sh <<= 1) s += __shfl_xor(s, sh, HM_WAVE);
-                    if ((lane & 15) == 0) red_i[l][16 * i + 4 * (lane >> 4) + q][wave] = s;
-                }
-        __syncthreads();
-        if (tid < kTileM && tid < nrows) {
-#pragma unroll
-            for (int l = 0; l < L; ++l) {
-                zdsum[((int64_t)l * R + g0 + tid) * nb + zb] =
-                    red_i[l][tid][0] + red_i[l][tid][1] + red_i[l][tid][2] + red_i[l][tid][3];
-            }
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// MFMA down kernel.  Workgroup tile: 64 contiguous grouped rows of one expert
-// x 256 output columns; wave w owns columns [64w, 64w+64).  K (= I) runs in
-// 64-wide MFMA steps; at the end of each 128-column Z segment the exact
-// int32 partials are recombined, scaled by that segment's s * scale_down and
-// accumulated in float with fmaf, segment by segment in ascending order.
-// ---------------------------------------------------------------------------
-template <int L>
-__global__ __launch_bounds__(kBlock) void down_i8_mfma_kernel(
-    const int8_t* __restrict__ zdig, const float* __restrict__ zscale,
-    const int32_t* __restrict__ zdsum, int64_t R, int64_t H, int64_t I,
-    int64_t experts, const int8_t* __restrict__ packed,
-    const float* __restrict__ scale, const int32_t* __restrict__ zp,
-    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
-    float* __restrict__ y) {
-    __shared__ __attribute__((aligned(16))) int8_t lds_a[L][kTileM][kLdsRow];
-    const int tid = threadIdx.x;
-    const int lane = tid & (HM_WAVE - 1);
-    const int wave = tid / HM_WAVE;
-    int64_t e, mt;
-    if (!locate_tile(counts, experts, kTileM, blockIdx.x, &e, &mt)) return;
-    const int64_t g0 = offsets[e] + mt * kTileM;
-    const int nrows = (int)min((int64_t)kTileM, (int64_t)counts[e] - mt * kTileM);
-    const int64_t n0 = (int64_t)blockIdx.y * kDownN;
-    const int a_row = tid >> 2, a_seg = tid & 3;
-    const int8_t* dbase = packed + e * 3 * H * I + 2 * H * I;
-    const int8_t* bptr[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int64_t col = n0 + 64 * wave + 16 * j + (lane & 15);
-        bptr[j] = dbase + col * I + 16 * (lane >> 4);
-    }
-    const float sd = scale[e * 3 + 2];
-    const int zd = zp[e * 3 + 2];
-    const int64_t nb = I / kZBlock;
-    v4i acc[4][4][L];
-    float facc[4][4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-#pragma unroll
-            for (int l = 0; l < L; ++l) acc[i][j][l] = v4i{0, 0, 0, 0};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) facc[i][j][q] = 0.0f;
-        }
-    for (int64_t k0 = 0; k0 < I; k0 += kStepK) {
-        v4i b[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const v4i*>(bptr[j] + k0);
-#pragma unroll
-        for (int l = 0; l < L; ++l) {
-            v4i v = v4i{0, 0, 0, 0};
-            if (a_row < nrows) {
-                v = *reinterpret_cast<const v4i*>(
-                    zdig + ((int64_t)l * R + g0 + a_row) * I + k0 + 16 * a_seg);
-            }
-            *reinterpret_cast<v4i*>(&lds_a[l][a_row][16 * a_seg]) = v;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-#pragma unroll
-            for (int l = 0; l < L; ++l) {
-                const v4i a = *reinterpret_cast<const v4i*>(
-                    &lds_a[l][16 * i + (lane & 15)][16 * (lane >> 4)]);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    acc[i][j][l] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[j], acc[i][j][l], 0, 0, 0);
-                }
-            }
-        }
-        __syncthreads();
-        if (((k0 + kStepK) % kZBlock) == 0) {  // end of a Z segment
-            const int64_t zb = (k0 + kStepK) / kZBlock - 1;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int r = 16 * i + 4 * (lane >> 4) + q;
-                    const int64_t grow = g0 + (r < nrows ? r : 0);
-                    const float alpha = __fmul_rn(zscale[grow * nb + zb], sd);
-                    int ds[L];
-#pragma unroll
-                    for (int l = 0; l < L; ++l) {
-                        ds[l] = zd ? zdsum[((int64_t)l * R + grow) * nb + zb] : 0;
-                    }
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        int p[L];
-#pragma unroll
-                        for (int l = 0; l < L; ++l) {
-                            p[l] = acc[i][j][l][q] - zd * ds[l];
-                            acc[i][j][l][q] = 0;
-                        }
-                        facc[i][j][q] = __builtin_fmaf(hm_recombine(p, L), alpha, facc[i][j][q]);
-                    }
-                }
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int r = 16 * i + 4 * (lane >> 4) + q;
-            if (r >= nrows) continue;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int64_t col = n0 + 64 * wave + 16 * j + (lane & 15);
-                y[(g0 + r) * H + col] = facc[i][j][q];
-            }
-        }
-}
-
-// ---------------------------------------------------------------------------
 // FP32 expert path (configs with FP32 weights).  Tiled FMA GEMMs, 64x64
 // output tiles, 4x4 outputs per thread, K staged through LDS in steps of 16.
 // ---------------------------------------------------------------------------
@@ -533,7 +210,7 @@ __global__ __launch_bounds__(kBlock) void gateup_f32_kernel(
     __shared__ int32_t row_token[kF32Tile];
     const int tid = threadIdx.x;
     int64_t e, mt;
-    if (!locate_tile(counts, experts, kF32Tile, blockIdx.x, &e, &mt)) return;
+    if (!hm_locate_tile(counts, experts, kF32Tile, blockIdx.x, &e, &mt)) return;
     const int64_t g0 = offsets[e] + mt * kF32Tile;
     const int nrows = (int)min((int64_t)kF32Tile, (int64_t)counts[e] - mt * kF32Tile);
     const int64_t n0 = (int64_t)blockIdx.y * kF32Tile;
@@ -592,7 +269,7 @@ __global__ __launch_bounds__(kBlock) void down_f32_kernel(
     __shared__ float bs[kF32K][kF32Tile + 1];
     const int tid = threadIdx.x;
     int64_t e, mt;
-    if (!locate_tile(counts, experts, kF32Tile, blockIdx.x, &e, &mt)) return;
+    if (!hm_locate_tile(counts, experts, kF32Tile, blockIdx.x, &e, &mt)) return;
     const int64_t g0 = offsets[e] + mt * kF32Tile;
     const int nrows = (int)min((int64_t)kF32Tile, (int64_t)counts[e] - mt * kF32Tile);
     const int64_t n0 = (int64_t)blockIdx.y * kF32Tile;
@@ -778,9 +455,16 @@ int hm_launch_quantize_rows(const float* x, int64_t rows, int64_t n, int32_t lim
     return HM_OK;
 }
 
-bool hm_mfma_shape_ok(int64_t H, int64_t I) {
-    return H % kDownN == 0 && H % kStepK == 0 && I % kGateUpN == 0 && I % kZBlock == 0;
-}
+bool hm_mfma_shape_ok(int64_t H, int64_t I);
+int hm_launch_gateup_i8_mfma(const hm_layer* layer, int32_t limbs, const int8_t* xdig,
+                             const float* xscale, const int32_t* xdsum, int64_t tokens,
+                             const int32_t* counts, const int32_t* offsets,
+                             const int32_t* perm_tokens, int64_t R, int8_t* zdig,
+                             float* zscale, int32_t* zdsum, hipStream_t stream);
+int hm_launch_down_i8_mfma(const hm_layer* layer, int32_t limbs, const int32_t* counts,
+                           const int32_t* offsets, int64_t R, const int8_t* zdig,
+                           const float* zscale, const int32_t* zdsum, float* y,
+                           hipStream_t stream);
 
 int64_t hm_max_tiles(int64_t pairs, int64_t experts, int64_t tile_m) {
     return (pairs < experts ? pairs : experts) + pairs / tile_m;
@@ -803,21 +487,8 @@ int hm_launch_gateup_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int
     const int8_t* packed = static_cast<const int8_t*>(layer->packed);
     if (R == 0) return HM_OK;
     if (hm_use_mfma(layer, lx, lz, force_generic)) {
-        const dim3 g1((unsigned)hm_max_tiles(R, E, kTileM), (unsigned)(I / kGateUpN));
-#define HM_GU_MFMA(LV)                                                                   \
-        hipLaunchKernelGGL(gateup_i8_mfma_kernel<LV>, g1, dim3(kBlock), 0, stream, xdig,  \
-                           xscale, xdsum, tokens, H, I, E, packed, layer->scale,          \
-                           layer->zero_point, counts, offsets, perm_tokens, R, zdig,      \
-                           zscale, zdsum)
-        switch (lx) {
-        case 1: HM_GU_MFMA(1); break;
-        case 2: HM_GU_MFMA(2); break;
-        case 3: HM_GU_MFMA(3); break;
-        default: return HM_ERR_INVALID;
-        }
-#undef HM_GU_MFMA
-        HM_LAUNCHED();
-        return HM_OK;
+        return hm_launch_gateup_i8_mfma(layer, lx, xdig, xscale, xdsum, tokens, counts, offsets,
+                                        perm_tokens, R, zdig, zscale, zdsum, stream);
     }
     const int64_t nb = (I + kZBlock - 1) / kZBlock;
     const unsigned g_gu = (unsigned)((R * I + kBlock - 1) / kBlock);
@@ -856,20 +527,8 @@ int hm_launch_down_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int32
     const int8_t* packed = static_cast<const int8_t*>(layer->packed);
     if (R == 0) return HM_OK;
     if (hm_use_mfma(layer, lx, lz, force_generic)) {
-        const dim3 g2((unsigned)hm_max_tiles(R, E, kTileM), (unsigned)(H / kDownN));
-#define HM_DN_MFMA(LV)                                                                   \
-        hipLaunchKernelGGL(down_i8_mfma_kernel<LV>, g2, dim3(kBlock), 0, stream, zdig,    \
-                           zscale, zdsum, R, H, I, E, packed, layer->scale,               \
-                           layer->zero_point, counts, offsets, y)
-        switch (lz) {
-        case 1: HM_DN_MFMA(1); break;
-        case 2: HM_DN_MFMA(2); break;
-        case 3: HM_DN_MFMA(3); break;
-        default: return HM_ERR_INVALID;
-        }
-#undef HM_DN_MFMA
-        HM_LAUNCHED();
-        return HM_OK;
+        return hm_launch_down_i8_mfma(layer, lz, counts, offsets, R, zdig, zscale, zdsum, y,
+                                      stream);
     }
     const unsigned g_dn = (unsigned)((R * H + kBlock - 1) / kBlock);
 #define HM_DN(LV)                                                                       \

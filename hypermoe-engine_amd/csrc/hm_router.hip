@@ -91,63 +91,101 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(
 // A2 router logits (src/router/CpuRouterBackend.cpp:41-49):
 //   logit[t,e] = float(sum_k double(h[t,k]) * double(w[k,e])), k ascending.
 // The product of two floats is exact in double, so fma(h, w, acc) rounds
-// exactly like the reference's multiply-then-add: each lane owns (t, e)
-// pairs and runs the k loop in order.  Tiles: 32 tokens x 64 experts per
-// workgroup, k staged through LDS as doubles; lane = expert, each wave owns
-// 8 tokens (8 independent FMA chains per lane).
-// Also zeroes the routing bitmask and per-expert counts for the select pass.
+// exactly like the reference's multiply-then-add, and each (t, e) chain runs
+// k in order.  Workgroup tile: 16 tokens x 128 experts; thread (tt, te) owns
+// tokens 2tt, 2tt+1 and experts 4te .. 4te+3 (8 independent FMA chains).
+// k is staged through LDS as doubles in 32-wide chunks, double buffered, the
+// next chunk prefetched into registers while the current one is consumed.
 // ---------------------------------------------------------------------------
-constexpr int kLogitTokens = 32;
-constexpr int kLogitExperts = 64;
-constexpr int kLogitK = 32;
+constexpr int kLT = 16;   // tokens per workgroup
+constexpr int kLE = 128;  // experts per workgroup
+constexpr int kLK = 32;   // k per chunk
 
 __global__ __launch_bounds__(kBlock) void router_logits_kernel(
     const float* __restrict__ h, const float* __restrict__ w, int64_t tokens,
-    int64_t hidden, int64_t experts, float* __restrict__ logits,
-    int32_t* status, uint32_t* __restrict__ zero_words, int64_t zero_count) {
-    __shared__ double hs[kLogitTokens][kLogitK + 1];
-    __shared__ double ws[kLogitK][kLogitExperts];
+    int64_t hidden, int64_t experts, float* __restrict__ logits, int32_t* status) {
+    __shared__ __attribute__((aligned(16))) double hs[2][kLK][kLT];
+    __shared__ __attribute__((aligned(16))) double ws[2][kLK][kLE];
     const int tid = threadIdx.x;
-    {   // clear the routing bitmask + counts (grid-stride)
-        const int64_t nthreads = (int64_t)gridDim.x * gridDim.y * kBlock;
-        const int64_t gid = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * kBlock + tid;
-        for (int64_t i = gid; i < zero_count; i += nthreads) zero_words[i] = 0u;
-    }
-    const int lane = tid & (HM_WAVE - 1);
-    const int wave = tid / HM_WAVE;
-    const int64_t t0 = (int64_t)blockIdx.x * kLogitTokens;
-    const int64_t e0 = (int64_t)blockIdx.y * kLogitExperts;
-    double acc[8];
+    const int tt = tid >> 5, te = tid & 31;
+    const int64_t t0 = (int64_t)blockIdx.x * kLT;
+    const int64_t e0 = (int64_t)blockIdx.y * kLE;
+    // staging: h chunk = 16 x 32 floats (2 per thread), w chunk = 32 x 128
+    // floats (16 per thread, 4 groups of 4 consecutive experts).
+    float hr[2], wr[4][4];
+    auto fetch = [&](int64_t k0) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = 0.0;
-    for (int64_t k0 = 0; k0 < hidden; k0 += kLogitK) {
-        for (int i = tid; i < kLogitTokens * kLogitK; i += kBlock) {
-            const int tt = i / kLogitK, kk = i % kLogitK;
-            const int64_t t = t0 + tt, k = k0 + kk;
-            hs[tt][kk] = (t < tokens && k < hidden) ? (double)h[t * hidden + k] : 0.0;
+        for (int c = 0; c < 2; ++c) {
+            const int idx = tid * 2 + c;
+            const int t = idx / kLK, kk = idx % kLK;
+            const int64_t tg = t0 + t, kg = k0 + kk;
+            hr[c] = (tg < tokens && kg < hidden) ? h[tg * hidden + kg] : 0.0f;
         }
-        for (int i = tid; i < kLogitK * kLogitExperts; i += kBlock) {
-            const int kk = i / kLogitExperts, ee = i % kLogitExperts;
-            const int64_t k = k0 + kk, e = e0 + ee;
-            ws[kk][ee] = (k < hidden && e < experts) ? (double)w[k * experts + e] : 0.0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int idx = tid + kBlock * c;  // 0 .. 1023
+            const int kk = idx >> 5, e4 = idx & 31;
+            const int64_t kg = k0 + kk;
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+                const int64_t eg = e0 + 4 * e4 + x;
+                wr[c][x] = (kg < hidden && eg < experts) ? w[kg * experts + eg] : 0.0f;
+            }
         }
-        __syncthreads();
-        const int kn = (int)((hidden - k0) < kLogitK ? (hidden - k0) : kLogitK);
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int idx = tid * 2 + c;
+            hs[buf][idx % kLK][idx / kLK] = (double)hr[c];
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int idx = tid + kBlock * c;
+            const int kk = idx >> 5, e4 = idx & 31;
+#pragma unroll
+            for (int x = 0; x < 4; ++x) ws[buf][kk][4 * e4 + x] = (double)wr[c][x];
+        }
+    };
+    double acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.0;
+    const int nchunks = (int)((hidden + kLK - 1) / kLK);
+    fetch(0);
+    stash(0);
+    __syncthreads();
+    for (int c = 0; c < nchunks; ++c) {
+        const int buf = c & 1;
+        if (c + 1 < nchunks) fetch((int64_t)(c + 1) * kLK);
+        const int64_t k0 = (int64_t)c * kLK;
+        const int kn = (int)((hidden - k0) < kLK ? (hidden - k0) : kLK);
         for (int kk = 0; kk < kn; ++kk) {
-            const double wv = ws[kk][lane];
+            const double h0 = hs[buf][kk][2 * tt], h1 = hs[buf][kk][2 * tt + 1];
+            double wv[4];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc[i] = __builtin_fma(hs[wave * 8 + i][kk], wv, acc[i]);
+            for (int j = 0; j < 4; ++j) wv[j] = ws[buf][kk][4 * te + j];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc[0][j] = __builtin_fma(h0, wv[j], acc[0][j]);
+                acc[1][j] = __builtin_fma(h1, wv[j], acc[1][j]);
+            }
         }
+        if (c + 1 < nchunks) stash(buf ^ 1);
         __syncthreads();
     }
-    const int64_t e = e0 + lane;
-    if (e >= experts) return;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int64_t t = t0 + wave * 8 + i;
-        if (t >= tokens) break;
-        if (!isfinite(acc[i])) hm_status_or(status, HM_STATUS_NONFINITE_SCORE);
-        logits[t * experts + e] = (float)acc[i];
+    for (int i = 0; i < 2; ++i) {
+        const int64_t t = t0 + 2 * tt + i;
+        if (t >= tokens) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t e = e0 + 4 * te + j;
+            if (e >= experts) continue;
+            if (!isfinite(acc[i][j])) hm_status_or(status, HM_STATUS_NONFINITE_SCORE);
+            logits[t * experts + e] = (float)acc[i][j];
+        }
     }
 }
 
@@ -163,15 +201,13 @@ __global__ __launch_bounds__(kBlock) void router_logits_kernel(
 //   top-k: k rounds of a wave argmax over hm_rank_key (score desc, id asc),
 //   i.e. std::partial_sort with the reference comparator.
 //   renorm: sum of the k selected scores in rank order in double.
-// Writes ids/scores [t, r] in rank order, sets bit t of row e of the routing
-// bitmask and counts[e] += 1 for every selected e.
+// Writes ids/scores [t, r] in rank order.
 // ---------------------------------------------------------------------------
 template <int EPL>
 __global__ __launch_bounds__(kBlock) void router_select_kernel(
     const float* __restrict__ logits, int64_t tokens, int64_t experts,
     int32_t top_k, uint32_t flags, uint32_t* __restrict__ ids,
-    float* __restrict__ scores, uint32_t* __restrict__ mask, int64_t mask_words,
-    int32_t* __restrict__ counts, int32_t* status) {
+    float* __restrict__ scores, int32_t* status) {
     extern __shared__ float seq_lds[];  // (kBlock/64) * experts floats
     const int lane = threadIdx.x & (HM_WAVE - 1);
     const int wave = threadIdx.x / HM_WAVE;
@@ -255,70 +291,80 @@ __global__ __launch_bounds__(kBlock) void router_select_kernel(
     if (lane < top_k) {
         ids[t * top_k + lane] = my_id;
         scores[t * top_k + lane] = my_score;
-        atomicOr(&mask[(int64_t)my_id * mask_words + (t >> 5)], 1u << (t & 31));
-        atomicAdd(&counts[my_id], 1);
     }
 }
 
 // ---------------------------------------------------------------------------
-// A3 permute (src/router/CpuRouterBackend.cpp:140-159): one workgroup per
-// expert.  Bit t of row e is set iff token t selected e; scanning the row in
-// ascending t gives the reference's group order (tokens ascending), and
-// offsets[e] = sum of counts of lower ids gives groups in ascending id.
+// A3 permute (src/router/CpuRouterBackend.cpp:140-159): one 1024-thread
+// workgroup per expert e.  The reference appends (t, score) to group ids[t,r]
+// walking tokens in ascending order and then sorts groups by id: a stable
+// counting sort.  Here: an LDS histogram of all ids gives counts[e] and
+// offsets[e] = sum of lower ids' counts; a block scan over token chunks
+// gives each token's rank inside the group, in ascending token order.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kBlock) void permute_kernel(
-    const uint32_t* __restrict__ ids, const float* __restrict__ scores,
-    int64_t tokens, int32_t top_k, int64_t experts,
-    const uint32_t* __restrict__ mask, int64_t mask_words,
-    const int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-    int32_t* __restrict__ perm_tokens, float* __restrict__ perm_weights,
-    int32_t* __restrict__ slots) {
-    __shared__ int red[kBlock];
+constexpr int kPermThreads = 1024;
+
+__device__ __forceinline__ int block_exclusive_scan(int v, int* lds_waves, int* total) {
+    // lds_waves holds kPermThreads/64 ints
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int incl = v;
+#pragma unroll
+    for (int s = 1; s < 64; s <<= 1) {
+        const int o = __shfl_up(incl, s, 64);
+        if (lane >= s) incl += o;
+    }
+    if (lane == 63) lds_waves[wave] = incl;
+    __syncthreads();
+    int base = 0, all = 0;
+    for (int w = 0; w < kPermThreads / 64; ++w) {
+        const int x = lds_waves[w];
+        if (w < wave) base += x;
+        all += x;
+    }
+    __syncthreads();
+    *total = all;
+    return base + incl - v;
+}
+
+__global__ __launch_bounds__(kPermThreads) void permute_kernel(
+    const uint32_t* __restrict__ ids, const float* __restrict__ scores, int64_t tokens,
+    int32_t top_k, int64_t experts, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ perm_tokens,
+    float* __restrict__ perm_weights, int32_t* __restrict__ slots) {
+    __shared__ int hist[1024];
+    __shared__ int waves[kPermThreads / 64];
     const int tid = threadIdx.x;
-    const int64_t e = blockIdx.x;
+    const uint32_t e = blockIdx.x;
+    const int64_t pairs = tokens * top_k;
+    for (int i = tid; i < experts; i += kPermThreads) hist[i] = 0;
+    __syncthreads();
+    for (int64_t p = tid; p < pairs; p += kPermThreads) atomicAdd(&hist[ids[p]], 1);
+    __syncthreads();
     int part = 0;
-    for (int64_t i = tid; i < e; i += kBlock) part += counts[i];
-    red[tid] = part;
-    __syncthreads();
-    for (int s = kBlock / 2; s > 0; s >>= 1) {
-        if (tid < s) red[tid] += red[tid + s];
-        __syncthreads();
-    }
-    const int offset = red[0];
-    __syncthreads();
+    for (int i = tid; i < (int)e; i += kPermThreads) part += hist[i];
+    int offset;
+    block_exclusive_scan(part, waves, &offset);
+    const int count = hist[e];
     if (tid == 0) {
+        counts[e] = count;
         offsets[e] = offset;
-        if (e == experts - 1) offsets[experts] = offset + counts[e];
+        if ((int64_t)e == experts - 1) offsets[experts] = offset + count;
     }
-    const uint32_t* row = mask + e * mask_words;
-    const int64_t chunk = (mask_words + kBlock - 1) / kBlock;
-    const int64_t w_begin = tid * chunk;
-    const int64_t w_end = (w_begin + chunk) < mask_words ? (w_begin + chunk) : mask_words;
+    if (count == 0) return;
+    const int64_t chunk = (tokens + kPermThreads - 1) / kPermThreads;
+    const int64_t t_begin = (int64_t)tid * chunk;
+    const int64_t t_end = (t_begin + chunk) < tokens ? (t_begin + chunk) : tokens;
     int mine = 0;
-    for (int64_t wi = w_begin; wi < w_end; ++wi) mine += __popc(row[wi]);
-    red[tid] = mine;
-    __syncthreads();
-    // inclusive Hillis-Steele scan over 256 entries
-    for (int s = 1; s < kBlock; s <<= 1) {
-        const int add = tid >= s ? red[tid - s] : 0;
-        __syncthreads();
-        red[tid] += add;
-        __syncthreads();
-    }
-    int pos = offset + red[tid] - mine;
-    for (int64_t wi = w_begin; wi < w_end; ++wi) {
-        uint32_t bits = row[wi];
-        while (bits) {
-            const int b = __ffs(bits) - 1;
-            bits &= bits - 1;
-            const int64_t t = wi * 32 + b;
-            int r = 0;
-            for (; r < top_k; ++r) if (ids[t * top_k + r] == (uint32_t)e) break;
+    for (int64_t t = t_begin; t < t_end; ++t)
+        for (int r = 0; r < top_k; ++r) mine += ids[t * top_k + r] == e;
+    int total;
+    int pos = offset + block_exclusive_scan(mine, waves, &total);
+    for (int64_t t = t_begin; t < t_end; ++t) {
+        for (int r = 0; r < top_k; ++r) {
+            if (ids[t * top_k + r] != e) continue;
             perm_tokens[pos] = (int32_t)t;
-            if (r < top_k) {
-                perm_weights[pos] = scores[t * top_k + r];
-                slots[t * top_k + r] = pos;
-            }
+            perm_weights[pos] = scores[t * top_k + r];
+            slots[t * top_k + r] = pos;
             ++pos;
         }
     }
@@ -337,12 +383,14 @@ __global__ void gather_rows_kernel(const float* __restrict__ in,
     }
 }
 
+
 // ---------------------------------------------------------------------------
 // A7 combine (src/core/runtime/MoERuntime.cpp:312-324): per token, the
 // reference adds w * y over groups in ascending expert id, starting from 0,
 // with a separate float multiply and add.  The k selected ids of a token are
-// distinct, so sorting them gives that order.  Optional residual added last
-// (TransformerBlock.cpp:101-104).
+// distinct, so ranking them gives that order.  One workgroup per token; each
+// thread owns 4-element column groups (float4 loads and stores).  Optional
+// residual added last (TransformerBlock.cpp:101-104).
 // ---------------------------------------------------------------------------
 constexpr int kMaxTopK = 64;
 
@@ -353,33 +401,42 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(
     const float* __restrict__ residual, float* __restrict__ out) {
     __shared__ int64_t srow[kMaxTopK];
     __shared__ float sw[kMaxTopK];
-    const int64_t t = blockIdx.y;
-    if (threadIdx.x == 0) {
-        // insertion sort of the (id, slot, weight) triples by id
-        uint32_t sid[kMaxTopK];
-        for (int r = 0; r < top_k; ++r) {
-            const uint32_t id = ids[t * top_k + r];
-            const int64_t row = slots[t * top_k + r];
-            const float wv = scores[t * top_k + r];
-            int j = r;
-            while (j > 0 && sid[j - 1] > id) {
-                sid[j] = sid[j - 1];
-                srow[j] = srow[j - 1];
-                sw[j] = sw[j - 1];
-                --j;
-            }
-            sid[j] = id;
-            srow[j] = row;
-            sw[j] = wv;
-        }
+    const int64_t t = blockIdx.x;
+    const int tid = threadIdx.x;
+    if (tid < top_k) {  // rank of this pair among the token's ids, ascending
+        const uint32_t id = ids[t * top_k + tid];
+        int rank = 0;
+        for (int r = 0; r < top_k; ++r) rank += ids[t * top_k + r] < id;
+        srow[rank] = slots[t * top_k + tid];
+        sw[rank] = scores[t * top_k + tid];
     }
     __syncthreads();
-    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < width;
-         i += (int64_t)gridDim.x * kBlock) {
-        float acc = 0.0f;
-        for (int r = 0; r < top_k; ++r) {
-            acc = __fadd_rn(acc, __fmul_rn(sw[r], y[srow[r] * width + i]));
+    if ((width & 3) == 0) {
+        const int64_t w4 = width >> 2;
+        for (int64_t i = tid; i < w4; i += kBlock) {
+            float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            for (int r = 0; r < top_k; ++r) {
+                const float4 v = reinterpret_cast<const float4*>(y + srow[r] * width)[i];
+                const float wv = sw[r];
+                acc.x = __fadd_rn(acc.x, __fmul_rn(wv, v.x));
+                acc.y = __fadd_rn(acc.y, __fmul_rn(wv, v.y));
+                acc.z = __fadd_rn(acc.z, __fmul_rn(wv, v.z));
+                acc.w = __fadd_rn(acc.w, __fmul_rn(wv, v.w));
+            }
+            if (residual) {
+                const float4 rv = reinterpret_cast<const float4*>(residual + t * width)[i];
+                acc.x = __fadd_rn(rv.x, acc.x);
+                acc.y = __fadd_rn(rv.y, acc.y);
+                acc.z = __fadd_rn(rv.z, acc.z);
+                acc.w = __fadd_rn(rv.w, acc.w);
+            }
+            reinterpret_cast<float4*>(out + t * width)[i] = acc;
         }
+        return;
+    }
+    for (int64_t i = tid; i < width; i += kBlock) {
+        float acc = 0.0f;
+        for (int r = 0; r < top_k; ++r) acc = __fadd_rn(acc, __fmul_rn(sw[r], y[srow[r] * width + i]));
         if (residual) acc = __fadd_rn(residual[t * width + i], acc);
         out[t * width + i] = acc;
     }
@@ -412,18 +469,8 @@ unsigned grid_for(int64_t n) {
     return (unsigned)g;
 }
 
+
 }  // namespace
-
-// Route workspace layout: logits [T x E] f32 | mask [E x ceil(T/32)] u32 |
-// counts [E] i32.
-static int64_t mask_words_for(int64_t tokens) { return (tokens + 31) / 32; }
-
-int32_t* hm_route_counts_ptr(void* route_ws, int64_t tokens, int64_t experts) {
-    char* ws = static_cast<char*>(route_ws);
-    const size_t logit_bytes = ((size_t)tokens * experts * sizeof(float) + 255) & ~(size_t)255;
-    uint32_t* mask = reinterpret_cast<uint32_t*>(ws + logit_bytes);
-    return reinterpret_cast<int32_t*>(mask + experts * mask_words_for(tokens));
-}
 
 extern "C" {
 
@@ -431,7 +478,7 @@ int hm_rmsnorm(const float* x, const float* gamma, float* y, int64_t rows,
                int64_t width, float eps, void* stream) {
     HM_REQUIRE(x && gamma && y && rows >= 0 && width > 0);
     HM_REQUIRE(std::isfinite(eps) && eps > 0.0f);  // RMSNorm.cpp:22
-    HM_REQUIRE(width <= 16384);              // row staged in LDS
+    HM_REQUIRE(width <= 16384);                     // row staged in LDS
     if (rows == 0) return HM_OK;
     HM_REQUIRE(rows <= INT_MAX);
     hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(kBlock),
@@ -441,11 +488,10 @@ int hm_rmsnorm(const float* x, const float* gamma, float* y, int64_t rows,
     return HM_OK;
 }
 
+// Route workspace: the float logits [T x E].
 size_t hm_route_workspace_bytes(int64_t tokens, int64_t experts) {
     if (tokens < 0 || experts <= 0) return 0;
-    const size_t logits = (size_t)tokens * (size_t)experts * sizeof(float);
-    const size_t mask = (size_t)experts * (size_t)mask_words_for(tokens) * sizeof(uint32_t);
-    return ((logits + 255) & ~(size_t)255) + mask + (size_t)experts * sizeof(int32_t);
+    return (size_t)tokens * (size_t)experts * sizeof(float);
 }
 
 int hm_router_topk(const float* h, const float* w, int64_t tokens,
@@ -455,20 +501,15 @@ int hm_router_topk(const float* h, const float* w, int64_t tokens,
                    void* stream) {
     // RouterConfig::validate (src/router/RouterConfig.cpp:9-22)
     HM_REQUIRE(experts > 0 && top_k > 0 && top_k <= experts);
-    HM_REQUIRE(h && w && ids && scores && route_ws && tokens > 0 && hidden > 0);
+    HM_REQUIRE(h && w && ids && scores && tokens > 0 && hidden > 0);
+    HM_REQUIRE(logits_out || route_ws);
     if (experts > 1024 || top_k > kMaxTopK) return HM_ERR_UNSUPPORTED;
-    if (tokens > ((int64_t)1 << 31) / kLogitTokens) return HM_ERR_OVERFLOW;
-    const int64_t mw = mask_words_for(tokens);
-    char* ws = static_cast<char*>(route_ws);
-    const size_t logit_bytes = ((size_t)tokens * experts * sizeof(float) + 255) & ~(size_t)255;
-    float* logits = logits_out ? logits_out : reinterpret_cast<float*>(ws);
-    uint32_t* mask = reinterpret_cast<uint32_t*>(ws + logit_bytes);
-    int32_t* counts = reinterpret_cast<int32_t*>(mask + experts * mw);
-    const dim3 lgrid((unsigned)((tokens + kLogitTokens - 1) / kLogitTokens),
-                     (unsigned)((experts + kLogitExperts - 1) / kLogitExperts));
+    if (tokens > ((int64_t)1 << 31) / kLT) return HM_ERR_OVERFLOW;
+    float* logits = logits_out ? logits_out : static_cast<float*>(route_ws);
+    const dim3 lgrid((unsigned)((tokens + kLT - 1) / kLT),
+                     (unsigned)((experts + kLE - 1) / kLE));
     hipLaunchKernelGGL(router_logits_kernel, lgrid, dim3(kBlock), 0, hm_stream(stream),
-                       h, w, tokens, hidden, experts, logits, status, mask,
-                       experts * mw + experts);
+                       h, w, tokens, hidden, experts, logits, status);
     HM_LAUNCHED();
     const dim3 sgrid((unsigned)((tokens + 3) / 4));
     const size_t seq_bytes = (size_t)(kBlock / HM_WAVE) * experts * sizeof(float);
@@ -476,7 +517,7 @@ int hm_router_topk(const float* h, const float* w, int64_t tokens,
 #define HM_SELECT(N)                                                                   \
     hipLaunchKernelGGL(router_select_kernel<N>, sgrid, dim3(kBlock), seq_bytes,        \
                        hm_stream(stream), logits, tokens, experts, top_k, flags, ids,  \
-                       scores, mask, mw, counts, status)
+                       scores, status)
     if (epl <= 1) HM_SELECT(1);
     else if (epl <= 2) HM_SELECT(2);
     else if (epl <= 4) HM_SELECT(4);
@@ -488,25 +529,17 @@ int hm_router_topk(const float* h, const float* w, int64_t tokens,
 }
 
 int hm_permute(const uint32_t* ids, const float* scores, int64_t tokens,
-               int32_t top_k, int64_t experts, void* route_ws, int32_t* counts,
-               int32_t* offsets, int32_t* perm_tokens, float* perm_weights,
-               int32_t* slots, void* stream) {
-    HM_REQUIRE(ids && scores && route_ws && offsets && perm_tokens && perm_weights && slots);
+               int32_t top_k, int64_t experts, int32_t* counts, int32_t* offsets,
+               int32_t* perm_tokens, float* perm_weights, int32_t* slots,
+               void* stream) {
+    HM_REQUIRE(ids && scores && counts && offsets && perm_tokens && perm_weights && slots);
     HM_REQUIRE(tokens > 0 && top_k > 0 && experts > 0 && top_k <= experts);
+    if (experts > 1024) return HM_ERR_UNSUPPORTED;
     if (tokens * top_k > INT_MAX) return HM_ERR_OVERFLOW;
-    const int64_t mw = mask_words_for(tokens);
-    char* ws = static_cast<char*>(route_ws);
-    const size_t logit_bytes = ((size_t)tokens * experts * sizeof(float) + 255) & ~(size_t)255;
-    const uint32_t* mask = reinterpret_cast<const uint32_t*>(ws + logit_bytes);
-    const int32_t* ws_counts = reinterpret_cast<const int32_t*>(mask + experts * mw);
-    hipLaunchKernelGGL(permute_kernel, dim3((unsigned)experts), dim3(kBlock), 0,
-                       hm_stream(stream), ids, scores, tokens, top_k, experts, mask,
-                       mw, ws_counts, offsets, perm_tokens, perm_weights, slots);
+    hipLaunchKernelGGL(permute_kernel, dim3((unsigned)experts), dim3(kPermThreads), 0,
+                       hm_stream(stream), ids, scores, tokens, top_k, experts, counts,
+                       offsets, perm_tokens, perm_weights, slots);
     HM_LAUNCHED();
-    if (counts) {
-        HM_HIP(hipMemcpyAsync(counts, ws_counts, (size_t)experts * sizeof(int32_t),
-                              hipMemcpyDeviceToDevice, hm_stream(stream)));
-    }
     return HM_OK;
 }
 
@@ -528,9 +561,8 @@ int hm_combine(const float* y_grouped, const uint32_t* ids, const int32_t* slots
     HM_REQUIRE(y_grouped && ids && slots && scores && out);
     HM_REQUIRE(tokens > 0 && top_k > 0 && width > 0);
     if (top_k > kMaxTopK) return HM_ERR_UNSUPPORTED;
-    HM_REQUIRE(tokens <= 65535);
-    const unsigned gx = (unsigned)((width + kBlock - 1) / kBlock > 8 ? 8 : (width + kBlock - 1) / kBlock);
-    hipLaunchKernelGGL(combine_kernel, dim3(gx, (unsigned)tokens), dim3(kBlock), 0,
+    HM_REQUIRE(tokens <= INT_MAX);
+    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)tokens), dim3(kBlock), 0,
                        hm_stream(stream), y_grouped, ids, slots, scores, tokens, top_k,
                        width, residual, out);
     HM_LAUNCHED();

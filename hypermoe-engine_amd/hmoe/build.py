@@ -37,7 +37,8 @@ HIP_FLAGS = [
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
     f"-I{INCLUDE}", f"-I{CSRC}",
 ]
-KERNEL_SOURCES = ["hm_runtime.hip", "hm_router.hip", "hm_gemm.hip", "hm_block.hip"]
+KERNEL_SOURCES = ["hm_runtime.hip", "hm_router.hip", "hm_gemm.hip", "hm_gemm_mfma.hip",
+                  "hm_block.hip"]
 HOST_SOURCES = ["hip_backend.cpp", "hip_tensor_backend.cpp", "moe_block.cpp"]
 
 KERNELS_SO = LIB / "libhm_kernels.so"

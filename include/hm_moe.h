@@ -104,9 +104,8 @@ int hm_rmsnorm(const float* x, const float* gamma, float* y, int64_t rows,
  * softmax with glibc-expf-exact float exp and double denominator; top-k by
  * (score desc, expert id asc); optional renormalisation by the double sum of
  * the selected scores in rank order.  ids/scores are [tokens x top_k] in
- * rank order.  Bit-exact.  logits_out may be NULL.
- * Also builds the per-expert routing bitmask and counts used by hm_permute;
- * `route_ws` must hold hm_route_workspace_bytes(tokens, experts) bytes. */
+ * rank order.  Bit-exact.  The logits go to logits_out, or, when it is NULL,
+ * to `route_ws` (hm_route_workspace_bytes(tokens, experts) bytes). */
 size_t hm_route_workspace_bytes(int64_t tokens, int64_t experts);
 int hm_router_topk(const float* h, const float* w, int64_t tokens,
                    int64_t hidden, int64_t experts, int32_t top_k,
@@ -118,12 +117,13 @@ int hm_router_topk(const float* h, const float* w, int64_t tokens,
  * Stable counting sort of the tokens*top_k (token, rank) pairs by expert id:
  * counts[E], offsets[E+1], perm_tokens/perm_weights[tokens*top_k] in group
  * order (groups by ascending expert id, tokens ascending inside a group),
- * slots[tokens*top_k]: the grouped row of pair (t, r).  Consumes the routing
- * bitmask and counts that hm_router_topk left in route_ws.  Bit-exact. */
+ * slots[tokens*top_k]: the grouped row of pair (t, r).  Bit-exact.  No
+ * global atomics: one workgroup per expert histograms the ids in LDS and
+ * ranks its tokens with a block scan. */
 int hm_permute(const uint32_t* ids, const float* scores, int64_t tokens,
-               int32_t top_k, int64_t experts, void* route_ws,
-               int32_t* counts, int32_t* offsets, int32_t* perm_tokens,
-               float* perm_weights, int32_t* slots, void* stream);
+               int32_t top_k, int64_t experts, int32_t* counts,
+               int32_t* offsets, int32_t* perm_tokens, float* perm_weights,
+               int32_t* slots, void* stream);
 
 /* ---- A4  Gather rows (src/core/runtime/MoERuntime.cpp:282-299) ----------
  * out[r,:] = in[rows[r],:]. */

@@ -83,7 +83,7 @@ def test_workspace_and_layer_sizes():
     b = lib.hm_moe_block_workspace_bytes(C.byref(layer), 4096, 8, 2, 2, capi.HM_EXEC_GENERIC)
     assert a > 0 and b - a >= 4096 * 8 * 768 * 4, "generic path needs the float Z buffer"
     assert lib.hm_moe_block_workspace_bytes(C.byref(layer), 0, 8, 2, 2, 0) == 0
-    assert lib.hm_route_workspace_bytes(4096, 128) >= 4096 * 128 * 4 + 128 * 128 * 4
+    assert lib.hm_route_workspace_bytes(4096, 128) == 4096 * 128 * 4
 
 
 def test_argument_validation_without_device():
