@@ -47,6 +47,10 @@ def parse():
     ap.add_argument("--cpu-sample", type=int, default=-1,
                     help="tokens timed on the CPU baseline (-1: per-workload default, 0: skip)")
     ap.add_argument("--quiet", action="store_true")
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="also run a plain device-to-device copy of this many MiB (3x) "
+                         "before the timed region: the known-size kernel that calibrates "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE")
     return ap.parse_args()
 
 
@@ -104,6 +108,15 @@ def main():
 
     stage_ev = [[new_event() for _ in range(capi.HM_BLOCK_EVENTS)] for _ in range(args.steps)]
     ev_start, ev_stop = new_event(), new_event()
+
+    if args.copy_mb > 0:
+        src = torch.empty(args.copy_mb << 20, dtype=torch.uint8, device="cuda")
+        src.fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            capi.call("hm_memcpy_d2d", dst.data_ptr(), src.data_ptr(), src.numel(), stream)
+        torch.cuda.synchronize()
+        del src, dst
 
     for _ in range(args.warmup):
         block.launch(d_h, d_w)

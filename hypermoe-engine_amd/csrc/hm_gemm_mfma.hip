@@ -5,16 +5,25 @@
 // planes (hm_device.h); every digit plane meets the same weight fragment in
 // one v_mfma_i32_16x16x64_i8, so the int32 partial of each plane is exact.
 //
-// Data movement per 64-wide K step: every thread issues its global loads for
-// step s+1 into registers, the waves run the MFMAs of step s out of one LDS
-// buffer, the prefetched registers go to the other buffer, one barrier.
-// LDS rows are padded to 80 bytes: the 16 lanes that read one 16-byte column
-// of 16 consecutive rows then hit 16 disjoint groups of 4 banks.
-//
 // MFMA operand layout (v_mfma_i32_16x16x64_i8): lane l supplies 16 bytes of
-// row (l % 16) of A and of column (l % 16) of B, holding K elements
-// 16*(l/16) .. 16*(l/16)+15 of the step in both operands; the 4 int32 results
-// of lane l are rows 4*(l/16) + 0..3 of column l % 16.
+// row (l % 16) of A and of column (l % 16) of B, K bytes 16*(l/16) ..
+// 16*(l/16)+15 of the 64-wide step in both operands; the 4 int32 results of
+// lane l are rows 4*(l/16) + 0..3 of column l % 16.
+//
+// Data movement: operands go straight from global memory to LDS with the
+// gfx950 16-byte global_load_lds (lane l's 16 bytes land at base + 16*l):
+// one wave-wide load fills one 1 KB fragment (16 rows x 64 K bytes) in a
+// swizzled order that keeps both the global reads coalesced per row and the
+// MFMA's ds_read_b128 bank-conflict free (frag_offset), and no registers
+// stage the data.  A ring of S stages keeps S-1 K steps of loads in flight; one
+// s_waitcnt vmcnt + barrier per step.  The K loop is unrolled by S so that
+// every step reads and fills distinct LDS arrays.
+//
+// Tile order: the grid is 1D; workgroup i runs on XCD i % 8 (round-robin
+// dispatch), so the linear tile index is remapped to give each XCD a
+// contiguous run of (m-tile major, n-block minor) tiles: the n-blocks of an
+// m-tile share its gathered activation rows, consecutive m-tiles of one
+// expert share its weight columns, all in one XCD's L2.
 #include "hm_device.h"
 
 #include <limits.h>
@@ -22,25 +31,149 @@
 namespace {
 
 constexpr int kThreads = 512;
+constexpr int kWaves = 8;
 constexpr int kStepK = 64;
-constexpr int kRow = kStepK + 16;   // padded LDS row, bytes
+constexpr int kFrag = 1024;         // bytes per MFMA operand fragment
 constexpr int kZBlock = 128;
 constexpr int kGateUpN = 128;       // columns per projection per gate/up tile
-constexpr int kDownN = 256;         // output columns per down tile
+constexpr int kDownN = 512;         // output columns per down tile (16 * Tile<L,true>::BFRAGS)
+constexpr int kXcds = 8;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-template <int L>
-struct Tiles {
-    // rows per workgroup: 2 row groups of waves x WM 16-row subtiles
-    static constexpr int WM = L >= 3 ? 2 : 4;
+// Tile traits: WM 16-row subtiles per wave, two row groups of waves.
+// gate/up: wave = 4*16 rows x (2 gate + 2 up) 16-column fragments, tile
+// 128 rows x 256 weight rows.  down: wave = WM*16 rows x 8 fragments (128
+// columns), tile 2*WM*16 rows x 512 columns.  A wave's (WM*L) A fragments
+// times its JB B fragments give MFMAs that each need 384 LDS bytes or
+// fewer (8 A x 4 B, 4 A x 8 B), within the LDS bandwidth at full MFMA rate.
+template <int L, bool DOWN>
+struct Tile {
+    static constexpr int WM = DOWN ? (L >= 3 ? 1 : 2) : 4;   // 16-row subtiles per wave
+    static constexpr int JB = DOWN ? 8 : 4;                   // B fragments per wave
     static constexpr int BM = 2 * 16 * WM;
+    static constexpr int BFRAGS = 4 * JB;                     // B fragments per tile
+    static constexpr int NA = L * BM / 16;                    // A fragments / stage
+    static constexpr int NF = NA + BFRAGS;                    // fragments / stage
+    static constexpr int LPW = (NF + kWaves - 1) / kWaves;    // loads per wave / stage
+    static constexpr int S = NF * 4 <= 128 ? 4 : 3;           // ring depth
+    static constexpr int STAGE_BYTES = NF * kFrag;
 };
 
-__device__ __forceinline__ v4i ld16(const int8_t* p) {
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt bits 3:0 and
+// 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    constexpr int imm = (N & 15) | (((N >> 4) & 3) << 14) | (7 << 4) | (15 << 8);
+    __builtin_amdgcn_s_waitcnt(imm);
+}
+
+// Ring barrier.  A release fence (__syncthreads, or an LDS-only fence) makes
+// the compiler wait for every outstanding DMA write into LDS (vmcnt(0)),
+// draining the stages still in flight.  Here the caller's s_waitcnt vmcnt(N)
+// has already completed this wave's loads of the stage being published; the
+// lgkmcnt(0) completes this wave's ds_reads of the slot that is refilled
+// right after the barrier.  The memory clobber keeps the compiler from moving
+// LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ v4i lds16(const int8_t* p) {
     return *reinterpret_cast<const v4i*>(p);
 }
-__device__ __forceinline__ void st16(int8_t* p, v4i v) { *reinterpret_cast<v4i*>(p) = v; }
+
+// Fragment layout in LDS.  The wave-wide load that fills a fragment gives
+// lane l row l/4 and 16-byte K chunk (l%4) ^ ((l/16)%4) of the 16 x 64 byte
+// block: four adjacent lanes read one row's 64 contiguous bytes (one request
+// per row instead of one per lane).  The MFMA reader lane m (row m%16, chunk
+// m/16) finds its bytes at 16*(4*row + (chunk ^ (row/4))); over any 16
+// consecutive reader lanes these are 16 distinct 16-byte bank groups, so the
+// ds_read_b128 stays conflict free.
+__device__ __forceinline__ int dma_row(int lane) { return lane >> 2; }
+__device__ __forceinline__ int dma_chunk(int lane) { return (lane & 3) ^ ((lane >> 4) & 3); }
+__device__ __forceinline__ int frag_offset(int m) {
+    const int r = m & 15, c = m >> 4;
+    return 16 * (4 * r + (c ^ (r >> 2)));
+}
+
+// One wave-wide 16-byte global -> LDS load: lane l's 16 bytes from its own
+// gsrc land at lds_base + 16*l (M0 holds the wave-uniform LDS base).
+//
+// Written as inline asm rather than __builtin_amdgcn_global_load_lds: the
+// compiler cannot follow which ring slot an in-flight LDS load targets across
+// the K loop's back edge and then drains every load (vmcnt(0)) once per
+// iteration.  Here the kernels order the loads themselves: wait_vmcnt before
+// reading a stage, lds_barrier before refilling a slot.  The statement sets
+// M0 itself, and the kernels hold nothing else in M0 (no LDS DMA through the
+// builtin, no indirect register indexing, no GWS or messages).  The memory
+// clobber keeps other memory accesses on their side of the load.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const int8_t* gsrc, int8_t* lds_base) {
+    const unsigned m0 = (unsigned)(uintptr_t)(lds_ptr_t)lds_base;
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(gsrc), "s"(m0) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// The K loop over nk steps with a ring of S LDS stages.  Stage ks lives in
+// ring (ks % S); step ks waits until at most S-2 later stages of this wave's
+// loads are outstanding, meets the other waves at the barrier (after which
+// every wave's loads of stage ks have landed and every read of the slot
+// refilled next is done), refills that slot with step ks+S-1 and computes
+// stage ks.  The steady state, where every step refills, runs unguarded; the
+// last steps drain the ring.  The stages are distinct arrays named at compile
+// time in every unrolled step.
+template <int S, int LPW, class Issue, class Compute>
+__device__ __forceinline__ void ring_loop(int nk, int8_t* r0, int8_t* r1, int8_t* r2, int8_t* r3,
+                                          Issue&& issue, Compute&& compute) {
+    auto slot = [&](int s) -> int8_t* {
+        return s == 0 ? r0 : s == 1 ? r1 : s == 2 ? r2 : r3;
+    };
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s) {
+        if (s < nk) issue(slot(s), (int64_t)s * kStepK);
+    }
+    int ks0 = 0;
+    for (; ks0 + 2 * S - 2 < nk; ks0 += S) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            wait_vmcnt<(S - 2) * LPW>();
+            lds_barrier();
+            issue(slot((s + S - 1) % S), (int64_t)(ks0 + s + S - 1) * kStepK);
+            compute(slot(s), ks0 + s);
+        }
+    }
+    for (; ks0 < nk; ks0 += S) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int ks = ks0 + s;
+            if (ks < nk) {
+                if (ks + S - 2 < nk) wait_vmcnt<(S - 2) * LPW>();
+                else wait_vmcnt<0>();
+                lds_barrier();
+                if (ks + S - 1 < nk) issue(slot((s + S - 1) % S), (int64_t)(ks + S - 1) * kStepK);
+                compute(slot(s), ks);
+            }
+        }
+    }
+}
+
+// Linear workgroup -> logical tile (m-tile major, n-block minor), grouped
+// per XCD.  Returns false for the padding workgroups of the last XCD.
+__device__ __forceinline__ bool xcd_tile(int64_t mtiles, int64_t nblocks, int64_t* mt,
+                                         int64_t* nb) {
+    const int64_t total = mtiles * nblocks;
+    const int64_t per = (total + kXcds - 1) / kXcds;
+    const int64_t i = blockIdx.x;
+    const int64_t j = (i % kXcds) * per + i / kXcds;
+    if (j >= total) return false;
+    *mt = j / nblocks;
+    *nb = j % nblocks;
+    return true;
+}
 
 // ---------------------------------------------------------------------------
 // gate/up: tile = BM grouped rows x (128 gate + 128 up) columns.
@@ -52,75 +185,56 @@ template <int L>
 __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
     const int8_t* __restrict__ xdig, const float* __restrict__ xscale,
     const int32_t* __restrict__ xdsum, int64_t tokens, int64_t H, int64_t I,
-    int64_t experts, const int8_t* __restrict__ packed,
+    int64_t experts, int64_t mtiles, const int8_t* __restrict__ packed,
     const float* __restrict__ scale, const int32_t* __restrict__ zp,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
     const int32_t* __restrict__ perm_tokens, int64_t R, int8_t* __restrict__ zdig,
     float* __restrict__ zscale, int32_t* __restrict__ zdsum) {
-    constexpr int WM = Tiles<L>::WM, BM = Tiles<L>::BM;
-    constexpr int A_CHUNKS = L * BM * 4;   // 16-byte chunks of A per step
-    constexpr int B_CHUNKS = 256 * 4;      // 256 weight rows x 4 chunks
-    __shared__ __attribute__((aligned(16))) int8_t lds_a[2][L][BM][kRow];
-    __shared__ __attribute__((aligned(16))) int8_t lds_b[2][256][kRow];
+    using T = Tile<L, false>;
+    constexpr int WM = T::WM, BM = T::BM, NA = T::NA, NF = T::NF, LPW = T::LPW, S = T::S;
+    __shared__ __attribute__((aligned(1024))) int8_t ring0[T::STAGE_BYTES];
+    __shared__ __attribute__((aligned(1024))) int8_t ring1[T::STAGE_BYTES];
+    __shared__ __attribute__((aligned(1024))) int8_t ring2[T::STAGE_BYTES];
+    __shared__ __attribute__((aligned(1024))) int8_t ring3[S > 3 ? T::STAGE_BYTES : 16];
     __shared__ int32_t row_token[BM];
     __shared__ float red[BM][4];
     __shared__ int red_i[L][BM][4];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 2, wn = wave & 3;
+    const int rd = frag_offset(lane);
+    int64_t gmt, nb;
+    if (!xcd_tile(mtiles, I / kGateUpN, &gmt, &nb)) return;
     int64_t e, mt;
-    if (!hm_locate_tile(counts, experts, BM, blockIdx.x, &e, &mt)) return;
+    if (!hm_locate_tile(counts, experts, BM, gmt, &e, &mt)) return;
     const int64_t g0 = offsets[e] + mt * BM;
     const int nrows = (int)min((int64_t)BM, (int64_t)counts[e] - mt * BM);
-    const int64_t n0 = (int64_t)blockIdx.y * kGateUpN;
-    if (tid < BM) row_token[tid] = tid < nrows ? perm_tokens[g0 + tid] : -1;
+    const int64_t n0 = nb * kGateUpN;
+    if (tid < BM) row_token[tid] = perm_tokens[g0 + (tid < nrows ? tid : 0)];
     __syncthreads();
 
-    // global -> register staging assignments
+    // Per-lane global source of each fragment this wave loads (K offset 0).
     const int8_t* ebase = packed + e * 3 * H * I;
-    const int8_t* a_src[(A_CHUNKS + kThreads - 1) / kThreads];
-    int a_dst[(A_CHUNKS + kThreads - 1) / kThreads];
+    const int8_t* src[LPW];
+    int dst[LPW];
 #pragma unroll
-    for (int c = 0; c < (A_CHUNKS + kThreads - 1) / kThreads; ++c) {
-        const int chunk = tid + c * kThreads;
-        a_src[c] = nullptr;
-        a_dst[c] = -1;
-        if (chunk < A_CHUNKS) {
-            const int l = chunk / (BM * 4), rem = chunk % (BM * 4);
-            const int r = rem >> 2, seg = rem & 3;
-            const int tok = row_token[r];
-            a_dst[c] = (l * BM + r) * kRow + 16 * seg;
-            if (tok >= 0) a_src[c] = xdig + ((int64_t)l * tokens + tok) * H + 16 * seg;
+    for (int c = 0; c < LPW; ++c) {
+        const int f = (wave + kWaves * c) % NF;
+        dst[c] = f * kFrag;
+        if (f < NA) {
+            const int l = f / (BM / 16), i = f % (BM / 16);
+            const int tok = row_token[16 * i + dma_row(lane)];
+            src[c] = xdig + ((int64_t)l * tokens + tok) * H + 16 * dma_chunk(lane);
+        } else {
+            const int brow = 16 * (f - NA) + dma_row(lane);
+            const int64_t col = n0 + (brow & 127);
+            src[c] = ebase + (brow >> 7) * H * I + col * H + 16 * dma_chunk(lane);
         }
     }
-    const int8_t* b_src[2];
-    int b_dst[2];
+    auto issue = [&](int8_t* stage, int64_t k0) {
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-        const int chunk = tid + c * kThreads;  // < 1024 = B_CHUNKS
-        const int r = chunk >> 2, seg = chunk & 3;
-        const int64_t col = n0 + (r & 127);
-        b_src[c] = ebase + (r >> 7) * H * I + col * H + 16 * seg;
-        b_dst[c] = r * kRow + 16 * seg;
-    }
-    static_assert(B_CHUNKS == 2 * kThreads, "two weight chunks per thread");
-
-    constexpr int NA = (A_CHUNKS + kThreads - 1) / kThreads;
-    v4i ra[NA], rb[2];
-    auto fetch = [&](int64_t k0) {
-#pragma unroll
-        for (int c = 0; c < NA; ++c) ra[c] = a_src[c] ? ld16(a_src[c] + k0) : v4i{0, 0, 0, 0};
-#pragma unroll
-        for (int c = 0; c < 2; ++c) rb[c] = ld16(b_src[c] + k0);
-    };
-    auto stash = [&](int buf) {
-        int8_t* a = &lds_a[buf][0][0][0];
-#pragma unroll
-        for (int c = 0; c < NA; ++c) if (a_dst[c] >= 0) st16(a + a_dst[c], ra[c]);
-        int8_t* b = &lds_b[buf][0][0];
-#pragma unroll
-        for (int c = 0; c < 2; ++c) st16(b + b_dst[c], rb[c]);
+        for (int c = 0; c < LPW; ++c) dma16(src[c] + k0, stage + dst[c]);  // wave-uniform base
     };
 
     v4i acc[WM][4][L];
@@ -131,35 +245,28 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
 #pragma unroll
             for (int l = 0; l < L; ++l) acc[i][j][l] = v4i{0, 0, 0, 0};
 
-    const int nk = (int)(H / kStepK);
-    fetch(0);
-    stash(0);
-    __syncthreads();
-    const int arow = wm * (BM / 2) + (lane & 15);
-    const int kofs = 16 * (lane >> 4);
-    for (int ks = 0; ks < nk; ++ks) {
-        const int buf = ks & 1;
-        if (ks + 1 < nk) fetch((int64_t)(ks + 1) * kStepK);
+    auto compute = [&](const int8_t* stage) {
         v4i b[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int brow = (j >> 1) * 128 + 32 * wn + 16 * (j & 1) + (lane & 15);
-            b[j] = ld16(&lds_b[buf][brow][kofs]);
+            const int bf = (j >> 1) * 8 + 2 * wn + (j & 1);  // 16-row fragment index
+            b[j] = lds16(stage + (NA + bf) * kFrag + rd);
         }
 #pragma unroll
         for (int i = 0; i < WM; ++i) {
 #pragma unroll
             for (int l = 0; l < L; ++l) {
-                const v4i a = ld16(&lds_a[buf][l][arow + 16 * i][kofs]);
+                const v4i a = lds16(stage + (l * (BM / 16) + wm * WM + i) * kFrag + rd);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     acc[i][j][l] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[j], acc[i][j][l], 0, 0, 0);
                 }
             }
         }
-        if (ks + 1 < nk) stash(buf ^ 1);
-        __syncthreads();
-    }
+    };
+
+    ring_loop<S, LPW>((int)(H / kStepK), ring0, ring1, ring2, ring3, issue,
+                      [&](const int8_t* stage, int) { compute(stage); });
 
     // ---- epilogue -------------------------------------------------------
     const float sg = scale[e * 3 + 0], su = scale[e * 3 + 1];
@@ -171,11 +278,12 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
         for (int q = 0; q < 4; ++q) {
             const int r = wm * (BM / 2) + 16 * i + 4 * (lane >> 4) + q;
             const int tok = row_token[r];
+            const bool live = r < nrows;
             float m = 0.0f;
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 float zv = 0.0f;
-                if (tok >= 0) {
+                if (live) {
                     int pg[L], pu[L];
 #pragma unroll
                     for (int l = 0; l < L; ++l) {
@@ -198,7 +306,7 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
     }
     __syncthreads();
     const float range = (float)hm_limb_range(L);
-    const int64_t nb = I / kZBlock;
+    const int64_t nbz = I / kZBlock;
     const int64_t zb = n0 / kZBlock;
 #pragma unroll
     for (int i = 0; i < WM; ++i) {
@@ -224,7 +332,7 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
                     }
                 }
                 if (wn == 0 && (lane & 15) == 0) {
-                    zscale[grow * nb + zb] = amax > 0.0f ? __fdiv_rn(amax, range) : 0.0f;
+                    zscale[grow * nbz + zb] = amax > 0.0f ? __fdiv_rn(amax, range) : 0.0f;
                 }
             }
             if (zd != 0) {
@@ -243,7 +351,7 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
         if (tid < nrows) {
 #pragma unroll
             for (int l = 0; l < L; ++l) {
-                zdsum[((int64_t)l * R + g0 + tid) * nb + zb] =
+                zdsum[((int64_t)l * R + g0 + tid) * nbz + zb] =
                     red_i[l][tid][0] + red_i[l][tid][1] + red_i[l][tid][2] + red_i[l][tid][3];
             }
         }
@@ -251,8 +359,8 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// down: tile = BM contiguous grouped rows x 256 output columns; wave (wm, wn)
-// owns rows [wm*BM/2, +BM/2) and columns [64 wn, 64 wn + 64).  At the end of
+// down: tile = BM contiguous grouped rows x 512 output columns; wave (wm, wn)
+// owns rows [wm*BM/2, +BM/2) and columns [128 wn, 128 wn + 128).  At the end of
 // each 128-column Z segment the exact partials are recombined and folded into
 // the float accumulator: acc = fmaf(c, s_segment * scale_down, acc).
 // ---------------------------------------------------------------------------
@@ -260,138 +368,125 @@ template <int L>
 __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
     const int8_t* __restrict__ zdig, const float* __restrict__ zscale,
     const int32_t* __restrict__ zdsum, int64_t R, int64_t H, int64_t I,
-    int64_t experts, const int8_t* __restrict__ packed,
+    int64_t experts, int64_t mtiles, const int8_t* __restrict__ packed,
     const float* __restrict__ scale, const int32_t* __restrict__ zp,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
     float* __restrict__ y) {
-    constexpr int WM = Tiles<L>::WM, BM = Tiles<L>::BM;
-    constexpr int A_CHUNKS = L * BM * 4;
-    constexpr int NA = (A_CHUNKS + kThreads - 1) / kThreads;
-    constexpr int MAXNB = 16;  // Z segments staged in LDS (I <= 2048)
-    __shared__ __attribute__((aligned(16))) int8_t lds_a[2][L][BM][kRow];
-    __shared__ __attribute__((aligned(16))) int8_t lds_b[2][256][kRow];
+    using T = Tile<L, true>;
+    constexpr int WM = T::WM, JB = T::JB, BM = T::BM, NA = T::NA, NF = T::NF, LPW = T::LPW,
+                  S = T::S;
+    constexpr int BN = 16 * T::BFRAGS;  // output columns per tile
+    constexpr int MAXNB = 16;           // Z segments (I <= 2048)
+    __shared__ __attribute__((aligned(1024))) int8_t ring0[T::STAGE_BYTES];
+    __shared__ __attribute__((aligned(1024))) int8_t ring1[T::STAGE_BYTES];
+    __shared__ __attribute__((aligned(1024))) int8_t ring2[T::STAGE_BYTES];
+    __shared__ __attribute__((aligned(1024))) int8_t ring3[S > 3 ? T::STAGE_BYTES : 16];
     __shared__ float s_alpha[MAXNB][BM];
-    __shared__ int s_dsum[L][MAXNB][BM];
+    __shared__ int32_t s_corr[MAXNB][L][BM];  // zp * digit sum of each Z segment
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 2, wn = wave & 3;
+    const int rd = frag_offset(lane);
+    int64_t gmt, nb;
+    if (!xcd_tile(mtiles, H / BN, &gmt, &nb)) return;
     int64_t e, mt;
-    if (!hm_locate_tile(counts, experts, BM, blockIdx.x, &e, &mt)) return;
+    if (!hm_locate_tile(counts, experts, BM, gmt, &e, &mt)) return;
     const int64_t g0 = offsets[e] + mt * BM;
     const int nrows = (int)min((int64_t)BM, (int64_t)counts[e] - mt * BM);
-    const int64_t n0 = (int64_t)blockIdx.y * kDownN;
-    const int nb = (int)(I / kZBlock);
+    const int64_t n0 = nb * BN;
+    const int nbz = (int)(I / kZBlock);
     const float sd = scale[e * 3 + 2];
     const int zd = zp[e * 3 + 2];
-    for (int i = tid; i < nb * BM; i += kThreads) {
+    for (int i = tid; i < nbz * BM; i += kThreads) {
         const int b = i / BM, r = i % BM;
-        const int64_t grow = g0 + (r < nrows ? r : 0);
-        s_alpha[b][r] = __fmul_rn(zscale[grow * nb + b], sd);
-        for (int l = 0; l < L; ++l) s_dsum[l][b][r] = zd ? zdsum[((int64_t)l * R + grow) * nb + b] : 0;
+        const int64_t g = g0 + (r < nrows ? r : 0);
+        s_alpha[b][r] = __fmul_rn(zscale[g * nbz + b], sd);
+#pragma unroll
+        for (int l = 0; l < L; ++l) s_corr[b][l][r] = zd ? zd * zdsum[((int64_t)l * R + g) * nbz + b] : 0;
     }
 
     const int8_t* dbase = packed + e * 3 * H * I + 2 * H * I;
-    const int8_t* a_src[NA];
-    int a_dst[NA];
+    const int8_t* src[LPW];
+    int dst[LPW];
 #pragma unroll
-    for (int c = 0; c < NA; ++c) {
-        const int chunk = tid + c * kThreads;
-        a_src[c] = nullptr;
-        a_dst[c] = -1;
-        if (chunk < A_CHUNKS) {
-            const int l = chunk / (BM * 4), rem = chunk % (BM * 4);
-            const int r = rem >> 2, seg = rem & 3;
-            a_dst[c] = (l * BM + r) * kRow + 16 * seg;
-            if (r < nrows) a_src[c] = zdig + ((int64_t)l * R + g0 + r) * I + 16 * seg;
+    for (int c = 0; c < LPW; ++c) {
+        const int f = (wave + kWaves * c) % NF;
+        dst[c] = f * kFrag;
+        if (f < NA) {
+            const int l = f / (BM / 16), i = f % (BM / 16);
+            const int r = 16 * i + dma_row(lane);
+            src[c] = zdig + ((int64_t)l * R + g0 + (r < nrows ? r : 0)) * I + 16 * dma_chunk(lane);
+        } else {
+            const int brow = 16 * (f - NA) + dma_row(lane);
+            src[c] = dbase + (n0 + brow) * I + 16 * dma_chunk(lane);
         }
     }
-    const int8_t* b_src[2];
-    int b_dst[2];
+    auto issue = [&](int8_t* stage, int64_t k0) {
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-        const int chunk = tid + c * kThreads;
-        const int r = chunk >> 2, seg = chunk & 3;
-        b_src[c] = dbase + (n0 + r) * I + 16 * seg;
-        b_dst[c] = r * kRow + 16 * seg;
-    }
-    v4i ra[NA], rb[2];
-    auto fetch = [&](int64_t k0) {
-#pragma unroll
-        for (int c = 0; c < NA; ++c) ra[c] = a_src[c] ? ld16(a_src[c] + k0) : v4i{0, 0, 0, 0};
-#pragma unroll
-        for (int c = 0; c < 2; ++c) rb[c] = ld16(b_src[c] + k0);
-    };
-    auto stash = [&](int buf) {
-        int8_t* a = &lds_a[buf][0][0][0];
-#pragma unroll
-        for (int c = 0; c < NA; ++c) if (a_dst[c] >= 0) st16(a + a_dst[c], ra[c]);
-        int8_t* b = &lds_b[buf][0][0];
-#pragma unroll
-        for (int c = 0; c < 2; ++c) st16(b + b_dst[c], rb[c]);
+        for (int c = 0; c < LPW; ++c) dma16(src[c] + k0, stage + dst[c]);  // wave-uniform base
     };
 
-    v4i acc[WM][4][L];
-    float facc[WM][4][4];
+    v4i acc[WM][JB][L];
+    float facc[WM][JB][4];
 #pragma unroll
     for (int i = 0; i < WM; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < JB; ++j) {
 #pragma unroll
             for (int l = 0; l < L; ++l) acc[i][j][l] = v4i{0, 0, 0, 0};
 #pragma unroll
             for (int q = 0; q < 4; ++q) facc[i][j][q] = 0.0f;
         }
 
-    const int nk = (int)(I / kStepK);
-    fetch(0);
-    stash(0);
-    __syncthreads();
-    const int arow = wm * (BM / 2) + (lane & 15);
-    const int kofs = 16 * (lane >> 4);
-    for (int ks = 0; ks < nk; ++ks) {
-        const int buf = ks & 1;
-        if (ks + 1 < nk) fetch((int64_t)(ks + 1) * kStepK);
-        v4i b[4];
+    // The WM*L A fragments stay in registers while the JB weight fragments
+    // stream through one register quad each (fewer live VGPRs than holding B).
+    auto compute = [&](const int8_t* stage) {
+        v4i a[WM][L];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) b[j] = ld16(&lds_b[buf][64 * wn + 16 * j + (lane & 15)][kofs]);
+        for (int i = 0; i < WM; ++i)
 #pragma unroll
-        for (int i = 0; i < WM; ++i) {
+            for (int l = 0; l < L; ++l)
+                a[i][l] = lds16(stage + (l * (BM / 16) + wm * WM + i) * kFrag + rd);
 #pragma unroll
-            for (int l = 0; l < L; ++l) {
-                const v4i a = ld16(&lds_a[buf][l][arow + 16 * i][kofs]);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    acc[i][j][l] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[j], acc[i][j][l], 0, 0, 0);
-                }
-            }
-        }
-        if (ks & 1) {  // end of a 128-column Z segment (two 64-wide steps)
-            const int zb = ks >> 1;
+        for (int j = 0; j < JB; ++j) {
+            const v4i b = lds16(stage + (NA + JB * wn + j) * kFrag + rd);
 #pragma unroll
             for (int i = 0; i < WM; ++i)
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int r = wm * (BM / 2) + 16 * i + 4 * (lane >> 4) + q;
-                    const float alpha = s_alpha[zb][r];
-                    int ds[L];
-#pragma unroll
-                    for (int l = 0; l < L; ++l) ds[l] = s_dsum[l][zb][r];
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        int p[L];
-#pragma unroll
-                        for (int l = 0; l < L; ++l) {
-                            p[l] = acc[i][j][l][q] - zd * ds[l];
-                            acc[i][j][l][q] = 0;
-                        }
-                        facc[i][j][q] = __builtin_fmaf(hm_recombine(p, L), alpha, facc[i][j][q]);
-                    }
-                }
+                for (int l = 0; l < L; ++l)
+                    acc[i][j][l] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][l], b, acc[i][j][l], 0, 0, 0);
         }
-        if (ks + 1 < nk) stash(buf ^ 1);
-        __syncthreads();
-    }
+    };
+    auto fold = [&](int zb) {  // end of Z segment zb: exact partials -> float
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int r = wm * (BM / 2) + 16 * i + 4 * (lane >> 4) + q;
+                const float alpha = s_alpha[zb][r];
+                int ds[L];
+#pragma unroll
+                for (int l = 0; l < L; ++l) ds[l] = s_corr[zb][l][r];
+#pragma unroll
+                for (int j = 0; j < JB; ++j) {
+                    int p[L];
+#pragma unroll
+                    for (int l = 0; l < L; ++l) {
+                        p[l] = acc[i][j][l][q] - ds[l];
+                        acc[i][j][l][q] = 0;
+                    }
+                    facc[i][j][q] = __builtin_fmaf(hm_recombine(p, L), alpha, facc[i][j][q]);
+                }
+            }
+    };
+
+    __syncthreads();  // s_alpha, s_corr visible (before any LDS DMA is in flight)
+    ring_loop<S, LPW>((int)(I / kStepK), ring0, ring1, ring2, ring3, issue,
+                      [&](const int8_t* stage, int ks) {
+                          compute(stage);
+                          if (ks & 1) fold(ks >> 1);
+                      });
 #pragma unroll
     for (int i = 0; i < WM; ++i)
 #pragma unroll
@@ -399,8 +494,8 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
             const int r = wm * (BM / 2) + 16 * i + 4 * (lane >> 4) + q;
             if (r >= nrows) continue;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int64_t col = n0 + 64 * wn + 16 * j + (lane & 15);
+            for (int j = 0; j < JB; ++j) {
+                const int64_t col = n0 + 16 * (JB * wn + j) + (lane & 15);
                 y[(g0 + r) * H + col] = facc[i][j][q];
             }
         }
@@ -410,11 +505,18 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
 
 // Shape preconditions of the MFMA kernels (checked by the caller):
 // H % 256 == 0, I % 128 == 0, I <= 2048.
+static_assert(16 * Tile<2, true>::BFRAGS == kDownN && 16 * Tile<3, true>::BFRAGS == kDownN, "down tile width");
+
 bool hm_mfma_shape_ok(int64_t H, int64_t I) {
     return H % kDownN == 0 && I % kGateUpN == 0 && I % kZBlock == 0 && I / kZBlock <= 16;
 }
 
 int64_t hm_max_tiles(int64_t pairs, int64_t experts, int64_t tile_m);
+
+static unsigned xcd_grid(int64_t mtiles, int64_t nblocks) {
+    const int64_t total = mtiles * nblocks;
+    return (unsigned)(((total + kXcds - 1) / kXcds) * kXcds);
+}
 
 template <int L>
 static int launch_gateup(const hm_layer* layer, const int8_t* xdig, const float* xscale,
@@ -422,11 +524,11 @@ static int launch_gateup(const hm_layer* layer, const int8_t* xdig, const float*
                          const int32_t* offsets, const int32_t* perm_tokens, int64_t R,
                          int8_t* zdig, float* zscale, int32_t* zdsum, hipStream_t stream) {
     const int64_t H = layer->hidden, I = layer->intermediate, E = layer->experts;
-    const dim3 grid((unsigned)hm_max_tiles(R, E, Tiles<L>::BM), (unsigned)(I / kGateUpN));
-    hipLaunchKernelGGL(gateup_mfma_kernel<L>, grid, dim3(kThreads), 0, stream, xdig, xscale,
-                       xdsum, tokens, H, I, E, static_cast<const int8_t*>(layer->packed),
-                       layer->scale, layer->zero_point, counts, offsets, perm_tokens, R, zdig,
-                       zscale, zdsum);
+    const int64_t mtiles = hm_max_tiles(R, E, Tile<L, false>::BM);
+    hipLaunchKernelGGL(gateup_mfma_kernel<L>, dim3(xcd_grid(mtiles, I / kGateUpN)),
+                       dim3(kThreads), 0, stream, xdig, xscale, xdsum, tokens, H, I, E, mtiles,
+                       static_cast<const int8_t*>(layer->packed), layer->scale,
+                       layer->zero_point, counts, offsets, perm_tokens, R, zdig, zscale, zdsum);
     HM_LAUNCHED();
     return HM_OK;
 }
@@ -436,10 +538,11 @@ static int launch_down(const hm_layer* layer, const int32_t* counts, const int32
                        int64_t R, const int8_t* zdig, const float* zscale,
                        const int32_t* zdsum, float* y, hipStream_t stream) {
     const int64_t H = layer->hidden, I = layer->intermediate, E = layer->experts;
-    const dim3 grid((unsigned)hm_max_tiles(R, E, Tiles<L>::BM), (unsigned)(H / kDownN));
-    hipLaunchKernelGGL(down_mfma_kernel<L>, grid, dim3(kThreads), 0, stream, zdig, zscale,
-                       zdsum, R, H, I, E, static_cast<const int8_t*>(layer->packed),
-                       layer->scale, layer->zero_point, counts, offsets, y);
+    const int64_t mtiles = hm_max_tiles(R, E, Tile<L, true>::BM);
+    hipLaunchKernelGGL(down_mfma_kernel<L>, dim3(xcd_grid(mtiles, H / kDownN)), dim3(kThreads),
+                       0, stream, zdig, zscale, zdsum, R, H, I, E, mtiles,
+                       static_cast<const int8_t*>(layer->packed), layer->scale,
+                       layer->zero_point, counts, offsets, y);
     HM_LAUNCHED();
     return HM_OK;
 }

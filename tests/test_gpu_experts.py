@@ -108,7 +108,9 @@ def _layer_inputs(seed, T, H, E, I, int8, skew=False):
 
 BLOCK_CASES = [  # (T, H, E, I, k, limbs) -- MFMA shapes and generic shapes
     (1, 2048, 128, 768, 8, 2), (4, 2048, 128, 768, 8, 3), (16, 2048, 128, 768, 8, 2),
-    (70, 512, 16, 256, 4, 2), (5, 64, 8, 32, 2, 2), (6, 96, 5, 40, 3, 3), (3, 2, 3, 2, 2, 2)]
+    (70, 512, 16, 256, 4, 2), (5, 64, 8, 32, 2, 2), (6, 96, 5, 40, 3, 3), (3, 2, 3, 2, 2, 2),
+    # several row tiles per expert (ragged last tile) through the MFMA kernels
+    (300, 512, 4, 256, 2, 2), (203, 1024, 3, 384, 2, 3), (150, 512, 2, 128, 1, 1)]
 
 
 @pytest.mark.parametrize("T,H,E,I,k,L", BLOCK_CASES)
@@ -131,6 +133,9 @@ def test_block_int8_bitexact_vs_limb_oracle(dev, T, H, E, I, k, L):
     assert_bitexact(res.ids, rids, "ids vs reference path")
     counts, offsets, ptok, pw, _ = O.group(rids, rsc, E)
     assert_bitexact(res.perm_tokens, ptok, "permutation vs reference path")
+    if L == 1:  # one digit = plain int8 activations: W8A8 accuracy, not the W8A32 contract
+        assert normwise(out, rout) < 5e-2
+        return
     assert_compare(out, rout, 1e-4, 1e-4, "block vs reference W8A32 (1e-4)")
     if L == 3:
         assert_compare(out, rout, 1e-5, 1e-5, "L=3 block vs reference W8A32 (1e-5)")
