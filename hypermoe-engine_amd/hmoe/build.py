@@ -96,7 +96,8 @@ def build_host() -> Path | None:
         return None
     LIB.mkdir(parents=True, exist_ok=True)
     tmp = HOST_SO.with_suffix(".so.tmp")
-    _run([HIPCC, "-std=c++20", "-O2", "-fPIC", "-shared", "-Wall", f"-I{INCLUDE}", f"-I{HOST}",
+    # host C++ only: every device call goes through the C ABI of libhm_kernels.so
+    _run(["g++", "-std=c++20", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra", f"-I{INCLUDE}",
           "-o", str(tmp), *map(str, srcs), f"-L{LIB}", "-lhm_kernels", "-Wl,-rpath,$ORIGIN"])
     os.replace(tmp, HOST_SO)
     return HOST_SO
