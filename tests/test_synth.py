@@ -61,15 +61,18 @@ def test_layer_is_thread_count_independent():
 
 
 def test_zipf_skew_makes_a_hot_expert():
-    """C4's routing skew: the hottest expert gets several times the mean load."""
+    """C4's routing skew (Zipf(1.1) ranking): on the C4 inputs the hottest
+    expert gets about 10x the mean load and no expert is starved."""
     import sys
     from pathlib import Path
     sys.path.insert(0, str(Path(__file__).resolve().parent.parent / "oracle"))
     import hm_oracle as O
-    T, H, E, k = 512, 2048, 128, 8
-    h = O.rmsnorm(synth.raw_hidden(3, T, H), np.ones(H, np.float32))
-    w = synth.router_weights(3, 0, H, E)
-    synth.apply_skew(h, w, synth.zipf_bias(3, E))
+    cfg = synth.CONFIGS["C4"]
+    T, H, E, k = cfg.tokens, cfg.hidden, cfg.experts, cfg.top_k
+    h = O.rmsnorm(synth.raw_hidden(cfg.seed, T, H), np.ones(H, np.float32))
+    w = synth.router_weights(cfg.seed, 0, H, E)
+    synth.apply_skew(h, w, synth.zipf_bias(cfg.seed, E))
     rc, ids, sc = O.route(h, w, k, 1, 1)
     counts = np.bincount(ids.ravel(), minlength=E)
-    assert counts.max() >= 5 * counts.mean()
+    assert 9.5 * counts.mean() <= counts.max() <= 10.5 * counts.mean()
+    assert counts.min() > 0
