@@ -25,6 +25,7 @@
 // m-tile share its gathered activation rows, consecutive m-tiles of one
 // expert share its weight columns, all in one XCD's L2.
 #include "hm_device.h"
+#include "hm_lds_dma.h"
 
 #include <limits.h>
 
@@ -40,7 +41,6 @@ constexpr int kDownN = 512;         // output columns per down tile (16 * Tile<L
 constexpr int kXcds = 8;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // Tile traits: WM 16-row subtiles per wave, two row groups of waves.
 // gate/up: wave = 4*16 rows x (2 gate + 2 up) 16-column fragments, tile
@@ -61,25 +61,6 @@ struct Tile {
     static constexpr int STAGE_BYTES = NF * kFrag;
 };
 
-// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt bits 3:0 and
-// 15:14, expcnt 6:4, lgkmcnt 11:8).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    constexpr int imm = (N & 15) | (((N >> 4) & 3) << 14) | (7 << 4) | (15 << 8);
-    __builtin_amdgcn_s_waitcnt(imm);
-}
-
-// Ring barrier.  A release fence (__syncthreads, or an LDS-only fence) makes
-// the compiler wait for every outstanding DMA write into LDS (vmcnt(0)),
-// draining the stages still in flight.  Here the caller's s_waitcnt vmcnt(N)
-// has already completed this wave's loads of the stage being published; the
-// lgkmcnt(0) completes this wave's ds_reads of the slot that is refilled
-// right after the barrier.  The memory clobber keeps the compiler from moving
-// LDS accesses across it.
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
 __device__ __forceinline__ v4i lds16(const int8_t* p) {
     return *reinterpret_cast<const v4i*>(p);
 }
@@ -98,25 +79,6 @@ __device__ __forceinline__ int frag_offset(int m) {
     return 16 * (4 * r + (c ^ (r >> 2)));
 }
 
-// One wave-wide 16-byte global -> LDS load: lane l's 16 bytes from its own
-// gsrc land at lds_base + 16*l (M0 holds the wave-uniform LDS base).
-//
-// Written as inline asm rather than __builtin_amdgcn_global_load_lds: the
-// compiler cannot follow which ring slot an in-flight LDS load targets across
-// the K loop's back edge and then drains every load (vmcnt(0)) once per
-// iteration.  Here the kernels order the loads themselves: wait_vmcnt before
-// reading a stage, lds_barrier before refilling a slot.  The statement sets
-// M0 itself, and the kernels hold nothing else in M0 (no LDS DMA through the
-// builtin, no indirect register indexing, no GWS or messages).  The memory
-// clobber keeps other memory accesses on their side of the load.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(const int8_t* gsrc, int8_t* lds_base) {
-    const unsigned m0 = (unsigned)(uintptr_t)(lds_ptr_t)lds_base;
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
-                 :: "v"(gsrc), "s"(m0) : "memory", "m0");
-}
-#pragma clang diagnostic pop
 
 // The K loop over nk steps with a ring of S LDS stages.  Stage ks lives in
 // ring (ks % S); step ks waits until at most S-2 later stages of this wave's

@@ -2,6 +2,7 @@
 // elementwise kernels for gfx950 (wave64).  Every kernel here reproduces the
 // reference CPU arithmetic bit for bit; the comments say how.
 #include "hm_device.h"
+#include "hm_lds_dma.h"
 
 #include <limits.h>
 
@@ -186,6 +187,164 @@ __global__ __launch_bounds__(kBlock) void router_logits_kernel(
             if (!isfinite(acc[i][j])) hm_status_or(status, HM_STATUS_NONFINITE_SCORE);
             logits[t * experts + e] = (float)acc[i][j];
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// A2 logits, tiled (prefill).  Same arithmetic as router_logits_kernel: one
+// sequential FP64 chain per (token, expert) in ascending k.  Workgroup tile
+// 32 tokens x 64 experts, 4 waves; lane = expert, wave w owns tokens
+// 8w..8w+7, so a lane runs 8 independent chains (enough to keep the FP64
+// pipe issuing) and the per-k LDS traffic is one 4-byte weight per lane plus
+// eight broadcast token values per wave.  W [32 k x 64 e] and h [32 t x 32 k]
+// chunks come straight from global memory into a 4-stage LDS ring
+// (global_load_lds); each chunk's h is widened to double once (one LDS
+// array, double buffered) rather than per use.  Needs E % 64 == 0,
+// H % 32 == 0 and 16-byte aligned h, w.
+// ---------------------------------------------------------------------------
+constexpr int kTT = 32;                // tokens per tile
+constexpr int kTE = 64;                // experts per tile
+constexpr int kTK = 32;                // k per chunk
+constexpr int kTS = 4;                 // ring stages
+constexpr int kTW = kTK * kTE * 4;     // W bytes per stage (8 KB)
+constexpr int kTH = kTT * kTK * 4;     // h bytes per stage (4 KB)
+constexpr int kTLPW = 3;               // 16-byte wave loads per wave per stage
+
+__global__ __launch_bounds__(256) void router_logits_tile_kernel(
+    const float* __restrict__ h, const float* __restrict__ w, int64_t tokens,
+    int64_t hidden, int64_t experts, float* __restrict__ logits, int32_t* status) {
+    __shared__ __attribute__((aligned(1024))) char ring[kTS][kTW + kTH];
+    __shared__ __attribute__((aligned(16))) double hd[2][kTK][kTT];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t t0 = (int64_t)blockIdx.x * kTT;
+    const int64_t e0 = (int64_t)blockIdx.y * kTE;
+    // this wave's loads per stage: W rows [8w, 8w+8) as two 1 KB pieces
+    // (4 rows of 64 floats each), h tokens [8w, 8w+8) x 32 k (8 lanes/token)
+    const float* wsrc0 = w + (8 * wave + (lane >> 4)) * experts + e0 + 4 * (lane & 15);
+    const float* wsrc1 = wsrc0 + 4 * experts;
+    const int64_t tok = min(t0 + 8 * wave + (lane >> 3), tokens - 1);
+    const float* hsrc = h + tok * hidden + 4 * (lane & 7);
+    auto issue = [&](int slot, int64_t k0) {
+        char* st = ring[slot];
+        dma16(wsrc0 + k0 * experts, st + 2048 * wave);
+        dma16(wsrc1 + k0 * experts, st + 2048 * wave + 1024);
+        dma16(hsrc + k0, st + kTW + 1024 * wave);
+    };
+    double acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0;
+    const int nk = (int)(hidden / kTK);
+#pragma unroll
+    for (int s = 0; s < kTS - 1; ++s)
+        if (s < nk) issue(s, (int64_t)s * kTK);
+    for (int c = 0; c < nk; ++c) {
+        const int slot = c % kTS;
+        if (c + kTS - 2 < nk) wait_vmcnt<(kTS - 2) * kTLPW>();
+        else wait_vmcnt<0>();
+        lds_barrier();  // stage c landed for every wave; stage c-1 fully read
+        if (c + kTS - 1 < nk) issue((c + kTS - 1) % kTS, (int64_t)(c + kTS - 1) * kTK);
+        {   // widen this chunk's h: thread -> token tid/8, k 4*(tid%8)..+3
+            const float4 v = *reinterpret_cast<const float4*>(ring[slot] + kTW + 16 * tid);
+            const int t = tid >> 3, kk = 4 * (tid & 7);
+            double* dst = &hd[c & 1][kk][t];
+            dst[0] = (double)v.x;
+            dst[kTT] = (double)v.y;
+            dst[2 * kTT] = (double)v.z;
+            dst[3 * kTT] = (double)v.w;
+        }
+        lds_barrier();
+        const float* ws = reinterpret_cast<const float*>(ring[slot]);
+        const double* hs = &hd[c & 1][0][8 * wave];
+#pragma unroll
+        for (int kk = 0; kk < kTK; ++kk) {
+            const double wv = (double)ws[kk * kTE + lane];
+            const double2 h01 = *reinterpret_cast<const double2*>(hs + kk * kTT);
+            const double2 h23 = *reinterpret_cast<const double2*>(hs + kk * kTT + 2);
+            const double2 h45 = *reinterpret_cast<const double2*>(hs + kk * kTT + 4);
+            const double2 h67 = *reinterpret_cast<const double2*>(hs + kk * kTT + 6);
+            acc[0] = __builtin_fma(h01.x, wv, acc[0]);
+            acc[1] = __builtin_fma(h01.y, wv, acc[1]);
+            acc[2] = __builtin_fma(h23.x, wv, acc[2]);
+            acc[3] = __builtin_fma(h23.y, wv, acc[3]);
+            acc[4] = __builtin_fma(h45.x, wv, acc[4]);
+            acc[5] = __builtin_fma(h45.y, wv, acc[5]);
+            acc[6] = __builtin_fma(h67.x, wv, acc[6]);
+            acc[7] = __builtin_fma(h67.y, wv, acc[7]);
+        }
+    }
+    const int64_t e = e0 + lane;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int64_t t = t0 + 8 * wave + i;
+        if (t >= tokens) continue;
+        if (!isfinite(acc[i])) hm_status_or(status, HM_STATUS_NONFINITE_SCORE);
+        logits[t * experts + e] = (float)acc[i];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// A2 logits for a few tokens (decode, T <= 16).  The sequential chain is
+// 2048 FP64 FMAs long whatever the batch, so the work is spread over many
+// CUs instead: one wave per 4 experts, lane = (token t = lane/4, expert
+// lane%4), one chain per lane; W [128 k x 4 e] and h [16 t x 128 k] chunks
+// stream through a 4-stage LDS ring.  Needs E % 4 == 0, H % 128 == 0 and
+// 16-byte aligned h, w.
+// ---------------------------------------------------------------------------
+constexpr int kSK = 128;                 // k per chunk
+constexpr int kSS = 4;                   // ring stages
+constexpr int kSW = kSK * 4 * 4;         // W bytes per stage (2 KB)
+constexpr int kSH = 16 * kSK * 4;        // h bytes per stage (8 KB)
+constexpr int kSLPW = 10;                // 16-byte wave loads per stage
+
+__global__ __launch_bounds__(64) void router_logits_small_kernel(
+    const float* __restrict__ h, const float* __restrict__ w, int64_t tokens,
+    int64_t hidden, int64_t experts, float* __restrict__ logits, int32_t* status) {
+    __shared__ __attribute__((aligned(1024))) char ring[kSS][kSW + kSH];
+    const int lane = threadIdx.x;
+    const int t = lane >> 2, ei = lane & 3;
+    const int64_t e0 = (int64_t)blockIdx.x * 4;
+    // loads: W rows k0+lane and k0+64+lane (16 bytes = 4 experts each);
+    // h: 8 loads of two token rows x 128 k (32 lanes per row)
+    const float* wsrc = w + (int64_t)lane * experts + e0;
+    const float* hsrc = h + 4 * (lane & 31);
+    auto issue = [&](int slot, int64_t k0) {
+        char* st = ring[slot];
+        dma16(wsrc + k0 * experts, st);
+        dma16(wsrc + (k0 + 64) * experts, st + 1024);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int64_t tk = min((int64_t)(2 * j) + (lane >> 5), tokens - 1);
+            dma16(hsrc + tk * hidden + k0, st + kSW + 1024 * j);
+        }
+    };
+    double acc = 0.0;
+    const int nk = (int)(hidden / kSK);
+#pragma unroll
+    for (int s = 0; s < kSS - 1; ++s)
+        if (s < nk) issue(s, (int64_t)s * kSK);
+    for (int c = 0; c < nk; ++c) {
+        const int slot = c % kSS;
+        if (c + kSS - 2 < nk) wait_vmcnt<(kSS - 2) * kSLPW>();
+        else wait_vmcnt<0>();
+        lds_barrier();
+        if (c + kSS - 1 < nk) issue((c + kSS - 1) % kSS, (int64_t)(c + kSS - 1) * kSK);
+        const float* ws = reinterpret_cast<const float*>(ring[slot]);
+        const float* hs = reinterpret_cast<const float*>(ring[slot] + kSW) + t * kSK;
+#pragma unroll
+        for (int kk = 0; kk < kSK; kk += 4) {
+            const float4 hv = *reinterpret_cast<const float4*>(hs + kk);
+            const double w0 = (double)ws[(kk + 0) * 4 + ei], w1 = (double)ws[(kk + 1) * 4 + ei];
+            const double w2 = (double)ws[(kk + 2) * 4 + ei], w3 = (double)ws[(kk + 3) * 4 + ei];
+            acc = __builtin_fma((double)hv.x, w0, acc);
+            acc = __builtin_fma((double)hv.y, w1, acc);
+            acc = __builtin_fma((double)hv.z, w2, acc);
+            acc = __builtin_fma((double)hv.w, w3, acc);
+        }
+    }
+    if (t < tokens) {
+        if (!isfinite(acc)) hm_status_or(status, HM_STATUS_NONFINITE_SCORE);
+        logits[(int64_t)t * experts + e0 + ei] = (float)acc;
     }
 }
 
@@ -506,10 +665,20 @@ int hm_router_topk(const float* h, const float* w, int64_t tokens,
     if (experts > 1024 || top_k > kMaxTopK) return HM_ERR_UNSUPPORTED;
     if (tokens > ((int64_t)1 << 31) / kLT) return HM_ERR_OVERFLOW;
     float* logits = logits_out ? logits_out : static_cast<float*>(route_ws);
-    const dim3 lgrid((unsigned)((tokens + kLT - 1) / kLT),
-                     (unsigned)((experts + kLE - 1) / kLE));
-    hipLaunchKernelGGL(router_logits_kernel, lgrid, dim3(kBlock), 0, hm_stream(stream),
-                       h, w, tokens, hidden, experts, logits, status);
+    const bool aligned = ((uintptr_t)h % 16 == 0) && ((uintptr_t)w % 16 == 0);
+    if (aligned && tokens <= 16 && experts % 4 == 0 && hidden % kSK == 0) {
+        hipLaunchKernelGGL(router_logits_small_kernel, dim3((unsigned)(experts / 4)), dim3(64),
+                           0, hm_stream(stream), h, w, tokens, hidden, experts, logits, status);
+    } else if (aligned && experts % kTE == 0 && hidden % kTK == 0) {
+        const dim3 grid((unsigned)((tokens + kTT - 1) / kTT), (unsigned)(experts / kTE));
+        hipLaunchKernelGGL(router_logits_tile_kernel, grid, dim3(256), 0, hm_stream(stream), h,
+                           w, tokens, hidden, experts, logits, status);
+    } else {
+        const dim3 lgrid((unsigned)((tokens + kLT - 1) / kLT),
+                         (unsigned)((experts + kLE - 1) / kLE));
+        hipLaunchKernelGGL(router_logits_kernel, lgrid, dim3(kBlock), 0, hm_stream(stream),
+                           h, w, tokens, hidden, experts, logits, status);
+    }
     HM_LAUNCHED();
     const dim3 sgrid((unsigned)((tokens + 3) / 4));
     const size_t seq_bytes = (size_t)(kBlock / HM_WAVE) * experts * sizeof(float);
