@@ -149,7 +149,14 @@ def main():
     out = res.output.cpu().numpy()
     tokens_per_s = T / (ms_per_step / 1e3)
 
-    if cfg.int8:
+    gemv = cfg.int8 and T <= capi.HM_GEMV_MAX_TOKENS
+    if gemv:
+        # W8A32 GEMV: gate+up weights of the selected experts, gathered FP32
+        # activation rows in, FP32 Z rows out
+        gu_ops = 2 * T * k * 2 * H * I
+        dn_ops = 2 * T * k * H * I
+        gu_bytes = unique * 2 * H * I + T * k * H * 4 + T * k * I * 4
+    elif cfg.int8:
         gu_ops = 2 * T * k * 2 * H * I
         dn_ops = 2 * T * k * H * I
         gu_bytes = unique * 2 * H * I + T * H * args.limbs + T * k * I * args.limbs
@@ -169,7 +176,9 @@ def main():
                 "hw_mfma_frac_with_limbs": round(achieved * (args.limbs if cfg.int8 else 1) / peak, 4)}
     else:
         achieved = gu_bytes / gu_s / 1e9
-        roof = {"bound": "hbm", "kernel": "gateup_i8_mfma_kernel" if cfg.int8 else "gateup_f32_kernel",
+        roof = {"bound": "hbm",
+                "kernel": ("gemv_w8_kernel (gate/up)" if gemv else
+                           "gateup_i8_mfma_kernel" if cfg.int8 else "gateup_f32_kernel"),
                 "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
                 "work_per_launch": gu_bytes, "launch_ms": round(stage["gate_up"], 5)}

@@ -25,6 +25,12 @@ int hm_launch_gateup_f32(const hm_layer* layer, const float* hidden, const int32
 int hm_launch_down_f32(const hm_layer* layer, const int32_t* counts, const int32_t* offsets,
                        int64_t R, const float* zf, float* y, hipStream_t stream);
 bool hm_mfma_shape_ok(int64_t H, int64_t I);
+bool hm_gemv_shape_ok(int64_t H, int64_t I);
+int hm_launch_gateup_gemv(const hm_layer* L, const float* hidden, const int32_t* counts,
+                          const int32_t* offsets, const int32_t* perm_tokens, int64_t pairs,
+                          float* z, hipStream_t s);
+int hm_launch_down_gemv(const hm_layer* L, const float* z, const int32_t* counts,
+                        const int32_t* offsets, int64_t pairs, float* y, hipStream_t s);
 
 namespace {
 
@@ -69,6 +75,12 @@ struct BlockPlan {
     int32_t* status;
 };
 
+// Decode-size INT8 blocks take the W8A32 GEMV kernels.
+bool use_gemv(const hm_layer* L, int64_t T, uint32_t flags) {
+    return L->dtype == HM_DTYPE_INT8 && (flags & (HM_EXEC_GENERIC | HM_EXEC_LIMBS)) == 0 &&
+           T <= HM_GEMV_MAX_TOKENS && hm_gemv_shape_ok(L->hidden, L->intermediate);
+}
+
 bool layer_valid(const hm_layer* L) {
     if (!L || !L->packed || L->experts <= 0 || L->hidden <= 0 || L->intermediate <= 0)
         return false;
@@ -78,7 +90,8 @@ bool layer_valid(const hm_layer* L) {
 
 // Lays the workspace out; with base == nullptr only computes the size.
 size_t plan_block(const hm_layer* L, int64_t T, int32_t k, int32_t lx, int32_t lz,
-                  bool generic, void* base, BlockPlan* p) {
+                  uint32_t flags, void* base, BlockPlan* p) {
+    const bool generic = (flags & HM_EXEC_GENERIC) != 0;
     const int64_t H = L->hidden, I = L->intermediate, E = L->experts;
     const int64_t P = T * k;
     const int64_t nb = (I + 127) / 128;
@@ -93,7 +106,9 @@ size_t plan_block(const hm_layer* L, int64_t T, int32_t k, int32_t lx, int32_t l
     q.perm_weights = c.take<float>((size_t)P);
     q.slots = c.take<int32_t>((size_t)P);
     q.status = c.take<int32_t>(1);
-    if (L->dtype == HM_DTYPE_INT8) {
+    if (use_gemv(L, T, flags)) {
+        q.zf = c.take<float>((size_t)P * I);
+    } else if (L->dtype == HM_DTYPE_INT8) {
         q.xdig = c.take<int8_t>((size_t)lx * T * H);
         q.xscale = c.take<float>((size_t)T);
         q.xdsum = c.take<int32_t>((size_t)lx * T);
@@ -117,8 +132,8 @@ extern "C" {
 size_t hm_moe_block_workspace_bytes(const hm_layer* layer, int64_t tokens, int32_t top_k,
                                     int32_t limbs_x, int32_t limbs_z, uint32_t exec_flags) {
     if (!layer_valid(layer) || tokens <= 0 || top_k <= 0) return 0;
-    const bool generic = (exec_flags & HM_EXEC_GENERIC) != 0;
-    return plan_block(layer, tokens, top_k, limbs_x, limbs_z, generic, nullptr, nullptr) + kAlign;
+    return plan_block(layer, tokens, top_k, limbs_x, limbs_z, exec_flags, nullptr, nullptr) +
+           kAlign;
 }
 
 int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float* router_w,
@@ -135,10 +150,12 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
     const bool generic = (route_flags & HM_EXEC_GENERIC) != 0;
     void* base = reinterpret_cast<void*>(
         (reinterpret_cast<uintptr_t>(workspace) + kAlign - 1) & ~(uintptr_t)(kAlign - 1));
-    const size_t need = plan_block(layer, tokens, top_k, limbs_x, limbs_z, generic, nullptr, nullptr);
+    const size_t need =
+        plan_block(layer, tokens, top_k, limbs_x, limbs_z, route_flags, nullptr, nullptr);
     HM_REQUIRE(workspace_bytes >= need + (size_t)(static_cast<char*>(base) - static_cast<char*>(workspace)));
     BlockPlan p;
-    plan_block(layer, tokens, top_k, limbs_x, limbs_z, generic, base, &p);
+    plan_block(layer, tokens, top_k, limbs_x, limbs_z, route_flags, base, &p);
+    const bool gemv = use_gemv(layer, tokens, route_flags);
     if (io->ids) p.ids = io->ids;
     if (io->scores) p.scores = io->scores;
     if (io->counts) p.counts = io->counts;
@@ -171,7 +188,12 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
                     p.perm_weights, p.slots, stream);
     if (rc || (rc = mark(2))) return rc;
     const int32_t* counts = p.counts;
-    if (layer->dtype == HM_DTYPE_INT8) {
+    if (gemv) {
+        if ((rc = mark(3))) return rc;
+        rc = hm_launch_gateup_gemv(layer, hidden, counts, p.offsets, p.perm_tokens, P, p.zf, s);
+        if (rc || (rc = mark(4))) return rc;
+        rc = hm_launch_down_gemv(layer, p.zf, counts, p.offsets, P, p.y, s);
+    } else if (layer->dtype == HM_DTYPE_INT8) {
         rc = hm_launch_quantize_rows(hidden, tokens, H, limbs_x, p.xdig, p.xscale, p.xdsum, s);
         if (rc || (rc = mark(3))) return rc;
         rc = hm_launch_gateup_i8(layer, limbs_x, limbs_z, p.xdig, p.xscale, p.xdsum, tokens,

@@ -1,0 +1,241 @@
+// hm_gemv.hip -- the decode-size INT8 expert path: W8A32 GEMVs in FP32 that
+// stream the selected experts' weights from HBM once.
+//
+// At decode (a few tokens, each expert sees one or two rows) the expert
+// GEMMs are pure weight streams: 4.5 MiB of INT8 per selected expert and a
+// handful of multiply-adds per byte.  These kernels split K across the 64
+// lanes of a wave (each lane owns fixed 16-byte slices of every weight row
+// and the matching activation slices), stream each weight row once from HBM
+// into LDS with coalesced 16-byte direct loads, and reduce each output's
+// per-lane partial dot products across the wave.
+//
+// Arithmetic: the reference computes y = sum_k x_k * (float(q_k - zp) * s)
+// in FP32 (CpuTensorBackend.cpp:173-186).  Here the dequantisation is
+// factored: with u_k = q_k + 128 (the byte XOR 0x80, converted by
+// v_cvt_f32_ubyteN),
+//     y = s * (sum_k x_k u_k - (128 + zp) * sum_k x_k),
+// summed in a different order; the result is within the north-star 1e-4 of
+// the reference (rounding of FP32 sums of 2048 terms), not bit-identical to
+// it.  SiLU(G)*U uses the same float operations as the other paths.
+#include "hm_device.h"
+#include "hm_lds_dma.h"
+
+namespace {
+
+constexpr int kGemvThreads = 256;
+constexpr int kRowsPerWave = 8;   // weight rows per wave
+
+// The slot-th expert (ascending id) with a non-zero group; -1 if none.
+// Every wave computes it redundantly from `counts` (E <= 1024).
+__device__ int hm_active_expert(const int32_t* __restrict__ counts, int64_t experts, int slot) {
+    const int lane = threadIdx.x & 63;
+    int seen = 0;
+    for (int64_t base = 0; base < experts; base += 64) {
+        const int64_t e = base + lane;
+        const bool nz = e < experts && counts[e] > 0;
+        const unsigned long long m = __ballot(nz);
+        const int c = __popcll(m);
+        if (slot < seen + c) {
+            // position of the (slot - seen)-th set bit
+            unsigned long long mm = m;
+            for (int i = 0; i < slot - seen; ++i) mm &= mm - 1;
+            return (int)(base + __ffsll((long long)mm) - 1);
+        }
+        seen += c;
+    }
+    return -1;
+}
+
+// Butterfly reduction of N (power of two, <= 64) values across the wave.
+// Afterwards lane l holds the full sum of value index (l >> (6 - log2 N)),
+// i.e. value i sits in lanes [i*64/N, (i+1)*64/N).
+template <int N>
+__device__ __forceinline__ float wave_reduce_many(float (&v)[N]) {
+    const int lane = threadIdx.x & 63;
+    int n = N;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        if (n > 1) {
+            const bool upper = (lane & m) != 0;
+#pragma unroll
+            for (int i = 0; i < N / 2; ++i) {
+                if (i < n / 2) {
+                    const float send = upper ? v[i] : v[i + n / 2];
+                    const float keep = upper ? v[i + n / 2] : v[i];
+                    v[i] = keep + __shfl_xor(send, m, 64);
+                }
+            }
+            n >>= 1;
+        } else {
+            v[0] += __shfl_xor(v[0], m, 64);
+        }
+    }
+    return v[0];
+}
+
+// 4 unsigned bytes of a dword (after XOR 0x80) -> 4 floats
+__device__ __forceinline__ void bytes_to_float(uint32_t d, float* f) {
+    const uint32_t u = d ^ 0x80808080u;   // v_cvt_f32_ubyte0..3 below
+    f[0] = (float)(u & 0xffu);
+    f[1] = (float)((u >> 8) & 0xffu);
+    f[2] = (float)((u >> 16) & 0xffu);
+    f[3] = (float)(u >> 24);
+}
+
+// Lane slices of a K-long row (K % 16 == 0, K <= 1024*P): piece p of lane
+// l is the 16 bytes at k = 1024 p + 16 l, present when that is below K.
+//
+// A wave owns kRowsPerWave weight rows.  All of them go straight to the
+// wave's own LDS region with 16-byte global_load_lds (row j, piece p at
+// (j*P + p) KB; lane l's bytes at +16 l), so no registers hold weights and
+// the occupancy stays high; each lane later reads back only the bytes it
+// loaded itself, so a vmcnt wait is the only synchronisation.  Every
+// activation row of the expert's group then sweeps the 8 rows from LDS, one
+// output at a time (a small live register set, so many waves per CU keep
+// many rows in flight): the weights are read from HBM once whatever the
+// group size.
+//
+// GATEUP: rows j < 4 are gate rows n0+j, rows j >= 4 the up rows of the same
+// n; the inputs are hidden[perm_tokens[g]]; the output z[g, n] = silu(g)*u.
+// DOWN: rows j are down rows n0+j; the inputs are z[g, :]; output y[g, n].
+template <int P, bool GATEUP>
+__global__ __launch_bounds__(kGemvThreads) void gemv_w8_kernel(
+    const float* __restrict__ x_src, const int32_t* __restrict__ perm_tokens, int64_t K,
+    int64_t N, int64_t experts, const int8_t* __restrict__ packed, int64_t hidden,
+    int64_t inter, const float* __restrict__ scale, const int32_t* __restrict__ zp,
+    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
+    float* __restrict__ out) {
+    constexpr int kWaves = kGemvThreads / 64;
+    __shared__ __attribute__((aligned(1024))) int8_t wl[kWaves][kRowsPerWave * P * 1024];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int e = hm_active_expert(counts, experts, (int)blockIdx.y);
+    if (e < 0) return;
+    const int8_t* ebase = packed + (int64_t)e * 3 * hidden * inter;
+    const int64_t n0 = GATEUP ? (int64_t)blockIdx.x * 16 + 4 * wave
+                              : (int64_t)blockIdx.x * 32 + 8 * wave;
+    int8_t* lds = wl[wave];
+    // weights -> LDS
+#pragma unroll
+    for (int j = 0; j < kRowsPerWave; ++j) {
+        const int proj = GATEUP ? (j >> 2) : 2;
+        const int64_t n = GATEUP ? n0 + (j & 3) : n0 + j;
+        const int8_t* row = ebase + proj * hidden * inter + n * K;
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const int64_t k = 1024 * p + 16 * lane;
+            if (k < K) dma16(row + k, lds + (j * P + p) * 1024);
+        }
+    }
+    const int64_t g0 = offsets[e];
+    const int rows = counts[e];
+    wait_vmcnt<0>();
+    for (int r = 0; r < rows; ++r) {
+        const int64_t src = GATEUP ? (int64_t)perm_tokens[g0 + r] : g0 + r;
+        const float* xr = x_src + src * K;
+        float x[P][16];
+        float xs = 0.0f;
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+            const int64_t k = 1024 * p + 16 * lane;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 v = k < K ? *reinterpret_cast<const float4*>(xr + k + 4 * i)
+                                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                x[p][4 * i] = v.x; x[p][4 * i + 1] = v.y;
+                x[p][4 * i + 2] = v.z; x[p][4 * i + 3] = v.w;
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) xs += x[p][i];
+        }
+        float xv[1] = {xs};
+        const float xsum = wave_reduce_many<1>(xv);
+        // one output at a time (gate and up rows of one n together): the
+        // live set stays at one row's 16*P weights
+#pragma unroll 1
+        for (int o = 0; o < (GATEUP ? 4 : kRowsPerWave); ++o) {
+            float v[GATEUP ? 2 : 1];
+#pragma unroll
+            for (int h = 0; h < (GATEUP ? 2 : 1); ++h) {
+                const int j = GATEUP ? o + 4 * h : o;
+                float a = 0.0f;
+#pragma unroll
+                for (int p = 0; p < P; ++p) {
+                    // lanes without a piece read their own unused slot; x is 0
+                    const uint4 wv =
+                        *reinterpret_cast<const uint4*>(lds + (j * P + p) * 1024 + 16 * lane);
+                    const uint32_t d[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        float f[4];
+                        bytes_to_float(d[q], f);
+#pragma unroll
+                        for (int b = 0; b < 4; ++b) a = __builtin_fmaf(x[p][4 * q + b], f[b], a);
+                    }
+                }
+                float av[1] = {a};
+                const float tot = wave_reduce_many<1>(av);
+                const int proj = GATEUP ? h : 2;
+                const float sc = scale[e * 3 + proj];
+                const float zc = (float)(128 + zp[e * 3 + proj]);
+                v[h] = __fmul_rn(__fsub_rn(tot, __fmul_rn(zc, xsum)), sc);
+            }
+            if (lane == 0) {
+                const float y = GATEUP ? __fmul_rn(hm_silu(v[0]), v[GATEUP ? 1 : 0]) : v[0];
+                out[(g0 + r) * N + n0 + o] = y;
+            }
+        }
+    }
+}
+
+template <int P, bool GATEUP>
+int launch_gemv(const float* x_src, const int32_t* perm_tokens, int64_t K, int64_t N,
+                const hm_layer* L, const int32_t* counts, const int32_t* offsets, int64_t slots,
+                float* out, hipStream_t s) {
+    const int64_t per_wg = GATEUP ? 16 : 32;
+    const dim3 grid((unsigned)(N / per_wg), (unsigned)slots);
+    hipLaunchKernelGGL((gemv_w8_kernel<P, GATEUP>), grid, dim3(kGemvThreads), 0, s, x_src,
+                       perm_tokens, K, N, L->experts,
+                       static_cast<const int8_t*>(L->packed), L->hidden, L->intermediate,
+                       L->scale, L->zero_point, counts, offsets, out);
+    HM_LAUNCHED();
+    return HM_OK;
+}
+
+template <bool GATEUP>
+int dispatch_gemv(int64_t K, const float* x_src, const int32_t* perm_tokens, int64_t N,
+                  const hm_layer* L, const int32_t* counts, const int32_t* offsets,
+                  int64_t slots, float* out, hipStream_t s) {
+    if (K <= 1024) return launch_gemv<1, GATEUP>(x_src, perm_tokens, K, N, L, counts, offsets, slots, out, s);
+    if (K <= 2048) return launch_gemv<2, GATEUP>(x_src, perm_tokens, K, N, L, counts, offsets, slots, out, s);
+    return HM_ERR_UNSUPPORTED;
+}
+
+// Rows up to 2048 bytes keep a wave's 8 weight rows within 16 KB of LDS.
+bool gemv_k_ok(int64_t K) { return K >= 16 && K % 16 == 0 && K <= 2048; }
+
+}  // namespace
+
+// Shapes the GEMV kernels take: H, I multiples of 16 up to 2048,
+// I % 16 == 0 (gate/up tiles), H % 32 == 0 (down tiles).
+bool hm_gemv_shape_ok(int64_t H, int64_t I) {
+    return gemv_k_ok(H) && gemv_k_ok(I) && I % 16 == 0 && H % 32 == 0;
+}
+
+// z[g, n] = silu(x_g . Wg[n]) * (x_g . Wu[n]) for every grouped row g, with
+// x_g = hidden[perm_tokens[g]]; `pairs` = T*k bounds the active experts.
+int hm_launch_gateup_gemv(const hm_layer* L, const float* hidden, const int32_t* counts,
+                          const int32_t* offsets, const int32_t* perm_tokens, int64_t pairs,
+                          float* z, hipStream_t s) {
+    const int64_t slots = pairs < L->experts ? pairs : L->experts;
+    return dispatch_gemv<true>(L->hidden, hidden, perm_tokens, L->intermediate, L, counts,
+                               offsets, slots, z, s);
+}
+
+// y[g, n] = z_g . Wd[n] for every grouped row g.
+int hm_launch_down_gemv(const hm_layer* L, const float* z, const int32_t* counts,
+                        const int32_t* offsets, int64_t pairs, float* y, hipStream_t s) {
+    const int64_t slots = pairs < L->experts ? pairs : L->experts;
+    return dispatch_gemv<false>(L->intermediate, z, nullptr, L->hidden, L, counts, offsets,
+                                slots, y, s);
+}

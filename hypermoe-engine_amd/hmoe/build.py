@@ -38,7 +38,7 @@ HIP_FLAGS = [
     f"-I{INCLUDE}", f"-I{CSRC}",
 ]
 KERNEL_SOURCES = ["hm_runtime.hip", "hm_router.hip", "hm_gemm.hip", "hm_gemm_mfma.hip",
-                  "hm_block.hip"]
+                  "hm_gemv.hip", "hm_block.hip"]
 HOST_SOURCES = ["hip_backend.cpp", "hip_tensor_backend.cpp", "moe_block.cpp"]
 
 KERNELS_SO = LIB / "libhm_kernels.so"

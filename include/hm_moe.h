@@ -61,6 +61,13 @@ typedef enum hm_status {
  * scalar reference kernels instead of MFMA (identical integers and float
  * operation sequence; used to pin the MFMA kernels). */
 #define HM_EXEC_GENERIC 0x100u
+/* Execution flag for hm_moe_block_forward: INT8 experts always take the
+ * integer-limb GEMMs.  Without it a block of at most HM_GEMV_MAX_TOKENS
+ * tokens (decode) takes the W8A32 GEMV kernels instead, which stream each
+ * selected expert's weights once and compute in FP32 (within 1e-4 of the
+ * reference, not bit-identical to the limb arithmetic). */
+#define HM_EXEC_LIMBS 0x200u
+#define HM_GEMV_MAX_TOKENS 16
 
 /* Expert weight dtypes (src/tensor/DType.hpp:9-14 numbering). */
 #define HM_DTYPE_FP32 0

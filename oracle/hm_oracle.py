@@ -191,6 +191,16 @@ def _layer_struct(payload, scale, zp, hidden, inter):
                     _p(scale) if is_int8 else None, _p(zp) if is_int8 else None)
 
 
+def expert_mlp(payload, scale, zp, expert, x, inter):
+    """ExpertMlpExecutor::execute for one expert on gathered rows x [n x H]."""
+    x = f32a(x)
+    n, H = x.shape
+    L = _layer_struct(payload, scale, zp, H, inter)
+    y = np.empty((n, H), np.float32)
+    _check(oracle().hmo_expert_mlp(C.byref(L), expert, _p(x), n, _p(y)), "hmo_expert_mlp")
+    return y
+
+
 def moe_block(payload, scale, zp, hidden, router_w, k, inter, softmax=True, renorm=True):
     hidden, router_w = f32a(hidden), f32a(router_w)
     T, H = hidden.shape

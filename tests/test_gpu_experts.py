@@ -119,7 +119,8 @@ def test_block_int8_bitexact_vs_limb_oracle(dev, T, H, E, I, k, L):
     payload, scale, zp, h, w = _layer_inputs(11 + T, T, H, E, I, True)
     layer = DeviceExpertLayer(payload, scale, zp, H, I)
     block = MoEBlock(layer, k, limbs_x=L, limbs_z=L)
-    res = block.execute_batch(dev.to(h), dev.to(w))
+    # the limb arithmetic at every batch size (decode sizes default to the GEMV)
+    res = block.execute_batch(dev.to(h), dev.to(w), exec_flags=capi.HM_EXEC_LIMBS)
     out = dev.host(res.output)
     lout, lids, lsc = O.moe_block_limbs(payload, scale, zp, h, w, k, I, L, L)
     assert_bitexact(res.ids, lids, "ids")
@@ -128,6 +129,12 @@ def test_block_int8_bitexact_vs_limb_oracle(dev, T, H, E, I, k, L):
     # generic (scalar) kernels give the same bits
     res2 = block.execute_batch(dev.to(h), dev.to(w), exec_flags=capi.HM_EXEC_GENERIC)
     assert_bitexact(dev.host(res2.output), out, "MFMA vs generic kernels")
+    if T <= capi.HM_GEMV_MAX_TOKENS:
+        # the default decode path (W8A32 GEMV in FP32) against the reference
+        rout_, _, _ = O.moe_block(payload, scale, zp, h, w, k, I)
+        gres = block.execute_batch(dev.to(h), dev.to(w))
+        assert_bitexact(gres.ids, res.ids, "GEMV path routing")
+        assert_compare(dev.host(gres.output), rout_, 1e-4, 1e-4, "GEMV block vs reference (1e-4)")
     # reference W8A32 numerics within the north-star tolerance
     rout, rids, rsc = O.moe_block(payload, scale, zp, h, w, k, I)
     assert_bitexact(res.ids, rids, "ids vs reference path")
@@ -151,8 +158,39 @@ def test_block_int8_nonzero_zero_points(dev):
     out = dev.host(block.execute_batch(dev.to(h), dev.to(w)).output)
     lout, _, _ = O.moe_block_limbs(payload, scale, zp, h, w, k, I, 2, 2)
     assert_bitexact(out, lout, "block with zero points vs limb oracle")
+    # decode-size batch with zero points through the GEMV
+    hs = np.ascontiguousarray(h[:5])
+    gout = dev.host(block.execute_batch(dev.to(hs), dev.to(w)).output)
+    rout, _, _ = O.moe_block(payload, scale, zp, hs, w, k, I)
+    assert_compare(gout, rout, 1e-4, 1e-4, "GEMV with zero points vs reference (1e-4)")
     gen = block.execute_batch(dev.to(h), dev.to(w), exec_flags=capi.HM_EXEC_GENERIC)
     assert_bitexact(dev.host(gen.output), out, "MFMA vs generic with zero points")
+
+
+@pytest.mark.parametrize("T,H,E,I,k,skew", [
+    (1, 2048, 128, 768, 8, False), (4, 2048, 128, 768, 8, False), (16, 2048, 128, 768, 8, True),
+    (16, 512, 4, 256, 2, False), (13, 1024, 3, 512, 3, False), (9, 256, 2, 1024, 1, False)])
+def test_block_gemv_decode(dev, T, H, E, I, k, skew):
+    """Decode-size blocks take the W8A32 GEMV (FP32): ids bit-exact, output
+    within 1e-4 of the reference; several rows per expert (the register
+    row blocks), skewed groups, every supported K length."""
+    print(f"[gpu] gemv T={T} H={H} E={E} I={I} k={k} skew={skew}", flush=True)
+    payload, scale, zp, h, w = _layer_inputs(7 + T, T, H, E, I, True, skew=skew)
+    block = MoEBlock(DeviceExpertLayer(payload, scale, zp, H, I), k)
+    res = block.execute_batch(dev.to(h), dev.to(w))
+    rout, rids, rsc = O.moe_block(payload, scale, zp, h, w, k, I)
+    assert_bitexact(res.ids, rids, "ids")
+    assert_bitexact(res.scores, rsc, "scores")
+    out = dev.host(res.output)
+    assert_compare(out, rout, 1e-4, 1e-4, "GEMV block vs reference W8A32 (1e-4)")
+    assert normwise(out, rout) < 1e-5
+    # per-expert outputs: the grouped rows equal the reference expert MLP
+    y = dev.host(res.expert_out)
+    for b in res.batches[:4]:
+        lo = int(res.offsets[b.expert_id])
+        xe = np.ascontiguousarray(h[b.token_indices])
+        ref = O.expert_mlp(payload, scale, zp, b.expert_id, xe, I)
+        assert_compare(y[lo:lo + len(b.token_indices)], ref, 1e-4, 1e-4, "expert rows")
 
 
 @pytest.mark.parametrize("T,E", [(16, 64), (40, 8)])
