@@ -7,14 +7,16 @@ Workloads (hmoe.synth.CONFIGS):
   C3-1, C3-4, C3-16   decode shapes (1/4/16 tokens)
   C1, C2 FP32 64-expert blocks
 
-One step = one MoE-block call (route -> permute -> INT8-MFMA SwiGLU experts
--> combine) over a batch already resident in HBM.  Prints ONE JSON line.
+One step = one MoE-block call (route -> permute -> INT8 SwiGLU experts:
+integer-limb MFMA GEMMs at prefill, W8A32 GEMVs at decode -> combine) over a
+batch already resident in HBM.  Prints ONE JSON line.
 
 Roofline: the dominant kernel's algorithmic work per launch divided by its
 average launch duration, measured with hipEvents recorded on the launch
-stream at the block's stage boundaries over the timed steps.
+stream at the block's stage boundaries over K further steps (the timed
+steps themselves carry no events).
   prefill (C4): gate/up GEMM, ops = 2*T*k*2*H*I, bound = INT8 MFMA (5.0 POP/s)
-  decode (C3):  gate/up GEMM, bytes = U*2*H*I (+ activations), bound = HBM 8 TB/s
+  decode (C3):  gate/up GEMV, bytes = U*2*H*I + activations, bound = HBM 8 TB/s
 The CPU baseline is the oracle's restatement of the reference CPU path
 (single thread, reference loop order) timed on a bounded token sample.
 """
@@ -47,6 +49,9 @@ def parse():
     ap.add_argument("--cpu-sample", type=int, default=-1,
                     help="tokens timed on the CPU baseline (-1: per-workload default, 0: skip)")
     ap.add_argument("--quiet", action="store_true")
+    ap.add_argument("--graph", action="store_true",
+                    help="replay one captured HIP graph of the block per step instead of "
+                         "launching every step from the host")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="also run a plain device-to-device copy of this many MiB (3x) "
                          "before the timed region: the known-size kernel that calibrates "
@@ -123,16 +128,46 @@ def main():
     torch.cuda.synchronize()
     log(f"[bench] warmup {args.warmup} done", q)
 
+    # Optionally one step captured as a HIP graph (the block's kernels only;
+    # no memset or copy nodes) and replayed; the replayed result must equal
+    # the eager one.
+    graph = None
+    if args.graph:
+        ref_out = block.launch(d_h, d_w)["out"].clone()
+        try:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                block.launch(d_h, d_w)
+            for _ in range(2):
+                g.replay()
+                torch.cuda.synchronize()
+                if not torch.equal(block._io_bufs["out"], ref_out):
+                    raise RuntimeError("graph replay differs from the eager launch")
+            graph = g
+        except Exception as ex:  # noqa: BLE001 -- report and time eagerly
+            log(f"[bench] graph capture unavailable ({ex}); timing eager launches", q)
+            graph = None
+        torch.cuda.synchronize()
+
+    # timed region: K steps, nothing else on the stream
     torch.cuda.synchronize()
     capi.call("hm_event_record", ev_start, stream)
     for i in range(args.steps):
-        block.launch(d_h, d_w, events=stage_ev[i])
+        if graph is not None:
+            graph.replay()
+        else:
+            block.launch(d_h, d_w)
     capi.call("hm_event_record", ev_stop, stream)
     torch.cuda.synchronize()
     ms = C.c_float()
     capi.call("hm_event_elapsed_ms", C.byref(ms), ev_start, ev_stop)
     total_ms = ms.value
     ms_per_step = total_ms / args.steps
+    # a second pass with the stage events recorded inside every step: the
+    # per-stage times and the dominant kernel's launch duration
+    for i in range(args.steps):
+        block.launch(d_h, d_w, events=stage_ev[i])
+    torch.cuda.synchronize()
     names = ["route", "permute", "quantize", "gate_up", "down", "combine"]
     stage = {n: 0.0 for n in names}
     for i in range(args.steps):
@@ -222,6 +257,7 @@ def main():
                    "intermediate": I, "top_k": k, "weights": "int8" if cfg.int8 else "fp32",
                    "skewed_routing": cfg.skew, "limbs": args.limbs if cfg.int8 else None,
                    "unique_experts": unique, "max_expert_rows": int(counts.max())},
+        "launch": "hip_graph_replay" if graph is not None else "eager",
         "roofline": roof, "layer_roofline": layer,
         "stages_ms": {n: round(v, 5) for n, v in stage.items()},
         "cpu_baseline": cpu, "parity": parity,

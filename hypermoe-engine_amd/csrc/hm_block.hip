@@ -57,6 +57,7 @@ struct Carve {
 
 struct BlockPlan {
     void* route_ws;
+    void* permute_ws;
     uint32_t* ids;
     float* scores;
     int32_t* counts;
@@ -98,6 +99,7 @@ size_t plan_block(const hm_layer* L, int64_t T, int32_t k, int32_t lx, int32_t l
     Carve c(base);
     BlockPlan q{};
     q.route_ws = c.take<char>(hm_route_workspace_bytes(T, E));
+    q.permute_ws = c.take<char>(hm_permute_workspace_bytes(T, k, E));
     q.ids = c.take<uint32_t>((size_t)P);
     q.scores = c.take<float>((size_t)P);
     q.counts = c.take<int32_t>((size_t)E);
@@ -185,7 +187,7 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
                         p.scores, nullptr, status, p.route_ws, stream);
     if (rc || (rc = mark(1))) return rc;
     rc = hm_permute(p.ids, p.scores, tokens, top_k, E, p.counts, p.offsets, p.perm_tokens,
-                    p.perm_weights, p.slots, stream);
+                    p.perm_weights, p.slots, p.permute_ws, stream);
     if (rc || (rc = mark(2))) return rc;
     const int32_t* counts = p.counts;
     if (gemv) {

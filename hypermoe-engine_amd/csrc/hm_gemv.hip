@@ -23,7 +23,8 @@
 namespace {
 
 constexpr int kGemvThreads = 256;
-constexpr int kRowsPerWave = 8;   // weight rows per wave
+constexpr int kRowsPerWave = 4;   // weight rows per wave
+constexpr int kNPW = kRowsPerWave / 2;  // gate/up: output columns per wave
 
 // The slot-th expert (ascending id) with a non-zero group; -1 if none.
 // Every wave computes it redundantly from `counts` (E <= 1024).
@@ -95,8 +96,9 @@ __device__ __forceinline__ void bytes_to_float(uint32_t d, float* f) {
 // many rows in flight): the weights are read from HBM once whatever the
 // group size.
 //
-// GATEUP: rows j < 4 are gate rows n0+j, rows j >= 4 the up rows of the same
-// n; the inputs are hidden[perm_tokens[g]]; the output z[g, n] = silu(g)*u.
+// GATEUP: rows j < kNPW are gate rows n0+j, the others the up rows of the
+// same n; the inputs are hidden[perm_tokens[g]]; the output z[g, n] =
+// silu(g)*u.
 // DOWN: rows j are down rows n0+j; the inputs are z[g, :]; output y[g, n].
 template <int P, bool GATEUP>
 __global__ __launch_bounds__(kGemvThreads) void gemv_w8_kernel(
@@ -112,14 +114,14 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_w8_kernel(
     const int e = hm_active_expert(counts, experts, (int)blockIdx.y);
     if (e < 0) return;
     const int8_t* ebase = packed + (int64_t)e * 3 * hidden * inter;
-    const int64_t n0 = GATEUP ? (int64_t)blockIdx.x * 16 + 4 * wave
-                              : (int64_t)blockIdx.x * 32 + 8 * wave;
+    const int64_t n0 = GATEUP ? ((int64_t)blockIdx.x * kWaves + wave) * kNPW
+                              : ((int64_t)blockIdx.x * kWaves + wave) * kRowsPerWave;
     int8_t* lds = wl[wave];
     // weights -> LDS
 #pragma unroll
     for (int j = 0; j < kRowsPerWave; ++j) {
-        const int proj = GATEUP ? (j >> 2) : 2;
-        const int64_t n = GATEUP ? n0 + (j & 3) : n0 + j;
+        const int proj = GATEUP ? j / kNPW : 2;
+        const int64_t n = GATEUP ? n0 + j % kNPW : n0 + j;
         const int8_t* row = ebase + proj * hidden * inter + n * K;
 #pragma unroll
         for (int p = 0; p < P; ++p) {
@@ -153,11 +155,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_w8_kernel(
         // one output at a time (gate and up rows of one n together): the
         // live set stays at one row's 16*P weights
 #pragma unroll 1
-        for (int o = 0; o < (GATEUP ? 4 : kRowsPerWave); ++o) {
+        for (int o = 0; o < (GATEUP ? kNPW : kRowsPerWave); ++o) {
             float v[GATEUP ? 2 : 1];
 #pragma unroll
             for (int h = 0; h < (GATEUP ? 2 : 1); ++h) {
-                const int j = GATEUP ? o + 4 * h : o;
+                const int j = GATEUP ? o + kNPW * h : o;
                 float a = 0.0f;
 #pragma unroll
                 for (int p = 0; p < P; ++p) {
@@ -192,7 +194,7 @@ template <int P, bool GATEUP>
 int launch_gemv(const float* x_src, const int32_t* perm_tokens, int64_t K, int64_t N,
                 const hm_layer* L, const int32_t* counts, const int32_t* offsets, int64_t slots,
                 float* out, hipStream_t s) {
-    const int64_t per_wg = GATEUP ? 16 : 32;
+    const int64_t per_wg = (kGemvThreads / 64) * (GATEUP ? kNPW : kRowsPerWave);
     const dim3 grid((unsigned)(N / per_wg), (unsigned)slots);
     hipLaunchKernelGGL((gemv_w8_kernel<P, GATEUP>), grid, dim3(kGemvThreads), 0, s, x_src,
                        perm_tokens, K, N, L->experts,
@@ -216,10 +218,10 @@ bool gemv_k_ok(int64_t K) { return K >= 16 && K % 16 == 0 && K <= 2048; }
 
 }  // namespace
 
-// Shapes the GEMV kernels take: H, I multiples of 16 up to 2048,
-// I % 16 == 0 (gate/up tiles), H % 32 == 0 (down tiles).
+// Shapes the GEMV kernels take: H, I multiples of 16 up to 2048 (the
+// tiles: 8 gate/up columns and 16 down rows per workgroup).
 bool hm_gemv_shape_ok(int64_t H, int64_t I) {
-    return gemv_k_ok(H) && gemv_k_ok(I) && I % 16 == 0 && H % 32 == 0;
+    return gemv_k_ok(H) && gemv_k_ok(I) && I % 8 == 0 && H % 16 == 0;
 }
 
 // z[g, n] = silu(x_g . Wg[n]) * (x_g . Wu[n]) for every grouped row g, with

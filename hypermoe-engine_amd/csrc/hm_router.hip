@@ -454,79 +454,99 @@ __global__ __launch_bounds__(kBlock) void router_select_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// A3 permute (src/router/CpuRouterBackend.cpp:140-159): one 1024-thread
-// workgroup per expert e.  The reference appends (t, score) to group ids[t,r]
-// walking tokens in ascending order and then sorts groups by id: a stable
-// counting sort.  Here: an LDS histogram of all ids gives counts[e] and
-// offsets[e] = sum of lower ids' counts; a block scan over token chunks
-// gives each token's rank inside the group, in ascending token order.
+// A3 permute (src/router/CpuRouterBackend.cpp:140-159).  The reference
+// appends (t, score) to group ids[t,r] walking tokens in ascending order and
+// then sorts the groups by id: a stable counting sort of the T*k pairs in
+// token-major order.  Here the pairs are cut into chunks of 1024:
+//   permute_count_kernel    one workgroup per chunk: the chunk's expert
+//                           histogram (LDS, order-free) -> hist[chunk][E]
+//   permute_scatter_kernel  one workgroup per chunk: offsets[e] (exclusive
+//                           scan of the column sums), the chunk's base per
+//                           expert (lower chunks' counts), and each pair's
+//                           rank among the chunk's earlier pairs of the same
+//                           expert (shuffles inside a wave, per-wave counts
+//                           across waves) -> its grouped position.
+// No global atomics; every position is a pure function of the ids.  A single
+// chunk (decode) needs no histogram pass.
 // ---------------------------------------------------------------------------
 constexpr int kPermThreads = 1024;
+constexpr int kPermWaves = kPermThreads / 64;
 
-__device__ __forceinline__ int block_exclusive_scan(int v, int* lds_waves, int* total) {
-    // lds_waves holds kPermThreads/64 ints
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    int incl = v;
-#pragma unroll
-    for (int s = 1; s < 64; s <<= 1) {
-        const int o = __shfl_up(incl, s, 64);
-        if (lane >= s) incl += o;
-    }
-    if (lane == 63) lds_waves[wave] = incl;
+__global__ __launch_bounds__(kPermThreads) void permute_count_kernel(
+    const uint32_t* __restrict__ ids, int64_t pairs, int64_t experts, int32_t* __restrict__ hist) {
+    __shared__ int h[1024];
+    const int tid = threadIdx.x;
+    for (int i = tid; i < experts; i += kPermThreads) h[i] = 0;
     __syncthreads();
-    int base = 0, all = 0;
-    for (int w = 0; w < kPermThreads / 64; ++w) {
-        const int x = lds_waves[w];
-        if (w < wave) base += x;
-        all += x;
-    }
+    const int64_t p = (int64_t)blockIdx.x * kPermThreads + tid;
+    if (p < pairs) atomicAdd(&h[ids[p]], 1);
     __syncthreads();
-    *total = all;
-    return base + incl - v;
+    for (int i = tid; i < experts; i += kPermThreads) hist[(int64_t)blockIdx.x * experts + i] = h[i];
 }
 
-__global__ __launch_bounds__(kPermThreads) void permute_kernel(
-    const uint32_t* __restrict__ ids, const float* __restrict__ scores, int64_t tokens,
-    int32_t top_k, int64_t experts, int32_t* __restrict__ counts,
-    int32_t* __restrict__ offsets, int32_t* __restrict__ perm_tokens,
-    float* __restrict__ perm_weights, int32_t* __restrict__ slots) {
-    __shared__ int hist[1024];
-    __shared__ int waves[kPermThreads / 64];
-    const int tid = threadIdx.x;
-    const uint32_t e = blockIdx.x;
-    const int64_t pairs = tokens * top_k;
-    for (int i = tid; i < experts; i += kPermThreads) hist[i] = 0;
+__global__ __launch_bounds__(kPermThreads) void permute_scatter_kernel(
+    const uint32_t* __restrict__ ids, const float* __restrict__ scores, int64_t pairs,
+    int32_t top_k, int64_t experts, const int32_t* __restrict__ hist, int64_t chunks,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ perm_tokens, float* __restrict__ perm_weights,
+    int32_t* __restrict__ slots) {
+    __shared__ int base[1024];                 // this chunk's first position per expert
+    __shared__ int wcount[kPermWaves][1024];   // per-wave counts (this chunk)
+    __shared__ int scan_w[kPermWaves];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t c = blockIdx.x;
+    const int64_t p = c * kPermThreads + tid;
+    const int e = p < pairs ? (int)ids[p] : -1;
+    for (int i = tid; i < kPermWaves * 1024; i += kPermThreads) (&wcount[0][0])[i] = 0;
     __syncthreads();
-    for (int64_t p = tid; p < pairs; p += kPermThreads) atomicAdd(&hist[ids[p]], 1);
+    if (e >= 0) atomicAdd(&wcount[wave][e], 1);
     __syncthreads();
-    int part = 0;
-    for (int i = tid; i < (int)e; i += kPermThreads) part += hist[i];
-    int offset;
-    block_exclusive_scan(part, waves, &offset);
-    const int count = hist[e];
-    if (tid == 0) {
-        counts[e] = count;
-        offsets[e] = offset;
-        if ((int64_t)e == experts - 1) offsets[experts] = offset + count;
-    }
-    if (count == 0) return;
-    const int64_t chunk = (tokens + kPermThreads - 1) / kPermThreads;
-    const int64_t t_begin = (int64_t)tid * chunk;
-    const int64_t t_end = (t_begin + chunk) < tokens ? (t_begin + chunk) : tokens;
-    int mine = 0;
-    for (int64_t t = t_begin; t < t_end; ++t)
-        for (int r = 0; r < top_k; ++r) mine += ids[t * top_k + r] == e;
-    int total;
-    int pos = offset + block_exclusive_scan(mine, waves, &total);
-    for (int64_t t = t_begin; t < t_end; ++t) {
-        for (int r = 0; r < top_k; ++r) {
-            if (ids[t * top_k + r] != e) continue;
-            perm_tokens[pos] = (int32_t)t;
-            perm_weights[pos] = scores[t * top_k + r];
-            slots[t * top_k + r] = pos;
-            ++pos;
+    // column sums over chunks (total per expert) and the lower chunks' part
+    int total = 0, before = 0;
+    if (tid < experts) {
+        if (hist) {
+            for (int64_t cc = 0; cc < chunks; ++cc) {
+                const int v = hist[cc * experts + tid];
+                total += v;
+                if (cc < c) before += v;
+            }
+        } else {
+            for (int w = 0; w < kPermWaves; ++w) total += wcount[w][tid];
         }
     }
+    // exclusive scan of the totals over experts (one value per thread)
+    int incl = total;
+#pragma unroll
+    for (int sft = 1; sft < 64; sft <<= 1) {
+        const int o = __shfl_up(incl, sft, 64);
+        if (lane >= sft) incl += o;
+    }
+    if (lane == 63) scan_w[wave] = incl;
+    __syncthreads();
+    int wbase = 0;
+    for (int w = 0; w < wave; ++w) wbase += scan_w[w];
+    const int offset = wbase + incl - total;
+    if (tid < experts) {
+        base[tid] = offset + before;
+        if (c == 0) {
+            counts[tid] = total;
+            offsets[tid] = offset;
+            if (tid == experts - 1) offsets[experts] = offset + total;
+        }
+    }
+    __syncthreads();
+    if (e < 0) return;
+    // rank among the chunk's earlier pairs of the same expert
+    int rank = 0;
+    for (int w = 0; w < wave; ++w) rank += wcount[w][e];
+    for (int l = 0; l < 64; ++l) {
+        const int other = __shfl(e, l, 64);
+        rank += (l < lane && other == e) ? 1 : 0;
+    }
+    const int pos = base[e] + rank;
+    perm_tokens[pos] = (int32_t)(p / top_k);
+    perm_weights[pos] = scores[p];
+    slots[p] = pos;
 }
 
 // A4 gather (MoERuntime.cpp:288-298).
@@ -697,17 +717,35 @@ int hm_router_topk(const float* h, const float* w, int64_t tokens,
     return HM_OK;
 }
 
+// Permute workspace: the per-chunk histograms [chunks x E] (none for one
+// chunk).
+size_t hm_permute_workspace_bytes(int64_t tokens, int32_t top_k, int64_t experts) {
+    if (tokens <= 0 || top_k <= 0 || experts <= 0) return 0;
+    const int64_t chunks = (tokens * top_k + kPermThreads - 1) / kPermThreads;
+    return chunks > 1 ? (size_t)chunks * (size_t)experts * sizeof(int32_t) : 0;
+}
+
 int hm_permute(const uint32_t* ids, const float* scores, int64_t tokens,
                int32_t top_k, int64_t experts, int32_t* counts, int32_t* offsets,
                int32_t* perm_tokens, float* perm_weights, int32_t* slots,
-               void* stream) {
+               void* workspace, void* stream) {
     HM_REQUIRE(ids && scores && counts && offsets && perm_tokens && perm_weights && slots);
     HM_REQUIRE(tokens > 0 && top_k > 0 && experts > 0 && top_k <= experts);
     if (experts > 1024) return HM_ERR_UNSUPPORTED;
     if (tokens * top_k > INT_MAX) return HM_ERR_OVERFLOW;
-    hipLaunchKernelGGL(permute_kernel, dim3((unsigned)experts), dim3(kPermThreads), 0,
-                       hm_stream(stream), ids, scores, tokens, top_k, experts, counts,
-                       offsets, perm_tokens, perm_weights, slots);
+    const int64_t pairs = tokens * top_k;
+    const int64_t chunks = (pairs + kPermThreads - 1) / kPermThreads;
+    int32_t* hist = nullptr;
+    if (chunks > 1) {
+        HM_REQUIRE(workspace);
+        hist = static_cast<int32_t*>(workspace);
+        hipLaunchKernelGGL(permute_count_kernel, dim3((unsigned)chunks), dim3(kPermThreads), 0,
+                           hm_stream(stream), ids, pairs, experts, hist);
+        HM_LAUNCHED();
+    }
+    hipLaunchKernelGGL(permute_scatter_kernel, dim3((unsigned)chunks), dim3(kPermThreads), 0,
+                       hm_stream(stream), ids, scores, pairs, top_k, experts, hist, chunks,
+                       counts, offsets, perm_tokens, perm_weights, slots);
     HM_LAUNCHED();
     return HM_OK;
 }

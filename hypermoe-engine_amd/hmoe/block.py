@@ -124,7 +124,8 @@ class MoEBlock:
         torch = _torch()
         tokens = hidden.shape[0]
         ws, b = self._buffers(tokens, exec_flags)
-        b["status"].zero_()
+        # b["status"] starts at zero and kernels only OR bits into it;
+        # execute_batch clears it after reporting a failure
         io = capi.HmBlockIO(b["out"].data_ptr(), b["ids"].data_ptr(), b["scores"].data_ptr(),
                             b["counts"].data_ptr(), b["offsets"].data_ptr(),
                             b["perm_tokens"].data_ptr(), b["perm_weights"].data_ptr(),
@@ -146,6 +147,7 @@ class MoEBlock:
         torch.cuda.synchronize()
         status = int(b["status"].cpu().item())
         if status:
+            b["status"].zero_()
             raise RuntimeError(f"router failed on the device (status bits {status:#x})")
         res = BlockResult(
             ids=b["ids"].cpu().numpy().view(np.uint32), scores=b["scores"].cpu().numpy(),

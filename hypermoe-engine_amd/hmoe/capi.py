@@ -66,7 +66,8 @@ SIGNATURES = {
     "hm_rmsnorm": (c_i32, [vp, vp, vp, c_i64, c_i64, c_f32, vp]),
     "hm_route_workspace_bytes": (c_sz, [c_i64, c_i64]),
     "hm_router_topk": (c_i32, [vp, vp, c_i64, c_i64, c_i64, c_i32, c_u32, vp, vp, vp, vp, vp, vp]),
-    "hm_permute": (c_i32, [vp, vp, c_i64, c_i32, c_i64, vp, vp, vp, vp, vp, vp]),
+    "hm_permute_workspace_bytes": (c_sz, [c_i64, c_i32, c_i64]),
+    "hm_permute": (c_i32, [vp, vp, c_i64, c_i32, c_i64, vp, vp, vp, vp, vp, vp, vp]),
     "hm_gather_rows": (c_i32, [vp, vp, c_i64, c_i64, vp, vp]),
     "hm_plan_int8_gemm": (c_i32, [c_i64, c_i64, c_i64, c_i32, C.POINTER(HmInt8GemmPlan)]),
     "hm_matmul_w8a32": (c_i32, [vp, vp, c_f32, c_i32, vp, c_i64, c_i64, c_i64, c_i32, vp, c_sz, vp]),

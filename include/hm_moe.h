@@ -125,12 +125,14 @@ int hm_router_topk(const float* h, const float* w, int64_t tokens,
  * counts[E], offsets[E+1], perm_tokens/perm_weights[tokens*top_k] in group
  * order (groups by ascending expert id, tokens ascending inside a group),
  * slots[tokens*top_k]: the grouped row of pair (t, r).  Bit-exact.  No
- * global atomics: one workgroup per expert histograms the ids in LDS and
- * ranks its tokens with a block scan. */
+ * global atomics: per-chunk LDS histograms, then each chunk ranks its pairs.
+ * `workspace`: hm_permute_workspace_bytes(...) bytes (may be NULL when that
+ * is 0, i.e. tokens*top_k <= 1024). */
+size_t hm_permute_workspace_bytes(int64_t tokens, int32_t top_k, int64_t experts);
 int hm_permute(const uint32_t* ids, const float* scores, int64_t tokens,
                int32_t top_k, int64_t experts, int32_t* counts,
                int32_t* offsets, int32_t* perm_tokens, float* perm_weights,
-               int32_t* slots, void* stream);
+               int32_t* slots, void* workspace, void* stream);
 
 /* ---- A4  Gather rows (src/core/runtime/MoERuntime.cpp:282-299) ----------
  * out[r,:] = in[rows[r],:]. */

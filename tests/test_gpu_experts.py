@@ -231,3 +231,30 @@ def test_block_c4_prefill_properties(dev):
     assert_bitexact(dev.host(r3.output), o1[sub], "token-slice invariance")
     lout, _, _ = O.moe_block_limbs(payload, scale, zp, np.ascontiguousarray(h[sub]), w, k, I, 2, 2)
     assert_bitexact(o1[sub], lout, "C4 slice vs limb oracle")
+
+
+@pytest.mark.parametrize("T", [1, 16, 300])
+def test_block_graph_replay(dev, T):
+    """The block's launch sequence captured as one HIP graph (kernels only:
+    no memset or copy nodes) replays to the eager result every time, with
+    eager work and synchronisations between the replays."""
+    import torch
+    print(f"[gpu] graph replay T={T}", flush=True)
+    H, E, I, k = 2048, 128, 768, 8
+    payload, scale, zp, h, w = _layer_inputs(31 + T, T, H, E, I, True)
+    block = MoEBlock(DeviceExpertLayer(payload, scale, zp, H, I), k)
+    dh, dw = dev.to(h), dev.to(w)
+    eager = block.launch(dh, dw)["out"].clone()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        block.launch(dh, dw)
+    for i in range(3):
+        block._io_bufs["out"].fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(block._io_bufs["out"], eager), f"replay {i} differs"
+        # eager work between replays
+        again = block.launch(dh, dw)["out"]
+        torch.cuda.synchronize()
+        assert torch.equal(again, eager)

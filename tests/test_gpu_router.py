@@ -32,9 +32,10 @@ def run_router(dev, h, w, k, flags):
     slots = dev.empty(T * k, np.int32)
     st = int(dev.host(status)[0])
     if st == 0:
+        pws = dev.empty(max(1, dev.lib.hm_permute_workspace_bytes(T, k, E)), np.uint8)
         dev.call("hm_permute", ids.data_ptr(), scores.data_ptr(), T, k, E, counts.data_ptr(),
                  offsets.data_ptr(), ptok.data_ptr(), pw.data_ptr(), slots.data_ptr(),
-                 dev.stream)
+                 pws.data_ptr(), dev.stream)
     return dict(status=st, ids=dev.host(ids, np.uint32), scores=dev.host(scores),
                 logits=dev.host(logits), counts=dev.host(counts), offsets=dev.host(offsets),
                 ptok=dev.host(ptok), pw=dev.host(pw), slots=dev.host(slots).reshape(T, k))
