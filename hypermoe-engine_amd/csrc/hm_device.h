@@ -109,15 +109,30 @@ __device__ __forceinline__ float hm_recombine(const int* p, int limbs) {
 __device__ __forceinline__ bool hm_locate_tile(const int32_t* __restrict__ counts,
                                                int64_t experts, int tile_m, int64_t tile,
                                                int64_t* expert_out, int64_t* tile_in_expert) {
-    int64_t acc = 0;
-    for (int64_t e = 0; e < experts; ++e) {
-        const int64_t n = (counts[e] + tile_m - 1) / tile_m;
-        if (tile < acc + n) {
-            *expert_out = e;
-            *tile_in_expert = tile - acc;
+    // Wave-parallel: 64 experts at a time, an inclusive scan of their tile
+    // counts, a ballot for the first expert whose tiles reach past `tile`.
+    // Every lane of the wave must be active.
+    const int lane = threadIdx.x & (HM_WAVE - 1);
+    int64_t base = 0;  // tiles of the experts before this chunk
+    for (int64_t c0 = 0; c0 < experts; c0 += HM_WAVE) {
+        const int64_t e = c0 + lane;
+        const int64_t n = e < experts ? ((int64_t)counts[e] + tile_m - 1) / tile_m : 0;
+        int64_t incl = n;
+#pragma unroll
+        for (int sft = 1; sft < HM_WAVE; sft <<= 1) {
+            const int64_t o = __shfl_up(incl, sft, HM_WAVE);
+            if (lane >= sft) incl += o;
+        }
+        const int64_t total = __shfl(incl, HM_WAVE - 1, HM_WAVE);
+        if (tile < base + total) {
+            const unsigned long long m = __ballot(base + incl > tile);
+            const int first = __ffsll((long long)m) - 1;
+            const int64_t before = __shfl(incl - n, first, HM_WAVE);
+            *expert_out = c0 + first;
+            *tile_in_expert = tile - base - before;
             return true;
         }
-        acc += n;
+        base += total;
     }
     return false;
 }

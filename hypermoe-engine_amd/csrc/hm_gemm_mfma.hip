@@ -11,13 +11,14 @@
 // lane l are rows 4*(l/16) + 0..3 of column l % 16.
 //
 // Data movement: operands go straight from global memory to LDS with the
-// gfx950 16-byte global_load_lds (lane l's 16 bytes land at base + 16*l):
-// one wave-wide load fills one 1 KB fragment (16 rows x 64 K bytes) in a
-// swizzled order that keeps both the global reads coalesced per row and the
-// MFMA's ds_read_b128 bank-conflict free (frag_offset), and no registers
-// stage the data.  A ring of S stages keeps S-1 K steps of loads in flight; one
-// s_waitcnt vmcnt + barrier per step.  The K loop is unrolled by S so that
-// every step reads and fills distinct LDS arrays.
+// gfx950 16-byte global_load_lds (lane l's 16 bytes land at base + 16*l)
+// into fragments of 16 rows x KB bytes (KB = 128 for gate/up: every row load
+// is a full 128-byte line; 64 for down) in a swizzled order that keeps both
+// the global reads coalesced per row and the MFMA's ds_read_b128 bank-
+// conflict free (Frag), and no registers stage the data.  A ring of S stages
+// keeps S-1 K steps of loads in flight; one s_waitcnt vmcnt + barrier per
+// step.  The K loop is unrolled by S so that every step reads and fills
+// distinct LDS arrays.
 //
 // Tile order: the grid is 1D; workgroup i runs on XCD i % 8 (round-robin
 // dispatch), so the linear tile index is remapped to give each XCD a
@@ -33,37 +34,13 @@ namespace {
 
 constexpr int kThreads = 512;
 constexpr int kWaves = 8;
-constexpr int kStepK = 64;
-constexpr int kFrag = 1024;         // bytes per MFMA operand fragment
+constexpr int kMfmaK = 64;          // K bytes of one v_mfma_i32_16x16x64_i8
 constexpr int kZBlock = 128;
 constexpr int kGateUpN = 128;       // columns per projection per gate/up tile
 constexpr int kDownN = 512;         // output columns per down tile (16 * Tile<L,true>::BFRAGS)
 constexpr int kXcds = 8;
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-
-// Tile traits: WM 16-row subtiles per wave, two row groups of waves.
-// gate/up: wave = 4*16 rows x (2 gate + 2 up) 16-column fragments, tile
-// 128 rows x 256 weight rows.  down: wave = WM*16 rows x 8 fragments (128
-// columns), tile 2*WM*16 rows x 512 columns.  A wave's (WM*L) A fragments
-// times its JB B fragments give MFMAs that each need 384 LDS bytes or
-// fewer (8 A x 4 B, 4 A x 8 B), within the LDS bandwidth at full MFMA rate.
-template <int L, bool DOWN>
-struct Tile {
-    static constexpr int WM = DOWN ? (L >= 3 ? 1 : 2) : 4;   // 16-row subtiles per wave
-    static constexpr int JB = DOWN ? 8 : 4;                   // B fragments per wave
-    static constexpr int BM = 2 * 16 * WM;
-    static constexpr int BFRAGS = 4 * JB;                     // B fragments per tile
-    static constexpr int NA = L * BM / 16;                    // A fragments / stage
-    static constexpr int NF = NA + BFRAGS;                    // fragments / stage
-    static constexpr int LPW = (NF + kWaves - 1) / kWaves;    // loads per wave / stage
-    static constexpr int S = NF * 4 <= 128 ? 4 : 3;           // ring depth
-    static constexpr int STAGE_BYTES = NF * kFrag;
-};
-
-__device__ __forceinline__ v4i lds16(const int8_t* p) {
-    return *reinterpret_cast<const v4i*>(p);
-}
 
 // Fragment layout in LDS.  The wave-wide load that fills a fragment gives
 // lane l row l/4 and 16-byte K chunk (l%4) ^ ((l/16)%4) of the 16 x 64 byte
@@ -72,12 +49,65 @@ __device__ __forceinline__ v4i lds16(const int8_t* p) {
 // m/16) finds its bytes at 16*(4*row + (chunk ^ (row/4))); over any 16
 // consecutive reader lanes these are 16 distinct 16-byte bank groups, so the
 // ds_read_b128 stays conflict free.
-__device__ __forceinline__ int dma_row(int lane) { return lane >> 2; }
-__device__ __forceinline__ int dma_chunk(int lane) { return (lane & 3) ^ ((lane >> 4) & 3); }
-__device__ __forceinline__ int frag_offset(int m) {
-    const int r = m & 15, c = m >> 4;
-    return 16 * (4 * r + (c ^ (r >> 2)));
+//
+// With 128 K bytes per ring step a fragment is 16 rows x 128 bytes, two
+// wave-wide loads (rows 0-7, 8-15): lane l takes row 8i + l/8 and 16-byte
+// chunk (l%8) ^ ((row/2)%8), so 8 lanes read one row's full 128-byte line;
+// reader lane m of K half h (row m%16, chunk 4h + m/16) finds its bytes at
+// 1024*(row/8) + 16*(8*(row%8) + (chunk ^ (row/2)%8)), again 16 distinct
+// bank groups over any 16 consecutive lanes.
+template <int KB>
+struct Frag {
+    static constexpr int BYTES = 16 * KB;   // 16 rows of KB bytes
+    static constexpr int LOADS = KB / 64;   // 1 KB wave-wide loads per fragment
+    static constexpr int SUB = KB / kMfmaK; // MFMA K steps per ring step
+    static_assert(KB == 64 || KB == 128, "fragment K width");
+    // row (0..15) and 16-byte chunk loaded by `lane` in load i
+    __device__ static int load_row(int lane, int i) {
+        return KB == 64 ? lane >> 2 : 8 * i + (lane >> 3);
+    }
+    __device__ static int load_chunk(int lane, int i) {
+        if (KB == 64) return (lane & 3) ^ ((lane >> 4) & 3);
+        const int r = load_row(lane, i);
+        return (lane & 7) ^ ((r >> 1) & 7);
+    }
+    // byte offset read by MFMA lane m in K step h of the fragment
+    __device__ static int read_offset(int m, int h) {
+        const int r = m & 15, c = 4 * h + (m >> 4);
+        if (KB == 64) return 16 * (4 * r + (c ^ (r >> 2)));
+        return 1024 * (r >> 3) + 16 * (8 * (r & 7) + (c ^ ((r >> 1) & 7)));
+    }
+};
+
+// Tile traits: WM 16-row subtiles per wave, two row groups of waves.
+// gate/up: wave = WM*16 rows (WM = 4, or 2 at three limbs) x (2 gate + 2 up)
+// 16-column fragments, tile 2*WM*16 rows x 256 weight rows.  down: wave =
+// WM*16 rows x 8 fragments (128
+// columns), tile 2*WM*16 rows x 512 columns.  A wave's (WM*L) A fragments
+// times its JB B fragments give MFMAs that each need 384 LDS bytes or
+// fewer (8 A x 4 B, 4 A x 8 B), within the LDS bandwidth at full MFMA rate.
+template <int L, bool DOWN>
+struct Tile {
+    static constexpr int WM = DOWN ? (L >= 3 ? 1 : 2) : (L >= 3 ? 2 : 4);  // 16-row subtiles per wave
+    static constexpr int JB = DOWN ? 8 : 4;                   // B fragments per wave
+    static constexpr int BM = 2 * 16 * WM;
+    static constexpr int BFRAGS = 4 * JB;                     // B fragments per tile
+    static constexpr int NA = L * BM / 16;                    // A fragments / stage
+    static constexpr int NF = NA + BFRAGS;                    // fragments / stage
+    static constexpr int KB = DOWN ? 64 : 128;                // K bytes per ring step
+    using F = Frag<KB>;
+    static constexpr int NL = NF * F::LOADS;                  // wave loads / stage
+    static constexpr int LPW = (NL + kWaves - 1) / kWaves;    // loads per wave / stage
+    // ring depth: as many stages as fit in ~136 KB of LDS, at least 2
+    static constexpr int S = NF * F::BYTES * 4 <= 139264 ? 4
+                           : NF * F::BYTES * 3 <= 139264 ? 3 : 2;
+    static constexpr int STAGE_BYTES = NF * F::BYTES;
+};
+
+__device__ __forceinline__ v4i lds16(const int8_t* p) {
+    return *reinterpret_cast<const v4i*>(p);
 }
+
 
 
 // The K loop over nk steps with a ring of S LDS stages.  Stage ks lives in
@@ -88,7 +118,7 @@ __device__ __forceinline__ int frag_offset(int m) {
 // stage ks.  The steady state, where every step refills, runs unguarded; the
 // last steps drain the ring.  The stages are distinct arrays named at compile
 // time in every unrolled step.
-template <int S, int LPW, class Issue, class Compute>
+template <int S, int LPW, int KB, class Issue, class Compute>
 __device__ __forceinline__ void ring_loop(int nk, int8_t* r0, int8_t* r1, int8_t* r2, int8_t* r3,
                                           Issue&& issue, Compute&& compute) {
     auto slot = [&](int s) -> int8_t* {
@@ -96,7 +126,7 @@ __device__ __forceinline__ void ring_loop(int nk, int8_t* r0, int8_t* r1, int8_t
     };
 #pragma unroll
     for (int s = 0; s < S - 1; ++s) {
-        if (s < nk) issue(slot(s), (int64_t)s * kStepK);
+        if (s < nk) issue(slot(s), (int64_t)s * KB);
     }
     int ks0 = 0;
     for (; ks0 + 2 * S - 2 < nk; ks0 += S) {
@@ -104,7 +134,7 @@ __device__ __forceinline__ void ring_loop(int nk, int8_t* r0, int8_t* r1, int8_t
         for (int s = 0; s < S; ++s) {
             wait_vmcnt<(S - 2) * LPW>();
             lds_barrier();
-            issue(slot((s + S - 1) % S), (int64_t)(ks0 + s + S - 1) * kStepK);
+            issue(slot((s + S - 1) % S), (int64_t)(ks0 + s + S - 1) * KB);
             compute(slot(s), ks0 + s);
         }
     }
@@ -116,7 +146,7 @@ __device__ __forceinline__ void ring_loop(int nk, int8_t* r0, int8_t* r1, int8_t
                 if (ks + S - 2 < nk) wait_vmcnt<(S - 2) * LPW>();
                 else wait_vmcnt<0>();
                 lds_barrier();
-                if (ks + S - 1 < nk) issue(slot((s + S - 1) % S), (int64_t)(ks + S - 1) * kStepK);
+                if (ks + S - 1 < nk) issue(slot((s + S - 1) % S), (int64_t)(ks + S - 1) * KB);
                 compute(slot(s), ks);
             }
         }
@@ -153,19 +183,25 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
     const int32_t* __restrict__ perm_tokens, int64_t R, int8_t* __restrict__ zdig,
     float* __restrict__ zscale, int32_t* __restrict__ zdsum) {
     using T = Tile<L, false>;
-    constexpr int WM = T::WM, BM = T::BM, NA = T::NA, NF = T::NF, LPW = T::LPW, S = T::S;
+    using F = typename T::F;
+    constexpr int WM = T::WM, BM = T::BM, NA = T::NA, NL = T::NL, LPW = T::LPW, S = T::S,
+                  KB = T::KB;
     __shared__ __attribute__((aligned(1024))) int8_t ring0[T::STAGE_BYTES];
     __shared__ __attribute__((aligned(1024))) int8_t ring1[T::STAGE_BYTES];
     __shared__ __attribute__((aligned(1024))) int8_t ring2[T::STAGE_BYTES];
     __shared__ __attribute__((aligned(1024))) int8_t ring3[S > 3 ? T::STAGE_BYTES : 16];
     __shared__ int32_t row_token[BM];
+    __shared__ float s_xscale[BM];
+    __shared__ int32_t s_xdsum[L][BM];
     __shared__ float red[BM][4];
     __shared__ int red_i[L][BM][4];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 2, wn = wave & 3;
-    const int rd = frag_offset(lane);
+    int rd[F::SUB];
+#pragma unroll
+    for (int h = 0; h < F::SUB; ++h) rd[h] = F::read_offset(lane, h);
     int64_t gmt, nb;
     if (!xcd_tile(mtiles, I / kGateUpN, &gmt, &nb)) return;
     int64_t e, mt;
@@ -175,6 +211,15 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
     const int64_t n0 = nb * kGateUpN;
     if (tid < BM) row_token[tid] = perm_tokens[g0 + (tid < nrows ? tid : 0)];
     __syncthreads();
+    // per-row activation scale (and digit sums if a zero point needs them)
+    // for the epilogue, fetched while the K loop runs
+    const int zg = zp[e * 3 + 0], zu = zp[e * 3 + 1];
+    if (tid < BM) {
+        const int tok = row_token[tid];
+        s_xscale[tid] = xscale[tok];
+#pragma unroll
+        for (int l = 0; l < L; ++l) s_xdsum[l][tid] = (zg | zu) ? xdsum[(int64_t)l * tokens + tok] : 0;
+    }
 
     // Per-lane global source of each fragment this wave loads (K offset 0).
     const int8_t* ebase = packed + e * 3 * H * I;
@@ -182,16 +227,18 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
     int dst[LPW];
 #pragma unroll
     for (int c = 0; c < LPW; ++c) {
-        const int f = (wave + kWaves * c) % NF;
-        dst[c] = f * kFrag;
+        const int u = (wave + kWaves * c) % NL;   // load unit: fragment f, part li
+        const int f = u / F::LOADS, li = u % F::LOADS;
+        const int fr = F::load_row(lane, li), ch = F::load_chunk(lane, li);
+        dst[c] = f * F::BYTES + 1024 * li;
         if (f < NA) {
             const int l = f / (BM / 16), i = f % (BM / 16);
-            const int tok = row_token[16 * i + dma_row(lane)];
-            src[c] = xdig + ((int64_t)l * tokens + tok) * H + 16 * dma_chunk(lane);
+            const int tok = row_token[16 * i + fr];
+            src[c] = xdig + ((int64_t)l * tokens + tok) * H + 16 * ch;
         } else {
-            const int brow = 16 * (f - NA) + dma_row(lane);
+            const int brow = 16 * (f - NA) + fr;
             const int64_t col = n0 + (brow & 127);
-            src[c] = ebase + (brow >> 7) * H * I + col * H + 16 * dma_chunk(lane);
+            src[c] = ebase + (brow >> 7) * H * I + col * H + 16 * ch;
         }
     }
     auto issue = [&](int8_t* stage, int64_t k0) {
@@ -208,38 +255,41 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
             for (int l = 0; l < L; ++l) acc[i][j][l] = v4i{0, 0, 0, 0};
 
     auto compute = [&](const int8_t* stage) {
-        v4i b[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int bf = (j >> 1) * 8 + 2 * wn + (j & 1);  // 16-row fragment index
-            b[j] = lds16(stage + (NA + bf) * kFrag + rd);
-        }
+        for (int h = 0; h < F::SUB; ++h) {
+            v4i b[4];
 #pragma unroll
-        for (int i = 0; i < WM; ++i) {
+            for (int j = 0; j < 4; ++j) {
+                const int bf = (j >> 1) * 8 + 2 * wn + (j & 1);  // 16-row fragment index
+                b[j] = lds16(stage + (NA + bf) * F::BYTES + rd[h]);
+            }
 #pragma unroll
-            for (int l = 0; l < L; ++l) {
-                const v4i a = lds16(stage + (l * (BM / 16) + wm * WM + i) * kFrag + rd);
+            for (int i = 0; i < WM; ++i) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    acc[i][j][l] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[j], acc[i][j][l], 0, 0, 0);
+                for (int l = 0; l < L; ++l) {
+                    const v4i a = lds16(stage + (l * (BM / 16) + wm * WM + i) * F::BYTES + rd[h]);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        acc[i][j][l] =
+                            __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[j], acc[i][j][l], 0, 0, 0);
+                    }
                 }
             }
         }
     };
 
-    ring_loop<S, LPW>((int)(H / kStepK), ring0, ring1, ring2, ring3, issue,
+    ring_loop<S, LPW, KB>((int)(H / KB), ring0, ring1, ring2, ring3, issue,
                       [&](const int8_t* stage, int) { compute(stage); });
 
     // ---- epilogue -------------------------------------------------------
     const float sg = scale[e * 3 + 0], su = scale[e * 3 + 1];
-    const int zg = zp[e * 3 + 0], zu = zp[e * 3 + 1], zd = zp[e * 3 + 2];
+    const int zd = zp[e * 3 + 2];
     float z[WM][2][4];
 #pragma unroll
     for (int i = 0; i < WM; ++i) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int r = wm * (BM / 2) + 16 * i + 4 * (lane >> 4) + q;
-            const int tok = row_token[r];
             const bool live = r < nrows;
             float m = 0.0f;
 #pragma unroll
@@ -249,11 +299,11 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
                     int pg[L], pu[L];
 #pragma unroll
                     for (int l = 0; l < L; ++l) {
-                        const int ds = (zg | zu) ? xdsum[(int64_t)l * tokens + tok] : 0;
+                        const int ds = s_xdsum[l][r];
                         pg[l] = acc[i][j][l][q] - zg * ds;
                         pu[l] = acc[i][j + 2][l][q] - zu * ds;
                     }
-                    const float sx = xscale[tok];
+                    const float sx = s_xscale[r];
                     const float g = __fmul_rn(hm_recombine(pg, L), __fmul_rn(sx, sg));
                     const float u = __fmul_rn(hm_recombine(pu, L), __fmul_rn(sx, su));
                     zv = __fmul_rn(hm_silu(g), u);
@@ -270,6 +320,9 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
     const float range = (float)hm_limb_range(L);
     const int64_t nbz = I / kZBlock;
     const int64_t zb = n0 / kZBlock;
+    // the digits of the tile's Z segment: [L][BM][128] bytes (staged in LDS,
+    // stored below with 16-byte writes)
+    int zfix[WM][2][4];
 #pragma unroll
     for (int i = 0; i < WM; ++i) {
 #pragma unroll
@@ -280,22 +333,15 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
             int dsum[L];
 #pragma unroll
             for (int l = 0; l < L; ++l) dsum[l] = 0;
-            if (r < nrows) {
-                const int64_t grow = g0 + r;
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const int64_t col = n0 + 32 * wn + 16 * j + (lane & 15);
-                    const int v = hm_fixed_point(z[i][j][q], inv, range);
+            for (int j = 0; j < 2; ++j) {
+                const int v = hm_fixed_point(z[i][j][q], inv, range);
+                zfix[i][j][q] = v;
 #pragma unroll
-                    for (int l = 0; l < L; ++l) {
-                        const int d = hm_digit(v, l);
-                        zdig[((int64_t)l * R + grow) * I + col] = (int8_t)d;
-                        dsum[l] += d;
-                    }
-                }
-                if (wn == 0 && (lane & 15) == 0) {
-                    zscale[grow * nbz + zb] = amax > 0.0f ? __fdiv_rn(amax, range) : 0.0f;
-                }
+                for (int l = 0; l < L; ++l) dsum[l] += hm_digit(v, l);
+            }
+            if (r < nrows && wn == 0 && (lane & 15) == 0) {
+                zscale[(g0 + r) * nbz + zb] = amax > 0.0f ? __fdiv_rn(amax, range) : 0.0f;
             }
             if (zd != 0) {
 #pragma unroll
@@ -308,8 +354,29 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
             }
         }
     }
-    if (zd != 0) {
+    // digit planes out through LDS (ring0, free after the K loop): byte
+    // writes into [BM][128], then 16-byte rows segments to zdig
+    int8_t* zst = ring0;
+#pragma unroll
+    for (int l = 0; l < L; ++l) {
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int r = wm * (BM / 2) + 16 * i + 4 * (lane >> 4) + q;
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    zst[r * kGateUpN + 32 * wn + 16 * j + (lane & 15)] = (int8_t)hm_digit(zfix[i][j][q], l);
+            }
         __syncthreads();
+        for (int c = tid; c < nrows * (kGateUpN / 16); c += kThreads) {
+            const int r = c / (kGateUpN / 16), c16 = c % (kGateUpN / 16);
+            const int4 v = *reinterpret_cast<const int4*>(zst + r * kGateUpN + 16 * c16);
+            *reinterpret_cast<int4*>(zdig + ((int64_t)l * R + g0 + r) * I + n0 + 16 * c16) = v;
+        }
+        __syncthreads();
+    }
+    if (zd != 0) {
         if (tid < nrows) {
 #pragma unroll
             for (int l = 0; l < L; ++l) {
@@ -335,8 +402,9 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
     float* __restrict__ y) {
     using T = Tile<L, true>;
-    constexpr int WM = T::WM, JB = T::JB, BM = T::BM, NA = T::NA, NF = T::NF, LPW = T::LPW,
-                  S = T::S;
+    using F = typename T::F;
+    constexpr int WM = T::WM, JB = T::JB, BM = T::BM, NA = T::NA, NL = T::NL, LPW = T::LPW,
+                  S = T::S, KB = T::KB;
     constexpr int BN = 16 * T::BFRAGS;  // output columns per tile
     constexpr int MAXNB = 16;           // Z segments (I <= 2048)
     __shared__ __attribute__((aligned(1024))) int8_t ring0[T::STAGE_BYTES];
@@ -349,7 +417,9 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 2, wn = wave & 3;
-    const int rd = frag_offset(lane);
+    int rd[F::SUB];
+#pragma unroll
+    for (int h = 0; h < F::SUB; ++h) rd[h] = F::read_offset(lane, h);
     int64_t gmt, nb;
     if (!xcd_tile(mtiles, H / BN, &gmt, &nb)) return;
     int64_t e, mt;
@@ -373,15 +443,17 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
     int dst[LPW];
 #pragma unroll
     for (int c = 0; c < LPW; ++c) {
-        const int f = (wave + kWaves * c) % NF;
-        dst[c] = f * kFrag;
+        const int u = (wave + kWaves * c) % NL;   // load unit: fragment f, part li
+        const int f = u / F::LOADS, li = u % F::LOADS;
+        const int fr = F::load_row(lane, li), ch = F::load_chunk(lane, li);
+        dst[c] = f * F::BYTES + 1024 * li;
         if (f < NA) {
             const int l = f / (BM / 16), i = f % (BM / 16);
-            const int r = 16 * i + dma_row(lane);
-            src[c] = zdig + ((int64_t)l * R + g0 + (r < nrows ? r : 0)) * I + 16 * dma_chunk(lane);
+            const int r = 16 * i + fr;
+            src[c] = zdig + ((int64_t)l * R + g0 + (r < nrows ? r : 0)) * I + 16 * ch;
         } else {
-            const int brow = 16 * (f - NA) + dma_row(lane);
-            src[c] = dbase + (n0 + brow) * I + 16 * dma_chunk(lane);
+            const int brow = 16 * (f - NA) + fr;
+            src[c] = dbase + (n0 + brow) * I + 16 * ch;
         }
     }
     auto issue = [&](int8_t* stage, int64_t k0) {
@@ -404,20 +476,24 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
     // The WM*L A fragments stay in registers while the JB weight fragments
     // stream through one register quad each (fewer live VGPRs than holding B).
     auto compute = [&](const int8_t* stage) {
-        v4i a[WM][L];
 #pragma unroll
-        for (int i = 0; i < WM; ++i)
-#pragma unroll
-            for (int l = 0; l < L; ++l)
-                a[i][l] = lds16(stage + (l * (BM / 16) + wm * WM + i) * kFrag + rd);
-#pragma unroll
-        for (int j = 0; j < JB; ++j) {
-            const v4i b = lds16(stage + (NA + JB * wn + j) * kFrag + rd);
+        for (int h = 0; h < F::SUB; ++h) {
+            v4i a[WM][L];
 #pragma unroll
             for (int i = 0; i < WM; ++i)
 #pragma unroll
                 for (int l = 0; l < L; ++l)
-                    acc[i][j][l] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][l], b, acc[i][j][l], 0, 0, 0);
+                    a[i][l] = lds16(stage + (l * (BM / 16) + wm * WM + i) * F::BYTES + rd[h]);
+#pragma unroll
+            for (int j = 0; j < JB; ++j) {
+                const v4i b = lds16(stage + (NA + JB * wn + j) * F::BYTES + rd[h]);
+#pragma unroll
+                for (int i = 0; i < WM; ++i)
+#pragma unroll
+                    for (int l = 0; l < L; ++l)
+                        acc[i][j][l] =
+                            __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][l], b, acc[i][j][l], 0, 0, 0);
+            }
         }
     };
     auto fold = [&](int zb) {  // end of Z segment zb: exact partials -> float
@@ -444,10 +520,12 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
     };
 
     __syncthreads();  // s_alpha, s_corr visible (before any LDS DMA is in flight)
-    ring_loop<S, LPW>((int)(I / kStepK), ring0, ring1, ring2, ring3, issue,
+    static_assert(kZBlock % KB == 0, "a ring step never straddles a Z segment");
+    constexpr int kStepsPerSeg = kZBlock / KB;
+    ring_loop<S, LPW, KB>((int)(I / KB), ring0, ring1, ring2, ring3, issue,
                       [&](const int8_t* stage, int ks) {
                           compute(stage);
-                          if (ks & 1) fold(ks >> 1);
+                          if (ks % kStepsPerSeg == kStepsPerSeg - 1) fold(ks / kStepsPerSeg);
                       });
 #pragma unroll
     for (int i = 0; i < WM; ++i)
