@@ -59,6 +59,31 @@ __device__ __forceinline__ unsigned long long hm_wave_max_u64(unsigned long long
     return v;
 }
 
+// Max / sum over each 16-lane row of the wave with DPP (quad_perm 1032,
+// quad_perm 2301, row_half_mirror, row_mirror): every lane of the row gets
+// the result.  Max and integer sums are order-free, so the result is exact.
+__device__ __forceinline__ float hm_dpp_f32(float v, int ctrl_sel) {
+    const int x = __builtin_bit_cast(int, v);
+    int y;
+    switch (ctrl_sel) {
+    case 0: y = __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false); break;
+    case 1: y = __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false); break;
+    case 2: y = __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false); break;
+    default: y = __builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false); break;
+    }
+    return __builtin_bit_cast(float, y);
+}
+__device__ __forceinline__ float hm_row16_max(float v) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v = fmaxf(v, hm_dpp_f32(v, c));
+    return v;
+}
+__device__ __forceinline__ int hm_row16_sum(int v) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v += __builtin_bit_cast(int, hm_dpp_f32(__builtin_bit_cast(float, v), c));
+    return v;
+}
+
 // glibc 2.35 expf restated for host and device (hm_expf.h); matches the host
 // libm expf on every float input (exhaustive check, tests/test_expf_parity.py).
 #include "hm_expf.h"
@@ -67,6 +92,15 @@ __device__ __forceinline__ unsigned long long hm_wave_max_u64(unsigned long long
 // value / (1 + expf(-value)) in float.
 __device__ __forceinline__ float hm_silu(float v) {
     return __fdiv_rn(v, __fadd_rn(1.0f, hm_expf(-v)));
+}
+// The same with the expf table in LDS (hm_load_exp2_table).
+__device__ __forceinline__ float hm_silu_t(float v, const unsigned long long* table) {
+    return __fdiv_rn(v, __fadd_rn(1.0f, hm_expf_t(-v, table)));
+}
+// Copies the expf table into a 32-entry LDS array (threads 0..31 write; the
+// caller synchronises before use).
+__device__ __forceinline__ void hm_load_exp2_table(unsigned long long* lds_table) {
+    if (threadIdx.x < 32) lds_table[threadIdx.x] = kHmExp2Table[threadIdx.x];
 }
 
 // ---------------------------------------------------------------------------

@@ -32,15 +32,15 @@ constexpr unsigned long long kHmExp2Table[32] = {
     0x3fef3720dcef9069ull, 0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full,
     0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
 
-HM_HD float hm_expf(float x) {
+// The restated expf with the table passed in: kHmExp2Table itself, or a
+// copy of it in LDS (device kernels that evaluate many exponentials per
+// thread keep the table there, since a per-lane index into a global table
+// costs a dependent memory load per call).  The common path is computed for
+// every input and the rare |x| >= 88 / inf / NaN cases are selected
+// afterwards, so there are no branches; every result equals glibc's.
+HM_HD float hm_expf_t(float x, const unsigned long long* table) {
     const unsigned int bits = __builtin_bit_cast(unsigned int, x);
     const unsigned int abstop = (bits >> 20) & 0x7ffu;
-    if (abstop >= 0x42bu) {                 // |x| >= 88 or NaN
-        if (bits == 0xff800000u) return 0.0f;               // -inf
-        if (abstop >= 0x7f8u) return x + x;                 // inf, nan
-        if (x > 0x1.62e42ep6f) return __builtin_inff();     // overflow
-        if (x < -0x1.9fe368p6f) return 0.0f;                // underflow
-    }
     const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
     const double shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
@@ -51,7 +51,7 @@ HM_HD float hm_expf(float x) {
     const unsigned long long ki = __builtin_bit_cast(unsigned long long, kd);
     kd -= shift;
     const double r = __builtin_fma(inv_ln2_n, xd, -kd);
-    unsigned long long t = kHmExp2Table[ki & 31u];
+    unsigned long long t = table[ki & 31u];
     t += ki << 47;
     const double s = __builtin_bit_cast(double, t);
     const double p = __builtin_fma(c0, r, c1);
@@ -59,5 +59,21 @@ HM_HD float hm_expf(float x) {
     double y = __builtin_fma(c2, r, 1.0);
     y = __builtin_fma(p, r2, y);
     y = y * s;
-    return (float)y;
+    const float common = (float)y;
+    // |x| >= 88 or NaN: -inf -> 0, inf/nan -> x + x, overflow -> inf,
+    // underflow -> 0, otherwise the common path.  Bit masks rather than
+    // conditionals, so that the device code has no branches.
+    const unsigned int m_big = 0u - (unsigned int)(abstop >= 0x42bu);
+    const unsigned int m_udf = 0u - (unsigned int)(x < -0x1.9fe368p6f);
+    const unsigned int m_ovf = 0u - (unsigned int)(x > 0x1.62e42ep6f);
+    const unsigned int m_nan = 0u - (unsigned int)(abstop >= 0x7f8u);
+    const unsigned int m_ninf = 0u - (unsigned int)(bits == 0xff800000u);
+    const unsigned int cbits = __builtin_bit_cast(unsigned int, common);
+    unsigned int sp = cbits & ~m_udf;
+    sp = (sp & ~m_ovf) | (0x7f800000u & m_ovf);
+    sp = (sp & ~m_nan) | (__builtin_bit_cast(unsigned int, x + x) & m_nan);
+    sp &= ~m_ninf;
+    return __builtin_bit_cast(float, (cbits & ~m_big) | (sp & m_big));
 }
+
+HM_HD float hm_expf(float x) { return hm_expf_t(x, kHmExp2Table); }

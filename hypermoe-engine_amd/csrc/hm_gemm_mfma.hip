@@ -191,6 +191,7 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
     __shared__ __attribute__((aligned(1024))) int8_t ring2[T::STAGE_BYTES];
     __shared__ __attribute__((aligned(1024))) int8_t ring3[S > 3 ? T::STAGE_BYTES : 16];
     __shared__ int32_t row_token[BM];
+    __shared__ unsigned long long s_exp2[32];
     __shared__ float s_xscale[BM];
     __shared__ int32_t s_xdsum[L][BM];
     __shared__ float red[BM][4];
@@ -210,6 +211,7 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
     const int nrows = (int)min((int64_t)BM, (int64_t)counts[e] - mt * BM);
     const int64_t n0 = nb * kGateUpN;
     if (tid < BM) row_token[tid] = perm_tokens[g0 + (tid < nrows ? tid : 0)];
+    hm_load_exp2_table(s_exp2);
     __syncthreads();
     // per-row activation scale (and digit sums if a zero point needs them)
     // for the epilogue, fetched while the K loop runs
@@ -285,34 +287,37 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
     const float sg = scale[e * 3 + 0], su = scale[e * 3 + 1];
     const int zd = zp[e * 3 + 2];
     float z[WM][2][4];
+    // every row is computed (rows past nrows repeat row 0's token and are
+    // zeroed at the end), so the epilogue runs without divergence
 #pragma unroll
     for (int i = 0; i < WM; ++i) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int r = wm * (BM / 2) + 16 * i + 4 * (lane >> 4) + q;
             const bool live = r < nrows;
+            const float sx = s_xscale[r];
+            const float fg = __fmul_rn(sx, sg), fu = __fmul_rn(sx, su);
+            int ds[L];
+#pragma unroll
+            for (int l = 0; l < L; ++l) ds[l] = s_xdsum[l][r];   // zeros without zero points
             float m = 0.0f;
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                float zv = 0.0f;
-                if (live) {
-                    int pg[L], pu[L];
+                int pg[L], pu[L];
 #pragma unroll
-                    for (int l = 0; l < L; ++l) {
-                        const int ds = s_xdsum[l][r];
-                        pg[l] = acc[i][j][l][q] - zg * ds;
-                        pu[l] = acc[i][j + 2][l][q] - zu * ds;
-                    }
-                    const float sx = s_xscale[r];
-                    const float g = __fmul_rn(hm_recombine(pg, L), __fmul_rn(sx, sg));
-                    const float u = __fmul_rn(hm_recombine(pu, L), __fmul_rn(sx, su));
-                    zv = __fmul_rn(hm_silu(g), u);
+                for (int l = 0; l < L; ++l) {
+                    pg[l] = acc[i][j][l][q] - zg * ds[l];
+                    pu[l] = acc[i][j + 2][l][q] - zu * ds[l];
                 }
+                const float g = __fmul_rn(hm_recombine(pg, L), fg);
+                const float u = __fmul_rn(hm_recombine(pu, L), fu);
+                float sv = hm_silu_t(g, s_exp2);
+                asm volatile("" : "+v"(sv));  // computed on every lane: no branch
+                const float zv = live ? __fmul_rn(sv, u) : 0.0f;
                 z[i][j][q] = zv;
                 m = fmaxf(m, fabsf(zv));
             }
-#pragma unroll
-            for (int s = 1; s < 16; s <<= 1) m = fmaxf(m, __shfl_xor(m, s, 64));
+            m = hm_row16_max(m);
             if ((lane & 15) == 0) red[r][wn] = m;
         }
     }
@@ -346,9 +351,7 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
             if (zd != 0) {
 #pragma unroll
                 for (int l = 0; l < L; ++l) {
-                    int s = dsum[l];
-#pragma unroll
-                    for (int sh = 1; sh < 16; sh <<= 1) s += __shfl_xor(s, sh, 64);
+                    const int s = hm_row16_sum(dsum[l]);
                     if ((lane & 15) == 0) red_i[l][r][wn] = s;
                 }
             }

@@ -109,6 +109,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_w8_kernel(
     float* __restrict__ out) {
     constexpr int kWaves = kGemvThreads / 64;
     __shared__ __attribute__((aligned(1024))) int8_t wl[kWaves][kRowsPerWave * P * 1024];
+    __shared__ unsigned long long s_exp2[32];
+    if (GATEUP) hm_load_exp2_table(s_exp2);
+    __syncthreads();
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int e = hm_active_expert(counts, experts, (int)blockIdx.y);
@@ -183,7 +186,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_w8_kernel(
                 v[h] = __fmul_rn(__fsub_rn(tot, __fmul_rn(zc, xsum)), sc);
             }
             if (lane == 0) {
-                const float y = GATEUP ? __fmul_rn(hm_silu(v[0]), v[GATEUP ? 1 : 0]) : v[0];
+                const float y = GATEUP ? __fmul_rn(hm_silu_t(v[0], s_exp2), v[GATEUP ? 1 : 0]) : v[0];
                 out[(g0 + r) * N + n0 + o] = y;
             }
         }
