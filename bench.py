@@ -52,6 +52,9 @@ def parse():
     ap.add_argument("--graph", action="store_true",
                     help="replay one captured HIP graph of the block per step instead of "
                          "launching every step from the host")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 --pmc child runs that measure the dominant "
+                         "kernel's HBM bytes per launch (roofline.traffic = null)")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="also run a plain device-to-device copy of this many MiB (3x) "
                          "before the timed region: the known-size kernel that calibrates "
@@ -62,6 +65,62 @@ def parse():
 def log(msg, quiet=False):
     if not quiet:
         print(msg, file=sys.stderr, flush=True)
+
+
+def pmc_traffic(workload: str, kernel_re: str, limbs: int, quiet: bool):
+    """HBM bytes per launch of the dominant kernel: two rocprofv3 --pmc runs
+    of a short child bench (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch),
+    each scaled by what the same counter reads for a plain 256 MiB
+    device-to-device copy recorded in the same child run.  None when
+    rocprofv3 is missing or a run fails."""
+    import csv
+    import re
+    import shutil
+    import subprocess
+    import tempfile
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None
+    copy_mib = 256
+    got = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        with tempfile.TemporaryDirectory(dir="/tmp") as d:
+            cmd = [exe, "--pmc", counter, "--kernel-include-regex", f"{kernel_re}|copyBuffer",
+                   "--output-format", "csv", "-d", d, "-o", "pmc", "--", sys.executable,
+                   str(REPO / "bench.py"), "--workload", workload, "--steps", "2", "--warmup",
+                   "1", "--cpu-sample", "0", "--quiet", "--no-traffic", "--limbs", str(limbs),
+                   "--copy-mb", str(copy_mib)]
+            env = dict(os.environ, TMPDIR="/tmp")
+            log(f"[bench] traffic: rocprofv3 --pmc {counter}", quiet)
+            try:
+                subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL,
+                               stderr=subprocess.DEVNULL, timeout=240)
+            except subprocess.TimeoutExpired:
+                return None
+            files = list(Path(d).rglob("*counter_collection.csv"))
+            if not files:
+                return None
+            kern, copies = [], []
+            with open(files[0]) as f:
+                for r in csv.DictReader(f):
+                    v = float(r["Counter_Value"])
+                    if re.search(kernel_re, r["Kernel_Name"]):
+                        kern.append(v)
+                    elif "copyBuffer" in r["Kernel_Name"]:
+                        copies.append(v)
+            if not kern or not copies:
+                return None
+            calib = max(copies)  # the 256 MiB calibration copies are the largest
+            got[counter] = (sum(kern) / len(kern), calib)
+    fetch, fcal = got["FETCH_SIZE"]
+    write, wcal = got["WRITE_SIZE"]
+    copy_kib = copy_mib * 1024.0
+    ff, wf = copy_kib / fcal, copy_kib / wcal
+    return {"bytes": int((fetch * ff + write * wf) * 1024), "fetch_kib_raw": round(fetch, 1),
+            "write_kib_raw": round(write, 1), "fetch_scale": round(ff, 4),
+            "write_scale": round(wf, 4),
+            "calibration": f"{copy_mib} MiB device copy: FETCH_SIZE {fcal:.0f} KiB, "
+                           f"WRITE_SIZE {wcal:.0f} KiB"}
 
 
 def main():
@@ -217,6 +276,13 @@ def main():
                 "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
                 "work_per_launch": gu_bytes, "launch_ms": round(stage["gate_up"], 5)}
+    if not args.no_traffic:
+        kre = "gemv_w8_kernel<[0-9]+, true>" if gemv else ("gateup_mfma_kernel" if cfg.int8
+                                                          else "gateup_f32_kernel")
+        tr = pmc_traffic(cfg.name, kre, args.limbs, q)
+        if tr is not None:
+            roof["traffic"] = tr.pop("bytes")
+            roof["traffic_detail"] = tr
     layer_bytes = synth.algorithmic_bytes(cfg, unique)
     layer_ops = synth.algorithmic_ops(cfg)
     layer = {"hbm_frac": round(layer_bytes / (ms_per_step / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
@@ -233,14 +299,21 @@ def main():
         sys.path.insert(0, str(REPO / "oracle"))
         import hm_oracle as O
         hs = np.ascontiguousarray(h_host[:sample])
+        # repeat the bounded sample until about 10 s of CPU work is timed
         t1 = time.time()
-        rout, rids, _ = O.moe_block(payload, scale, zp, hs, w, k, I)
+        runs = 0
+        while True:
+            rout, rids, _ = O.moe_block(payload, scale, zp, hs, w, k, I)
+            runs += 1
+            if time.time() - t1 >= 10.0:
+                break
         dt = time.time() - t1
-        cpu = {"value": round(sample / dt, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
+        cpu = {"value": round(sample * runs / dt, 3), "unit": "tokens/s", "cores": 1,
+               "kind": "port",
                "sample": f"first {sample} of the {T} tokens of {cfg.name} (same weights and "
-                         f"router), oracle restatement of the reference CPU path "
+                         f"router) x {runs} runs, oracle restatement of the reference CPU path "
                          f"(MoERuntime CPU branch, single thread, -O3 -ffp-contract=off), "
-                         f"{dt:.1f}s on {os.cpu_count()} host cores"}
+                         f"{dt:.1f}s on a host with {os.cpu_count()} cores"}
         ids_ok = bool(np.array_equal(res.ids[:sample], rids))
         d = np.abs(out[:sample].astype(np.float64) - rout)
         parity = {"tokens_checked": sample, "ids_bitexact": ids_ok,
