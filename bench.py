@@ -67,11 +67,13 @@ def log(msg, quiet=False):
         print(msg, file=sys.stderr, flush=True)
 
 
-def pmc_traffic(workload: str, kernel_re: str, limbs: int, quiet: bool):
-    """HBM bytes per launch of the dominant kernel: two rocprofv3 --pmc runs
+def pmc_traffic(workload: str, kernel_re: str, primary_re: str, limbs: int, quiet: bool):
+    """HBM bytes per launch of the dominant stage: two rocprofv3 --pmc runs
     of a short child bench (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch),
     each scaled by what the same counter reads for a plain 256 MiB
-    device-to-device copy recorded in the same child run.  None when
+    device-to-device copy recorded in the same child run.  The stage may be
+    several kernels (kernel_re): their dispatches are summed and divided by
+    the dispatch count of its first kernel (primary_re).  None when
     rocprofv3 is missing or a run fails."""
     import csv
     import re
@@ -100,18 +102,19 @@ def pmc_traffic(workload: str, kernel_re: str, limbs: int, quiet: bool):
             files = list(Path(d).rglob("*counter_collection.csv"))
             if not files:
                 return None
-            kern, copies = [], []
+            kern, copies, launches = [], [], 0
             with open(files[0]) as f:
                 for r in csv.DictReader(f):
                     v = float(r["Counter_Value"])
                     if re.search(kernel_re, r["Kernel_Name"]):
                         kern.append(v)
+                        launches += bool(re.search(primary_re, r["Kernel_Name"]))
                     elif "copyBuffer" in r["Kernel_Name"]:
                         copies.append(v)
-            if not kern or not copies:
+            if not kern or not copies or not launches:
                 return None
             calib = max(copies)  # the 256 MiB calibration copies are the largest
-            got[counter] = (sum(kern) / len(kern), calib)
+            got[counter] = (sum(kern) / launches, calib)
     fetch, fcal = got["FETCH_SIZE"]
     write, wcal = got["WRITE_SIZE"]
     copy_kib = copy_mib * 1024.0
@@ -263,7 +266,9 @@ def main():
     if prefill:
         achieved = gu_ops / gu_s / 1e12
         peak = PEAK_INT8_TOPS if cfg.int8 else PEAK_FP32_TFLOPS
-        roof = {"bound": "mfma", "kernel": "gateup_i8_mfma_kernel" if cfg.int8 else "gateup_f32_kernel",
+        roof = {"bound": "mfma",
+                "kernel": ("gate/up stage: gateup_mfma_kernel + swiglu_quant_kernel" if cfg.int8
+                           else "gateup_f32_kernel"),
                 "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                 "frac": round(achieved / peak, 4), "traffic": None,
                 "work_per_launch": gu_ops, "launch_ms": round(stage["gate_up"], 5),
@@ -272,14 +277,19 @@ def main():
         achieved = gu_bytes / gu_s / 1e9
         roof = {"bound": "hbm",
                 "kernel": ("gemv_w8_kernel (gate/up)" if gemv else
-                           "gateup_i8_mfma_kernel" if cfg.int8 else "gateup_f32_kernel"),
+                           "gate/up stage: gateup_mfma_kernel + swiglu_quant_kernel" if cfg.int8
+                           else "gateup_f32_kernel"),
                 "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
                 "work_per_launch": gu_bytes, "launch_ms": round(stage["gate_up"], 5)}
     if not args.no_traffic:
-        kre = "gemv_w8_kernel<[0-9]+, true>" if gemv else ("gateup_mfma_kernel" if cfg.int8
-                                                          else "gateup_f32_kernel")
-        tr = pmc_traffic(cfg.name, kre, args.limbs, q)
+        if gemv:
+            kre = prim = "gemv_w8_kernel<[0-9]+, true>"
+        elif cfg.int8:
+            kre, prim = "gateup_mfma_kernel|swiglu_quant_kernel", "gateup_mfma_kernel"
+        else:
+            kre = prim = "gateup_f32_kernel"
+        tr = pmc_traffic(cfg.name, kre, prim, args.limbs, q)
         if tr is not None:
             roof["traffic"] = tr.pop("bytes")
             roof["traffic_detail"] = tr

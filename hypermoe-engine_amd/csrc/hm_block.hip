@@ -9,7 +9,7 @@
 int hm_launch_quantize_rows(const float* x, int64_t rows, int64_t n, int32_t limbs,
                             int8_t* digits, float* scales, int32_t* dsum,
                             hipStream_t stream);
-bool hm_use_mfma(const hm_layer* layer, int32_t lx, int32_t lz, bool force_generic);
+bool hm_use_mfma_gateup(const hm_layer* layer, int32_t lx, int32_t lz, bool force_generic);
 int hm_launch_gateup_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int8_t* xdig,
                         const float* xscale, const int32_t* xdsum, int64_t tokens,
                         const int32_t* counts, const int32_t* offsets,
@@ -24,7 +24,6 @@ int hm_launch_gateup_f32(const hm_layer* layer, const float* hidden, const int32
                          float* zf, hipStream_t stream);
 int hm_launch_down_f32(const hm_layer* layer, const int32_t* counts, const int32_t* offsets,
                        int64_t R, const float* zf, float* y, hipStream_t stream);
-bool hm_mfma_shape_ok(int64_t H, int64_t I);
 bool hm_gemv_shape_ok(int64_t H, int64_t I);
 int hm_launch_gateup_gemv(const hm_layer* L, const float* hidden, const int32_t* counts,
                           const int32_t* offsets, const int32_t* perm_tokens, int64_t pairs,
@@ -117,7 +116,7 @@ size_t plan_block(const hm_layer* L, int64_t T, int32_t k, int32_t lx, int32_t l
         q.zdig = c.take<int8_t>((size_t)lz * P * I);
         q.zscale = c.take<float>((size_t)P * nb);
         q.zdsum = c.take<int32_t>((size_t)lz * P * nb);
-        q.zf = hm_use_mfma(L, lx, lz, generic) ? nullptr : c.take<float>((size_t)P * I);
+        q.zf = c.take<float>((size_t)P * I * (hm_use_mfma_gateup(L, lx, lz, generic) ? 2 : 1));
     } else {
         q.zf = c.take<float>((size_t)P * I);
     }

@@ -84,6 +84,22 @@ __device__ __forceinline__ int hm_row16_sum(int v) {
     return v;
 }
 
+// Whole-wave max / integer sum without LDS: DPP within each 16-lane row,
+// then the four row results through v_readlane (uniform result).
+__device__ __forceinline__ float hm_wave_max_dpp(float v) {
+    const float r = hm_row16_max(v);
+    const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, r), 0));
+    const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, r), 16));
+    const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, r), 32));
+    const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, r), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+__device__ __forceinline__ int hm_wave_sum_dpp(int v) {
+    const int r = hm_row16_sum(v);
+    return __builtin_amdgcn_readlane(r, 0) + __builtin_amdgcn_readlane(r, 16) +
+           __builtin_amdgcn_readlane(r, 32) + __builtin_amdgcn_readlane(r, 48);
+}
+
 // glibc 2.35 expf restated for host and device (hm_expf.h); matches the host
 // libm expf on every float input (exhaustive check, tests/test_expf_parity.py).
 #include "hm_expf.h"
@@ -96,6 +112,10 @@ __device__ __forceinline__ float hm_silu(float v) {
 // The same with the expf table in LDS (hm_load_exp2_table).
 __device__ __forceinline__ float hm_silu_t(float v, const unsigned long long* table) {
     return __fdiv_rn(v, __fadd_rn(1.0f, hm_expf_t(-v, table)));
+}
+// hm_silu_t for |v| < 88 (hm_expf_small_t).
+__device__ __forceinline__ float hm_silu_small_t(float v, const unsigned long long* table) {
+    return __fdiv_rn(v, __fadd_rn(1.0f, hm_expf_small_t(-v, table)));
 }
 // Copies the expf table into a 32-entry LDS array (threads 0..31 write; the
 // caller synchronises before use).
@@ -128,6 +148,19 @@ __device__ __forceinline__ int hm_digit(int n, int l) {
         n = (n - d) / 256;
     }
     return d;
+}
+
+// All L digits of n (|n| <= range(L)): the same digits as hm_digit, with
+// shifts (n - d is a multiple of 256, so >> 8 divides exactly); the top
+// digit is what remains, already in [-128, 127].
+template <int L>
+__device__ __forceinline__ void hm_digits(int n, int (&d)[L]) {
+#pragma unroll
+    for (int l = 0; l < L - 1; ++l) {
+        d[l] = ((n + 128) & 255) - 128;
+        n = (n - d[l]) >> 8;
+    }
+    d[L - 1] = n;
 }
 
 // c = (float)P_{L-1}; c = fmaf(c, 256, (float)P_l) for l = L-2 .. 0.

@@ -77,3 +77,28 @@ HM_HD float hm_expf_t(float x, const unsigned long long* table) {
 }
 
 HM_HD float hm_expf(float x) { return hm_expf_t(x, kHmExp2Table); }
+
+// The common path alone: equal to hm_expf_t for |x| < 88 (where none of the
+// special cases applies).  Callers check the range, e.g. once for a whole
+// wave, and use hm_expf_t otherwise.
+HM_HD float hm_expf_small_t(float x, const unsigned long long* table) {
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * 32.0;
+    const double shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    const double c1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    const double c2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double xd = (double)x;
+    double kd = __builtin_fma(inv_ln2_n, xd, shift);
+    const unsigned long long ki = __builtin_bit_cast(unsigned long long, kd);
+    kd -= shift;
+    const double r = __builtin_fma(inv_ln2_n, xd, -kd);
+    unsigned long long t = table[ki & 31u];
+    t += ki << 47;
+    const double s = __builtin_bit_cast(double, t);
+    const double p = __builtin_fma(c0, r, c1);
+    const double r2 = r * r;
+    double y = __builtin_fma(c2, r, 1.0);
+    y = __builtin_fma(p, r2, y);
+    y = y * s;
+    return (float)y;
+}

@@ -455,11 +455,12 @@ int hm_launch_quantize_rows(const float* x, int64_t rows, int64_t n, int32_t lim
     return HM_OK;
 }
 
-bool hm_mfma_shape_ok(int64_t H, int64_t I);
+bool hm_mfma_gateup_ok(int64_t H, int64_t I, int64_t E, int32_t limbs);
+bool hm_mfma_down_ok(int64_t H, int64_t I, int64_t E, int32_t limbs);
 int hm_launch_gateup_i8_mfma(const hm_layer* layer, int32_t limbs, const int8_t* xdig,
                              const float* xscale, const int32_t* xdsum, int64_t tokens,
                              const int32_t* counts, const int32_t* offsets,
-                             const int32_t* perm_tokens, int64_t R, int8_t* zdig,
+                             const int32_t* perm_tokens, int64_t R, float* gu, int8_t* zdig,
                              float* zscale, int32_t* zdsum, hipStream_t stream);
 int hm_launch_down_i8_mfma(const hm_layer* layer, int32_t limbs, const int32_t* counts,
                            const int32_t* offsets, int64_t R, const int8_t* zdig,
@@ -472,10 +473,16 @@ int64_t hm_max_tiles(int64_t pairs, int64_t experts, int64_t tile_m) {
 
 // INT8 expert GEMMs, in two launches (gate/up, then down) so callers can
 // record events between them.  xdig/xscale/xdsum come from
-// hm_launch_quantize_rows over all tokens; zf ([R x I] floats) is only used
-// by the generic path.
-bool hm_use_mfma(const hm_layer* layer, int32_t lx, int32_t lz, bool force_generic) {
-    return !force_generic && hm_mfma_shape_ok(layer->hidden, layer->intermediate) && lx == lz;
+// hm_launch_quantize_rows over all tokens; zf is scratch: [R x I] floats of
+// z on the generic path, [2 x R x I] floats of g and u on the MFMA path.
+// gate/up quantises Z in its epilogue with the same digit count as X; down
+// reads Z digits from either gate/up path.
+bool hm_use_mfma_gateup(const hm_layer* layer, int32_t lx, int32_t lz, bool force_generic) {
+    return !force_generic && lx == lz &&
+           hm_mfma_gateup_ok(layer->hidden, layer->intermediate, layer->experts, lx);
+}
+bool hm_use_mfma_down(const hm_layer* layer, int32_t lz, bool force_generic) {
+    return !force_generic && hm_mfma_down_ok(layer->hidden, layer->intermediate, layer->experts, lz);
 }
 
 int hm_launch_gateup_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int8_t* xdig,
@@ -486,9 +493,9 @@ int hm_launch_gateup_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int
     const int64_t H = layer->hidden, I = layer->intermediate, E = layer->experts;
     const int8_t* packed = static_cast<const int8_t*>(layer->packed);
     if (R == 0) return HM_OK;
-    if (hm_use_mfma(layer, lx, lz, force_generic)) {
+    if (hm_use_mfma_gateup(layer, lx, lz, force_generic)) {
         return hm_launch_gateup_i8_mfma(layer, lx, xdig, xscale, xdsum, tokens, counts, offsets,
-                                        perm_tokens, R, zdig, zscale, zdsum, stream);
+                                        perm_tokens, R, zf, zdig, zscale, zdsum, stream);
     }
     const int64_t nb = (I + kZBlock - 1) / kZBlock;
     const unsigned g_gu = (unsigned)((R * I + kBlock - 1) / kBlock);
@@ -526,7 +533,7 @@ int hm_launch_down_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int32
     const int64_t H = layer->hidden, I = layer->intermediate, E = layer->experts;
     const int8_t* packed = static_cast<const int8_t*>(layer->packed);
     if (R == 0) return HM_OK;
-    if (hm_use_mfma(layer, lx, lz, force_generic)) {
+    if (hm_use_mfma_down(layer, lz, force_generic)) {
         return hm_launch_down_i8_mfma(layer, lz, counts, offsets, R, zdig, zscale, zdsum, y,
                                       stream);
     }

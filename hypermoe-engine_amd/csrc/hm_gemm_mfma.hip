@@ -1,604 +1,827 @@
 // hm_gemm_mfma.hip -- grouped INT8-MFMA expert GEMMs for gfx950.
 //
-// Both kernels run 512-thread workgroups (8 wave64s) over one tile of one
-// expert's grouped rows.  The activation operand is L fixed-point digit
-// planes (hm_device.h); every digit plane meets the same weight fragment in
-// one v_mfma_i32_16x16x64_i8, so the int32 partial of each plane is exact.
+// Both kernels are persistent: one 512-thread workgroup (8 wave64s, two per
+// SIMD) per CU walks a list of output tiles of the grouped problem.  The
+// activation operand is L fixed-point digit planes (hm_device.h); every digit plane
+// meets the same weight fragment in one v_mfma_i32_32x32x32_i8, so the
+// int32 partial of each plane is exact.
 //
-// MFMA operand layout (v_mfma_i32_16x16x64_i8): lane l supplies 16 bytes of
-// row (l % 16) of A and of column (l % 16) of B, K bytes 16*(l/16) ..
-// 16*(l/16)+15 of the 64-wide step in both operands; the 4 int32 results of
-// lane l are rows 4*(l/16) + 0..3 of column l % 16.
+// MFMA operand layout (v_mfma_i32_32x32x32_i8): lane l supplies 16 bytes of
+// row (l % 32) of A and of column (l % 32) of B, K bytes 16*(l/32) ..
+// 16*(l/32)+15 of the 32-wide step; the 16 int32 results of lane l are
+// column l % 32, rows 8*(v/4) + 4*(l/32) + v%4 for v = 0..15.  (The
+// 16x16x64 form issues at half this rate on gfx950 unless a wave keeps many
+// more independent accumulators in flight.)
 //
 // Data movement: operands go straight from global memory to LDS with the
-// gfx950 16-byte global_load_lds (lane l's 16 bytes land at base + 16*l)
-// into fragments of 16 rows x KB bytes (KB = 128 for gate/up: every row load
-// is a full 128-byte line; 64 for down) in a swizzled order that keeps both
-// the global reads coalesced per row and the MFMA's ds_read_b128 bank-
-// conflict free (Frag), and no registers stage the data.  A ring of S stages
-// keeps S-1 K steps of loads in flight; one s_waitcnt vmcnt + barrier per
-// step.  The K loop is unrolled by S so that every step reads and fills
-// distinct LDS arrays.
+// 16-byte global_load_lds (lane l's 16 bytes land at base + 16*l) into
+// fragments of 32 rows x 64 K bytes, swizzled so that the global reads stay
+// coalesced per row and the MFMA's ds_read_b128 stays bank-conflict free.
+// A ring of kS stages (64 K bytes each) keeps kS-1 stages in flight; the
+// fragments of stage ks+1 are read into registers while the MFMAs of stage
+// ks run, so a stage's LDS slot is free for refill one step after it lands.
 //
-// Tile order: the grid is 1D; workgroup i runs on XCD i % 8 (round-robin
-// dispatch), so the linear tile index is remapped to give each XCD a
-// contiguous run of (m-tile major, n-block minor) tiles: the n-blocks of an
-// m-tile share its gathered activation rows, consecutive m-tiles of one
-// expert share its weight columns, all in one XCD's L2.
+// Tile stream: each workgroup's tiles form one stream of K stages.  The
+// first kS-1 stages of the next tile are issued while the current tile
+// finishes, and its per-row metadata (token ids, scales) is fetched into a
+// second LDS buffer by the same in-order DMA queue, so the epilogue of a
+// tile runs while the next tile's operands are already landing.  All global
+// loads inside the stream are LDS DMA: the compiler's own waits for a
+// register load would otherwise drain the queue.
+//
+// Tile order: the real tile count comes from the routed counts on the
+// device.  Tiles are numbered m-tile major, n-block minor and split into 8
+// contiguous ranges, one per XCD (workgroup i runs on XCD i % 8), so the
+// n-blocks of an m-tile (sharing its activation rows) and consecutive
+// m-tiles of one expert (sharing its weight columns) meet in one XCD's L2.
 #include "hm_device.h"
 #include "hm_lds_dma.h"
 
 #include <limits.h>
 
+#include <type_traits>
+
 namespace {
 
-constexpr int kThreads = 512;
-constexpr int kWaves = 8;
-constexpr int kMfmaK = 64;          // K bytes of one v_mfma_i32_16x16x64_i8
-constexpr int kZBlock = 128;
+constexpr int kWaves = 8;           // wave64s per workgroup
+constexpr int kThreads = 64 * kWaves;
+constexpr int kKB = 64;             // K bytes per ring stage: two 32-byte MFMA K steps
+constexpr int kS = 4;               // ring stages
+constexpr int kFragBytes = 32 * kKB;  // one 32-row fragment of a stage
+constexpr int kZBlock = 128;        // Z fixed-point segment (columns of Z = K of down)
 constexpr int kGateUpN = 128;       // columns per projection per gate/up tile
-constexpr int kDownN = 512;         // output columns per down tile (16 * Tile<L,true>::BFRAGS)
 constexpr int kXcds = 8;
+constexpr int kMaxExperts = 256;    // expert tables live in LDS
+constexpr int kMaxZSeg = 6;         // down: Z segments per row held in LDS (I <= 768)
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 
-// Fragment layout in LDS.  The wave-wide load that fills a fragment gives
-// lane l row l/4 and 16-byte K chunk (l%4) ^ ((l/16)%4) of the 16 x 64 byte
-// block: four adjacent lanes read one row's 64 contiguous bytes (one request
-// per row instead of one per lane).  The MFMA reader lane m (row m%16, chunk
-// m/16) finds its bytes at 16*(4*row + (chunk ^ (row/4))); over any 16
-// consecutive reader lanes these are 16 distinct 16-byte bank groups, so the
-// ds_read_b128 stays conflict free.
-//
-// With 128 K bytes per ring step a fragment is 16 rows x 128 bytes, two
-// wave-wide loads (rows 0-7, 8-15): lane l takes row 8i + l/8 and 16-byte
-// chunk (l%8) ^ ((row/2)%8), so 8 lanes read one row's full 128-byte line;
-// reader lane m of K half h (row m%16, chunk 4h + m/16) finds its bytes at
-// 1024*(row/8) + 16*(8*(row%8) + (chunk ^ (row/2)%8)), again 16 distinct
-// bank groups over any 16 consecutive lanes.
-template <int KB>
-struct Frag {
-    static constexpr int BYTES = 16 * KB;   // 16 rows of KB bytes
-    static constexpr int LOADS = KB / 64;   // 1 KB wave-wide loads per fragment
-    static constexpr int SUB = KB / kMfmaK; // MFMA K steps per ring step
-    static_assert(KB == 64 || KB == 128, "fragment K width");
-    // row (0..15) and 16-byte chunk loaded by `lane` in load i
-    __device__ static int load_row(int lane, int i) {
-        return KB == 64 ? lane >> 2 : 8 * i + (lane >> 3);
-    }
-    __device__ static int load_chunk(int lane, int i) {
-        if (KB == 64) return (lane & 3) ^ ((lane >> 4) & 3);
-        const int r = load_row(lane, i);
-        return (lane & 7) ^ ((r >> 1) & 7);
-    }
-    // byte offset read by MFMA lane m in K step h of the fragment
-    __device__ static int read_offset(int m, int h) {
-        const int r = m & 15, c = 4 * h + (m >> 4);
-        if (KB == 64) return 16 * (4 * r + (c ^ (r >> 2)));
-        return 1024 * (r >> 3) + 16 * (8 * (r & 7) + (c ^ ((r >> 1) & 7)));
-    }
-};
-
-// Tile traits: WM 16-row subtiles per wave, two row groups of waves.
-// gate/up: wave = WM*16 rows (WM = 4, or 2 at three limbs) x (2 gate + 2 up)
-// 16-column fragments, tile 2*WM*16 rows x 256 weight rows.  down: wave =
-// WM*16 rows x 8 fragments (128
-// columns), tile 2*WM*16 rows x 512 columns.  A wave's (WM*L) A fragments
-// times its JB B fragments give MFMAs that each need 384 LDS bytes or
-// fewer (8 A x 4 B, 4 A x 8 B), within the LDS bandwidth at full MFMA rate.
-template <int L, bool DOWN>
-struct Tile {
-    static constexpr int WM = DOWN ? (L >= 3 ? 1 : 2) : (L >= 3 ? 2 : 4);  // 16-row subtiles per wave
-    static constexpr int JB = DOWN ? 8 : 4;                   // B fragments per wave
-    static constexpr int BM = 2 * 16 * WM;
-    static constexpr int BFRAGS = 4 * JB;                     // B fragments per tile
-    static constexpr int NA = L * BM / 16;                    // A fragments / stage
-    static constexpr int NF = NA + BFRAGS;                    // fragments / stage
-    static constexpr int KB = DOWN ? 64 : 128;                // K bytes per ring step
-    using F = Frag<KB>;
-    static constexpr int NL = NF * F::LOADS;                  // wave loads / stage
-    static constexpr int LPW = (NL + kWaves - 1) / kWaves;    // loads per wave / stage
-    // ring depth: as many stages as fit in ~136 KB of LDS, at least 2
-    static constexpr int S = NF * F::BYTES * 4 <= 139264 ? 4
-                           : NF * F::BYTES * 3 <= 139264 ? 3 : 2;
-    static constexpr int STAGE_BYTES = NF * F::BYTES;
-};
+// Fragment layout in LDS (32 rows x 64 bytes = two 1 KB halves of 16 rows).
+// The wave-wide load that fills half hf gives lane l row 16*hf + l/4 and
+// 16-byte K chunk (l%4) ^ ((l/16)%4): four adjacent lanes read one row's 64
+// contiguous bytes.  The MFMA reader lane m of K step h (row r = m%32,
+// chunk c = 2h + m/32) finds its bytes at
+//   1024*(r/16) + 16*(4*(r%16) + (c ^ ((r/4)%4)))
+// and over any 16 consecutive reader lanes these are 16 distinct 16-byte
+// bank groups.
+__device__ __forceinline__ int frag_load_row(int lane, int hf) { return 16 * hf + (lane >> 2); }
+__device__ __forceinline__ int frag_load_chunk(int lane) { return (lane & 3) ^ ((lane >> 4) & 3); }
+__device__ __forceinline__ int frag_read_offset(int lane, int h) {
+    const int r = lane & 31, c = 2 * h + (lane >> 5);
+    return 1024 * (r >> 4) + 16 * (4 * (r & 15) + (c ^ ((r >> 2) & 3)));
+}
 
 __device__ __forceinline__ v4i lds16(const int8_t* p) {
     return *reinterpret_cast<const v4i*>(p);
 }
 
-
-
-// The K loop over nk steps with a ring of S LDS stages.  Stage ks lives in
-// ring (ks % S); step ks waits until at most S-2 later stages of this wave's
-// loads are outstanding, meets the other waves at the barrier (after which
-// every wave's loads of stage ks have landed and every read of the slot
-// refilled next is done), refills that slot with step ks+S-1 and computes
-// stage ks.  The steady state, where every step refills, runs unguarded; the
-// last steps drain the ring.  The stages are distinct arrays named at compile
-// time in every unrolled step.
-template <int S, int LPW, int KB, class Issue, class Compute>
-__device__ __forceinline__ void ring_loop(int nk, int8_t* r0, int8_t* r1, int8_t* r2, int8_t* r3,
-                                          Issue&& issue, Compute&& compute) {
-    auto slot = [&](int s) -> int8_t* {
-        return s == 0 ? r0 : s == 1 ? r1 : s == 2 ? r2 : r3;
-    };
-#pragma unroll
-    for (int s = 0; s < S - 1; ++s) {
-        if (s < nk) issue(slot(s), (int64_t)s * KB);
-    }
-    int ks0 = 0;
-    for (; ks0 + 2 * S - 2 < nk; ks0 += S) {
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-            wait_vmcnt<(S - 2) * LPW>();
-            lds_barrier();
-            issue(slot((s + S - 1) % S), (int64_t)(ks0 + s + S - 1) * KB);
-            compute(slot(s), ks0 + s);
-        }
-    }
-    for (; ks0 < nk; ks0 += S) {
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-            const int ks = ks0 + s;
-            if (ks < nk) {
-                if (ks + S - 2 < nk) wait_vmcnt<(S - 2) * LPW>();
-                else wait_vmcnt<0>();
-                lds_barrier();
-                if (ks + S - 1 < nk) issue(slot((s + S - 1) % S), (int64_t)(ks + S - 1) * KB);
-                compute(slot(s), ks);
-            }
-        }
-    }
+__device__ __forceinline__ v16i mfma32(v4i a, v4i b, v16i c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
 
-// Linear workgroup -> logical tile (m-tile major, n-block minor), grouped
-// per XCD.  Returns false for the padding workgroups of the last XCD.
-__device__ __forceinline__ bool xcd_tile(int64_t mtiles, int64_t nblocks, int64_t* mt,
-                                         int64_t* nb) {
-    const int64_t total = mtiles * nblocks;
-    const int64_t per = (total + kXcds - 1) / kXcds;
-    const int64_t i = blockIdx.x;
-    const int64_t j = (i % kXcds) * per + i / kXcds;
-    if (j >= total) return false;
-    *mt = j / nblocks;
-    *nb = j % nblocks;
-    return true;
+// Exclusive prefix of the m-tiles of every expert (ceil(count / bm)) into
+// prefix[0..E], prefix[E] = total.  One full wave.
+__device__ __forceinline__ void tile_prefix(const int32_t* cnt, int E, int bm, int32_t* prefix) {
+    const int lane = threadIdx.x & (HM_WAVE - 1);
+    int base = 0;
+    for (int c0 = 0; c0 < E; c0 += HM_WAVE) {
+        const int e = c0 + lane;
+        const int n = e < E ? (cnt[e] + bm - 1) / bm : 0;
+        int incl = n;
+#pragma unroll
+        for (int sft = 1; sft < HM_WAVE; sft <<= 1) {
+            const int o = __shfl_up(incl, sft, HM_WAVE);
+            if (lane >= sft) incl += o;
+        }
+        if (e < E) prefix[e] = base + incl - n;
+        base += __shfl(incl, HM_WAVE - 1, HM_WAVE);
+    }
+    if (lane == 0) prefix[E] = base;
+}
+
+// Expert owning global m-tile gm: the last expert whose first tile is <= gm
+// (prefix is non-decreasing; experts with no tiles share their successor's
+// start and are skipped).  Every lane of the wave must be active.
+__device__ __forceinline__ int locate_expert(const int32_t* prefix, int E, int gm) {
+    const int lane = threadIdx.x & (HM_WAVE - 1);
+    int n = 0;
+    for (int c0 = 0; c0 < E; c0 += HM_WAVE) {
+        const int e = c0 + lane;
+        n += __popcll(__ballot(e < E && prefix[e] <= gm));
+    }
+    return __builtin_amdgcn_readfirstlane(n - 1);
+}
+
+// The workgroup's share of the tile list: tiles jbeg, jbeg + step, ... < jend
+// of the XCD range [x*per, (x+1)*per).
+struct TileRange {
+    int jbeg, jend, step, ntiles;
+};
+__device__ __forceinline__ TileRange tile_range(int total) {
+    TileRange t;
+    const int per = (total + kXcds - 1) / kXcds;
+    const int x = blockIdx.x % kXcds;
+    t.step = gridDim.x / kXcds;
+    t.jbeg = x * per + blockIdx.x / kXcds;
+    t.jend = min((x + 1) * per, total);
+    t.ntiles = t.jbeg < t.jend ? (t.jend - t.jbeg + t.step - 1) / t.step : 0;
+    return t;
+}
+
+// Tile row of accumulator element v of lane `lane` in the 32-row fragment
+// starting at row r0.
+__device__ __forceinline__ int acc_row(int r0, int lane, int v) {
+    return r0 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
 }
 
 // ---------------------------------------------------------------------------
-// gate/up: tile = BM grouped rows x (128 gate + 128 up) columns.
-// wave (wm, wn) = (wave / 4, wave % 4): rows [wm*BM/2, +BM/2), gate and up
-// columns [32 wn, 32 wn + 32) of the tile.  Epilogue: z = silu(g) * u, the
+// gate/up: tile = BM grouped rows x (128 gate + 128 up) weight columns.
+// wave (wr, wc): rows [32*WR*wr, +32*WR), gate and up columns
+// [32*WCP*wc, +32*WCP) of the tile.  Epilogue: z = silu(g) * u; the tile's
 // 128-column fixed-point segment of each Z row is quantised to L digits.
 // ---------------------------------------------------------------------------
 template <int L>
+struct GateUpTile {
+    static constexpr int WR = 1;                        // 32-row fragments per wave
+    static constexpr int WCP = L >= 3 ? 1 : 2;          // gate (and up) fragments per wave
+    static constexpr int NWC = kGateUpN / 32 / WCP;     // waves across the columns
+    static constexpr int NWR = kWaves / NWC;            // waves across the rows
+    static constexpr int BM = 32 * WR * NWR;            // 128 rows (64 at three limbs)
+    static constexpr int NA = L * BM / 32;              // A fragments per stage
+    static constexpr int NB = 2 * kGateUpN / 32;        // 8 B fragments (4 gate, 4 up)
+    static constexpr int NF = NA + NB;
+    static constexpr int NL = 2 * NF;                   // wave-wide loads per stage
+    static constexpr int LPW = (NL + kWaves - 1) / kWaves;
+    static constexpr int STAGE = NF * kFragBytes;
+};
+
+template <int L>
 __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
     const int8_t* __restrict__ xdig, const float* __restrict__ xscale,
-    const int32_t* __restrict__ xdsum, int64_t tokens, int64_t H, int64_t I,
-    int64_t experts, int64_t mtiles, const int8_t* __restrict__ packed,
-    const float* __restrict__ scale, const int32_t* __restrict__ zp,
-    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
-    const int32_t* __restrict__ perm_tokens, int64_t R, int8_t* __restrict__ zdig,
-    float* __restrict__ zscale, int32_t* __restrict__ zdsum) {
-    using T = Tile<L, false>;
-    using F = typename T::F;
-    constexpr int WM = T::WM, BM = T::BM, NA = T::NA, NL = T::NL, LPW = T::LPW, S = T::S,
-                  KB = T::KB;
-    __shared__ __attribute__((aligned(1024))) int8_t ring0[T::STAGE_BYTES];
-    __shared__ __attribute__((aligned(1024))) int8_t ring1[T::STAGE_BYTES];
-    __shared__ __attribute__((aligned(1024))) int8_t ring2[T::STAGE_BYTES];
-    __shared__ __attribute__((aligned(1024))) int8_t ring3[S > 3 ? T::STAGE_BYTES : 16];
-    __shared__ int32_t row_token[BM];
-    __shared__ unsigned long long s_exp2[32];
-    __shared__ float s_xscale[BM];
-    __shared__ int32_t s_xdsum[L][BM];
-    __shared__ float red[BM][4];
-    __shared__ int red_i[L][BM][4];
+    const int32_t* __restrict__ xdsum, int tokens, int H, int I, int experts,
+    const int8_t* __restrict__ packed, const float* __restrict__ scale,
+    const int32_t* __restrict__ zp, const int32_t* __restrict__ counts,
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ perm_tokens, int R,
+    float* __restrict__ gout, float* __restrict__ uout) {
+    using T = GateUpTile<L>;
+    constexpr int BM = T::BM, NA = T::NA, NL = T::NL, LPW = T::LPW, WR = T::WR, WCP = T::WCP,
+                  NWC = T::NWC, STAGE = T::STAGE;
+    constexpr int RW = BM / HM_WAVE;  // waves that move one value per tile row
+    __shared__ __attribute__((aligned(1024))) int8_t ring[kS * STAGE];
+    __shared__ int32_t s_prefix[kMaxExperts + 1];
+    __shared__ int32_t s_off[kMaxExperts], s_cnt[kMaxExperts];
+    __shared__ float s_sg[kMaxExperts], s_su[kMaxExperts];
+    __shared__ int32_t s_zg[kMaxExperts], s_zu[kMaxExperts];
+    __shared__ __attribute__((aligned(16))) int32_t s_rt[2][BM];     // token of each tile row
+    __shared__ __attribute__((aligned(16))) float s_xs[2][BM];       // its activation scale
+    __shared__ __attribute__((aligned(16))) int32_t s_xd[2][L][BM];  // its digit sums
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 2, wn = wave & 3;
-    int rd[F::SUB];
-#pragma unroll
-    for (int h = 0; h < F::SUB; ++h) rd[h] = F::read_offset(lane, h);
-    int64_t gmt, nb;
-    if (!xcd_tile(mtiles, I / kGateUpN, &gmt, &nb)) return;
-    int64_t e, mt;
-    if (!hm_locate_tile(counts, experts, BM, gmt, &e, &mt)) return;
-    const int64_t g0 = offsets[e] + mt * BM;
-    const int nrows = (int)min((int64_t)BM, (int64_t)counts[e] - mt * BM);
-    const int64_t n0 = nb * kGateUpN;
-    if (tid < BM) row_token[tid] = perm_tokens[g0 + (tid < nrows ? tid : 0)];
-    hm_load_exp2_table(s_exp2);
-    __syncthreads();
-    // per-row activation scale (and digit sums if a zero point needs them)
-    // for the epilogue, fetched while the K loop runs
-    const int zg = zp[e * 3 + 0], zu = zp[e * 3 + 1];
-    if (tid < BM) {
-        const int tok = row_token[tid];
-        s_xscale[tid] = xscale[tok];
-#pragma unroll
-        for (int l = 0; l < L; ++l) s_xdsum[l][tid] = (zg | zu) ? xdsum[(int64_t)l * tokens + tok] : 0;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = wave / NWC, wc = wave % NWC;
+    const int E = (int)experts;
+    for (int e = tid; e < E; e += kThreads) {
+        s_cnt[e] = counts[e];
+        s_off[e] = offsets[e];
+        s_sg[e] = scale[3 * e + 0];
+        s_su[e] = scale[3 * e + 1];
+        s_zg[e] = zp[3 * e + 0];
+        s_zu[e] = zp[3 * e + 1];
     }
+    __syncthreads();
+    if (wave == 0) tile_prefix(s_cnt, E, BM, s_prefix);
+    __syncthreads();
+    const int nbn = I / kGateUpN;
+    const TileRange tr = tile_range(s_prefix[E] * nbn);
+    if (tr.ntiles == 0) return;
+    const int nk = (int)(H / kKB);
 
-    // Per-lane global source of each fragment this wave loads (K offset 0).
-    const int8_t* ebase = packed + e * 3 * H * I;
-    const int8_t* src[LPW];
+    struct Info {
+        int e, nrows, g0, n0;
+    };
+    auto info = [&](int i) {
+        const int j = tr.jbeg + i * tr.step;
+        const int gm = j / nbn;
+        Info t;
+        t.e = locate_expert(s_prefix, E, gm);
+        const int mt = gm - s_prefix[t.e];
+        t.g0 = s_off[t.e] + mt * BM;
+        t.nrows = min(BM, s_cnt[t.e] - mt * BM);
+        t.n0 = (j % nbn) * kGateUpN;
+        return t;
+    };
+    // token ids of the tile rows (rows past nrows repeat the last row)
+    auto fetch_rows = [&](const Info& t, int m) {
+        if (wave < RW) {
+            const int r = HM_WAVE * wave + lane;
+            dma4(perm_tokens + t.g0 + min(r, t.nrows - 1), &s_rt[m][HM_WAVE * wave]);
+        }
+    };
+    // activation scales and digit sums of those tokens (needs s_rt[m])
+    auto fetch_row_meta = [&](int m) {
+        if (wave < RW) {
+            const int tok = s_rt[m][HM_WAVE * wave + lane];
+            dma4(xscale + tok, &s_xs[m][HM_WAVE * wave]);
+#pragma unroll
+            for (int l = 0; l < L; ++l) dma4(xdsum + (int64_t)l * tokens + tok, &s_xd[m][l][HM_WAVE * wave]);
+        }
+    };
     int dst[LPW];
 #pragma unroll
     for (int c = 0; c < LPW; ++c) {
-        const int u = (wave + kWaves * c) % NL;   // load unit: fragment f, part li
-        const int f = u / F::LOADS, li = u % F::LOADS;
-        const int fr = F::load_row(lane, li), ch = F::load_chunk(lane, li);
-        dst[c] = f * F::BYTES + 1024 * li;
-        if (f < NA) {
-            const int l = f / (BM / 16), i = f % (BM / 16);
-            const int tok = row_token[16 * i + fr];
-            src[c] = xdig + ((int64_t)l * tokens + tok) * H + 16 * ch;
-        } else {
-            const int brow = 16 * (f - NA) + fr;
-            const int64_t col = n0 + (brow & 127);
-            src[c] = ebase + (brow >> 7) * H * I + col * H + 16 * ch;
-        }
+        const int u = (wave + kWaves * c) % NL;   // load unit: fragment u/2, half u%2
+        dst[c] = (u >> 1) * kFragBytes + 1024 * (u & 1);
     }
-    auto issue = [&](int8_t* stage, int64_t k0) {
+    auto make_src = [&](const Info& t, int m, const int8_t* (&src)[LPW]) {
+        const int8_t* ebase = packed + (int64_t)t.e * 3 * H * I;
+        const int ch = frag_load_chunk(lane);
 #pragma unroll
-        for (int c = 0; c < LPW; ++c) dma16(src[c] + k0, stage + dst[c]);  // wave-uniform base
+        for (int c = 0; c < LPW; ++c) {
+            const int u = (wave + kWaves * c) % NL;
+            const int f = u >> 1, row = frag_load_row(lane, u & 1);
+            if (f < NA) {
+                const int l = f / (BM / 32), i = f % (BM / 32);
+                const int tok = s_rt[m][32 * i + row];
+                src[c] = xdig + ((int64_t)l * tokens + tok) * H + 16 * ch;
+            } else {
+                const int fb = f - NA;
+                const int64_t col = t.n0 + 32 * (fb & 3) + row;
+                src[c] = ebase + (int64_t)(fb >> 2) * H * I + col * H + 16 * ch;
+            }
+        }
+    };
+    auto issue = [&](int slot, const int8_t* const (&src)[LPW], int ks) {
+        int8_t* st = ring + slot * STAGE;
+#pragma unroll
+        for (int c = 0; c < LPW; ++c) dma16(src[c] + (int64_t)ks * kKB, st + dst[c]);
     };
 
-    v4i acc[WM][4][L];
+    int rd[2];
 #pragma unroll
-    for (int i = 0; i < WM; ++i)
+    for (int h = 0; h < 2; ++h) rd[h] = frag_read_offset(lane, h);
+    v4i fa[2][WR][L], fb[2][2 * WCP];
+    auto read_frags = [&](int slot, int h) {
+        const int8_t* st = ring + slot * STAGE;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int ii = 0; ii < WR; ++ii)
 #pragma unroll
-            for (int l = 0; l < L; ++l) acc[i][j][l] = v4i{0, 0, 0, 0};
+            for (int l = 0; l < L; ++l)
+                fa[h][ii][l] = lds16(st + (l * (BM / 32) + wr * WR + ii) * kFragBytes + rd[h]);
+#pragma unroll
+        for (int j = 0; j < 2 * WCP; ++j) {
+            const int fbi = j < WCP ? wc * WCP + j : 4 + wc * WCP + (j - WCP);
+            fb[h][j] = lds16(st + (NA + fbi) * kFragBytes + rd[h]);
+        }
+    };
+    v16i acc[WR][L][2 * WCP];
+    // `first`: the tile's first K step starts the accumulators from zero
+    auto mfma_step = [&](int h, auto first) {
+#pragma unroll
+        for (int ii = 0; ii < WR; ++ii)
+#pragma unroll
+            for (int l = 0; l < L; ++l)
+#pragma unroll
+                for (int j = 0; j < 2 * WCP; ++j) {
+                    if constexpr (decltype(first)::value)
+                        acc[ii][l][j] = mfma32(fa[h][ii][l], fb[h][j], v16i{});
+                    else
+                        acc[ii][l][j] = mfma32(fa[h][ii][l], fb[h][j], acc[ii][l][j]);
+                }
+    };
 
-    auto compute = [&](const int8_t* stage) {
+    // ---- stream prologue: tile 0's rows, metadata and first kS-1 stages
+    Info cur = info(0);
+    int m = 0;
+    fetch_rows(cur, 0);
+    wait_vmcnt<0>();
+    lds_barrier();
+    fetch_row_meta(0);
+    // per-lane sources of this wave's loads; from step nk-kS on (when this
+    // tile has issued its last stage) they hold the next tile's
+    const int8_t* src[LPW];
+    make_src(cur, 0, src);
+    int slot0 = 0;  // ring slot of the current tile's stage 0
 #pragma unroll
-        for (int h = 0; h < F::SUB; ++h) {
-            v4i b[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int bf = (j >> 1) * 8 + 2 * wn + (j & 1);  // 16-row fragment index
-                b[j] = lds16(stage + (NA + bf) * F::BYTES + rd[h]);
+    for (int s = 0; s < kS - 1; ++s) issue(s, src, s);
+
+    for (int i = 0; i < tr.ntiles; ++i) {
+        const bool has_next = i + 1 < tr.ntiles;
+        const int mn = m ^ 1;
+        Info nxt = cur;
+        if (has_next) nxt = info(i + 1);
+        // stage 0 has landed once at most the kS-2 later stages are in flight
+        wait_vmcnt<(kS - 2) * LPW>();
+        lds_barrier();
+        issue((slot0 + kS - 1) % kS, src, kS - 1);
+        if (has_next) fetch_rows(nxt, mn);
+        read_frags(slot0, 0);
+        read_frags(slot0, 1);
+        // One K step: wait for stage ks+1, publish it, refill the slot of
+        // stage ks (its fragments are in registers) with stage ks+kS of the
+        // stream, and run stage ks while reading stage ks+1's fragments.
+        // Phase A (`next` false) refills with this tile's stages; phase B
+        // (the last kS steps) with the next tile's first kS-1 stages.
+        auto kstep = [&](int ks, auto first, auto next) {
+            const int slot = (slot0 + ks) % kS;
+            if (ks + 1 < nk) {
+                // the stages after ks+1 still in flight are ks+2 .. ks+kS-1
+                // of the stream (fewer at the stream's end)
+                if (has_next || ks + kS - 1 < nk) wait_vmcnt<(kS - 2) * LPW>();
+                else wait_vmcnt<0>();
             }
+            lds_barrier();
+            if constexpr (!decltype(next)::value) {
+                issue(slot, src, ks + kS);
+            } else {
+                if (has_next && ks + kS - nk <= kS - 2) issue(slot, src, ks + kS - nk);
+            }
+            const int nslot = (slot + 1) % kS;
+            mfma_step(0, first);
+            if (ks + 1 < nk) read_frags(nslot, 0);
+            mfma_step(1, std::false_type{});
+            if (ks + 1 < nk) read_frags(nslot, 1);
+        };
+        int ks = 0;
+        if (nk > kS) {
+            kstep(0, std::true_type{}, std::false_type{});
+#pragma clang loop unroll(disable)
+            for (ks = 1; ks < nk - kS; ++ks) kstep(ks, std::false_type{}, std::false_type{});
+        }
+        if (has_next) {
+            // the next tile's row tokens (fetched at this tile's start) have
+            // landed once a stage issued after them has
+            if (nk < 2 * kS) {
+                wait_vmcnt<0>();
+                lds_barrier();
+            }
+            make_src(nxt, mn, src);
+            fetch_row_meta(mn);
+        }
+        if (ks == 0) {
+            kstep(0, std::true_type{}, std::true_type{});
+            ks = 1;
+        }
+#pragma clang loop unroll(disable)
+        for (; ks < nk; ++ks) kstep(ks, std::false_type{}, std::true_type{});
+
+        // ---- epilogue (the next tile's first kS-1 stages are in flight):
+        // g and u rows out as floats (SiLU and the Z digits follow in
+        // swiglu_quant_kernel, at full occupancy)
+        {
+            const int e = cur.e, nrows = cur.nrows;
+            const float sg = s_sg[e], su = s_su[e];
+            const int zg = s_zg[e], zu = s_zu[e];
 #pragma unroll
-            for (int i = 0; i < WM; ++i) {
+            for (int ii = 0; ii < WR; ++ii) {
+                const int r0 = 32 * (wr * WR + ii);
 #pragma unroll
-                for (int l = 0; l < L; ++l) {
-                    const v4i a = lds16(stage + (l * (BM / 16) + wm * WM + i) * F::BYTES + rd[h]);
+                for (int q = 0; q < 4; ++q) {
+                    const int rq = acc_row(r0, lane, 4 * q);
+                    const float4 sx4 = *reinterpret_cast<const float4*>(&s_xs[m][rq]);
+                    int4 ds4[L];
+                    if ((zg | zu) != 0) {
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        acc[i][j][l] =
-                            __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b[j], acc[i][j][l], 0, 0, 0);
+                        for (int l = 0; l < L; ++l) ds4[l] = *reinterpret_cast<const int4*>(&s_xd[m][l][rq]);
+                    }
+#pragma unroll
+                    for (int t4 = 0; t4 < 4; ++t4) {
+                        const int v = 4 * q + t4;
+                        const float sx = t4 == 0 ? sx4.x : t4 == 1 ? sx4.y : t4 == 2 ? sx4.z : sx4.w;
+                        const float fg = __fmul_rn(sx, sg), fu = __fmul_rn(sx, su);
+                        const bool live = rq + t4 < nrows;
+                        float* grow = gout + (int64_t)(cur.g0 + rq + t4) * I + cur.n0 + 32 * wc * WCP + (lane & 31);
+                        float* urow = uout + (grow - gout);
+#pragma unroll
+                        for (int j = 0; j < WCP; ++j) {
+                            int pg[L], pu[L];
+#pragma unroll
+                            for (int l = 0; l < L; ++l) {
+                                pg[l] = acc[ii][l][j][v];
+                                pu[l] = acc[ii][l][WCP + j][v];
+                            }
+                            if ((zg | zu) != 0) {
+#pragma unroll
+                                for (int l = 0; l < L; ++l) {
+                                    const int ds = t4 == 0 ? ds4[l].x : t4 == 1 ? ds4[l].y : t4 == 2 ? ds4[l].z : ds4[l].w;
+                                    pg[l] -= zg * ds;
+                                    pu[l] -= zu * ds;
+                                }
+                            }
+                            const float g = __fmul_rn(hm_recombine(pg, L), fg);
+                            const float u = __fmul_rn(hm_recombine(pu, L), fu);
+                            if (live) {
+                                grow[32 * j] = g;
+                                urow[32 * j] = u;
+                            }
+                        }
                     }
                 }
             }
         }
-    };
-
-    ring_loop<S, LPW, KB>((int)(H / KB), ring0, ring1, ring2, ring3, issue,
-                      [&](const int8_t* stage, int) { compute(stage); });
-
-    // ---- epilogue -------------------------------------------------------
-    const float sg = scale[e * 3 + 0], su = scale[e * 3 + 1];
-    const int zd = zp[e * 3 + 2];
-    float z[WM][2][4];
-    // every row is computed (rows past nrows repeat row 0's token and are
-    // zeroed at the end), so the epilogue runs without divergence
-#pragma unroll
-    for (int i = 0; i < WM; ++i) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int r = wm * (BM / 2) + 16 * i + 4 * (lane >> 4) + q;
-            const bool live = r < nrows;
-            const float sx = s_xscale[r];
-            const float fg = __fmul_rn(sx, sg), fu = __fmul_rn(sx, su);
-            int ds[L];
-#pragma unroll
-            for (int l = 0; l < L; ++l) ds[l] = s_xdsum[l][r];   // zeros without zero points
-            float m = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                int pg[L], pu[L];
-#pragma unroll
-                for (int l = 0; l < L; ++l) {
-                    pg[l] = acc[i][j][l][q] - zg * ds[l];
-                    pu[l] = acc[i][j + 2][l][q] - zu * ds[l];
-                }
-                const float g = __fmul_rn(hm_recombine(pg, L), fg);
-                const float u = __fmul_rn(hm_recombine(pu, L), fu);
-                float sv = hm_silu_t(g, s_exp2);
-                asm volatile("" : "+v"(sv));  // computed on every lane: no branch
-                const float zv = live ? __fmul_rn(sv, u) : 0.0f;
-                z[i][j][q] = zv;
-                m = fmaxf(m, fabsf(zv));
-            }
-            m = hm_row16_max(m);
-            if ((lane & 15) == 0) red[r][wn] = m;
-        }
-    }
-    __syncthreads();
-    const float range = (float)hm_limb_range(L);
-    const int64_t nbz = I / kZBlock;
-    const int64_t zb = n0 / kZBlock;
-    // the digits of the tile's Z segment: [L][BM][128] bytes (staged in LDS,
-    // stored below with 16-byte writes)
-    int zfix[WM][2][4];
-#pragma unroll
-    for (int i = 0; i < WM; ++i) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int r = wm * (BM / 2) + 16 * i + 4 * (lane >> 4) + q;
-            const float amax = fmaxf(fmaxf(red[r][0], red[r][1]), fmaxf(red[r][2], red[r][3]));
-            const float inv = amax > 0.0f ? __fdiv_rn(range, amax) : 0.0f;
-            int dsum[L];
-#pragma unroll
-            for (int l = 0; l < L; ++l) dsum[l] = 0;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int v = hm_fixed_point(z[i][j][q], inv, range);
-                zfix[i][j][q] = v;
-#pragma unroll
-                for (int l = 0; l < L; ++l) dsum[l] += hm_digit(v, l);
-            }
-            if (r < nrows && wn == 0 && (lane & 15) == 0) {
-                zscale[(g0 + r) * nbz + zb] = amax > 0.0f ? __fdiv_rn(amax, range) : 0.0f;
-            }
-            if (zd != 0) {
-#pragma unroll
-                for (int l = 0; l < L; ++l) {
-                    const int s = hm_row16_sum(dsum[l]);
-                    if ((lane & 15) == 0) red_i[l][r][wn] = s;
-                }
-            }
-        }
-    }
-    // digit planes out through LDS (ring0, free after the K loop): byte
-    // writes into [BM][128], then 16-byte rows segments to zdig
-    int8_t* zst = ring0;
-#pragma unroll
-    for (int l = 0; l < L; ++l) {
-#pragma unroll
-        for (int i = 0; i < WM; ++i)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int r = wm * (BM / 2) + 16 * i + 4 * (lane >> 4) + q;
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    zst[r * kGateUpN + 32 * wn + 16 * j + (lane & 15)] = (int8_t)hm_digit(zfix[i][j][q], l);
-            }
-        __syncthreads();
-        for (int c = tid; c < nrows * (kGateUpN / 16); c += kThreads) {
-            const int r = c / (kGateUpN / 16), c16 = c % (kGateUpN / 16);
-            const int4 v = *reinterpret_cast<const int4*>(zst + r * kGateUpN + 16 * c16);
-            *reinterpret_cast<int4*>(zdig + ((int64_t)l * R + g0 + r) * I + n0 + 16 * c16) = v;
-        }
-        __syncthreads();
-    }
-    if (zd != 0) {
-        if (tid < nrows) {
-#pragma unroll
-            for (int l = 0; l < L; ++l) {
-                zdsum[((int64_t)l * R + g0 + tid) * nbz + zb] =
-                    red_i[l][tid][0] + red_i[l][tid][1] + red_i[l][tid][2] + red_i[l][tid][3];
-            }
-        }
+        // next tile
+        slot0 = (slot0 + nk) % kS;
+        m = mn;
+        cur = nxt;
     }
 }
 
 // ---------------------------------------------------------------------------
-// down: tile = BM contiguous grouped rows x 512 output columns; wave (wm, wn)
-// owns rows [wm*BM/2, +BM/2) and columns [128 wn, 128 wn + 128).  At the end of
-// each 128-column Z segment the exact partials are recombined and folded into
-// the float accumulator: acc = fmaf(c, s_segment * scale_down, acc).
+// down: tile = BM contiguous grouped rows x BN output columns; wave (wr, wc)
+// owns rows [32*WR*wr, +32*WR) and columns [32*WCN*wc, +32*WCN).  After each
+// 128-column Z segment (two stages) the exact partials are recombined and
+// folded into the float accumulator: acc = fmaf(c, s_segment * scale_down, acc).
 // ---------------------------------------------------------------------------
+template <int L>
+struct DownTile {
+    static constexpr int WR = 1;                        // 32-row fragments per wave
+    static constexpr int WCN = 2;                       // 32-column fragments per wave
+    static constexpr int NWR = 4, NWC = 2;
+    static constexpr int BM = 32 * WR * NWR;            // 128 rows
+    static constexpr int BN = 32 * WCN * NWC;           // 128 columns
+    static constexpr int NA = L * BM / 32;
+    static constexpr int NB = BN / 32;
+    static constexpr int NF = NA + NB;
+    static constexpr int NL = 2 * NF;
+    static constexpr int LPW = (NL + kWaves - 1) / kWaves;
+    static constexpr int STAGE = NF * kFragBytes;
+    static constexpr int NMETA = (1 + L) * kMaxZSeg * (BM / HM_WAVE);  // metadata DMAs per tile
+};
+
 template <int L>
 __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
     const int8_t* __restrict__ zdig, const float* __restrict__ zscale,
-    const int32_t* __restrict__ zdsum, int64_t R, int64_t H, int64_t I,
-    int64_t experts, int64_t mtiles, const int8_t* __restrict__ packed,
-    const float* __restrict__ scale, const int32_t* __restrict__ zp,
-    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
-    float* __restrict__ y) {
-    using T = Tile<L, true>;
-    using F = typename T::F;
-    constexpr int WM = T::WM, JB = T::JB, BM = T::BM, NA = T::NA, NL = T::NL, LPW = T::LPW,
-                  S = T::S, KB = T::KB;
-    constexpr int BN = 16 * T::BFRAGS;  // output columns per tile
-    constexpr int MAXNB = 16;           // Z segments (I <= 2048)
-    __shared__ __attribute__((aligned(1024))) int8_t ring0[T::STAGE_BYTES];
-    __shared__ __attribute__((aligned(1024))) int8_t ring1[T::STAGE_BYTES];
-    __shared__ __attribute__((aligned(1024))) int8_t ring2[T::STAGE_BYTES];
-    __shared__ __attribute__((aligned(1024))) int8_t ring3[S > 3 ? T::STAGE_BYTES : 16];
-    __shared__ float s_alpha[MAXNB][BM];
-    __shared__ int32_t s_corr[MAXNB][L][BM];  // zp * digit sum of each Z segment
+    const int32_t* __restrict__ zdsum, int R, int H, int I, int experts,
+    const int8_t* __restrict__ packed, const float* __restrict__ scale,
+    const int32_t* __restrict__ zp, const int32_t* __restrict__ counts,
+    const int32_t* __restrict__ offsets, float* __restrict__ y) {
+    using T = DownTile<L>;
+    constexpr int BM = T::BM, BN = T::BN, NA = T::NA, NL = T::NL, LPW = T::LPW, WR = T::WR,
+                  WCN = T::WCN, NWC = T::NWC, STAGE = T::STAGE;
+    constexpr int RC = BM / HM_WAVE;  // 64-row chunks of a tile
+    __shared__ __attribute__((aligned(1024))) int8_t ring[kS * STAGE];
+    __shared__ int32_t s_prefix[kMaxExperts + 1];
+    __shared__ int32_t s_off[kMaxExperts], s_cnt[kMaxExperts];
+    __shared__ float s_sd[kMaxExperts];
+    __shared__ int32_t s_zd[kMaxExperts];
+    __shared__ __attribute__((aligned(16))) float s_zs[2][kMaxZSeg][BM];       // Z segment scales
+    __shared__ __attribute__((aligned(16))) int32_t s_zds[2][L][kMaxZSeg][BM]; // Z digit sums
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 2, wn = wave & 3;
-    int rd[F::SUB];
-#pragma unroll
-    for (int h = 0; h < F::SUB; ++h) rd[h] = F::read_offset(lane, h);
-    int64_t gmt, nb;
-    if (!xcd_tile(mtiles, H / BN, &gmt, &nb)) return;
-    int64_t e, mt;
-    if (!hm_locate_tile(counts, experts, BM, gmt, &e, &mt)) return;
-    const int64_t g0 = offsets[e] + mt * BM;
-    const int nrows = (int)min((int64_t)BM, (int64_t)counts[e] - mt * BM);
-    const int64_t n0 = nb * BN;
-    const int nbz = (int)(I / kZBlock);
-    const float sd = scale[e * 3 + 2];
-    const int zd = zp[e * 3 + 2];
-    for (int i = tid; i < nbz * BM; i += kThreads) {
-        const int b = i / BM, r = i % BM;
-        const int64_t g = g0 + (r < nrows ? r : 0);
-        s_alpha[b][r] = __fmul_rn(zscale[g * nbz + b], sd);
-#pragma unroll
-        for (int l = 0; l < L; ++l) s_corr[b][l][r] = zd ? zd * zdsum[((int64_t)l * R + g) * nbz + b] : 0;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = wave / NWC, wc = wave % NWC;
+    const int E = (int)experts;
+    for (int e = tid; e < E; e += kThreads) {
+        s_cnt[e] = counts[e];
+        s_off[e] = offsets[e];
+        s_sd[e] = scale[3 * e + 2];
+        s_zd[e] = zp[3 * e + 2];
     }
+    __syncthreads();
+    if (wave == 0) tile_prefix(s_cnt, E, BM, s_prefix);
+    __syncthreads();
+    const int nbn = H / BN;
+    const TileRange tr = tile_range(s_prefix[E] * nbn);
+    if (tr.ntiles == 0) return;
+    const int nk = (int)(I / kKB);
+    const int nbz = (int)(I / kZBlock);
 
-    const int8_t* dbase = packed + e * 3 * H * I + 2 * H * I;
-    const int8_t* src[LPW];
+    struct Info {
+        int e, nrows, g0, n0;
+    };
+    auto info = [&](int i) {
+        const int j = tr.jbeg + i * tr.step;
+        const int gm = j / nbn;
+        Info t;
+        t.e = locate_expert(s_prefix, E, gm);
+        const int mt = gm - s_prefix[t.e];
+        t.g0 = s_off[t.e] + mt * BM;
+        t.nrows = min(BM, s_cnt[t.e] - mt * BM);
+        t.n0 = (j % nbn) * BN;
+        return t;
+    };
+    // Z segment scales and digit sums of the tile rows (rows past nrows read
+    // the last row); units spread over the waves
+    auto fetch_meta = [&](const Info& t, int m) {
+        for (int u = wave; u < (1 + L) * nbz * RC; u += kWaves) {
+            const int kind = u / (nbz * RC), rem = u % (nbz * RC);
+            const int b = rem / RC, ch = rem % RC;
+            const int r = HM_WAVE * ch + lane;
+            const int64_t g = t.g0 + min(r, t.nrows - 1);
+            if (kind == 0) dma4(zscale + g * nbz + b, &s_zs[m][b][HM_WAVE * ch]);
+            else dma4(zdsum + ((int64_t)(kind - 1) * R + g) * nbz + b, &s_zds[m][kind - 1][b][HM_WAVE * ch]);
+        }
+    };
     int dst[LPW];
 #pragma unroll
     for (int c = 0; c < LPW; ++c) {
-        const int u = (wave + kWaves * c) % NL;   // load unit: fragment f, part li
-        const int f = u / F::LOADS, li = u % F::LOADS;
-        const int fr = F::load_row(lane, li), ch = F::load_chunk(lane, li);
-        dst[c] = f * F::BYTES + 1024 * li;
-        if (f < NA) {
-            const int l = f / (BM / 16), i = f % (BM / 16);
-            const int r = 16 * i + fr;
-            src[c] = zdig + ((int64_t)l * R + g0 + (r < nrows ? r : 0)) * I + 16 * ch;
-        } else {
-            const int brow = 16 * (f - NA) + fr;
-            src[c] = dbase + (n0 + brow) * I + 16 * ch;
-        }
+        const int u = (wave + kWaves * c) % NL;
+        dst[c] = (u >> 1) * kFragBytes + 1024 * (u & 1);
     }
-    auto issue = [&](int8_t* stage, int64_t k0) {
+    auto make_src = [&](const Info& t, const int8_t* (&src)[LPW]) {
+        const int8_t* dbase = packed + (int64_t)t.e * 3 * H * I + 2 * H * I;
+        const int ch = frag_load_chunk(lane);
 #pragma unroll
-        for (int c = 0; c < LPW; ++c) dma16(src[c] + k0, stage + dst[c]);  // wave-uniform base
-    };
-
-    v4i acc[WM][JB][L];
-    float facc[WM][JB][4];
-#pragma unroll
-    for (int i = 0; i < WM; ++i)
-#pragma unroll
-        for (int j = 0; j < JB; ++j) {
-#pragma unroll
-            for (int l = 0; l < L; ++l) acc[i][j][l] = v4i{0, 0, 0, 0};
-#pragma unroll
-            for (int q = 0; q < 4; ++q) facc[i][j][q] = 0.0f;
-        }
-
-    // The WM*L A fragments stay in registers while the JB weight fragments
-    // stream through one register quad each (fewer live VGPRs than holding B).
-    auto compute = [&](const int8_t* stage) {
-#pragma unroll
-        for (int h = 0; h < F::SUB; ++h) {
-            v4i a[WM][L];
-#pragma unroll
-            for (int i = 0; i < WM; ++i)
-#pragma unroll
-                for (int l = 0; l < L; ++l)
-                    a[i][l] = lds16(stage + (l * (BM / 16) + wm * WM + i) * F::BYTES + rd[h]);
-#pragma unroll
-            for (int j = 0; j < JB; ++j) {
-                const v4i b = lds16(stage + (NA + JB * wn + j) * F::BYTES + rd[h]);
-#pragma unroll
-                for (int i = 0; i < WM; ++i)
-#pragma unroll
-                    for (int l = 0; l < L; ++l)
-                        acc[i][j][l] =
-                            __builtin_amdgcn_mfma_i32_16x16x64_i8(a[i][l], b, acc[i][j][l], 0, 0, 0);
+        for (int c = 0; c < LPW; ++c) {
+            const int u = (wave + kWaves * c) % NL;
+            const int f = u >> 1, row = frag_load_row(lane, u & 1);
+            if (f < NA) {
+                const int l = f / (BM / 32), i = f % (BM / 32);
+                const int r = 32 * i + row;
+                src[c] = zdig + ((int64_t)l * R + t.g0 + min(r, t.nrows - 1)) * I + 16 * ch;
+            } else {
+                src[c] = dbase + (t.n0 + 32 * (f - NA) + row) * I + 16 * ch;
             }
         }
     };
-    auto fold = [&](int zb) {  // end of Z segment zb: exact partials -> float
+    auto issue = [&](int slot, const int8_t* const (&src)[LPW], int ks) {
+        int8_t* st = ring + slot * STAGE;
 #pragma unroll
-        for (int i = 0; i < WM; ++i)
+        for (int c = 0; c < LPW; ++c) dma16(src[c] + (int64_t)ks * kKB, st + dst[c]);
+    };
+
+    int rd[2];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int r = wm * (BM / 2) + 16 * i + 4 * (lane >> 4) + q;
-                const float alpha = s_alpha[zb][r];
-                int ds[L];
+    for (int h = 0; h < 2; ++h) rd[h] = frag_read_offset(lane, h);
+    v4i fa[2][WR][L], fb[2][WCN];
+    auto read_frags = [&](int slot, int h) {
+        const int8_t* st = ring + slot * STAGE;
 #pragma unroll
-                for (int l = 0; l < L; ++l) ds[l] = s_corr[zb][l][r];
+        for (int ii = 0; ii < WR; ++ii)
 #pragma unroll
-                for (int j = 0; j < JB; ++j) {
-                    int p[L];
+            for (int l = 0; l < L; ++l)
+                fa[h][ii][l] = lds16(st + (l * (BM / 32) + wr * WR + ii) * kFragBytes + rd[h]);
 #pragma unroll
-                    for (int l = 0; l < L; ++l) {
-                        p[l] = acc[i][j][l][q] - ds[l];
-                        acc[i][j][l][q] = 0;
-                    }
-                    facc[i][j][q] = __builtin_fmaf(hm_recombine(p, L), alpha, facc[i][j][q]);
+        for (int j = 0; j < WCN; ++j) fb[h][j] = lds16(st + (NA + wc * WCN + j) * kFragBytes + rd[h]);
+    };
+    v16i acc[WR][L][WCN];
+    float facc[WR][WCN][16];
+    // `first`: the first K step of a Z segment starts the partials from zero
+    auto mfma_step = [&](int h, auto first) {
+#pragma unroll
+        for (int ii = 0; ii < WR; ++ii)
+#pragma unroll
+            for (int l = 0; l < L; ++l)
+#pragma unroll
+                for (int j = 0; j < WCN; ++j) {
+                    if constexpr (decltype(first)::value)
+                        acc[ii][l][j] = mfma32(fa[h][ii][l], fb[h][j], v16i{});
+                    else
+                        acc[ii][l][j] = mfma32(fa[h][ii][l], fb[h][j], acc[ii][l][j]);
                 }
-            }
     };
 
-    __syncthreads();  // s_alpha, s_corr visible (before any LDS DMA is in flight)
-    static_assert(kZBlock % KB == 0, "a ring step never straddles a Z segment");
-    constexpr int kStepsPerSeg = kZBlock / KB;
-    ring_loop<S, LPW, KB>((int)(I / KB), ring0, ring1, ring2, ring3, issue,
-                      [&](const int8_t* stage, int ks) {
-                          compute(stage);
-                          if (ks % kStepsPerSeg == kStepsPerSeg - 1) fold(ks / kStepsPerSeg);
-                      });
+    Info cur = info(0);
+    int m = 0;
+    fetch_meta(cur, 0);
+    const int8_t* src[LPW];  // this tile's sources, the next tile's from step nk-kS
+    make_src(cur, src);
+    int slot0 = 0;
 #pragma unroll
-    for (int i = 0; i < WM; ++i)
+    for (int s = 0; s < kS - 1; ++s) issue(s, src, s);
+
+    for (int i = 0; i < tr.ntiles; ++i) {
+        const bool has_next = i + 1 < tr.ntiles;
+        const int mn = m ^ 1;
+        Info nxt = cur;
+        if (has_next) nxt = info(i + 1);
+        wait_vmcnt<(kS - 2) * LPW>();
+        lds_barrier();
+        issue((slot0 + kS - 1) % kS, src, kS - 1);
+        if (has_next) fetch_meta(nxt, mn);
+        read_frags(slot0, 0);
+        read_frags(slot0, 1);
+        const float sd = s_sd[cur.e];
+        const int zd = s_zd[cur.e];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int r = wm * (BM / 2) + 16 * i + 4 * (lane >> 4) + q;
-            if (r >= nrows) continue;
+        for (int ii = 0; ii < WR; ++ii)
 #pragma unroll
-            for (int j = 0; j < JB; ++j) {
-                const int64_t col = n0 + 16 * (JB * wn + j) + (lane & 15);
-                y[(g0 + r) * H + col] = facc[i][j][q];
+            for (int j = 0; j < WCN; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) facc[ii][j][v] = 0.0f;
+        auto dstep = [&](int ks, auto first, auto next) {
+            const int slot = (slot0 + ks) % kS;
+            if (ks + 1 < nk) {
+                if (has_next || ks + kS - 1 < nk) wait_vmcnt<(kS - 2) * LPW>();
+                else wait_vmcnt<0>();
+            }
+            lds_barrier();
+            if constexpr (!decltype(next)::value) {
+                issue(slot, src, ks + kS);
+            } else {
+                if (has_next && ks + kS - nk <= kS - 2) issue(slot, src, ks + kS - nk);
+            }
+            const int nslot = (slot + 1) % kS;
+            mfma_step(0, first);
+            if (ks + 1 < nk) read_frags(nslot, 0);
+            mfma_step(1, std::false_type{});
+            if (ks + 1 < nk) read_frags(nslot, 1);
+        };
+        // end of Z segment zb: exact partials -> float.  Within one 128-wide
+        // segment |P_l| <= 2^22 (with a zero-point correction), so two
+        // limbs combine exactly in int32 and convert with the single
+        // rounding of fmaf((float)P_1, 256, (float)P_0).
+        auto fold = [&](int zb) {
+#pragma unroll
+            for (int ii = 0; ii < WR; ++ii)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int rq = acc_row(32 * (wr * WR + ii), lane, 4 * q);
+                    const float4 zs4 = *reinterpret_cast<const float4*>(&s_zs[m][zb][rq]);
+                    int4 dz4[L];
+                    if (zd != 0) {
+#pragma unroll
+                        for (int l = 0; l < L; ++l) dz4[l] = *reinterpret_cast<const int4*>(&s_zds[m][l][zb][rq]);
+                    }
+#pragma unroll
+                    for (int t4 = 0; t4 < 4; ++t4) {
+                        const int v = 4 * q + t4;
+                        const float zs = t4 == 0 ? zs4.x : t4 == 1 ? zs4.y : t4 == 2 ? zs4.z : zs4.w;
+                        const float alpha = __fmul_rn(zs, sd);
+#pragma unroll
+                        for (int j = 0; j < WCN; ++j) {
+                            int p[L];
+#pragma unroll
+                            for (int l = 0; l < L; ++l) p[l] = acc[ii][l][j][v];
+                            if (zd != 0) {
+#pragma unroll
+                                for (int l = 0; l < L; ++l)
+                                    p[l] -= zd * (t4 == 0 ? dz4[l].x : t4 == 1 ? dz4[l].y : t4 == 2 ? dz4[l].z : dz4[l].w);
+                            }
+                            float c;
+                            if constexpr (L == 1) c = (float)p[0];
+                            else if constexpr (L == 2) c = (float)(p[1] * 256 + p[0]);
+                            else c = hm_recombine(p, L);
+                            facc[ii][j][v] = __builtin_fmaf(c, alpha, facc[ii][j][v]);
+                        }
+                    }
+                }
+        };
+        // nk and kS are even, so a Z segment (two stages) never straddles
+        // the two phases
+        int ks = 0;
+#pragma clang loop unroll(disable)
+        for (; ks < nk - kS; ks += 2) {
+            dstep(ks, std::true_type{}, std::false_type{});
+            dstep(ks + 1, std::false_type{}, std::false_type{});
+            fold(ks >> 1);
+        }
+        if (has_next) make_src(nxt, src);
+#pragma clang loop unroll(disable)
+        for (; ks < nk; ks += 2) {
+            dstep(ks, std::true_type{}, std::true_type{});
+            dstep(ks + 1, std::false_type{}, std::true_type{});
+            fold(ks >> 1);
+        }
+        // ---- epilogue: float rows out (the next tile's stages are in flight)
+#pragma unroll
+        for (int ii = 0; ii < WR; ++ii)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int r = acc_row(32 * (wr * WR + ii), lane, v);
+            if (r < cur.nrows) {
+                float* yr = y + (cur.g0 + r) * H + cur.n0 + 32 * wc * WCN + (lane & 31);
+#pragma unroll
+                for (int j = 0; j < WCN; ++j) yr[32 * j] = facc[ii][j][v];
             }
         }
+        slot0 = (slot0 + nk) % kS;
+        m = mn;
+        cur = nxt;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// z = silu(g) * u and its fixed-point digits, one wave per 128-column
+// segment of a grouped row (lane: columns 2*lane, 2*lane+1).  The segment
+// max gives the step: inv = range / max|z|, digits of rint(z * inv); the
+// segment scale max|z| / range and the digit sums go out beside them.
+// The same arithmetic as zquant_generic_kernel over the z of
+// gateup_generic_kernel.
+// ---------------------------------------------------------------------------
+constexpr int kSqThreads = 256;
+
+template <int L>
+__global__ __launch_bounds__(kSqThreads) void swiglu_quant_kernel(
+    const float* __restrict__ gin, const float* __restrict__ uin, int R, int I,
+    int8_t* __restrict__ zdig, float* __restrict__ zscale, int32_t* __restrict__ zdsum) {
+    __shared__ unsigned long long s_exp2[32];
+    hm_load_exp2_table(s_exp2);
+    __syncthreads();
+    const int lane = threadIdx.x & (HM_WAVE - 1);
+    const int nbz = I / kZBlock;
+    const int seg = blockIdx.x * (kSqThreads / HM_WAVE) + (int)(threadIdx.x / HM_WAVE);
+    if (seg >= R * nbz) return;
+    const int row = seg / nbz, b = seg % nbz;
+    const int64_t off = (int64_t)row * I + b * kZBlock + 2 * lane;
+    const float2 g = *reinterpret_cast<const float2*>(gin + off);
+    const float2 u = *reinterpret_cast<const float2*>(uin + off);
+    float s0, s1;
+    if (__all(fabsf(g.x) < 88.0f && fabsf(g.y) < 88.0f)) {
+        s0 = hm_silu_small_t(g.x, s_exp2);
+        s1 = hm_silu_small_t(g.y, s_exp2);
+    } else {
+        s0 = hm_silu_t(g.x, s_exp2);
+        s1 = hm_silu_t(g.y, s_exp2);
+    }
+    const float z0 = __fmul_rn(s0, u.x), z1 = __fmul_rn(s1, u.y);
+    const float amax = hm_wave_max_dpp(fmaxf(fabsf(z0), fabsf(z1)));
+    const float range = (float)hm_limb_range(L);
+    const float inv = amax > 0.0f ? __fdiv_rn(range, amax) : 0.0f;
+    int d0[L], d1[L];
+    hm_digits<L>(hm_fixed_point(z0, inv, range), d0);
+    hm_digits<L>(hm_fixed_point(z1, inv, range), d1);
+#pragma unroll
+    for (int l = 0; l < L; ++l) {
+        const uint16_t pair = (uint16_t)((d0[l] & 255) | ((d1[l] & 255) << 8));
+        *reinterpret_cast<uint16_t*>(zdig + (int64_t)l * R * I + off) = pair;
+        const int sum = hm_wave_sum_dpp(d0[l] + d1[l]);
+        if (lane == 0) zdsum[((int64_t)l * R + row) * nbz + b] = sum;
+    }
+    if (lane == 0) zscale[(int64_t)row * nbz + b] = amax > 0.0f ? __fdiv_rn(amax, range) : 0.0f;
+}
+
+int persistent_grid() {
+    static int cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (cached[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        cached[dev] = cus;
+    }
+    const int g = cached[dev] / kXcds * kXcds;
+    return g < kXcds ? kXcds : g;
+}
+
+template <int L>
+int launch_gateup(const hm_layer* layer, const int8_t* xdig, const float* xscale,
+                  const int32_t* xdsum, int64_t tokens, const int32_t* counts,
+                  const int32_t* offsets, const int32_t* perm_tokens, int64_t R, float* gu,
+                  int8_t* zdig, float* zscale, int32_t* zdsum, hipStream_t stream) {
+    const int64_t I = layer->intermediate;
+    if (tokens > INT_MAX || R > INT_MAX || R * (I / kZBlock) > INT_MAX) return HM_ERR_OVERFLOW;
+    float* gout = gu;
+    float* uout = gu + R * I;
+    hipLaunchKernelGGL(gateup_mfma_kernel<L>, dim3((unsigned)persistent_grid()), dim3(kThreads), 0,
+                       stream, xdig, xscale, xdsum, (int)tokens, (int)layer->hidden, (int)I,
+                       (int)layer->experts, static_cast<const int8_t*>(layer->packed),
+                       layer->scale, layer->zero_point, counts, offsets, perm_tokens, (int)R,
+                       gout, uout);
+    HM_LAUNCHED();
+    const int64_t segs = R * (I / kZBlock);
+    const int64_t per_block = kSqThreads / HM_WAVE;
+    hipLaunchKernelGGL(swiglu_quant_kernel<L>, dim3((unsigned)((segs + per_block - 1) / per_block)),
+                       dim3(kSqThreads), 0, stream, gout, uout, (int)R, (int)I, zdig, zscale, zdsum);
+    HM_LAUNCHED();
+    return HM_OK;
+}
+
+template <int L>
+int launch_down(const hm_layer* layer, const int32_t* counts, const int32_t* offsets, int64_t R,
+                const int8_t* zdig, const float* zscale, const int32_t* zdsum, float* y,
+                hipStream_t stream) {
+    if (R > INT_MAX) return HM_ERR_OVERFLOW;
+    hipLaunchKernelGGL(down_mfma_kernel<L>, dim3((unsigned)persistent_grid()), dim3(kThreads), 0,
+                       stream, zdig, zscale, zdsum, (int)R, (int)layer->hidden,
+                       (int)layer->intermediate, (int)layer->experts,
+                       static_cast<const int8_t*>(layer->packed), layer->scale, layer->zero_point,
+                       counts, offsets, y);
+    HM_LAUNCHED();
+    return HM_OK;
 }
 
 }  // namespace
 
-// Shape preconditions of the MFMA kernels (checked by the caller):
-// H % 256 == 0, I % 128 == 0, I <= 2048.
-static_assert(16 * Tile<2, true>::BFRAGS == kDownN && 16 * Tile<3, true>::BFRAGS == kDownN, "down tile width");
-
-bool hm_mfma_shape_ok(int64_t H, int64_t I) {
-    return H % kDownN == 0 && I % kGateUpN == 0 && I % kZBlock == 0 && I / kZBlock <= 16;
+// Shape preconditions of the MFMA kernels.  gate/up: K = H in 64-byte
+// stages, at least kS of them; I in 128-column blocks.  down: K = I in
+// 64-byte stages (at least kS), 128-wide Z segments (at most kMaxZSeg held
+// per row), H in tiles of the down tile width.  Both keep the expert
+// tables in LDS (E <= kMaxExperts).
+bool hm_mfma_gateup_ok(int64_t H, int64_t I, int64_t E, int32_t limbs) {
+    return limbs >= 1 && limbs <= 3 && E >= 1 && E <= kMaxExperts && H <= (1 << 20) &&
+           I <= (1 << 20) && H % kKB == 0 &&
+           H / kKB >= kS && I % kGateUpN == 0 && I >= kGateUpN;
 }
 
-int64_t hm_max_tiles(int64_t pairs, int64_t experts, int64_t tile_m);
-
-static unsigned xcd_grid(int64_t mtiles, int64_t nblocks) {
-    const int64_t total = mtiles * nblocks;
-    return (unsigned)(((total + kXcds - 1) / kXcds) * kXcds);
+bool hm_mfma_down_ok(int64_t H, int64_t I, int64_t E, int32_t limbs) {
+    if (limbs < 1 || limbs > 3 || E < 1 || E > kMaxExperts || H > (1 << 20) || I > (1 << 20))
+        return false;
+    const int64_t bn = limbs == 1 ? DownTile<1>::BN : limbs == 2 ? DownTile<2>::BN : DownTile<3>::BN;
+    return H % bn == 0 && H >= bn && I % kZBlock == 0 && I / kKB >= kS && I / kZBlock <= kMaxZSeg;
 }
 
-template <int L>
-static int launch_gateup(const hm_layer* layer, const int8_t* xdig, const float* xscale,
-                         const int32_t* xdsum, int64_t tokens, const int32_t* counts,
-                         const int32_t* offsets, const int32_t* perm_tokens, int64_t R,
-                         int8_t* zdig, float* zscale, int32_t* zdsum, hipStream_t stream) {
-    const int64_t H = layer->hidden, I = layer->intermediate, E = layer->experts;
-    const int64_t mtiles = hm_max_tiles(R, E, Tile<L, false>::BM);
-    hipLaunchKernelGGL(gateup_mfma_kernel<L>, dim3(xcd_grid(mtiles, I / kGateUpN)),
-                       dim3(kThreads), 0, stream, xdig, xscale, xdsum, tokens, H, I, E, mtiles,
-                       static_cast<const int8_t*>(layer->packed), layer->scale,
-                       layer->zero_point, counts, offsets, perm_tokens, R, zdig, zscale, zdsum);
-    HM_LAUNCHED();
-    return HM_OK;
-}
-
-template <int L>
-static int launch_down(const hm_layer* layer, const int32_t* counts, const int32_t* offsets,
-                       int64_t R, const int8_t* zdig, const float* zscale,
-                       const int32_t* zdsum, float* y, hipStream_t stream) {
-    const int64_t H = layer->hidden, I = layer->intermediate, E = layer->experts;
-    const int64_t mtiles = hm_max_tiles(R, E, Tile<L, true>::BM);
-    hipLaunchKernelGGL(down_mfma_kernel<L>, dim3(xcd_grid(mtiles, H / kDownN)), dim3(kThreads),
-                       0, stream, zdig, zscale, zdsum, R, H, I, E, mtiles,
-                       static_cast<const int8_t*>(layer->packed), layer->scale,
-                       layer->zero_point, counts, offsets, y);
-    HM_LAUNCHED();
-    return HM_OK;
-}
-
+// gu: scratch for the exact g and u rows, 2 x R x I floats.
 int hm_launch_gateup_i8_mfma(const hm_layer* layer, int32_t limbs, const int8_t* xdig,
                              const float* xscale, const int32_t* xdsum, int64_t tokens,
                              const int32_t* counts, const int32_t* offsets,
-                             const int32_t* perm_tokens, int64_t R, int8_t* zdig,
+                             const int32_t* perm_tokens, int64_t R, float* gu, int8_t* zdig,
                              float* zscale, int32_t* zdsum, hipStream_t stream) {
     switch (limbs) {
-    case 1: return launch_gateup<1>(layer, xdig, xscale, xdsum, tokens, counts, offsets, perm_tokens, R, zdig, zscale, zdsum, stream);
-    case 2: return launch_gateup<2>(layer, xdig, xscale, xdsum, tokens, counts, offsets, perm_tokens, R, zdig, zscale, zdsum, stream);
-    case 3: return launch_gateup<3>(layer, xdig, xscale, xdsum, tokens, counts, offsets, perm_tokens, R, zdig, zscale, zdsum, stream);
+    case 1: return launch_gateup<1>(layer, xdig, xscale, xdsum, tokens, counts, offsets, perm_tokens, R, gu, zdig, zscale, zdsum, stream);
+    case 2: return launch_gateup<2>(layer, xdig, xscale, xdsum, tokens, counts, offsets, perm_tokens, R, gu, zdig, zscale, zdsum, stream);
+    case 3: return launch_gateup<3>(layer, xdig, xscale, xdsum, tokens, counts, offsets, perm_tokens, R, gu, zdig, zscale, zdsum, stream);
     default: return HM_ERR_INVALID;
     }
 }

@@ -43,4 +43,12 @@ __device__ __forceinline__ void dma16(const void* gsrc, void* lds_base) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
                  :: "v"(gsrc), "s"(m0) : "memory", "m0");
 }
+// The same with 4 bytes per lane: lane l's dword lands at lds_base + 4*l.
+// Used for per-row metadata gathers (token ids, scales) that ride in the
+// same in-order load queue as the operand stages.
+__device__ __forceinline__ void dma4(const void* gsrc, void* lds_base) {
+    const unsigned m0 = (unsigned)(uintptr_t)(lds_ptr_t)lds_base;
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
+                 :: "v"(gsrc), "s"(m0) : "memory", "m0");
+}
 #pragma clang diagnostic pop

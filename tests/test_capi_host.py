@@ -81,7 +81,8 @@ def test_workspace_and_layer_sizes():
     layer = capi.HmLayer(128, 2048, 768, capi.HM_DTYPE_INT8, 1, 1, 1)
     a = lib.hm_moe_block_workspace_bytes(C.byref(layer), 4096, 8, 2, 2, 0)
     b = lib.hm_moe_block_workspace_bytes(C.byref(layer), 4096, 8, 2, 2, capi.HM_EXEC_GENERIC)
-    assert a > 0 and b - a >= 4096 * 8 * 768 * 4, "generic path needs the float Z buffer"
+    # scratch floats: z [P x I] on the generic path, g and u [2 x P x I] on the MFMA path
+    assert a > 0 and a - b == 4096 * 8 * 768 * 4, "MFMA path holds g and u, generic path z"
     assert lib.hm_moe_block_workspace_bytes(C.byref(layer), 0, 8, 2, 2, 0) == 0
     assert lib.hm_route_workspace_bytes(4096, 128) == 4096 * 128 * 4
 

@@ -1,8 +1,9 @@
 """The libm boundary.  The reference's softmax and SiLU call glibc expf
 (CpuRouterBackend.cpp:54, Activation.cpp:44); the kernels use the restated
 algorithm in csrc/hm_expf.h.  That same header, compiled for the host with
-g++, must equal the host expf on every float input it is checked on, and its
-32-entry table must equal bits(2^(i/32)) - (i << 47) computed in long double.
+g++, must equal the host expf on every float input it is checked on (and so
+must its short path hm_expf_small_t on |x| < 88), and its 32-entry table must
+equal bits(2^(i/32)) - (i << 47) computed in long double.
 
 The default run strides through all 2^32 bit patterns (every 3rd); set
 HM_EXPF_EXHAUSTIVE=1 to check every float (about a minute)."""
@@ -40,6 +41,10 @@ PROGRAM = textwrap.dedent(r"""
             float a = expf(x), m = hm_expf(x);
             ++n;
             if (memcmp(&a, &m, 4)) { if (bad < 5) fprintf(stderr, "x=%a libm=%a mine=%a\n", x, a, m); ++bad; }
+            if (fabsf(x) < 88.0f) {  /* the range where the kernels take the short path */
+                float s = hm_expf_small_t(x, kHmExp2Table);
+                if (memcmp(&a, &s, 4)) { if (bad < 5) fprintf(stderr, "small x=%a libm=%a mine=%a\n", x, a, s); ++bad; }
+            }
         }
         printf("%lld %lld %lld\n", bad_tab, n, bad);
         return 0;
