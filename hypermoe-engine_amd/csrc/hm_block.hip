@@ -182,7 +182,8 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
     }
     const int64_t E = layer->experts, H = layer->hidden;
     const int64_t P = tokens * top_k;
-    rc = hm_router_topk(hidden, router_w, tokens, H, E, top_k, route_flags & 3u, p.ids,
+    rc = hm_router_topk(hidden, router_w, tokens, H, E, top_k,
+                        route_flags & (HM_ROUTE_SOFTMAX | HM_ROUTE_RENORM | HM_EXEC_ROUTE_SEQUENTIAL), p.ids,
                         p.scores, nullptr, status, p.route_ws, stream);
     if (rc || (rc = mark(1))) return rc;
     rc = hm_permute(p.ids, p.scores, tokens, top_k, E, p.counts, p.offsets, p.perm_tokens,

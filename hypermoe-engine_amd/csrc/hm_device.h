@@ -100,6 +100,45 @@ __device__ __forceinline__ int hm_wave_sum_dpp(int v) {
            __builtin_amdgcn_readlane(r, 32) + __builtin_amdgcn_readlane(r, 48);
 }
 
+// The same for 64-bit values (both halves through the same DPP pattern).
+__device__ __forceinline__ unsigned long long hm_dpp_u64(unsigned long long v, int ctrl_sel) {
+    const float lo = hm_dpp_f32(__builtin_bit_cast(float, (unsigned)(v & 0xffffffffull)), ctrl_sel);
+    const float hi = hm_dpp_f32(__builtin_bit_cast(float, (unsigned)(v >> 32)), ctrl_sel);
+    return ((unsigned long long)__builtin_bit_cast(unsigned, hi) << 32) | __builtin_bit_cast(unsigned, lo);
+}
+__device__ __forceinline__ unsigned long long hm_readlane_u64(unsigned long long v, int l) {
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(v & 0xffffffffull), l);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(v >> 32), l);
+    return ((unsigned long long)hi << 32) | lo;
+}
+__device__ __forceinline__ unsigned long long hm_wave_max_u64_dpp(unsigned long long v) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const unsigned long long o = hm_dpp_u64(v, c);
+        v = o > v ? o : v;
+    }
+    unsigned long long m = hm_readlane_u64(v, 0);
+#pragma unroll
+    for (int r = 16; r < HM_WAVE; r += 16) {
+        const unsigned long long o = hm_readlane_u64(v, r);
+        m = o > m ? o : m;
+    }
+    return m;
+}
+// Sum of doubles over the wave (row DPP, then the four rows in ascending
+// row order); callers use it only where any summation order gives the
+// same result.
+__device__ __forceinline__ double hm_wave_sum_f64_dpp(double v) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        v += __builtin_bit_cast(double, hm_dpp_u64(__builtin_bit_cast(unsigned long long, v), c));
+    double s = __builtin_bit_cast(double, hm_readlane_u64(__builtin_bit_cast(unsigned long long, v), 0));
+#pragma unroll
+    for (int r = 16; r < HM_WAVE; r += 16)
+        s += __builtin_bit_cast(double, hm_readlane_u64(__builtin_bit_cast(unsigned long long, v), r));
+    return s;
+}
+
 // glibc 2.35 expf restated for host and device (hm_expf.h); matches the host
 // libm expf on every float input (exhaustive check, tests/test_expf_parity.py).
 #include "hm_expf.h"

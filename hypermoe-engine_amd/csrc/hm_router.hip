@@ -284,68 +284,123 @@ __global__ __launch_bounds__(256) void router_logits_tile_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// A2 logits for a few tokens (decode, T <= 16).  The sequential chain is
-// 2048 FP64 FMAs long whatever the batch, so the work is spread over many
-// CUs instead: one wave per 4 experts, lane = (token t = lane/4, expert
-// lane%4), one chain per lane; W [128 k x 4 e] and h [16 t x 128 k] chunks
-// stream through a 4-stage LDS ring.  Needs E % 4 == 0, H % 128 == 0 and
-// 16-byte aligned h, w.
+// A2 logits for a few tokens (decode, T <= 16), certified parallel form.
+// The reference's logit is float(s_n) with s_k = fl(s_{k-1} + p_k) and
+// p_k = h_k w_k (exact in double), k ascending: a chain of H dependent
+// additions.  Here H is cut into kNB blocks of b = H/kNB.  Block j is summed
+// sequentially from +0 (partials l_jm) beside R_j = sum_m |l_jm| and
+// Q_j = sum_m |p_jm| (router_partial_kernel, one wave per block, expert
+// group and token); then, per logit, the block sums are added sequentially:
+// A_0 = 0, A_{j+1} = fl(A_j + B_j), S' = A_kNB, SA = sum_j |A_{j+1}|.
+// Each rounding of the reference errs by at most u|s_k| (u = 2^-53), and
+// |s_k| <= |A_j| + |l_jm| plus the (bounded) errors of those, so with
+// R = sum R_j and P = sum Q_j
+//   |s_n - S'| <= u ((b+1) SA + 2R) + u^2 (H (R + SA) + 1.01 (b^2 + H^2) P).
+// Float rounding is monotone: if both ends of S' +- (that bound, inflated
+// for the rounding of its own evaluation) round to the same float, it is
+// the reference's logit.  Otherwise (about one logit in 10^4 - 10^5 for
+// random data, and every non-finite case) the lane runs the reference's
+// sequential chain.  HM_EXEC_ROUTE_SEQUENTIAL sends every logit there.
 // ---------------------------------------------------------------------------
-constexpr int kSK = 128;                 // k per chunk
-constexpr int kSS = 4;                   // ring stages
-constexpr int kSW = kSK * 4 * 4;         // W bytes per stage (2 KB)
-constexpr int kSH = 16 * kSK * 4;        // h bytes per stage (8 KB)
-constexpr int kSLPW = 10;                // 16-byte wave loads per stage
+constexpr int kNB = 32;  // K blocks per logit (a multiple of 8)
 
-__global__ __launch_bounds__(64) void router_logits_small_kernel(
-    const float* __restrict__ h, const float* __restrict__ w, int64_t tokens,
-    int64_t hidden, int64_t experts, float* __restrict__ logits, int32_t* status) {
-    __shared__ __attribute__((aligned(1024))) char ring[kSS][kSW + kSH];
+// part[t][j][c][e], c = 0, 1, 2: B_j, R_j, Q_j (expert-minor, so that the
+// select kernel's lanes read consecutive experts); grid (kNB, ceil(E/64), T),
+// one wave, lane = expert.  The block's W rows (64 experts wide) go to LDS
+// in one burst of 16-byte DMA loads (E % 64 == 0, b % 4 == 0, w 16-byte
+// aligned), else per lane.
+constexpr int kPK = 64;  // k per LDS chunk of a block
+
+__global__ __launch_bounds__(64) void router_partial_kernel(
+    const float* __restrict__ h, const float* __restrict__ w, int hidden, int experts,
+    double* __restrict__ part) {
+    __shared__ double s_h[kPK];                                        // broadcast reads
+    __shared__ __attribute__((aligned(1024))) float s_w[kPK][HM_WAVE];  // [k][lane]
     const int lane = threadIdx.x;
-    const int t = lane >> 2, ei = lane & 3;
-    const int64_t e0 = (int64_t)blockIdx.x * 4;
-    // loads: W rows k0+lane and k0+64+lane (16 bytes = 4 experts each);
-    // h: 8 loads of two token rows x 128 k (32 lanes per row)
-    const float* wsrc = w + (int64_t)lane * experts + e0;
-    const float* hsrc = h + 4 * (lane & 31);
-    auto issue = [&](int slot, int64_t k0) {
-        char* st = ring[slot];
-        dma16(wsrc + k0 * experts, st);
-        dma16(wsrc + (k0 + 64) * experts, st + 1024);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int64_t tk = min((int64_t)(2 * j) + (lane >> 5), tokens - 1);
-            dma16(hsrc + tk * hidden + k0, st + kSW + 1024 * j);
+    const int j = blockIdx.x, t = blockIdx.z;
+    const int e0 = blockIdx.y * HM_WAVE;
+    const int e = e0 + lane;
+    const bool live = e < experts;
+    const int b = hidden / kNB;
+    const bool full = experts % HM_WAVE == 0 && b % 4 == 0 && (uintptr_t)w % 16 == 0;
+    const int k0 = j * b;
+    const float* hp = h + (int64_t)t * hidden + k0;
+    double acc = 0.0, rs = 0.0, qs = 0.0;
+    for (int c0 = 0; c0 < b; c0 += kPK) {
+        const int kc = min(kPK, b - c0);
+        __builtin_amdgcn_wave_barrier();
+        s_h[lane] = lane < kc ? (double)hp[c0 + lane] : 0.0;
+        if (full) {
+            // lane l: row 4i + l/16, floats 4*(l%16) .. +3 of the 64-expert row
+            const float* src = w + (int64_t)(k0 + c0 + (lane >> 4)) * experts + e0 + 4 * (lane & 15);
+            for (int i = 0; i < kc / 4; ++i) dma16(src + (int64_t)4 * i * experts, &s_w[4 * i][0]);
+            wait_vmcnt<0>();
+        } else {
+            for (int i = 0; i < kc; ++i) s_w[i][lane] = live ? w[(int64_t)(k0 + c0 + i) * experts + e] : 0.0f;
         }
-    };
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        for (int i = 0; i < kc; ++i) {
+            const double hk = s_h[i];
+            const double wd = (double)s_w[i][lane];
+            acc = __builtin_fma(hk, wd, acc);  // == acc + hk * wd (the product is exact)
+            rs += fabs(acc);
+            qs = __builtin_fma(fabs(hk), fabs(wd), qs);
+        }
+    }
+    if (live) {
+        double* o = part + (((int64_t)t * kNB + j) * 3) * experts + e;
+        o[0] = acc;
+        o[experts] = rs;
+        o[2 * experts] = qs;
+    }
+}
+
+// One logit from its block partials (see above), or from the sequential
+// chain when the bound does not settle the float.
+// pp: this logit's B_0 (part + t*kNB*3*E + e); component c of block j is at
+// pp[(3j + c) * E].
+__device__ __forceinline__ float certified_logit(const double* __restrict__ pp,
+                                                 const float* __restrict__ hrow,
+                                                 const float* __restrict__ wcol, int64_t hidden,
+                                                 int64_t experts, bool force_seq,
+                                                 int32_t* status) {
+    double a = 0.0, sa = 0.0, sr = 0.0, sp = 0.0;
+    // 8 blocks at a time: their 24 loads go out before the dependent chain
+    constexpr int G = 8;
+    const int64_t stride = 3 * experts;
+    for (int j0 = 0; j0 < kNB; j0 += G) {
+        double bv[G], rv[G], qv[G];
+        const double* q = pp + j0 * stride;
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            bv[i] = q[i * stride];
+            rv[i] = q[i * stride + experts];
+            qv[i] = q[i * stride + 2 * experts];
+        }
+#pragma unroll
+        for (int i = 0; i < G; ++i) {
+            a += bv[i];
+            sa += fabs(a);
+            sr += rv[i];
+            sp += qv[i];
+        }
+    }
+    const double u = 0x1p-53;
+    const double n = (double)hidden, bw = (double)(hidden / kNB);
+    const double infl = 1.0 + 4.0 * n * u;  // the magnitude sums' own rounding
+    const double b0 = (u * ((bw + 1.0) * sa + 2.0 * sr) +
+                       2.0 * u * u * (n * (sr + sa) + 1.01 * (bw * bw + n * n) * sp)) * infl;
+    const double bc = (b0 * (1.0 + 0x1p-40) + u * fabs(a)) * (1.0 + 0x1p-50);
+    const double lo = a - bc, hi = a + bc;
+    const bool ok = !force_seq && isfinite(lo) && isfinite(hi) &&
+                    __float_as_uint((float)lo) == __float_as_uint((float)hi);
+    if (ok) return (float)a;
     double acc = 0.0;
-    const int nk = (int)(hidden / kSK);
-#pragma unroll
-    for (int s = 0; s < kSS - 1; ++s)
-        if (s < nk) issue(s, (int64_t)s * kSK);
-    for (int c = 0; c < nk; ++c) {
-        const int slot = c % kSS;
-        if (c + kSS - 2 < nk) wait_vmcnt<(kSS - 2) * kSLPW>();
-        else wait_vmcnt<0>();
-        lds_barrier();
-        if (c + kSS - 1 < nk) issue((c + kSS - 1) % kSS, (int64_t)(c + kSS - 1) * kSK);
-        const float* ws = reinterpret_cast<const float*>(ring[slot]);
-        const float* hs = reinterpret_cast<const float*>(ring[slot] + kSW) + t * kSK;
-#pragma unroll
-        for (int kk = 0; kk < kSK; kk += 4) {
-            const float4 hv = *reinterpret_cast<const float4*>(hs + kk);
-            const double w0 = (double)ws[(kk + 0) * 4 + ei], w1 = (double)ws[(kk + 1) * 4 + ei];
-            const double w2 = (double)ws[(kk + 2) * 4 + ei], w3 = (double)ws[(kk + 3) * 4 + ei];
-            acc = __builtin_fma((double)hv.x, w0, acc);
-            acc = __builtin_fma((double)hv.y, w1, acc);
-            acc = __builtin_fma((double)hv.z, w2, acc);
-            acc = __builtin_fma((double)hv.w, w3, acc);
-        }
-    }
-    if (t < tokens) {
-        if (!isfinite(acc)) hm_status_or(status, HM_STATUS_NONFINITE_SCORE);
-        logits[(int64_t)t * experts + e0 + ei] = (float)acc;
-    }
+    for (int64_t k = 0; k < hidden; ++k)
+        acc = __builtin_fma((double)hrow[k], (double)wcol[k * experts], acc);
+    if (!isfinite(acc)) hm_status_or(status, HM_STATUS_NONFINITE_SCORE);
+    return (float)acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -362,30 +417,19 @@ __global__ __launch_bounds__(64) void router_logits_small_kernel(
 //   renorm: sum of the k selected scores in rank order in double.
 // Writes ids/scores [t, r] in rank order.
 // ---------------------------------------------------------------------------
+// Softmax, top-k and renormalisation of one token's logits v (one wave; lane
+// holds experts lane + 64 j); writes ids/scores [t, r] in rank order.
 template <int EPL>
-__global__ __launch_bounds__(kBlock) void router_select_kernel(
-    const float* __restrict__ logits, int64_t tokens, int64_t experts,
-    int32_t top_k, uint32_t flags, uint32_t* __restrict__ ids,
-    float* __restrict__ scores, int32_t* status) {
-    extern __shared__ float seq_lds[];  // (kBlock/64) * experts floats
-    const int lane = threadIdx.x & (HM_WAVE - 1);
-    const int wave = threadIdx.x / HM_WAVE;
-    const int64_t t = (int64_t)blockIdx.x * (kBlock / HM_WAVE) + wave;
-    if (t >= tokens) return;
-    const float* lt = logits + t * experts;
-    float v[EPL];
-    bool valid[EPL];
-#pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-        const int64_t e = lane + (int64_t)HM_WAVE * j;
-        valid[j] = e < experts;
-        v[j] = valid[j] ? lt[e] : 0.0f;
-    }
+__device__ __forceinline__ void select_token(float (&v)[EPL], const bool (&valid)[EPL], int lane,
+                                             int wave, int64_t t, int64_t experts, int32_t top_k,
+                                             uint32_t flags, uint32_t* __restrict__ ids,
+                                             float* __restrict__ scores, int32_t* status,
+                                             float* seq_lds) {
     if (flags & HM_ROUTE_SOFTMAX) {
         float m = -__uint_as_float(0x7f800000u);
 #pragma unroll
         for (int j = 0; j < EPL; ++j) if (valid[j]) m = fmaxf(m, v[j]);
-        m = hm_wave_max_f32(m);
+        m = hm_wave_max_dpp(m);
         bool exact = true;
         double part = 0.0;
 #pragma unroll
@@ -397,7 +441,7 @@ __global__ __launch_bounds__(kBlock) void router_select_kernel(
         }
         double den;
         if (__all(exact) && experts <= 2048) {
-            den = hm_wave_sum_f64(part);
+            den = hm_wave_sum_f64_dpp(part);
         } else {
             float* seq = seq_lds + (int64_t)wave * experts;
 #pragma unroll
@@ -427,7 +471,7 @@ __global__ __launch_bounds__(kBlock) void router_select_kernel(
         unsigned long long best = 0ull;
 #pragma unroll
         for (int j = 0; j < EPL; ++j) best = key[j] > best ? key[j] : best;
-        best = hm_wave_max_u64(best);
+        best = hm_wave_max_u64_dpp(best);
         const uint32_t id = 0xffffffffu - (uint32_t)(best & 0xffffffffull);
         const int owner = (int)(id % HM_WAVE);
         const int slot = (int)(id / HM_WAVE);
@@ -451,6 +495,58 @@ __global__ __launch_bounds__(kBlock) void router_select_kernel(
         ids[t * top_k + lane] = my_id;
         scores[t * top_k + lane] = my_score;
     }
+}
+
+template <int EPL>
+__global__ __launch_bounds__(kBlock) void router_select_kernel(
+    const float* __restrict__ logits, int64_t tokens, int64_t experts,
+    int32_t top_k, uint32_t flags, uint32_t* __restrict__ ids,
+    float* __restrict__ scores, int32_t* status) {
+    extern __shared__ float seq_lds[];  // (kBlock/64) * experts floats
+    const int lane = threadIdx.x & (HM_WAVE - 1);
+    const int wave = threadIdx.x / HM_WAVE;
+    const int64_t t = (int64_t)blockIdx.x * (kBlock / HM_WAVE) + wave;
+    if (t >= tokens) return;
+    const float* lt = logits + t * experts;
+    float v[EPL];
+    bool valid[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        const int64_t e = lane + (int64_t)HM_WAVE * j;
+        valid[j] = e < experts;
+        v[j] = valid[j] ? lt[e] : 0.0f;
+    }
+    select_token<EPL>(v, valid, lane, wave, t, experts, top_k, flags, ids, scores, status, seq_lds);
+}
+
+// Select over logits formed from the decode partials (and written to
+// `logits` too).
+template <int EPL>
+__global__ __launch_bounds__(kBlock) void router_select_partial_kernel(
+    const float* __restrict__ h, const float* __restrict__ w, const double* __restrict__ part,
+    int64_t tokens, int64_t hidden, int64_t experts, int32_t top_k, uint32_t flags,
+    float* __restrict__ logits, uint32_t* __restrict__ ids, float* __restrict__ scores,
+    int32_t* status) {
+    extern __shared__ float seq_lds[];  // (kBlock/64) * experts floats
+    const int lane = threadIdx.x & (HM_WAVE - 1);
+    const int wave = threadIdx.x / HM_WAVE;
+    const int64_t t = (int64_t)blockIdx.x * (kBlock / HM_WAVE) + wave;
+    if (t >= tokens) return;
+    const bool force_seq = (flags & HM_EXEC_ROUTE_SEQUENTIAL) != 0;
+    float v[EPL];
+    bool valid[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        const int64_t e = lane + (int64_t)HM_WAVE * j;
+        valid[j] = e < experts;
+        v[j] = 0.0f;
+        if (valid[j]) {
+            v[j] = certified_logit(part + t * kNB * 3 * experts + e, h + t * hidden, w + e,
+                                   hidden, experts, force_seq, status);
+            logits[t * experts + e] = v[j];
+        }
+    }
+    select_token<EPL>(v, valid, lane, wave, t, experts, top_k, flags, ids, scores, status, seq_lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -668,9 +764,20 @@ int hm_rmsnorm(const float* x, const float* gamma, float* y, int64_t rows,
 }
 
 // Route workspace: the float logits [T x E].
+// Route workspace: the logits [T x E] floats, and for decode batches
+// (T <= kDecodeTokens) the block partials [T x E x kNB x 3] doubles after
+// them (8-byte aligned).
+constexpr int64_t kDecodeTokens = 16;
+
+static size_t route_logits_bytes(int64_t tokens, int64_t experts) {
+    return ((size_t)tokens * (size_t)experts * sizeof(float) + 7) & ~(size_t)7;
+}
+
 size_t hm_route_workspace_bytes(int64_t tokens, int64_t experts) {
     if (tokens < 0 || experts <= 0) return 0;
-    return (size_t)tokens * (size_t)experts * sizeof(float);
+    if (tokens > kDecodeTokens) return (size_t)tokens * (size_t)experts * sizeof(float);
+    return route_logits_bytes(tokens, experts) +
+           (size_t)tokens * (size_t)experts * kNB * 3 * sizeof(double);
 }
 
 int hm_router_topk(const float* h, const float* w, int64_t tokens,
@@ -685,11 +792,34 @@ int hm_router_topk(const float* h, const float* w, int64_t tokens,
     if (experts > 1024 || top_k > kMaxTopK) return HM_ERR_UNSUPPORTED;
     if (tokens > ((int64_t)1 << 31) / kLT) return HM_ERR_OVERFLOW;
     float* logits = logits_out ? logits_out : static_cast<float*>(route_ws);
+    const int epl = (int)((experts + HM_WAVE - 1) / HM_WAVE);
+    const dim3 sgrid((unsigned)((tokens + 3) / 4));
+    const size_t seq_bytes = (size_t)(kBlock / HM_WAVE) * experts * sizeof(float);
+    if (route_ws && tokens <= kDecodeTokens && hidden % kNB == 0 && hidden <= INT_MAX) {
+        // decode: certified block partials, then select over the logits
+        // formed from them
+        double* part = reinterpret_cast<double*>(static_cast<char*>(route_ws) +
+                                                 route_logits_bytes(tokens, experts));
+        const dim3 pgrid((unsigned)kNB, (unsigned)((experts + HM_WAVE - 1) / HM_WAVE),
+                         (unsigned)tokens);
+        hipLaunchKernelGGL(router_partial_kernel, pgrid, dim3(HM_WAVE), 0, hm_stream(stream), h,
+                           w, (int)hidden, (int)experts, part);
+        HM_LAUNCHED();
+#define HM_SELECTP(N)                                                                     \
+        hipLaunchKernelGGL(router_select_partial_kernel<N>, sgrid, dim3(kBlock), seq_bytes,  \
+                           hm_stream(stream), h, w, part, tokens, hidden, experts, top_k,    \
+                           flags, logits, ids, scores, status)
+        if (epl <= 1) HM_SELECTP(1);
+        else if (epl <= 2) HM_SELECTP(2);
+        else if (epl <= 4) HM_SELECTP(4);
+        else if (epl <= 8) HM_SELECTP(8);
+        else HM_SELECTP(16);
+#undef HM_SELECTP
+        HM_LAUNCHED();
+        return HM_OK;
+    }
     const bool aligned = ((uintptr_t)h % 16 == 0) && ((uintptr_t)w % 16 == 0);
-    if (aligned && tokens <= 16 && experts % 4 == 0 && hidden % kSK == 0) {
-        hipLaunchKernelGGL(router_logits_small_kernel, dim3((unsigned)(experts / 4)), dim3(64),
-                           0, hm_stream(stream), h, w, tokens, hidden, experts, logits, status);
-    } else if (aligned && experts % kTE == 0 && hidden % kTK == 0) {
+    if (aligned && experts % kTE == 0 && hidden % kTK == 0) {
         const dim3 grid((unsigned)((tokens + kTT - 1) / kTT), (unsigned)(experts / kTE));
         hipLaunchKernelGGL(router_logits_tile_kernel, grid, dim3(256), 0, hm_stream(stream), h,
                            w, tokens, hidden, experts, logits, status);
@@ -700,9 +830,6 @@ int hm_router_topk(const float* h, const float* w, int64_t tokens,
                            h, w, tokens, hidden, experts, logits, status);
     }
     HM_LAUNCHED();
-    const dim3 sgrid((unsigned)((tokens + 3) / 4));
-    const size_t seq_bytes = (size_t)(kBlock / HM_WAVE) * experts * sizeof(float);
-    const int epl = (int)((experts + HM_WAVE - 1) / HM_WAVE);
 #define HM_SELECT(N)                                                                   \
     hipLaunchKernelGGL(router_select_kernel<N>, sgrid, dim3(kBlock), seq_bytes,        \
                        hm_stream(stream), logits, tokens, experts, top_k, flags, ids,  \

@@ -68,6 +68,11 @@ typedef enum hm_status {
  * reference, not bit-identical to the limb arithmetic). */
 #define HM_EXEC_LIMBS 0x200u
 #define HM_GEMV_MAX_TOKENS 16
+/* Execution flag for hm_router_topk / hm_moe_block_forward: decode batches
+ * (at most 16 tokens) compute every router logit with the reference's
+ * sequential FP64 chain instead of certifying the parallel block sums (the
+ * results are identical; the flag exercises the fallback). */
+#define HM_EXEC_ROUTE_SEQUENTIAL 0x400u
 
 /* Expert weight dtypes (src/tensor/DType.hpp:9-14 numbering). */
 #define HM_DTYPE_FP32 0
@@ -112,7 +117,10 @@ int hm_rmsnorm(const float* x, const float* gamma, float* y, int64_t rows,
  * (score desc, expert id asc); optional renormalisation by the double sum of
  * the selected scores in rank order.  ids/scores are [tokens x top_k] in
  * rank order.  Bit-exact.  The logits go to logits_out, or, when it is NULL,
- * to `route_ws` (hm_route_workspace_bytes(tokens, experts) bytes). */
+ * to `route_ws` (hm_route_workspace_bytes(tokens, experts) bytes).  With
+ * route_ws given, batches of at most 16 tokens take the certified parallel
+ * form of the logit sums (their block partials live in route_ws).  `flags`:
+ * HM_ROUTE_* bits, optionally HM_EXEC_ROUTE_SEQUENTIAL. */
 size_t hm_route_workspace_bytes(int64_t tokens, int64_t experts);
 int hm_router_topk(const float* h, const float* w, int64_t tokens,
                    int64_t hidden, int64_t experts, int32_t top_k,

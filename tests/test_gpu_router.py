@@ -139,6 +139,58 @@ def test_router_nonfinite_sets_status(dev):
     assert rc == -3  # HMO_E_RUNTIME
 
 
+def test_router_decode_sequential_flag_same_bits(dev):
+    """Decode batches certify parallel block sums of the logits; forcing the
+    reference's sequential chain for every logit gives the same bits."""
+    from hmoe import capi
+    for T, H, E in ((1, 2048, 128), (16, 2048, 128), (5, 512, 64)):
+        print(f"[gpu] decode router sequential flag T={T} H={H} E={E}", flush=True)
+        rng = np.random.default_rng(T + H)
+        h = O.rmsnorm(rng.standard_normal((T, H)).astype(np.float32), np.ones(H, np.float32))
+        w = (0.02 * rng.standard_normal((H, E))).astype(np.float32)
+        a = run_router(dev, h, w, 8, 3)
+        b = run_router(dev, h, w, 8, 3 | capi.HM_EXEC_ROUTE_SEQUENTIAL)
+        rc, logits = O.router_logits(h, w)
+        assert_bitexact(a["logits"], logits, "certified logits")
+        assert_bitexact(b["logits"], logits, "sequential logits")
+        assert_bitexact(a["ids"], b["ids"], "ids")
+        assert_bitexact(a["scores"], b["scores"], "scores")
+
+
+def test_router_decode_uncertifiable_logits(dev):
+    """Logits the bound cannot settle fall back to the sequential chain:
+    an exact float midpoint (1 + 2^-24 ties to even: 1.0) and an exact
+    cancellation (the sequential sum ends at +0, the interval spans -0/+0)."""
+    H, E = 64, 4
+    h = np.zeros((2, H), np.float32)
+    w = np.zeros((H, E), np.float32)
+    h[0, 0], h[0, 1] = 1.0, 2.0 ** -24
+    w[0, :], w[1, :] = 1.0, 1.0            # expert logits 1 + 2^-24 -> 1.0
+    h[1, 0], h[1, 5] = 1.0, 1.0
+    w[0, 2], w[5, 2] = 0.375, -0.375       # expert 2 of token 1: exactly 0
+    w[0, 3], w[5, 3] = 3.0, 2.0 ** -22     # expert 3 of token 1: 3 + 2^-22 (exact)
+    g = run_router(dev, h, w, 2, 3)
+    rc, logits = O.router_logits(h, w)
+    assert rc == 0
+    assert_bitexact(g["logits"], logits, "logits at rounding boundaries")
+    assert g["logits"][0, 0] == 1.0
+    assert np.signbit(g["logits"][1, 2]) == np.signbit(logits[1, 2]) and g["logits"][1, 2] == 0.0
+    rc, ids, scores = O.route(h, w, 2, 1, 1)
+    assert_bitexact(g["ids"], ids, "ids")
+    assert_bitexact(g["scores"], scores, "scores")
+
+
+def test_router_decode_nonfinite_sets_status(dev):
+    """A non-finite logit on the decode path (it always takes the
+    sequential chain) sets HM_STATUS_NONFINITE_SCORE."""
+    H, E = 64, 8
+    h = np.ones((1, H), np.float32)
+    w = np.full((H, E), 0.01, np.float32)
+    w[3, 5] = np.inf
+    g = run_router(dev, h, w, 2, 3)
+    assert g["status"] & 1
+
+
 def test_permute_invariants_large(dev):
     """C4 shape (T=4096, E=128, k=8) with Zipf-skewed routing: permutation
     bit-exact against the oracle grouping of the oracle's routing."""
