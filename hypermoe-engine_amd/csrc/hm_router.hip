@@ -193,14 +193,13 @@ __global__ __launch_bounds__(kBlock) void router_logits_kernel(
 // ---------------------------------------------------------------------------
 // A2 logits, tiled (prefill).  Same arithmetic as router_logits_kernel: one
 // sequential FP64 chain per (token, expert) in ascending k.  Workgroup tile
-// 32 tokens x 64 experts, 4 waves; lane = expert, wave w owns tokens
-// 8w..8w+7, so a lane runs 8 independent chains (enough to keep the FP64
-// pipe issuing) and the per-k LDS traffic is one 4-byte weight per lane plus
-// eight broadcast token values per wave.  W [32 k x 64 e] and h [32 t x 32 k]
-// chunks come straight from global memory into a 4-stage LDS ring
-// (global_load_lds); each chunk's h is widened to double once (one LDS
-// array, double buffered) rather than per use.  Needs E % 64 == 0,
-// H % 32 == 0 and 16-byte aligned h, w.
+// 32 tokens x 64 experts, 256 threads; thread (lt, le) = (tid/16, tid%16)
+// runs the 8 chains of tokens 2lt, 2lt+1 x experts 4le..4le+3, so each k
+// costs three 16-byte LDS reads (two h doubles, four w doubles; the h read
+// is a broadcast across the 16 threads of a token pair) for eight FMAs.
+// W [32 k x 64 e] and h [32 t x 32 k] chunks come straight from global
+// memory into a 4-stage LDS ring (global_load_lds) and are widened to double
+// once per chunk.  Needs E % 64 == 0, H % 32 == 0 and 16-byte aligned h, w.
 // ---------------------------------------------------------------------------
 constexpr int kTT = 32;                // tokens per tile
 constexpr int kTE = 64;                // experts per tile
@@ -214,9 +213,11 @@ __global__ __launch_bounds__(256) void router_logits_tile_kernel(
     const float* __restrict__ h, const float* __restrict__ w, int64_t tokens,
     int64_t hidden, int64_t experts, float* __restrict__ logits, int32_t* status) {
     __shared__ __attribute__((aligned(1024))) char ring[kTS][kTW + kTH];
-    __shared__ __attribute__((aligned(16))) double hd[2][kTK][kTT];
+    __shared__ __attribute__((aligned(16))) double hd[kTK][kTT];  // [k][token]
+    __shared__ __attribute__((aligned(16))) double wd[kTK][kTE];  // [k][expert]
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lt = tid >> 4, le = tid & 15;
     const int64_t t0 = (int64_t)blockIdx.x * kTT;
     const int64_t e0 = (int64_t)blockIdx.y * kTE;
     // this wave's loads per stage: W rows [8w, 8w+8) as two 1 KB pieces
@@ -231,9 +232,11 @@ __global__ __launch_bounds__(256) void router_logits_tile_kernel(
         dma16(wsrc1 + k0 * experts, st + 2048 * wave + 1024);
         dma16(hsrc + k0, st + kTW + 1024 * wave);
     };
-    double acc[8];
+    double acc[2][4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = 0.0;
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.0;
     const int nk = (int)(hidden / kTK);
 #pragma unroll
     for (int s = 0; s < kTS - 1; ++s)
@@ -242,44 +245,47 @@ __global__ __launch_bounds__(256) void router_logits_tile_kernel(
         const int slot = c % kTS;
         if (c + kTS - 2 < nk) wait_vmcnt<(kTS - 2) * kTLPW>();
         else wait_vmcnt<0>();
-        lds_barrier();  // stage c landed for every wave; stage c-1 fully read
+        lds_barrier();  // stage c landed for every wave; chunk c-1 fully computed
         if (c + kTS - 1 < nk) issue((c + kTS - 1) % kTS, (int64_t)(c + kTS - 1) * kTK);
-        {   // widen this chunk's h: thread -> token tid/8, k 4*(tid%8)..+3
+        {   // widen the chunk: h thread -> token tid/8, k 4*(tid%8)..+3;
+            // W thread -> floats 4*tid..+3 and 1024+4*tid..+3 of [k][64]
             const float4 v = *reinterpret_cast<const float4*>(ring[slot] + kTW + 16 * tid);
             const int t = tid >> 3, kk = 4 * (tid & 7);
-            double* dst = &hd[c & 1][kk][t];
-            dst[0] = (double)v.x;
-            dst[kTT] = (double)v.y;
-            dst[2 * kTT] = (double)v.z;
-            dst[3 * kTT] = (double)v.w;
+            hd[kk][t] = (double)v.x;
+            hd[kk + 1][t] = (double)v.y;
+            hd[kk + 2][t] = (double)v.z;
+            hd[kk + 3][t] = (double)v.w;
+            const float4 a = *reinterpret_cast<const float4*>(ring[slot] + 16 * tid);
+            const float4 b = *reinterpret_cast<const float4*>(ring[slot] + 4096 + 16 * tid);
+            double* w0 = &wd[0][0] + 4 * tid;
+            w0[0] = (double)a.x; w0[1] = (double)a.y; w0[2] = (double)a.z; w0[3] = (double)a.w;
+            w0[1024] = (double)b.x; w0[1025] = (double)b.y; w0[1026] = (double)b.z; w0[1027] = (double)b.w;
         }
         lds_barrier();
-        const float* ws = reinterpret_cast<const float*>(ring[slot]);
-        const double* hs = &hd[c & 1][0][8 * wave];
 #pragma unroll
         for (int kk = 0; kk < kTK; ++kk) {
-            const double wv = (double)ws[kk * kTE + lane];
-            const double2 h01 = *reinterpret_cast<const double2*>(hs + kk * kTT);
-            const double2 h23 = *reinterpret_cast<const double2*>(hs + kk * kTT + 2);
-            const double2 h45 = *reinterpret_cast<const double2*>(hs + kk * kTT + 4);
-            const double2 h67 = *reinterpret_cast<const double2*>(hs + kk * kTT + 6);
-            acc[0] = __builtin_fma(h01.x, wv, acc[0]);
-            acc[1] = __builtin_fma(h01.y, wv, acc[1]);
-            acc[2] = __builtin_fma(h23.x, wv, acc[2]);
-            acc[3] = __builtin_fma(h23.y, wv, acc[3]);
-            acc[4] = __builtin_fma(h45.x, wv, acc[4]);
-            acc[5] = __builtin_fma(h45.y, wv, acc[5]);
-            acc[6] = __builtin_fma(h67.x, wv, acc[6]);
-            acc[7] = __builtin_fma(h67.y, wv, acc[7]);
+            const double2 hv = *reinterpret_cast<const double2*>(&hd[kk][2 * lt]);
+            const double2 w01 = *reinterpret_cast<const double2*>(&wd[kk][4 * le]);
+            const double2 w23 = *reinterpret_cast<const double2*>(&wd[kk][4 * le + 2]);
+            acc[0][0] = __builtin_fma(hv.x, w01.x, acc[0][0]);
+            acc[0][1] = __builtin_fma(hv.x, w01.y, acc[0][1]);
+            acc[0][2] = __builtin_fma(hv.x, w23.x, acc[0][2]);
+            acc[0][3] = __builtin_fma(hv.x, w23.y, acc[0][3]);
+            acc[1][0] = __builtin_fma(hv.y, w01.x, acc[1][0]);
+            acc[1][1] = __builtin_fma(hv.y, w01.y, acc[1][1]);
+            acc[1][2] = __builtin_fma(hv.y, w23.x, acc[1][2]);
+            acc[1][3] = __builtin_fma(hv.y, w23.y, acc[1][3]);
         }
     }
-    const int64_t e = e0 + lane;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int64_t t = t0 + 8 * wave + i;
+    for (int i = 0; i < 2; ++i) {
+        const int64_t t = t0 + 2 * lt + i;
         if (t >= tokens) continue;
-        if (!isfinite(acc[i])) hm_status_or(status, HM_STATUS_NONFINITE_SCORE);
-        logits[t * experts + e] = (float)acc[i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (!isfinite(acc[i][j])) hm_status_or(status, HM_STATUS_NONFINITE_SCORE);
+            logits[t * experts + e0 + 4 * le + j] = (float)acc[i][j];
+        }
     }
 }
 
