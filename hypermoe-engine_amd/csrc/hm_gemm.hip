@@ -3,8 +3,8 @@
 // INT8 experts (W8A32 in the reference, CpuTensorBackend.cpp:173-186) run on
 // INT8 MFMA through the integer-limb format (hm_device.h): activations are
 // fixed point split into L balanced signed INT8 digit planes, one
-// v_mfma_i32_16x16x64_i8 per plane, exact int32 partials, recombined in the
-// epilogue.  The generic kernels compute the identical integers with scalar
+// v_mfma_i32_32x32x32_i8 per plane, exact int32 partials, recombined in the
+// epilogue (hm_gemm_mfma.hip).  The generic kernels compute the identical integers with scalar
 // loops; they serve shapes the MFMA tiles do not cover and pin the MFMA
 // kernels in tests (bit-for-bit).
 //
@@ -52,6 +52,61 @@ __global__ __launch_bounds__(kBlock) void limb_quantize_rows_kernel(
 #pragma unroll
     for (int l = 0; l < L; ++l) {
         const int s = hm_wave_sum_i32(dl[l]);
+        if (lane == 0 && dsum) dsum[(int64_t)l * rows + r] = s;
+    }
+    if (lane == 0) scales[r] = amax > 0.0f ? __fdiv_rn(amax, range) : 0.0f;
+}
+
+// The same for rows of n = 256 * nv floats (nv <= 16, 16-byte aligned):
+// the row is read once into registers (lane: floats 4*(lane + 64 i) .. +3),
+// reduced with DPP, and each lane stores its four digits of a plane as one
+// 32-bit word.
+constexpr int kQMaxV = 16;
+
+template <int L>
+__global__ __launch_bounds__(kBlock) void limb_quantize_rows_vec_kernel(
+    const float* __restrict__ x, int64_t rows, int64_t n, int nv,
+    int8_t* __restrict__ digits, float* __restrict__ scales, int32_t* __restrict__ dsum) {
+    const int lane = threadIdx.x & (HM_WAVE - 1);
+    const int64_t r = (int64_t)blockIdx.x * (kBlock / HM_WAVE) + threadIdx.x / HM_WAVE;
+    if (r >= rows) return;
+    const float4* xr = reinterpret_cast<const float4*>(x + r * n);
+    float4 v[kQMaxV];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kQMaxV; ++i) {
+        if (i < nv) {
+            v[i] = xr[lane + HM_WAVE * i];
+            amax = fmaxf(fmaxf(amax, fmaxf(fabsf(v[i].x), fabsf(v[i].y))),
+                         fmaxf(fabsf(v[i].z), fabsf(v[i].w)));
+        }
+    }
+    amax = hm_wave_max_dpp(amax);
+    const float range = (float)hm_limb_range(L);
+    const float inv = amax > 0.0f ? __fdiv_rn(range, amax) : 0.0f;
+    int dl[L];
+#pragma unroll
+    for (int l = 0; l < L; ++l) dl[l] = 0;
+#pragma unroll
+    for (int i = 0; i < kQMaxV; ++i) {
+        if (i < nv) {
+            int d0[L], d1[L], d2[L], d3[L];
+            hm_digits<L>(hm_fixed_point(v[i].x, inv, range), d0);
+            hm_digits<L>(hm_fixed_point(v[i].y, inv, range), d1);
+            hm_digits<L>(hm_fixed_point(v[i].z, inv, range), d2);
+            hm_digits<L>(hm_fixed_point(v[i].w, inv, range), d3);
+#pragma unroll
+            for (int l = 0; l < L; ++l) {
+                const uint32_t word = (uint32_t)(d0[l] & 255) | ((uint32_t)(d1[l] & 255) << 8) |
+                                      ((uint32_t)(d2[l] & 255) << 16) | ((uint32_t)(d3[l] & 255) << 24);
+                reinterpret_cast<uint32_t*>(digits + ((int64_t)l * rows + r) * n)[lane + HM_WAVE * i] = word;
+                dl[l] += d0[l] + d1[l] + d2[l] + d3[l];
+            }
+        }
+    }
+#pragma unroll
+    for (int l = 0; l < L; ++l) {
+        const int s = hm_wave_sum_dpp(dl[l]);
         if (lane == 0 && dsum) dsum[(int64_t)l * rows + r] = s;
     }
     if (lane == 0) scales[r] = amax > 0.0f ? __fdiv_rn(amax, range) : 0.0f;
@@ -445,6 +500,17 @@ int hm_launch_quantize_rows(const float* x, int64_t rows, int64_t n, int32_t lim
                             hipStream_t stream) {
     if (rows == 0) return HM_OK;
     const dim3 grid((unsigned)((rows + 3) / 4));
+    const int64_t nv = n / 256;
+    if (n % 256 == 0 && nv >= 1 && nv <= kQMaxV && (uintptr_t)x % 16 == 0 && (uintptr_t)digits % 4 == 0) {
+        switch (limbs) {
+        case 1: hipLaunchKernelGGL(limb_quantize_rows_vec_kernel<1>, grid, dim3(kBlock), 0, stream, x, rows, n, (int)nv, digits, scales, dsum); break;
+        case 2: hipLaunchKernelGGL(limb_quantize_rows_vec_kernel<2>, grid, dim3(kBlock), 0, stream, x, rows, n, (int)nv, digits, scales, dsum); break;
+        case 3: hipLaunchKernelGGL(limb_quantize_rows_vec_kernel<3>, grid, dim3(kBlock), 0, stream, x, rows, n, (int)nv, digits, scales, dsum); break;
+        default: return HM_ERR_INVALID;
+        }
+        HM_LAUNCHED();
+        return HM_OK;
+    }
     switch (limbs) {
     case 1: hipLaunchKernelGGL(limb_quantize_rows_kernel<1>, grid, dim3(kBlock), 0, stream, x, rows, n, digits, scales, dsum); break;
     case 2: hipLaunchKernelGGL(limb_quantize_rows_kernel<2>, grid, dim3(kBlock), 0, stream, x, rows, n, digits, scales, dsum); break;
@@ -475,8 +541,8 @@ int64_t hm_max_tiles(int64_t pairs, int64_t experts, int64_t tile_m) {
 // record events between them.  xdig/xscale/xdsum come from
 // hm_launch_quantize_rows over all tokens; zf is scratch: [R x I] floats of
 // z on the generic path, [2 x R x I] floats of g and u on the MFMA path.
-// gate/up quantises Z in its epilogue with the same digit count as X; down
-// reads Z digits from either gate/up path.
+// The MFMA gate/up path quantises Z (swiglu_quant_kernel) with the same
+// digit count as X; down reads Z digits from either gate/up path.
 bool hm_use_mfma_gateup(const hm_layer* layer, int32_t lx, int32_t lz, bool force_generic) {
     return !force_generic && lx == lz &&
            hm_mfma_gateup_ok(layer->hidden, layer->intermediate, layer->experts, lx);

@@ -692,14 +692,33 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// z = silu(g) * u and its fixed-point digits, one wave per 128-column
-// segment of a grouped row (lane: columns 2*lane, 2*lane+1).  The segment
-// max gives the step: inv = range / max|z|, digits of rint(z * inv); the
-// segment scale max|z| / range and the digit sums go out beside them.
-// The same arithmetic as zquant_generic_kernel over the z of
-// gateup_generic_kernel.
+// z = silu(g) * u and its fixed-point digits: one half-wave per 128-column
+// segment of a grouped row (lane: columns 4*(lane%32) .. +3 of segment
+// 2*wave_id + lane/32).  The segment max gives the step: inv = range /
+// max|z|, digits of rint(z * inv); the segment scale max|z| / range and the
+// digit sums go out beside them.  The same arithmetic as
+// zquant_generic_kernel over the z of gateup_generic_kernel.
 // ---------------------------------------------------------------------------
 constexpr int kSqThreads = 256;
+
+// Max / integer sum over each 32-lane half of the wave (both halves at once).
+__device__ __forceinline__ float half_wave_max(float v) {
+    const float r = hm_row16_max(v);
+    const int lane = threadIdx.x & (HM_WAVE - 1);
+    const int b = __builtin_bit_cast(int, r);
+    const float a0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    const float a1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    const float a2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+    const float a3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    return lane < 32 ? fmaxf(a0, a1) : fmaxf(a2, a3);
+}
+__device__ __forceinline__ int half_wave_sum(int v) {
+    const int r = hm_row16_sum(v);
+    const int lane = threadIdx.x & (HM_WAVE - 1);
+    const int s0 = __builtin_amdgcn_readlane(r, 0) + __builtin_amdgcn_readlane(r, 16);
+    const int s1 = __builtin_amdgcn_readlane(r, 32) + __builtin_amdgcn_readlane(r, 48);
+    return lane < 32 ? s0 : s1;
+}
 
 template <int L>
 __global__ __launch_bounds__(kSqThreads) void swiglu_quant_kernel(
@@ -710,35 +729,44 @@ __global__ __launch_bounds__(kSqThreads) void swiglu_quant_kernel(
     __syncthreads();
     const int lane = threadIdx.x & (HM_WAVE - 1);
     const int nbz = I / kZBlock;
-    const int seg = blockIdx.x * (kSqThreads / HM_WAVE) + (int)(threadIdx.x / HM_WAVE);
-    if (seg >= R * nbz) return;
+    const int pair = blockIdx.x * (kSqThreads / HM_WAVE) + (int)(threadIdx.x / HM_WAVE);
+    if (2 * pair >= R * nbz) return;
+    // a wave's two segments; an odd total leaves the last wave's upper half
+    // on a repeat of its lower segment (computed, not stored)
+    const int seg_raw = 2 * pair + (lane >> 5);
+    const bool store = seg_raw < R * nbz;
+    const int seg = store ? seg_raw : 2 * pair;
     const int row = seg / nbz, b = seg % nbz;
-    const int64_t off = (int64_t)row * I + b * kZBlock + 2 * lane;
-    const float2 g = *reinterpret_cast<const float2*>(gin + off);
-    const float2 u = *reinterpret_cast<const float2*>(uin + off);
-    float s0, s1;
-    if (__all(fabsf(g.x) < 88.0f && fabsf(g.y) < 88.0f)) {
-        s0 = hm_silu_small_t(g.x, s_exp2);
-        s1 = hm_silu_small_t(g.y, s_exp2);
+    const int64_t off = (int64_t)row * I + b * kZBlock + 4 * (lane & 31);
+    const float4 g = *reinterpret_cast<const float4*>(gin + off);
+    const float4 u = *reinterpret_cast<const float4*>(uin + off);
+    float sv[4];
+    const float gv[4] = {g.x, g.y, g.z, g.w};
+    if (__all(fabsf(g.x) < 88.0f && fabsf(g.y) < 88.0f && fabsf(g.z) < 88.0f && fabsf(g.w) < 88.0f)) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[i] = hm_silu_small_t(gv[i], s_exp2);
     } else {
-        s0 = hm_silu_t(g.x, s_exp2);
-        s1 = hm_silu_t(g.y, s_exp2);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[i] = hm_silu_t(gv[i], s_exp2);
     }
-    const float z0 = __fmul_rn(s0, u.x), z1 = __fmul_rn(s1, u.y);
-    const float amax = hm_wave_max_dpp(fmaxf(fabsf(z0), fabsf(z1)));
+    const float z[4] = {__fmul_rn(sv[0], u.x), __fmul_rn(sv[1], u.y), __fmul_rn(sv[2], u.z),
+                        __fmul_rn(sv[3], u.w)};
+    const float amax = half_wave_max(fmaxf(fmaxf(fabsf(z[0]), fabsf(z[1])), fmaxf(fabsf(z[2]), fabsf(z[3]))));
     const float range = (float)hm_limb_range(L);
     const float inv = amax > 0.0f ? __fdiv_rn(range, amax) : 0.0f;
-    int d0[L], d1[L];
-    hm_digits<L>(hm_fixed_point(z0, inv, range), d0);
-    hm_digits<L>(hm_fixed_point(z1, inv, range), d1);
+    int d[4][L];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hm_digits<L>(hm_fixed_point(z[i], inv, range), d[i]);
 #pragma unroll
     for (int l = 0; l < L; ++l) {
-        const uint16_t pair = (uint16_t)((d0[l] & 255) | ((d1[l] & 255) << 8));
-        *reinterpret_cast<uint16_t*>(zdig + (int64_t)l * R * I + off) = pair;
-        const int sum = hm_wave_sum_dpp(d0[l] + d1[l]);
-        if (lane == 0) zdsum[((int64_t)l * R + row) * nbz + b] = sum;
+        const uint32_t word = (uint32_t)(d[0][l] & 255) | ((uint32_t)(d[1][l] & 255) << 8) |
+                              ((uint32_t)(d[2][l] & 255) << 16) | ((uint32_t)(d[3][l] & 255) << 24);
+        if (store) *reinterpret_cast<uint32_t*>(zdig + (int64_t)l * R * I + off) = word;
+        const int sum = half_wave_sum(d[0][l] + d[1][l] + d[2][l] + d[3][l]);
+        if (store && (lane & 31) == 0) zdsum[((int64_t)l * R + row) * nbz + b] = sum;
     }
-    if (lane == 0) zscale[(int64_t)row * nbz + b] = amax > 0.0f ? __fdiv_rn(amax, range) : 0.0f;
+    if (store && (lane & 31) == 0)
+        zscale[(int64_t)row * nbz + b] = amax > 0.0f ? __fdiv_rn(amax, range) : 0.0f;
 }
 
 int persistent_grid() {
@@ -770,9 +798,9 @@ int launch_gateup(const hm_layer* layer, const int8_t* xdig, const float* xscale
                        layer->scale, layer->zero_point, counts, offsets, perm_tokens, (int)R,
                        gout, uout);
     HM_LAUNCHED();
-    const int64_t segs = R * (I / kZBlock);
+    const int64_t pairs = (R * (I / kZBlock) + 1) / 2;
     const int64_t per_block = kSqThreads / HM_WAVE;
-    hipLaunchKernelGGL(swiglu_quant_kernel<L>, dim3((unsigned)((segs + per_block - 1) / per_block)),
+    hipLaunchKernelGGL(swiglu_quant_kernel<L>, dim3((unsigned)((pairs + per_block - 1) / per_block)),
                        dim3(kSqThreads), 0, stream, gout, uout, (int)R, (int)I, zdig, zscale, zdsum);
     HM_LAUNCHED();
     return HM_OK;

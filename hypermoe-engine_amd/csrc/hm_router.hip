@@ -696,13 +696,22 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(
         const int64_t w4 = width >> 2;
         for (int64_t i = tid; i < w4; i += kBlock) {
             float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            for (int r = 0; r < top_k; ++r) {
-                const float4 v = reinterpret_cast<const float4*>(y + srow[r] * width)[i];
-                const float wv = sw[r];
-                acc.x = __fadd_rn(acc.x, __fmul_rn(wv, v.x));
-                acc.y = __fadd_rn(acc.y, __fmul_rn(wv, v.y));
-                acc.z = __fadd_rn(acc.z, __fmul_rn(wv, v.z));
-                acc.w = __fadd_rn(acc.w, __fmul_rn(wv, v.w));
+            for (int r0 = 0; r0 < top_k; r0 += 8) {
+                // eight rows' loads in flight, then the adds in ascending order
+                float4 v[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q)
+                    if (r0 + q < top_k) v[q] = reinterpret_cast<const float4*>(y + srow[r0 + q] * width)[i];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    if (r0 + q < top_k) {
+                        const float wv = sw[r0 + q];
+                        acc.x = __fadd_rn(acc.x, __fmul_rn(wv, v[q].x));
+                        acc.y = __fadd_rn(acc.y, __fmul_rn(wv, v[q].y));
+                        acc.z = __fadd_rn(acc.z, __fmul_rn(wv, v[q].z));
+                        acc.w = __fadd_rn(acc.w, __fmul_rn(wv, v[q].w));
+                    }
+                }
             }
             if (residual) {
                 const float4 rv = reinterpret_cast<const float4*>(residual + t * width)[i];
