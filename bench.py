@@ -140,6 +140,8 @@ def main():
     from hmoe.block import DeviceExpertLayer, MoEBlock
 
     cfg = synth.CONFIGS[args.workload]
+    if cfg.layers > 1:
+        return run_stack(args, cfg)
     T, H, E, I, k = cfg.tokens, cfg.hidden, cfg.experts, cfg.inter, cfg.top_k
     q = args.quiet
     log(f"[bench] workload {cfg.name}: T={T} H={H} E={E} I={I} k={k} int8={cfg.int8} "
@@ -346,6 +348,119 @@ def main():
         "cpu_baseline": cpu, "parity": parity,
     }
     print(json.dumps(line), flush=True)
+
+
+def run_stack(args, cfg):
+    """C5: the 48-layer stack (RMSNorm + MoE block + residual per layer, all
+    experts resident): a `tokens`-token prefill, then DECODE_STEPS single-token
+    decode steps, each step's output feeding the next (the decode step is
+    captured once as a HIP graph and replayed).  One bench step = the whole
+    job; `value` = (prefill tokens + decode steps) / job time."""
+    import numpy as np
+    import torch
+    from hmoe import synth
+    from hmoe.stack import build_stack
+    decode_steps = 128
+    q = args.quiet
+    T, H, E, I, k = cfg.tokens, cfg.hidden, cfg.experts, cfg.inter, cfg.top_k
+    log(f"[bench] workload {cfg.name}: {cfg.layers} layers, prefill T={T}, {decode_steps} decode "
+        f"steps, H={H} E={E} I={I} k={k} limbs={args.limbs}", q)
+    torch.cuda.set_device(0)
+    t0 = time.time()
+    stack = build_stack(cfg, limbs=args.limbs,
+                        log=lambda l: log(f"[bench] layer {l + 1}/{cfg.layers} resident "
+                                          f"({time.time() - t0:.0f}s)", q or (l + 1) % 8))
+    resident = sum(l.packed.numel() for l in stack.layers)
+    h_prefill = torch.from_numpy(synth.raw_hidden(cfg.seed, T, H)).cuda()
+    h_tok = torch.from_numpy(synth.raw_hidden(cfg.seed + 1, 1, H)).cuda()
+    torch.cuda.synchronize()
+    log(f"[bench] setup {time.time() - t0:.1f}s, {resident / 2**30:.1f} GiB of experts resident", q)
+
+    # the decode step as a graph: static input -> stack -> copy back into the input
+    static_in = h_tok.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        stack.launch(static_in)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            out = stack.launch(static_in)
+            static_in.copy_(out)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    # the prefill needs its own buffers (the stack re-plans per token count)
+    prefill_stack = build_prefill_view(stack)
+
+    def job():
+        prefill_stack.launch(h_prefill)
+        static_in.copy_(h_tok)
+        for _ in range(decode_steps):
+            g.replay()
+
+    for _ in range(args.warmup):
+        job()
+    torch.cuda.synchronize()
+    stack.check_status()
+    prefill_stack.check_status()
+    log(f"[bench] warmup {args.warmup} done", q)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    torch.cuda.synchronize()
+    ev[0].record()
+    for _ in range(args.steps):
+        prefill_stack.launch(h_prefill)
+    ev[1].record()
+    for _ in range(args.steps):
+        static_in.copy_(h_tok)
+        for _ in range(decode_steps):
+            g.replay()
+    ev[2].record()
+    torch.cuda.synchronize()
+    prefill_ms = ev[0].elapsed_time(ev[1]) / args.steps
+    decode_ms = ev[1].elapsed_time(ev[2]) / args.steps
+    job_ms = prefill_ms + decode_ms
+    stack.check_status()
+    prefill_stack.check_status()
+    # per-layer times from one eager pass of each shape with events between layers
+    lev = [torch.cuda.Event(enable_timing=True) for _ in range(cfg.layers + 1)]
+    prefill_stack.launch(h_prefill, events=lev)
+    torch.cuda.synchronize()
+    per_prefill = [lev[i].elapsed_time(lev[i + 1]) for i in range(cfg.layers)]
+    stack.launch(h_tok.clone(), events=lev)
+    torch.cuda.synchronize()
+    per_decode = [lev[i].elapsed_time(lev[i + 1]) for i in range(cfg.layers)]
+    log(f"[bench] prefill {prefill_ms:.3f} ms, {decode_steps} decode steps {decode_ms:.3f} ms", q)
+    tokens = T + decode_steps
+    line = {
+        "metric": METRIC, "value": round(tokens / (job_ms / 1e3), 1), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(job_ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": cfg.name, "layers": cfg.layers, "prefill_tokens": T,
+                   "decode_steps": decode_steps, "hidden": H, "experts": E, "intermediate": I,
+                   "top_k": k, "weights": "int8", "limbs": args.limbs,
+                   "experts_resident_bytes": int(resident)},
+        "launch": "prefill eager, decode step as one HIP graph (all layers) replayed",
+        "prefill_ms": round(prefill_ms, 4),
+        "prefill_tokens_per_s": round(T / (prefill_ms / 1e3), 1),
+        "decode_ms_per_token": round(decode_ms / decode_steps, 5),
+        "decode_tokens_per_s": round(decode_steps / (decode_ms / 1e3), 1),
+        "per_layer_ms": {"prefill_mean": round(float(np.mean(per_prefill)), 5),
+                         "prefill_max": round(float(np.max(per_prefill)), 5),
+                         "decode_mean": round(float(np.mean(per_decode)), 5),
+                         "decode_max": round(float(np.max(per_decode)), 5)},
+        "roofline": None, "cpu_baseline": None,
+        "note": "per-layer rooflines and the CPU baseline are reported by the single-layer "
+                "workloads (C3-1 decode, C4 prefill)",
+    }
+    print(json.dumps(line), flush=True)
+
+
+def build_prefill_view(stack):
+    """A second executor over the same resident layers (its own buffers, so
+    the captured decode step's buffers stay untouched)."""
+    from hmoe.stack import MoEStack
+    return MoEStack(stack.layers, stack.router_w, stack.top_k, eps=stack.eps,
+                    limbs=stack.limbs, flags=stack.flags)
 
 
 if __name__ == "__main__":
