@@ -149,7 +149,12 @@ def main():
     t0 = time.time()
     payload, scale, zp = synth.expert_layer(cfg.seed, 0, E, H, I, cfg.int8,
                                             threads=min(16, os.cpu_count() or 1))
-    raw = synth.raw_hidden(cfg.seed, T, H)
+    # Decode-size steps rotate through a pool of distinct token batches so
+    # that consecutive steps select different experts: the weights a step
+    # streams are not the ones the previous step left in the 256 MB
+    # Infinity Cache.  A prefill batch already touches every expert.
+    pool = 1 if T >= 256 else 16
+    raw = synth.raw_hidden(cfg.seed, T * pool, H)
     w = synth.router_weights(cfg.seed, 0, H, E)
     torch.cuda.set_device(0)
     lib = capi.load()
@@ -158,7 +163,9 @@ def main():
     d_raw = torch.from_numpy(raw).cuda()
     gamma = torch.ones(H, dtype=torch.float32, device="cuda")
     d_h = torch.empty_like(d_raw)
-    capi.call("hm_rmsnorm", d_raw.data_ptr(), gamma.data_ptr(), d_h.data_ptr(), T, H, 1e-6, stream)
+    capi.call("hm_rmsnorm", d_raw.data_ptr(), gamma.data_ptr(), d_h.data_ptr(), T * pool, H, 1e-6,
+              stream)
+    batches = [d_h[i * T:(i + 1) * T] for i in range(pool)]
     if cfg.skew:
         bias = synth.zipf_bias(cfg.seed, E)
         d_h[:, -1] = 1.0
@@ -187,27 +194,30 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    for _ in range(args.warmup):
-        block.launch(d_h, d_w)
+    for i in range(max(args.warmup, pool)):
+        block.launch(batches[i % pool], d_w)
     torch.cuda.synchronize()
     log(f"[bench] warmup {args.warmup} done", q)
 
     # Optionally one step captured as a HIP graph (the block's kernels only;
     # no memset or copy nodes) and replayed; the replayed result must equal
     # the eager one.
+    # (one graph per pool batch).
     graph = None
     if args.graph:
-        ref_out = block.launch(d_h, d_w)["out"].clone()
         try:
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                block.launch(d_h, d_w)
-            for _ in range(2):
-                g.replay()
-                torch.cuda.synchronize()
-                if not torch.equal(block._io_bufs["out"], ref_out):
-                    raise RuntimeError("graph replay differs from the eager launch")
-            graph = g
+            graph = []
+            for b in batches:
+                ref_out = block.launch(b, d_w)["out"].clone()
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    block.launch(b, d_w)
+                for _ in range(2):
+                    g.replay()
+                    torch.cuda.synchronize()
+                    if not torch.equal(block._io_bufs["out"], ref_out):
+                        raise RuntimeError("graph replay differs from the eager launch")
+                graph.append(g)
         except Exception as ex:  # noqa: BLE001 -- report and time eagerly
             log(f"[bench] graph capture unavailable ({ex}); timing eager launches", q)
             graph = None
@@ -218,9 +228,9 @@ def main():
     capi.call("hm_event_record", ev_start, stream)
     for i in range(args.steps):
         if graph is not None:
-            graph.replay()
+            graph[i % pool].replay()
         else:
-            block.launch(d_h, d_w)
+            block.launch(batches[i % pool], d_w)
     capi.call("hm_event_record", ev_stop, stream)
     torch.cuda.synchronize()
     ms = C.c_float()
@@ -230,7 +240,7 @@ def main():
     # a second pass with the stage events recorded inside every step: the
     # per-stage times and the dominant kernel's launch duration
     for i in range(args.steps):
-        block.launch(d_h, d_w, events=stage_ev[i])
+        block.launch(batches[i % pool], d_w, events=stage_ev[i])
     torch.cuda.synchronize()
     names = ["route", "permute", "quantize", "gate_up", "down", "combine"]
     stage = {n: 0.0 for n in names}
@@ -241,10 +251,12 @@ def main():
     log(f"[bench] timed {args.steps} steps: {ms_per_step:.4f} ms/step", q)
 
     # one checked call: routing stats + parity of a token sample
-    res = block.execute_batch(d_h, d_w)
+    res = block.execute_batch(batches[0], d_w)
     counts = res.counts
-    unique = int((counts > 0).sum())
-    h_host = d_h.cpu().numpy()
+    # distinct experts per step, averaged over the pool
+    unique = float(np.mean([int((block.execute_batch(b, d_w).counts > 0).sum())
+                            for b in batches]))
+    h_host = batches[0].cpu().numpy()
     out = res.output.cpu().numpy()
     tokens_per_s = T / (ms_per_step / 1e3)
 
@@ -341,7 +353,8 @@ def main():
         "config": {"workload": cfg.name, "tokens": T, "hidden": H, "experts": E,
                    "intermediate": I, "top_k": k, "weights": "int8" if cfg.int8 else "fp32",
                    "skewed_routing": cfg.skew, "limbs": args.limbs if cfg.int8 else None,
-                   "unique_experts": unique, "max_expert_rows": int(counts.max())},
+                   "unique_experts": unique, "max_expert_rows": int(counts.max()),
+                   "input_batches": pool},
         "launch": "hip_graph_replay" if graph is not None else "eager",
         "roofline": roof, "layer_roofline": layer,
         "stages_ms": {n: round(v, 5) for n, v in stage.items()},

@@ -97,7 +97,7 @@ size_t plan_block(const hm_layer* L, int64_t T, int32_t k, int32_t lx, int32_t l
     const int64_t nb = (I + 127) / 128;
     Carve c(base);
     BlockPlan q{};
-    q.route_ws = c.take<char>(hm_route_workspace_bytes(T, E));
+    q.route_ws = c.take<char>(hm_route_workspace_bytes(T, L->hidden, E));
     q.permute_ws = c.take<char>(hm_permute_workspace_bytes(T, k, E));
     q.ids = c.take<uint32_t>((size_t)P);
     q.scores = c.take<float>((size_t)P);
@@ -190,24 +190,44 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
                     p.perm_weights, p.slots, p.permute_ws, stream);
     if (rc || (rc = mark(2))) return rc;
     const int32_t* counts = p.counts;
+    // The gate/up stage's two events are taken by its own kernels (start of
+    // the first, end of the last) rather than by markers around them.
+    const bool kernel_timed = ev[3] && ev[4];
+    auto gate_up = [&](auto&& launch) -> int {
+        if (!kernel_timed) {
+            const int r = mark(3);
+            if (r) return r;
+        } else {
+            hm_timer() = {ev[3], ev[4]};
+        }
+        const int r = launch();
+        hm_timer() = {nullptr, nullptr};
+        return r ? r : (kernel_timed ? HM_OK : mark(4));
+    };
     if (gemv) {
-        if ((rc = mark(3))) return rc;
-        rc = hm_launch_gateup_gemv(layer, hidden, counts, p.offsets, p.perm_tokens, P, p.zf, s);
-        if (rc || (rc = mark(4))) return rc;
+        rc = gate_up([&] {
+            return hm_launch_gateup_gemv(layer, hidden, counts, p.offsets, p.perm_tokens, P,
+                                         p.zf, s);
+        });
+        if (rc) return rc;
         rc = hm_launch_down_gemv(layer, p.zf, counts, p.offsets, P, p.y, s);
     } else if (layer->dtype == HM_DTYPE_INT8) {
         rc = hm_launch_quantize_rows(hidden, tokens, H, limbs_x, p.xdig, p.xscale, p.xdsum, s);
-        if (rc || (rc = mark(3))) return rc;
-        rc = hm_launch_gateup_i8(layer, limbs_x, limbs_z, p.xdig, p.xscale, p.xdsum, tokens,
-                                 counts, p.offsets, p.perm_tokens, P, p.zdig, p.zscale,
-                                 p.zdsum, p.zf, generic, s);
-        if (rc || (rc = mark(4))) return rc;
+        if (rc) return rc;
+        rc = gate_up([&] {
+            return hm_launch_gateup_i8(layer, limbs_x, limbs_z, p.xdig, p.xscale, p.xdsum,
+                                       tokens, counts, p.offsets, p.perm_tokens, P, p.zdig,
+                                       p.zscale, p.zdsum, p.zf, generic, s);
+        });
+        if (rc) return rc;
         rc = hm_launch_down_i8(layer, limbs_x, limbs_z, counts, p.offsets, P, p.zdig,
                                p.zscale, p.zdsum, p.y, generic, s);
     } else {
-        if ((rc = mark(3))) return rc;
-        rc = hm_launch_gateup_f32(layer, hidden, counts, p.offsets, p.perm_tokens, P, p.zf, s);
-        if (rc || (rc = mark(4))) return rc;
+        rc = gate_up([&] {
+            return hm_launch_gateup_f32(layer, hidden, counts, p.offsets, p.perm_tokens, P,
+                                        p.zf, s);
+        });
+        if (rc) return rc;
         rc = hm_launch_down_f32(layer, counts, p.offsets, P, p.zf, p.y, s);
     }
     if (rc || (rc = mark(5))) return rc;

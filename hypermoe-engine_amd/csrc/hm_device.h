@@ -4,6 +4,7 @@
 // integer-limb fixed-point split used by the INT8 expert GEMMs.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -28,6 +29,23 @@ void hm_record_hip_error(hipError_t e);
     do { if (!(cond)) return HM_ERR_INVALID; } while (0)
 
 static inline hipStream_t hm_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+// Stage timing.  While a block call times a stage, `start` and `stop` hold
+// two events: the stage's first kernel is launched with hipExtLaunchKernelGGL
+// taking `start` at its own start, the last one `stop` at its own end, so
+// the pair brackets the stage's kernels and none of the gaps around them
+// (hipEventRecord between launches adds a marker packet and its gap).  Both
+// are null otherwise and HM_STAGE_LAUNCH is an ordinary launch.  Per host
+// thread (hm_runtime.hip), like the reference's single-caller backends.
+struct hm_stage_timer {
+    hipEvent_t start;
+    hipEvent_t stop;
+};
+hm_stage_timer& hm_timer();
+#define HM_STAGE_LAUNCH(first, last, kernel, grid, block, lds, stream, ...)                  \
+    hipExtLaunchKernelGGL(kernel, grid, block, lds, stream,                                 \
+                          (first) ? hm_timer().start : nullptr,                             \
+                          (last) ? hm_timer().stop : nullptr, 0, __VA_ARGS__)
 
 // ---------------------------------------------------------------------------
 // Wave64 reductions (all 64 lanes must be active).

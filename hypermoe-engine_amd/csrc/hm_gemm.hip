@@ -566,13 +566,13 @@ int hm_launch_gateup_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int
     const int64_t nb = (I + kZBlock - 1) / kZBlock;
     const unsigned g_gu = (unsigned)((R * I + kBlock - 1) / kBlock);
     const unsigned g_zq = (unsigned)((R * nb + 3) / 4);
-#define HM_GU(LV)                                                                       \
-    hipLaunchKernelGGL(gateup_generic_kernel<LV>, dim3(g_gu), dim3(kBlock), 0, stream,   \
-                       xdig, xscale, tokens, H, I, E, packed, layer->scale,              \
-                       layer->zero_point, offsets, perm_tokens, R, zf)
-#define HM_ZQ(LV)                                                                       \
-    hipLaunchKernelGGL(zquant_generic_kernel<LV>, dim3(g_zq), dim3(kBlock), 0, stream,   \
-                       zf, R, I, zdig, zscale, zdsum)
+#define HM_GU(LV)                                                                         \
+    HM_STAGE_LAUNCH(true, false, gateup_generic_kernel<LV>, dim3(g_gu), dim3(kBlock), 0, stream, \
+                    xdig, xscale, tokens, H, I, E, packed, layer->scale, layer->zero_point,   \
+                    offsets, perm_tokens, R, zf)
+#define HM_ZQ(LV)                                                                         \
+    HM_STAGE_LAUNCH(false, true, zquant_generic_kernel<LV>, dim3(g_zq), dim3(kBlock), 0, stream, \
+                    zf, R, I, zdig, zscale, zdsum)
     switch (lx) {
     case 1: HM_GU(1); break;
     case 2: HM_GU(2); break;
@@ -625,8 +625,8 @@ int hm_launch_gateup_f32(const hm_layer* layer, const float* hidden, const int32
     const int64_t H = layer->hidden, I = layer->intermediate, E = layer->experts;
     if (R == 0) return HM_OK;
     const dim3 g1((unsigned)hm_max_tiles(R, E, kF32Tile), (unsigned)((I + kF32Tile - 1) / kF32Tile));
-    hipLaunchKernelGGL(gateup_f32_kernel, g1, dim3(kBlock), 0, stream, hidden, H, I, E,
-                       static_cast<const float*>(layer->packed), counts, offsets, perm_tokens, zf);
+    HM_STAGE_LAUNCH(true, true, gateup_f32_kernel, g1, dim3(kBlock), 0, stream, hidden, H, I, E,
+                    static_cast<const float*>(layer->packed), counts, offsets, perm_tokens, zf);
     HM_LAUNCHED();
     return HM_OK;
 }

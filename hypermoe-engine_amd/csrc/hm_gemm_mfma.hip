@@ -792,16 +792,17 @@ int launch_gateup(const hm_layer* layer, const int8_t* xdig, const float* xscale
     if (tokens > INT_MAX || R > INT_MAX || R * (I / kZBlock) > INT_MAX) return HM_ERR_OVERFLOW;
     float* gout = gu;
     float* uout = gu + R * I;
-    hipLaunchKernelGGL(gateup_mfma_kernel<L>, dim3((unsigned)persistent_grid()), dim3(kThreads), 0,
-                       stream, xdig, xscale, xdsum, (int)tokens, (int)layer->hidden, (int)I,
-                       (int)layer->experts, static_cast<const int8_t*>(layer->packed),
-                       layer->scale, layer->zero_point, counts, offsets, perm_tokens, (int)R,
-                       gout, uout);
+    HM_STAGE_LAUNCH(true, false, gateup_mfma_kernel<L>, dim3((unsigned)persistent_grid()),
+                    dim3(kThreads), 0, stream, xdig, xscale, xdsum, (int)tokens,
+                    (int)layer->hidden, (int)I, (int)layer->experts,
+                    static_cast<const int8_t*>(layer->packed), layer->scale, layer->zero_point,
+                    counts, offsets, perm_tokens, (int)R, gout, uout);
     HM_LAUNCHED();
     const int64_t pairs = (R * (I / kZBlock) + 1) / 2;
     const int64_t per_block = kSqThreads / HM_WAVE;
-    hipLaunchKernelGGL(swiglu_quant_kernel<L>, dim3((unsigned)((pairs + per_block - 1) / per_block)),
-                       dim3(kSqThreads), 0, stream, gout, uout, (int)R, (int)I, zdig, zscale, zdsum);
+    HM_STAGE_LAUNCH(false, true, swiglu_quant_kernel<L>,
+                    dim3((unsigned)((pairs + per_block - 1) / per_block)), dim3(kSqThreads), 0,
+                    stream, gout, uout, (int)R, (int)I, zdig, zscale, zdsum);
     HM_LAUNCHED();
     return HM_OK;
 }

@@ -199,10 +199,10 @@ int launch_gemv(const float* x_src, const int32_t* perm_tokens, int64_t K, int64
                 float* out, hipStream_t s) {
     const int64_t per_wg = (kGemvThreads / 64) * (GATEUP ? kNPW : kRowsPerWave);
     const dim3 grid((unsigned)(N / per_wg), (unsigned)slots);
-    hipLaunchKernelGGL((gemv_w8_kernel<P, GATEUP>), grid, dim3(kGemvThreads), 0, s, x_src,
-                       perm_tokens, K, N, L->experts,
-                       static_cast<const int8_t*>(L->packed), L->hidden, L->intermediate,
-                       L->scale, L->zero_point, counts, offsets, out);
+    // (the timer, when armed, brackets the gate/up launch)
+    HM_STAGE_LAUNCH(true, true, (gemv_w8_kernel<P, GATEUP>), grid, dim3(kGemvThreads), 0, s,
+                    x_src, perm_tokens, K, N, L->experts, static_cast<const int8_t*>(L->packed),
+                    L->hidden, L->intermediate, L->scale, L->zero_point, counts, offsets, out);
     HM_LAUNCHED();
     return HM_OK;
 }

@@ -362,6 +362,20 @@ __global__ __launch_bounds__(64) void router_partial_kernel(
     }
 }
 
+// Whether the bound above settles float(s_n) given the block-sum chain's
+// result a and the magnitude sums SA (sa), R (sr), P (sp).
+__device__ __forceinline__ bool block_sums_settle(double a, double sa, double sr, double sp,
+                                                  int64_t hidden) {
+    const double u = 0x1p-53;
+    const double n = (double)hidden, bw = (double)(hidden / kNB);
+    const double infl = 1.0 + 4.0 * n * u;  // the magnitude sums' own rounding
+    const double b0 = (u * ((bw + 1.0) * sa + 2.0 * sr) +
+                       2.0 * u * u * (n * (sr + sa) + 1.01 * (bw * bw + n * n) * sp)) * infl;
+    const double bc = (b0 * (1.0 + 0x1p-40) + u * fabs(a)) * (1.0 + 0x1p-50);
+    const double lo = a - bc, hi = a + bc;
+    return isfinite(lo) && isfinite(hi) && __float_as_uint((float)lo) == __float_as_uint((float)hi);
+}
+
 // One logit from its block partials (see above), or from the sequential
 // chain when the bound does not settle the float.
 // pp: this logit's B_0 (part + t*kNB*3*E + e); component c of block j is at
@@ -392,16 +406,7 @@ __device__ __forceinline__ float certified_logit(const double* __restrict__ pp,
             sp += qv[i];
         }
     }
-    const double u = 0x1p-53;
-    const double n = (double)hidden, bw = (double)(hidden / kNB);
-    const double infl = 1.0 + 4.0 * n * u;  // the magnitude sums' own rounding
-    const double b0 = (u * ((bw + 1.0) * sa + 2.0 * sr) +
-                       2.0 * u * u * (n * (sr + sa) + 1.01 * (bw * bw + n * n) * sp)) * infl;
-    const double bc = (b0 * (1.0 + 0x1p-40) + u * fabs(a)) * (1.0 + 0x1p-50);
-    const double lo = a - bc, hi = a + bc;
-    const bool ok = !force_seq && isfinite(lo) && isfinite(hi) &&
-                    __float_as_uint((float)lo) == __float_as_uint((float)hi);
-    if (ok) return (float)a;
+    if (!force_seq && block_sums_settle(a, sa, sr, sp, hidden)) return (float)a;
     double acc = 0.0;
     for (int64_t k = 0; k < hidden; ++k)
         acc = __builtin_fma((double)hrow[k], (double)wcol[k * experts], acc);
@@ -553,6 +558,392 @@ __global__ __launch_bounds__(kBlock) void router_select_partial_kernel(
         }
     }
     select_token<EPL>(v, valid, lane, wave, t, experts, top_k, flags, ids, scores, status, seq_lds);
+}
+
+// ---------------------------------------------------------------------------
+// A2 logits for prefill batches on the FP64 matrix cores, certified.
+//
+// router_mfma_kernel sums the exact products p_k = h_k w_k (double) with
+// v_mfma_f64_16x16x4_f64 in an order of its own: K is cut into `splits`
+// ranges (one per workgroup layer of the grid) and each range into chunks
+// of 16, of which MFMA step j takes k = 4g + j for the four k-slots g.  Any
+// summation tree of n terms whose additions round to nearest errs by at
+// most gamma_{n-1} SA, SA = sum |p_k| <= ||h|| ||w_e|| (Cauchy-Schwarz), and
+// so does the reference's sequential chain; the kernel therefore also
+// returns the squared norms of h's rows and W's columns per range.
+// router_select_split_kernel adds the ranges (ascending), bounds
+//   |S' - s_n| <= 3 gamma_n ||h|| ||w_e||
+// (one gamma for the reference, two for the matrix-core sums to cover an
+// internal rounding mode of up to 2u), inflated for the norms' own
+// rounding, and keeps float(S') when both ends of S' +- bound round to the
+// same float; otherwise (about 0.5% of the logits for N(0,1) rows and
+// N(0, 0.02) weights at H = 2048, and every non-finite case) the lane runs
+// the reference's chain.
+//
+// Workgroup: 4 waves x 16 tokens, 64 experts as 4 interleaved MFMA chains
+// (chain q holds experts e0 + 4n + q, n = 0..15), so that each W load is a
+// float4 of 4 consecutive experts (one per chain) and each h load a float4
+// of 4 consecutive k (one per MFMA step).  Lane (g, i) = (lane/16, lane%16)
+// supplies A = h[t0 + i][k] and B = W[k][e0 + 4i + q]; its result register
+// r holds D[g + 4r][i] = the logit of token t0 + g + 4r, expert e0 + 4i + q.
+// Needs E % 64 == 0, H % (16 * splits) == 0, 16-byte aligned h and w.
+// ---------------------------------------------------------------------------
+constexpr int kMT = 64;   // tokens per workgroup
+constexpr int kME = 64;   // experts per workgroup
+constexpr int kMaxSplits = 8;
+constexpr int kMS = 4;    // LDS ring stages of one 16-k chunk each
+constexpr int kMW = 4096; // W bytes per stage: [16 k][64 e] floats
+constexpr int kMH = 4096; // h bytes per stage: [64 t][16 k] floats
+typedef double hm_double4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void router_mfma_kernel(
+    const float* __restrict__ h, const float* __restrict__ w, int tokens, int hidden,
+    int experts, int ksplit, double* __restrict__ part, float* __restrict__ wt,
+    double* __restrict__ hn2, double* __restrict__ wn2) {
+    __shared__ __attribute__((aligned(1024))) char ring[kMS][kMW + kMH];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, i = lane & 15;
+    const int eblocks = experts / kME;
+    const int tblocks = (tokens + kMT - 1) / kMT;
+    const int eb = blockIdx.x % eblocks;
+    const int tb = (blockIdx.x / eblocks) % tblocks;
+    const int sp = blockIdx.x / (eblocks * tblocks);
+    const int t0 = tb * kMT + 16 * wave;
+    const int e0 = eb * kME;
+    const int tok = t0 + i;
+    const bool live = tok < tokens;
+    const int kb = sp * ksplit;
+    const int nk = ksplit / 16;
+    // Each wave stages a quarter of a chunk: W rows 4*wave .. +3 (1 KB, lane
+    // l: row 4*wave + l/16, experts 4*(l%16) .. +3) and its own 16 tokens' h
+    // (1 KB, lane l: token 16*wave + l/4, k 4*(l%4) .. +3); rows of tokens
+    // past the end repeat the last token and are masked below.
+    const float* wsrc = w + (int64_t)(kb + 4 * wave + (lane >> 4)) * experts + e0 + 4 * (lane & 15);
+    const int htok = min(t0 + (lane >> 2), tokens - 1);
+    const float* hsrc = h + (int64_t)htok * hidden + kb + 4 * (lane & 3);
+    auto issue = [&](int slot, int c) {
+        dma16(wsrc + (int64_t)16 * c * experts, ring[slot] + 1024 * wave);
+        dma16(hsrc + 16 * c, ring[slot] + kMW + 1024 * wave);
+    };
+    const bool wnorm = tb == 0 && wave == 0;  // one wave per (range, expert block)
+    hm_double4 acc[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc[q] = hm_double4{0.0, 0.0, 0.0, 0.0};
+    double hsq = 0.0, wsq[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int c = 0; c < kMS - 1; ++c)
+        if (c < nk) issue(c, c);
+    for (int c = 0; c < nk; ++c) {
+        const int slot = c % kMS;
+        if (c + kMS - 2 < nk) wait_vmcnt<(kMS - 2) * 2>();
+        else wait_vmcnt<0>();
+        lds_barrier();  // chunk c landed for every wave; chunk c-1 fully read
+        if (c + kMS - 1 < nk) issue((c + kMS - 1) % kMS, c + kMS - 1);
+        const char* st = ring[slot];
+        if (tb == 0) {
+            // the first token block also writes the chunk of W transposed:
+            // lane l -> expert e0 + 16*wave + l/4, k 4*(l%4) .. +3
+            const int ex = 16 * wave + (lane >> 2), kq = 4 * (lane & 3);
+            const float* sw = reinterpret_cast<const float*>(st) + kq * kME + ex;
+            *reinterpret_cast<float4*>(wt + (int64_t)(e0 + ex) * hidden + kb + 16 * c + kq) =
+                make_float4(sw[0], sw[kME], sw[2 * kME], sw[3 * kME]);
+        }
+        const float4 a = *reinterpret_cast<const float4*>(st + kMW + (16 * wave + i) * 64 + 16 * g);
+        float4 wv[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            wv[j] = *reinterpret_cast<const float4*>(st + (4 * g + j) * 256 + 16 * i);
+        const double ad[4] = {live ? (double)a.x : 0.0, live ? (double)a.y : 0.0,
+                              live ? (double)a.z : 0.0, live ? (double)a.w : 0.0};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            hsq = __builtin_fma(ad[j], ad[j], hsq);
+            const double bd[4] = {(double)wv[j].x, (double)wv[j].y, (double)wv[j].z,
+                                  (double)wv[j].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(ad[j], bd[q], acc[q], 0, 0, 0);
+            // (every wave sums the squares, one writes them: a branch here
+            // splits the loop and costs more than the 16 FMAs)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) wsq[q] = __builtin_fma(bd[q], bd[q], wsq[q]);
+        }
+    }
+    // partial logits: register r of lane (g, i) holds D[g + 4r][i], i.e.
+    // token t0 + g + 4r, experts e0 + 4i .. +3
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int t = t0 + g + 4 * r;
+        if (t < tokens) {
+            double* o = part + ((int64_t)sp * tokens + t) * experts + e0 + 4 * i;
+            *reinterpret_cast<double2*>(o) = double2{acc[0][r], acc[1][r]};
+            *reinterpret_cast<double2*>(o + 2) = double2{acc[2][r], acc[3][r]};
+        }
+    }
+    // norms over this range: the four k-slots of a token / expert are the
+    // lanes i, i + 16, i + 32, i + 48
+    hsq += __shfl_xor(hsq, 16, HM_WAVE);
+    hsq += __shfl_xor(hsq, 32, HM_WAVE);
+    if (eb == 0 && g == 0 && live) hn2[(int64_t)sp * tokens + tok] = hsq;
+    if (wnorm) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            wsq[q] += __shfl_xor(wsq[q], 16, HM_WAVE);
+            wsq[q] += __shfl_xor(wsq[q], 32, HM_WAVE);
+        }
+        if (g == 0) {
+            double* o = wn2 + (int64_t)sp * experts + e0 + 4 * i;
+            *reinterpret_cast<double2*>(o) = double2{wsq[0], wsq[1]};
+            *reinterpret_cast<double2*>(o + 2) = double2{wsq[2], wsq[3]};
+        }
+    }
+}
+
+// Fallback chains of the split select.  A wave's uncertified logits are
+// taken kFN at a time: lane f < kFN runs the reference's chain (k
+// ascending) for the f-th of them, while the whole wave stages the next
+// kFK-long piece of their W columns (rows of the transposed copy the
+// matrix-core kernel wrote) and of the token's h row into LDS with 16-byte
+// DMA (double-buffered), so the chains wait on LDS rather than on one
+// global load per step.
+constexpr int kFK = 256;                        // k per staged piece
+constexpr int kFN = 2;                          // chains per round
+constexpr int kFBuf = (kFN + 1) * kFK * 4;      // one buffer: columns + h (3 KB)
+constexpr int kFDma = kFN + 1;                  // 16-byte DMA instructions per piece
+static_assert(kFK == 4 * HM_WAVE, "one 16-byte DMA per staged row piece");
+
+__device__ __forceinline__ void fallback_issue(char* buf, const float* __restrict__ hrow,
+                                               const float* __restrict__ wt, int64_t hidden,
+                                               int64_t k0, const int (&fe)[kFN], int lane) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this buffer's last reads are done
+    const int64_t k = min(k0 + 4 * lane, hidden - 4);  // past the end: unused
+#pragma unroll
+    for (int f = 0; f < kFN; ++f) dma16(wt + (int64_t)fe[f] * hidden + k, buf + 4 * kFK * f);
+    dma16(hrow + k, buf + 4 * kFK * kFN);
+}
+
+// The idx-th set bit over the masks need[0..EPL) in (j, lane) order:
+// its lane and j.
+template <int EPL>
+__device__ __forceinline__ void locate_fallback(const unsigned long long (&need)[EPL], int idx,
+                                                int& owner, int& slot) {
+    int jj = 0;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        const int c = __popcll(need[j]);
+        if (jj == j && idx >= c) { idx -= c; jj = j + 1; }
+    }
+    unsigned long long m = need[0];
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) if (j == jj) m = need[j];
+    for (int b = 0; b < idx; ++b) m &= m - 1;
+    owner = __ffsll((long long)m) - 1;
+    slot = jj;
+}
+
+template <int EPL>
+__global__ __launch_bounds__(kBlock) void router_select_split_kernel(
+    const float* __restrict__ h, const float* __restrict__ wt, const double* __restrict__ part,
+    const double* __restrict__ hn2, const double* __restrict__ wn2, int64_t tokens,
+    int64_t hidden, int64_t experts, int splits, int32_t top_k, uint32_t flags,
+    float* __restrict__ logits, uint32_t* __restrict__ ids, float* __restrict__ scores,
+    int32_t* status) {
+    // per wave: experts floats for the sequential softmax sum, then two
+    // fallback buffers (kFBuf each, 16-byte aligned)
+    extern __shared__ __attribute__((aligned(16))) char dyn_lds[];
+    const int lane = threadIdx.x & (HM_WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / HM_WAVE);
+    const int64_t t = (int64_t)blockIdx.x * (kBlock / HM_WAVE) + wave;
+    if (t >= tokens) return;
+    const int64_t seq_stride = ((experts * 4 + 15) / 16) * 16;
+    float* seq_lds = reinterpret_cast<float*>(dyn_lds);  // indexed by wave * experts
+    char* fb = dyn_lds + (kBlock / HM_WAVE) * seq_stride + (int64_t)wave * 2 * kFBuf;
+    const double u = 0x1p-53;
+    const double n = (double)hidden;
+    const double gam = n * u / (1.0 - n * u);
+    // 3 gamma_n, times (1 + 4 gamma_n) for the norms' own rounding
+    const double cb = 3.0 * gam * (1.0 + 4.0 * gam) * (1.0 + 0x1p-30);
+    // (all loads of the range sums go out before the additions:
+    // unconditional loads from clamped ranges, so that no branch splits
+    // them from their uses)
+    double hv[kMaxSplits];
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplits; ++sp)
+        hv[sp] = hn2[(int64_t)min(sp, splits - 1) * tokens + t];
+    double hh = 0.0;
+#pragma unroll
+    for (int sp = 0; sp < kMaxSplits; ++sp)
+        if (sp < splits) hh += hv[sp];
+    const double hnorm = sqrt(hh);
+    float v[EPL];
+    bool valid[EPL];
+    unsigned long long need[EPL];
+    int total = 0;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        const int64_t e = lane + (int64_t)HM_WAVE * j;
+        valid[j] = e < experts;
+        bool nd = false;
+        v[j] = 0.0f;
+        if (valid[j]) {
+            double pa[kMaxSplits], pw[kMaxSplits];
+#pragma unroll
+            for (int sp = 0; sp < kMaxSplits; ++sp) {
+                const int64_t sc = min(sp, splits - 1);
+                pa[sp] = part[(sc * tokens + t) * experts + e];
+                pw[sp] = wn2[sc * experts + e];
+            }
+            double a = 0.0, ww = 0.0;
+#pragma unroll
+            for (int sp = 0; sp < kMaxSplits; ++sp) {
+                if (sp < splits) {
+                    a += pa[sp];
+                    ww += pw[sp];
+                }
+            }
+            const double bc = (cb * hnorm * sqrt(ww) + u * fabs(a)) * (1.0 + 0x1p-50);
+            const double lo = a - bc, hi = a + bc;
+            nd = !(isfinite(lo) && isfinite(hi) &&
+                   __float_as_uint((float)lo) == __float_as_uint((float)hi));
+            v[j] = (float)a;
+        }
+        need[j] = __ballot(nd);
+        total += __popcll(need[j]);
+    }
+    const float* hrow = h + t * hidden;
+    if (total > 0 && hidden % (kNB * 16) == 0) {
+        // Second level: the decode path's block form and its much tighter
+        // bound, two logits at a time, lane 32*half + j summing block j of
+        // the half's logit (b = H/32 terms, sequentially from +0) beside
+        // R_j and Q_j; the block sums are then chained in order.  Logits it
+        // settles leave the list; the rest take the full chain below.
+        const int half = lane >> 5, bj = lane & 31;
+        const int64_t bw = hidden / kNB;
+        bool left[EPL];
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) left[j] = (need[j] >> lane) & 1ull;
+        for (int done = 0; done < total; done += 2) {  // wave-uniform
+            const int idx = min(done + half, total - 1);
+            int owner, js;
+            locate_fallback<EPL>(need, idx, owner, js);
+            const int64_t e = owner + (int64_t)HM_WAVE * js;
+            const float* hp = hrow + bj * bw;
+            const float* wp = wt + e * hidden + bj * bw;
+            double acc = 0.0, rs = 0.0, qs = 0.0;
+            for (int64_t k0 = 0; k0 < bw; k0 += 16) {
+                float4 hv[4], wv[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    hv[q] = *reinterpret_cast<const float4*>(hp + k0 + 4 * q);
+                    wv[q] = *reinterpret_cast<const float4*>(wp + k0 + 4 * q);
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float hq[4] = {hv[q].x, hv[q].y, hv[q].z, hv[q].w};
+                    const float wq[4] = {wv[q].x, wv[q].y, wv[q].z, wv[q].w};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const double hk = (double)hq[r], wk = (double)wq[r];
+                        acc = __builtin_fma(hk, wk, acc);  // == acc + hk * wk
+                        rs += fabs(acc);
+                        qs = __builtin_fma(fabs(hk), fabs(wk), qs);
+                    }
+                }
+            }
+            double a = 0.0, sa = 0.0, sr = 0.0, sp = 0.0;
+            for (int j = 0; j < kNB; ++j) {
+                a += __shfl(acc, 32 * half + j, HM_WAVE);
+                sa += fabs(a);
+                sr += __shfl(rs, 32 * half + j, HM_WAVE);
+                sp += __shfl(qs, 32 * half + j, HM_WAVE);
+            }
+            const bool ok = block_sums_settle(a, sa, sr, sp, hidden);
+            // the owners of this pass's logits take the settled values
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+                const int o = __shfl(owner, 32 * hf, HM_WAVE);
+                const int jo = __shfl(js, 32 * hf, HM_WAVE);
+                const bool okh = __shfl((int)ok, 32 * hf, HM_WAVE) != 0;
+                const float vh = __shfl((float)a, 32 * hf, HM_WAVE);
+                if (okh && lane == o && (hf == 0 || done + 1 < total)) {
+#pragma unroll
+                    for (int j = 0; j < EPL; ++j) if (j == jo) { v[j] = vh; left[j] = false; }
+                }
+            }
+        }
+        total = 0;
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            need[j] = __ballot(left[j]);
+            total += __popcll(need[j]);
+        }
+    }
+    for (int done = 0; done < total; done += kFN) {  // wave-uniform
+        // the experts of fallbacks done .. done + kFN - 1 (in (j, lane)
+        // order; slots past the last repeat it)
+        int fe[kFN];
+        int owner[kFN], slot[kFN];
+#pragma unroll
+        for (int f = 0; f < kFN; ++f) {
+            locate_fallback<EPL>(need, min(done + f, total - 1), owner[f], slot[f]);
+            fe[f] = owner[f] + HM_WAVE * slot[f];
+        }
+        const int nf = min(kFN, total - done);
+        double acc = 0.0;
+        const int64_t pieces = (hidden + kFK - 1) / kFK;
+        fallback_issue(fb, hrow, wt, hidden, 0, fe, lane);
+        for (int64_t c = 0; c < pieces; ++c) {
+            char* cur = fb + (c & 1) * kFBuf;
+            if (c + 1 < pieces) {
+                fallback_issue(fb + ((c + 1) & 1) * kFBuf, hrow, wt, hidden, (c + 1) * kFK, fe,
+                               lane);
+                wait_vmcnt<kFDma>();
+            } else {
+                wait_vmcnt<0>();
+            }
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            const int kc = (int)min((int64_t)kFK, hidden - c * kFK);  // a multiple of 16
+            if (lane < nf) {
+                // 16 k per step; the next step's LDS reads go out before
+                // this step's dependent chain
+                const float4* c4 = reinterpret_cast<const float4*>(cur) + lane * (kFK / 4);
+                const float4* h4 = reinterpret_cast<const float4*>(cur + 4 * kFN * kFK);
+                float4 ha[4], wa[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) { ha[q] = h4[q]; wa[q] = c4[q]; }
+                for (int kk = 0; kk < kc; kk += 16) {
+                    const int nx = kk + 16 < kc ? (kk + 16) / 4 : kk / 4;
+                    float4 hb[4], wb[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) { hb[q] = h4[nx + q]; wb[q] = c4[nx + q]; }
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        acc = __builtin_fma((double)ha[q].x, (double)wa[q].x, acc);
+                        acc = __builtin_fma((double)ha[q].y, (double)wa[q].y, acc);
+                        acc = __builtin_fma((double)ha[q].z, (double)wa[q].z, acc);
+                        acc = __builtin_fma((double)ha[q].w, (double)wa[q].w, acc);
+                    }
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) { ha[q] = hb[q]; wa[q] = wb[q]; }
+                }
+            }
+        }
+        if (lane < nf && !isfinite(acc)) hm_status_or(status, HM_STATUS_NONFINITE_SCORE);
+#pragma unroll
+        for (int f = 0; f < kFN; ++f) {
+            const double r = __shfl(acc, f, HM_WAVE);
+            if (f < nf && lane == owner[f]) {
+#pragma unroll
+                for (int j = 0; j < EPL; ++j) if (j == slot[f]) v[j] = (float)r;
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < EPL; ++j)
+        if (valid[j] && logits) logits[t * experts + lane + HM_WAVE * j] = v[j];
+    select_token<EPL>(v, valid, lane, wave, t, experts, top_k, flags, ids, scores, status,
+                      seq_lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -778,19 +1169,40 @@ int hm_rmsnorm(const float* x, const float* gamma, float* y, int64_t rows,
     return HM_OK;
 }
 
-// Route workspace: the float logits [T x E].
-// Route workspace: the logits [T x E] floats, and for decode batches
-// (T <= kDecodeTokens) the block partials [T x E x kNB x 3] doubles after
-// them (8-byte aligned).
+// Route workspace: the logits [T x E] floats (rounded up to 256 bytes),
+// then for decode batches (T <= kDecodeTokens) the block partials
+// [T x E x kNB x 3] doubles, and for prefill batches with E % 64 == 0 the
+// matrix-core range partials [S x T x E] doubles, W transposed [E x H]
+// floats, row norms [S x T] and column norms [S x E] doubles
+// (S = prefill_splits).
 constexpr int64_t kDecodeTokens = 16;
 
 static size_t route_logits_bytes(int64_t tokens, int64_t experts) {
-    return ((size_t)tokens * (size_t)experts * sizeof(float) + 7) & ~(size_t)7;
+    return ((size_t)tokens * (size_t)experts * sizeof(float) + 255) & ~(size_t)255;
 }
 
-size_t hm_route_workspace_bytes(int64_t tokens, int64_t experts) {
-    if (tokens < 0 || experts <= 0) return 0;
-    if (tokens > kDecodeTokens) return (size_t)tokens * (size_t)experts * sizeof(float);
+// K ranges of the prefill logits: enough workgroups (>= 512) to give every
+// SIMD two waves; H must also be a multiple of 16 per range (the launcher
+// halves S until it is).
+static int prefill_splits(int64_t tokens, int64_t experts) {
+    const int64_t base = ((tokens + kMT - 1) / kMT) * (experts / kME);
+    int sp = 1;
+    while (sp < kMaxSplits && base * sp < 512) sp *= 2;
+    return sp;
+}
+
+size_t hm_route_workspace_bytes(int64_t tokens, int64_t hidden, int64_t experts) {
+    if (tokens < 0 || experts <= 0 || hidden <= 0) return 0;
+    if (tokens > kDecodeTokens) {
+        size_t b = route_logits_bytes(tokens, experts);
+        if (experts % kME == 0) {
+            const size_t sp = (size_t)prefill_splits(tokens, experts);
+            b += sp * ((size_t)tokens * (size_t)experts + (size_t)tokens + (size_t)experts) *
+                     sizeof(double) +
+                 (size_t)experts * (size_t)hidden * sizeof(float);
+        }
+        return b;
+    }
     return route_logits_bytes(tokens, experts) +
            (size_t)tokens * (size_t)experts * kNB * 3 * sizeof(double);
 }
@@ -834,6 +1246,37 @@ int hm_router_topk(const float* h, const float* w, int64_t tokens,
         return HM_OK;
     }
     const bool aligned = ((uintptr_t)h % 16 == 0) && ((uintptr_t)w % 16 == 0);
+    if (route_ws && !(flags & HM_EXEC_ROUTE_SEQUENTIAL) && aligned && experts % kME == 0 &&
+        hidden % 16 == 0 && hidden <= INT_MAX && tokens <= INT_MAX &&
+        (uintptr_t)route_ws % 16 == 0) {
+        // prefill: matrix-core range partials, then certify + select
+        int sp = prefill_splits(tokens, experts);
+        while (sp > 1 && hidden % (16 * sp) != 0) sp /= 2;
+        double* part = reinterpret_cast<double*>(static_cast<char*>(route_ws) +
+                                                 route_logits_bytes(tokens, experts));
+        float* wt = reinterpret_cast<float*>(part + (int64_t)sp * tokens * experts);
+        double* hn2 = reinterpret_cast<double*>(wt + experts * hidden);
+        double* wn2 = hn2 + (int64_t)sp * tokens;
+        const int64_t grid = ((tokens + kMT - 1) / kMT) * (experts / kME) * sp;
+        hipLaunchKernelGGL(router_mfma_kernel, dim3((unsigned)grid), dim3(256), 0,
+                           hm_stream(stream), h, w, (int)tokens, (int)hidden, (int)experts,
+                           (int)(hidden / sp), part, wt, hn2, wn2);
+        HM_LAUNCHED();
+        const size_t split_bytes =
+            (kBlock / HM_WAVE) * ((((size_t)experts * 4 + 15) / 16) * 16 + 2 * (size_t)kFBuf);
+#define HM_SELECTS(N)                                                                     \
+        hipLaunchKernelGGL(router_select_split_kernel<N>, sgrid, dim3(kBlock), split_bytes, \
+                           hm_stream(stream), h, wt, part, hn2, wn2, tokens, hidden, experts, \
+                           sp, top_k, flags, logits, ids, scores, status)
+        if (epl <= 1) HM_SELECTS(1);
+        else if (epl <= 2) HM_SELECTS(2);
+        else if (epl <= 4) HM_SELECTS(4);
+        else if (epl <= 8) HM_SELECTS(8);
+        else HM_SELECTS(16);
+#undef HM_SELECTS
+        HM_LAUNCHED();
+        return HM_OK;
+    }
     if (aligned && experts % kTE == 0 && hidden % kTK == 0) {
         const dim3 grid((unsigned)((tokens + kTT - 1) / kTT), (unsigned)(experts / kTE));
         hipLaunchKernelGGL(router_logits_tile_kernel, grid, dim3(256), 0, hm_stream(stream), h,

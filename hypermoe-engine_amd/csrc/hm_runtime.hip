@@ -7,6 +7,9 @@
 #include <string.h>
 
 static thread_local int tl_last_hip_error = 0;
+static thread_local hm_stage_timer tl_stage_timer = {nullptr, nullptr};
+
+hm_stage_timer& hm_timer() { return tl_stage_timer; }
 
 void hm_record_hip_error(hipError_t e) { tl_last_hip_error = static_cast<int>(e); }
 

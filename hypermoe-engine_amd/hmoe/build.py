@@ -39,6 +39,9 @@ HIP_FLAGS = [
 ]
 KERNEL_SOURCES = ["hm_runtime.hip", "hm_router.hip", "hm_gemm.hip", "hm_gemm_mfma.hip",
                   "hm_gemv.hip", "hm_block.hip"]
+# Per-source flags.  The FP64 router MFMAs keep their accumulators in VGPRs
+# (otherwise the compiler copies them to AGPRs and back on every K chunk).
+SOURCE_FLAGS = {"hm_router.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 HOST_SOURCES = ["hip_backend.cpp", "hip_tensor_backend.cpp", "moe_block.cpp"]
 
 KERNELS_SO = LIB / "libhm_kernels.so"
@@ -59,7 +62,7 @@ def _quiet_filter(text: str) -> str:
 
 
 def _compile_hip(src: Path, obj: Path) -> str:
-    cmd = [HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *HIP_FLAGS, *SOURCE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}")

@@ -65,7 +65,7 @@ SIGNATURES = {
     "hm_event_elapsed_ms": (c_i32, [C.POINTER(c_f32), vp, vp]),
     "hm_mem_info": (c_i32, [C.POINTER(c_sz), C.POINTER(c_sz)]),
     "hm_rmsnorm": (c_i32, [vp, vp, vp, c_i64, c_i64, c_f32, vp]),
-    "hm_route_workspace_bytes": (c_sz, [c_i64, c_i64]),
+    "hm_route_workspace_bytes": (c_sz, [c_i64, c_i64, c_i64]),
     "hm_router_topk": (c_i32, [vp, vp, c_i64, c_i64, c_i64, c_i32, c_u32, vp, vp, vp, vp, vp, vp]),
     "hm_permute_workspace_bytes": (c_sz, [c_i64, c_i32, c_i64]),
     "hm_permute": (c_i32, [vp, vp, c_i64, c_i32, c_i64, vp, vp, vp, vp, vp, vp, vp]),

@@ -68,10 +68,10 @@ typedef enum hm_status {
  * reference, not bit-identical to the limb arithmetic). */
 #define HM_EXEC_LIMBS 0x200u
 #define HM_GEMV_MAX_TOKENS 16
-/* Execution flag for hm_router_topk / hm_moe_block_forward: decode batches
- * (at most 16 tokens) compute every router logit with the reference's
- * sequential FP64 chain instead of certifying the parallel block sums (the
- * results are identical; the flag exercises the fallback). */
+/* Execution flag for hm_router_topk / hm_moe_block_forward: every router
+ * logit is computed with the reference's sequential FP64 chain instead of
+ * certifying the parallel sums (the results are identical; the flag
+ * exercises the fallback). */
 #define HM_EXEC_ROUTE_SEQUENTIAL 0x400u
 
 /* Expert weight dtypes (src/tensor/DType.hpp:9-14 numbering). */
@@ -117,11 +117,15 @@ int hm_rmsnorm(const float* x, const float* gamma, float* y, int64_t rows,
  * (score desc, expert id asc); optional renormalisation by the double sum of
  * the selected scores in rank order.  ids/scores are [tokens x top_k] in
  * rank order.  Bit-exact.  The logits go to logits_out, or, when it is NULL,
- * to `route_ws` (hm_route_workspace_bytes(tokens, experts) bytes).  With
- * route_ws given, batches of at most 16 tokens take the certified parallel
- * form of the logit sums (their block partials live in route_ws).  `flags`:
- * HM_ROUTE_* bits, optionally HM_EXEC_ROUTE_SEQUENTIAL. */
-size_t hm_route_workspace_bytes(int64_t tokens, int64_t experts);
+ * to `route_ws` (hm_route_workspace_bytes(tokens, hidden, experts) bytes, 16-byte
+ * aligned).  With route_ws given, the logit sums take a certified parallel
+ * form whose partials live in route_ws: FP64 block chains for batches of at
+ * most 16 tokens, FP64 matrix-core sums for larger batches when E % 64 == 0
+ * and H % 16 == 0.  A logit whose float the error bound does not settle is
+ * recomputed by the sequential chain, so the results are those of the
+ * sequential form.  `flags`: HM_ROUTE_* bits, optionally
+ * HM_EXEC_ROUTE_SEQUENTIAL. */
+size_t hm_route_workspace_bytes(int64_t tokens, int64_t hidden, int64_t experts);
 int hm_router_topk(const float* h, const float* w, int64_t tokens,
                    int64_t hidden, int64_t experts, int32_t top_k,
                    uint32_t flags, uint32_t* ids, float* scores,
@@ -249,7 +253,10 @@ typedef struct hm_block_io {
      * src/profiling/GpuEventQueue.hpp:17-69): HM_BLOCK_EVENTS hipEvent_t
      * handles recorded on `stream` at the stage boundaries
      * [start, routed, permuted, quantised, gate/up done, down done,
-     * combined].  NULL = no recording. */
+     * combined].  Events 3 and 4 bracket the gate/up kernels themselves:
+     * they are taken at the first kernel's start and the last kernel's end
+     * (hipExtLaunchKernelGGL), so their span is the stage's kernel time.
+     * NULL = no recording. */
     void* const* events;
 } hm_block_io;
 #define HM_BLOCK_EVENTS 7

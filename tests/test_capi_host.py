@@ -84,7 +84,10 @@ def test_workspace_and_layer_sizes():
     # scratch floats: z [P x I] on the generic path, g and u [2 x P x I] on the MFMA path
     assert a > 0 and a - b == 4096 * 8 * 768 * 4, "MFMA path holds g and u, generic path z"
     assert lib.hm_moe_block_workspace_bytes(C.byref(layer), 0, 8, 2, 2, 0) == 0
-    assert lib.hm_route_workspace_bytes(4096, 128) == 4096 * 128 * 4
+    # logits, then 4 K ranges of FP64 partials and norms, then W transposed
+    assert lib.hm_route_workspace_bytes(4096, 2048, 128) == (
+        4096 * 128 * 4 + 4 * (4096 * 128 + 4096 + 128) * 8 + 128 * 2048 * 4)
+    assert lib.hm_route_workspace_bytes(100, 2048, 96) == (100 * 96 * 4 + 255) // 256 * 256
 
 
 def test_argument_validation_without_device():

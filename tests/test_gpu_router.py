@@ -17,7 +17,7 @@ pytestmark = pytest.mark.gpu
 def run_router(dev, h, w, k, flags):
     T, H = h.shape
     E = w.shape[1]
-    ws = dev.empty(dev.lib.hm_route_workspace_bytes(T, E), np.uint8)
+    ws = dev.empty(dev.lib.hm_route_workspace_bytes(T, H, E), np.uint8)
     ids = dev.empty((T, k), np.int32)
     scores = dev.empty((T, k), np.float32)
     logits = dev.empty((T, E), np.float32)
@@ -139,12 +139,14 @@ def test_router_nonfinite_sets_status(dev):
     assert rc == -3  # HMO_E_RUNTIME
 
 
-def test_router_decode_sequential_flag_same_bits(dev):
-    """Decode batches certify parallel block sums of the logits; forcing the
-    reference's sequential chain for every logit gives the same bits."""
+def test_router_sequential_flag_same_bits(dev):
+    """Decode batches certify parallel block sums of the logits, prefill
+    batches FP64 matrix-core sums; forcing the reference's sequential chain
+    for every logit gives the same bits."""
     from hmoe import capi
-    for T, H, E in ((1, 2048, 128), (16, 2048, 128), (5, 512, 64)):
-        print(f"[gpu] decode router sequential flag T={T} H={H} E={E}", flush=True)
+    for T, H, E in ((1, 2048, 128), (16, 2048, 128), (5, 512, 64), (40, 2048, 128),
+                    (300, 2048, 128), (100, 512, 64), (70, 64, 192)):
+        print(f"[gpu] router sequential flag T={T} H={H} E={E}", flush=True)
         rng = np.random.default_rng(T + H)
         h = O.rmsnorm(rng.standard_normal((T, H)).astype(np.float32), np.ones(H, np.float32))
         w = (0.02 * rng.standard_normal((H, E))).astype(np.float32)
@@ -157,13 +159,18 @@ def test_router_decode_sequential_flag_same_bits(dev):
         assert_bitexact(a["scores"], b["scores"], "scores")
 
 
-def test_router_decode_uncertifiable_logits(dev):
+@pytest.mark.parametrize("T,E", [(2, 4), (2, 64), (40, 64)])
+def test_router_uncertifiable_logits(dev, T, E):
     """Logits the bound cannot settle fall back to the sequential chain:
     an exact float midpoint (1 + 2^-24 ties to even: 1.0) and an exact
-    cancellation (the sequential sum ends at +0, the interval spans -0/+0)."""
-    H, E = 64, 4
-    h = np.zeros((2, H), np.float32)
+    cancellation (the sequential sum ends at +0, the interval spans -0/+0).
+    T = 2: decode block sums; T = 40, E = 64: matrix-core sums."""
+    H = 64
+    rng = np.random.default_rng(T + E)
+    h = np.zeros((T, H), np.float32)
     w = np.zeros((H, E), np.float32)
+    h[2:] = rng.standard_normal((T - 2, H)).astype(np.float32)
+    w[:, 4:] = (0.02 * rng.standard_normal((H, E - 4))).astype(np.float32)
     h[0, 0], h[0, 1] = 1.0, 2.0 ** -24
     w[0, :], w[1, :] = 1.0, 1.0            # expert logits 1 + 2^-24 -> 1.0
     h[1, 0], h[1, 5] = 1.0, 1.0
@@ -180,11 +187,12 @@ def test_router_decode_uncertifiable_logits(dev):
     assert_bitexact(g["scores"], scores, "scores")
 
 
-def test_router_decode_nonfinite_sets_status(dev):
-    """A non-finite logit on the decode path (it always takes the
+@pytest.mark.parametrize("T,E", [(1, 8), (1, 64), (20, 64)])
+def test_router_parallel_nonfinite_sets_status(dev, T, E):
+    """A non-finite logit on the certified paths (it always takes the
     sequential chain) sets HM_STATUS_NONFINITE_SCORE."""
-    H, E = 64, 8
-    h = np.ones((1, H), np.float32)
+    H = 64
+    h = np.ones((T, H), np.float32)
     w = np.full((H, E), 0.01, np.float32)
     w[3, 5] = np.inf
     g = run_router(dev, h, w, 2, 3)
