@@ -27,20 +27,27 @@ constexpr int kRowsPerWave = 4;   // weight rows per wave
 constexpr int kNPW = kRowsPerWave / 2;  // gate/up: output columns per wave
 
 // The slot-th expert (ascending id) with a non-zero group; -1 if none.
-// Every wave computes it redundantly from `counts` (E <= 1024).
+// Every wave computes it redundantly from `counts` (E <= 1024); the loads
+// of all 64-expert groups go out together (two groups at E = 128).
 __device__ int hm_active_expert(const int32_t* __restrict__ counts, int64_t experts, int slot) {
     const int lane = threadIdx.x & 63;
+    constexpr int kGroups = 16;
+    int cnt[kGroups];
+#pragma unroll
+    for (int b = 0; b < kGroups; ++b) {
+        const int64_t e = (int64_t)b * 64 + lane;
+        cnt[b] = e < experts ? counts[e] : 0;
+    }
     int seen = 0;
-    for (int64_t base = 0; base < experts; base += 64) {
-        const int64_t e = base + lane;
-        const bool nz = e < experts && counts[e] > 0;
-        const unsigned long long m = __ballot(nz);
+#pragma unroll
+    for (int b = 0; b < kGroups; ++b) {
+        const unsigned long long m = __ballot(cnt[b] > 0);
         const int c = __popcll(m);
         if (slot < seen + c) {
             // position of the (slot - seen)-th set bit
             unsigned long long mm = m;
             for (int i = 0; i < slot - seen; ++i) mm &= mm - 1;
-            return (int)(base + __ffsll((long long)mm) - 1);
+            return b * 64 + __ffsll((long long)mm) - 1;
         }
         seen += c;
     }
@@ -120,6 +127,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_w8_kernel(
     const int64_t n0 = GATEUP ? ((int64_t)blockIdx.x * kWaves + wave) * kNPW
                               : ((int64_t)blockIdx.x * kWaves + wave) * kRowsPerWave;
     int8_t* lds = wl[wave];
+    const int64_t g0 = offsets[e];
+    const int rows = counts[e];
     // weights -> LDS
 #pragma unroll
     for (int j = 0; j < kRowsPerWave; ++j) {
@@ -132,14 +141,12 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_w8_kernel(
             if (k < K) dma16(row + k, lds + (j * P + p) * 1024);
         }
     }
-    const int64_t g0 = offsets[e];
-    const int rows = counts[e];
-    wait_vmcnt<0>();
+    // each row's activations are loaded before the wait: the first row's
+    // stream in beside the weights
     for (int r = 0; r < rows; ++r) {
         const int64_t src = GATEUP ? (int64_t)perm_tokens[g0 + r] : g0 + r;
         const float* xr = x_src + src * K;
         float x[P][16];
-        float xs = 0.0f;
 #pragma unroll
         for (int p = 0; p < P; ++p) {
             const int64_t k = 1024 * p + 16 * lane;
@@ -150,9 +157,13 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_w8_kernel(
                 x[p][4 * i] = v.x; x[p][4 * i + 1] = v.y;
                 x[p][4 * i + 2] = v.z; x[p][4 * i + 3] = v.w;
             }
+        }
+        if (r == 0) wait_vmcnt<0>();  // the weights (and these rows) have landed
+        float xs = 0.0f;
+#pragma unroll
+        for (int p = 0; p < P; ++p)
 #pragma unroll
             for (int i = 0; i < 16; ++i) xs += x[p][i];
-        }
         float xv[1] = {xs};
         const float xsum = wave_reduce_many<1>(xv);
         // one output at a time (gate and up rows of one n together): the
