@@ -30,6 +30,10 @@ int hm_launch_gateup_gemv(const hm_layer* L, const float* hidden, const int32_t*
                           float* z, hipStream_t s);
 int hm_launch_down_gemv(const hm_layer* L, const float* z, const int32_t* counts,
                         const int32_t* offsets, int64_t pairs, float* y, hipStream_t s);
+int hm_route_permute_decode(const float* h, const float* w, int64_t tokens, int64_t hidden,
+                            int64_t experts, int32_t top_k, uint32_t flags, uint32_t* ids,
+                            float* scores, int32_t* status, void* route_ws,
+                            const hm_decode_fusion* fused, void* stream);
 
 namespace {
 
@@ -73,6 +77,7 @@ struct BlockPlan {
     float* zf;
     float* y;
     int32_t* status;
+    int32_t* counters;  // decode: the fused select's completion counter
 };
 
 // Decode-size INT8 blocks take the W8A32 GEMV kernels.
@@ -109,6 +114,7 @@ size_t plan_block(const hm_layer* L, int64_t T, int32_t k, int32_t lx, int32_t l
     q.status = c.take<int32_t>(1);
     if (use_gemv(L, T, flags)) {
         q.zf = c.take<float>((size_t)P * I);
+        q.counters = c.take<int32_t>(1);
     } else if (L->dtype == HM_DTYPE_INT8) {
         q.xdig = c.take<int8_t>((size_t)lx * T * H);
         q.xscale = c.take<float>((size_t)T);
@@ -182,13 +188,25 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
     }
     const int64_t E = layer->experts, H = layer->hidden;
     const int64_t P = tokens * top_k;
-    rc = hm_router_topk(hidden, router_w, tokens, H, E, top_k,
-                        route_flags & (HM_ROUTE_SOFTMAX | HM_ROUTE_RENORM | HM_EXEC_ROUTE_SEQUENTIAL), p.ids,
-                        p.scores, nullptr, status, p.route_ws, stream);
-    if (rc || (rc = mark(1))) return rc;
-    rc = hm_permute(p.ids, p.scores, tokens, top_k, E, p.counts, p.offsets, p.perm_tokens,
-                    p.perm_weights, p.slots, p.permute_ws, stream);
-    if (rc || (rc = mark(2))) return rc;
+    const uint32_t route_bits =
+        route_flags & (HM_ROUTE_SOFTMAX | HM_ROUTE_RENORM | HM_EXEC_ROUTE_SEQUENTIAL);
+    // decode: the grouping is fused into the router's select (one launch
+    // fewer)
+    const bool fuse = gemv && H % 32 == 0 && E <= 1024 && top_k <= 64 && P <= 1024;
+    if (fuse) {
+        const hm_decode_fusion f = {p.counters, 1, p.counts, p.offsets, p.perm_tokens,
+                                    p.perm_weights, p.slots};
+        rc = hm_route_permute_decode(hidden, router_w, tokens, H, E, top_k, route_bits, p.ids,
+                                     p.scores, status, p.route_ws, &f, stream);
+        if (rc || (rc = mark(1)) || (rc = mark(2))) return rc;
+    } else {
+        rc = hm_router_topk(hidden, router_w, tokens, H, E, top_k, route_bits, p.ids, p.scores,
+                            nullptr, status, p.route_ws, stream);
+        if (rc || (rc = mark(1))) return rc;
+        rc = hm_permute(p.ids, p.scores, tokens, top_k, E, p.counts, p.offsets, p.perm_tokens,
+                        p.perm_weights, p.slots, p.permute_ws, stream);
+        if (rc || (rc = mark(2))) return rc;
+    }
     const int32_t* counts = p.counts;
     // The gate/up stage's two events are taken by its own kernels (start of
     // the first, end of the last) rather than by markers around them.

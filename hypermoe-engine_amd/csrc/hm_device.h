@@ -47,6 +47,19 @@ hm_stage_timer& hm_timer();
                           (first) ? hm_timer().start : nullptr,                             \
                           (last) ? hm_timer().stop : nullptr, 0, __VA_ARGS__)
 
+// A decode step (T <= 16) fuses the grouping into the router's select
+// kernel; its last workgroup is found with a device counter that the
+// step's first kernel zeroes.
+struct hm_decode_fusion {
+    int32_t* counters;   // [0]: the select's completion counter
+    int n_counters;
+    int32_t* counts;
+    int32_t* offsets;
+    int32_t* perm_tokens;
+    float* perm_weights;
+    int32_t* slots;
+};
+
 // ---------------------------------------------------------------------------
 // Wave64 reductions (all 64 lanes must be active).
 // ---------------------------------------------------------------------------

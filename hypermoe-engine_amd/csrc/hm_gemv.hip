@@ -108,25 +108,17 @@ __device__ __forceinline__ void bytes_to_float(uint32_t d, float* f) {
 // silu(g)*u.
 // DOWN: rows j are down rows n0+j; the inputs are z[g, :]; output y[g, n].
 template <int P, bool GATEUP>
-__global__ __launch_bounds__(kGemvThreads) void gemv_w8_kernel(
+__device__ __forceinline__ void gemv_body(
     const float* __restrict__ x_src, const int32_t* __restrict__ perm_tokens, int64_t K,
-    int64_t N, int64_t experts, const int8_t* __restrict__ packed, int64_t hidden,
-    int64_t inter, const float* __restrict__ scale, const int32_t* __restrict__ zp,
+    int64_t N, const int8_t* __restrict__ packed, int64_t hidden, int64_t inter,
+    const float* __restrict__ scale, const int32_t* __restrict__ zp,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
-    float* __restrict__ out) {
+    float* __restrict__ out, const unsigned long long* s_exp2, int8_t* lds, int e, int lane,
+    int wave) {
     constexpr int kWaves = kGemvThreads / 64;
-    __shared__ __attribute__((aligned(1024))) int8_t wl[kWaves][kRowsPerWave * P * 1024];
-    __shared__ unsigned long long s_exp2[32];
-    if (GATEUP) hm_load_exp2_table(s_exp2);
-    __syncthreads();
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int e = hm_active_expert(counts, experts, (int)blockIdx.y);
-    if (e < 0) return;
     const int8_t* ebase = packed + (int64_t)e * 3 * hidden * inter;
     const int64_t n0 = GATEUP ? ((int64_t)blockIdx.x * kWaves + wave) * kNPW
                               : ((int64_t)blockIdx.x * kWaves + wave) * kRowsPerWave;
-    int8_t* lds = wl[wave];
     const int64_t g0 = offsets[e];
     const int rows = counts[e];
     // weights -> LDS
@@ -202,6 +194,26 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_w8_kernel(
             }
         }
     }
+}
+
+template <int P, bool GATEUP>
+__global__ __launch_bounds__(kGemvThreads) void gemv_w8_kernel(
+    const float* __restrict__ x_src, const int32_t* __restrict__ perm_tokens, int64_t K,
+    int64_t N, int64_t experts, const int8_t* __restrict__ packed, int64_t hidden,
+    int64_t inter, const float* __restrict__ scale, const int32_t* __restrict__ zp,
+    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
+    float* __restrict__ out) {
+    constexpr int kWaves = kGemvThreads / 64;
+    __shared__ __attribute__((aligned(1024))) int8_t wl[kWaves][kRowsPerWave * P * 1024];
+    __shared__ unsigned long long s_exp2[32];
+    if (GATEUP) hm_load_exp2_table(s_exp2);
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int e = hm_active_expert(counts, experts, (int)blockIdx.y);
+    if (e < 0) return;
+    gemv_body<P, GATEUP>(x_src, perm_tokens, K, N, packed, hidden, inter, scale, zp, counts,
+                         offsets, out, s_exp2, wl[wave], e, lane, wave);
 }
 
 template <int P, bool GATEUP>

@@ -319,10 +319,14 @@ constexpr int kPK = 64;  // k per LDS chunk of a block
 
 __global__ __launch_bounds__(64) void router_partial_kernel(
     const float* __restrict__ h, const float* __restrict__ w, int hidden, int experts,
-    double* __restrict__ part) {
+    double* __restrict__ part, int32_t* __restrict__ zero_ctr, int n_zero) {
     __shared__ double s_h[kPK];                                        // broadcast reads
     __shared__ __attribute__((aligned(1024))) float s_w[kPK][HM_WAVE];  // [k][lane]
     const int lane = threadIdx.x;
+    // completion counters of the later kernels of a fused decode step start
+    // at zero (they run after this kernel has finished)
+    if (zero_ctr && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0)
+        for (int i = lane; i < n_zero; i += HM_WAVE) zero_ctr[i] = 0;
     const int j = blockIdx.x, t = blockIdx.z;
     const int e0 = blockIdx.y * HM_WAVE;
     const int e = e0 + lane;
@@ -530,34 +534,127 @@ __global__ __launch_bounds__(kBlock) void router_select_kernel(
     select_token<EPL>(v, valid, lane, wave, t, experts, top_k, flags, ids, scores, status, seq_lds);
 }
 
+// The stable counting sort of permute_count/scatter for at most
+// kSmallPairs pairs, by one workgroup (kBlock threads): counts and offsets
+// from an LDS histogram and a block scan, each pair's rank among the
+// earlier pairs of its expert by a scan of the ids in LDS.  Ids past the
+// expert count (left behind by a routing failure the status word reports)
+// are treated as the last expert so that every position stays in range.
+constexpr int kSmallPairs = 1024;
+
+__device__ void permute_small(const uint32_t* __restrict__ ids, const float* __restrict__ scores,
+                              int pairs, int top_k, int experts, int32_t* __restrict__ counts,
+                              int32_t* __restrict__ offsets, int32_t* __restrict__ perm_tokens,
+                              float* __restrict__ perm_weights, int32_t* __restrict__ slots) {
+    __shared__ int s_cnt[1024];
+    __shared__ int s_off[1024];
+    __shared__ int s_ids[kSmallPairs];
+    __shared__ int s_wsum[kBlock / HM_WAVE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < experts; i += kBlock) s_cnt[i] = 0;
+    __syncthreads();
+    for (int p = tid; p < pairs; p += kBlock) {
+        const uint32_t e = ids[p];
+        const int ec = e < (uint32_t)experts ? (int)e : experts - 1;
+        s_ids[p] = ec;
+        atomicAdd(&s_cnt[ec], 1);
+    }
+    __syncthreads();
+    // exclusive scan over experts: thread tid owns experts 4*tid .. +3
+    int v[4], tot = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int e = 4 * tid + q;
+        v[q] = e < experts ? s_cnt[e] : 0;
+        tot += v[q];
+    }
+    int incl = tot;
+#pragma unroll
+    for (int sft = 1; sft < 64; sft <<= 1) {
+        const int o = __shfl_up(incl, sft, 64);
+        if (lane >= sft) incl += o;
+    }
+    if (lane == 63) s_wsum[wave] = incl;
+    __syncthreads();
+    int base = incl - tot;
+    for (int wv = 0; wv < wave; ++wv) base += s_wsum[wv];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int e = 4 * tid + q;
+        if (e < experts) {
+            s_off[e] = base;
+            counts[e] = v[q];
+            offsets[e] = base;
+            if (e == experts - 1) offsets[experts] = base + v[q];
+        }
+        base += v[q];
+    }
+    __syncthreads();
+    for (int p = tid; p < pairs; p += kBlock) {
+        const int e = s_ids[p];
+        int rank = 0;
+        for (int q = 0; q < p; ++q) rank += s_ids[q] == e;
+        const int pos = s_off[e] + rank;
+        perm_tokens[pos] = p / top_k;
+        perm_weights[pos] = scores[p];
+        slots[p] = pos;
+    }
+}
+
 // Select over logits formed from the decode partials (and written to
-// `logits` too).
-template <int EPL>
+// `logits` too).  With PERMUTE the workgroup that finishes last (a device
+// counter, zeroed by router_partial_kernel) also sorts the pairs into
+// expert groups, which is hm_permute's result: one launch fewer per decode
+// step.
+template <int EPL, bool PERMUTE>
 __global__ __launch_bounds__(kBlock) void router_select_partial_kernel(
     const float* __restrict__ h, const float* __restrict__ w, const double* __restrict__ part,
     int64_t tokens, int64_t hidden, int64_t experts, int32_t top_k, uint32_t flags,
     float* __restrict__ logits, uint32_t* __restrict__ ids, float* __restrict__ scores,
-    int32_t* status) {
+    int32_t* status, int32_t* __restrict__ done_ctr, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ perm_tokens,
+    float* __restrict__ perm_weights, int32_t* __restrict__ slots) {
     extern __shared__ float seq_lds[];  // (kBlock/64) * experts floats
     const int lane = threadIdx.x & (HM_WAVE - 1);
     const int wave = threadIdx.x / HM_WAVE;
     const int64_t t = (int64_t)blockIdx.x * (kBlock / HM_WAVE) + wave;
-    if (t >= tokens) return;
     const bool force_seq = (flags & HM_EXEC_ROUTE_SEQUENTIAL) != 0;
-    float v[EPL];
-    bool valid[EPL];
+    if (t < tokens) {
+        float v[EPL];
+        bool valid[EPL];
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-        const int64_t e = lane + (int64_t)HM_WAVE * j;
-        valid[j] = e < experts;
-        v[j] = 0.0f;
-        if (valid[j]) {
-            v[j] = certified_logit(part + t * kNB * 3 * experts + e, h + t * hidden, w + e,
-                                   hidden, experts, force_seq, status);
-            logits[t * experts + e] = v[j];
+        for (int j = 0; j < EPL; ++j) {
+            const int64_t e = lane + (int64_t)HM_WAVE * j;
+            valid[j] = e < experts;
+            v[j] = 0.0f;
+            if (valid[j]) {
+                v[j] = certified_logit(part + t * kNB * 3 * experts + e, h + t * hidden, w + e,
+                                       hidden, experts, force_seq, status);
+                logits[t * experts + e] = v[j];
+            }
         }
+        select_token<EPL>(v, valid, lane, wave, t, experts, top_k, flags, ids, scores, status,
+                          seq_lds);
     }
-    select_token<EPL>(v, valid, lane, wave, t, experts, top_k, flags, ids, scores, status, seq_lds);
+    if constexpr (PERMUTE) {
+        if (gridDim.x > 1) {
+            // (the device-scope fences write back and invalidate this XCD's
+            // L2: only taken when several workgroups share the batch)
+            __shared__ int s_last;
+            __threadfence();  // this workgroup's ids and scores, before its arrival
+            __syncthreads();
+            if (threadIdx.x == 0)
+                s_last = __hip_atomic_fetch_add(done_ctr, 1, __ATOMIC_ACQ_REL,
+                                                __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1;
+            __syncthreads();
+            if (!s_last) return;
+            __threadfence();  // every workgroup's ids and scores are visible
+        } else {
+            __syncthreads();  // one workgroup: its own ids and scores
+        }
+        permute_small(ids, scores, (int)(tokens * top_k), top_k, (int)experts, counts, offsets,
+                      perm_tokens, perm_weights, slots);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1207,6 +1304,65 @@ size_t hm_route_workspace_bytes(int64_t tokens, int64_t hidden, int64_t experts)
            (size_t)tokens * (size_t)experts * kNB * 3 * sizeof(double);
 }
 
+}  // extern "C"
+
+// The decode router's two launches.  With `fused`, the select kernel also
+// forms the expert groups (the workgroup that finishes last) and the
+// partial kernel zeroes the fused step's completion counters first.
+static int launch_decode_router(const float* h, const float* w, int64_t tokens, int64_t hidden,
+                                int64_t experts, int32_t top_k, uint32_t flags, float* logits,
+                                uint32_t* ids, float* scores, int32_t* status, void* route_ws,
+                                const hm_decode_fusion* fused, void* stream) {
+    const int epl = (int)((experts + HM_WAVE - 1) / HM_WAVE);
+    const dim3 sgrid((unsigned)((tokens + 3) / 4));
+    const size_t seq_bytes = (size_t)(kBlock / HM_WAVE) * experts * sizeof(float);
+    double* part = reinterpret_cast<double*>(static_cast<char*>(route_ws) +
+                                             route_logits_bytes(tokens, experts));
+    const dim3 pgrid((unsigned)kNB, (unsigned)((experts + HM_WAVE - 1) / HM_WAVE),
+                     (unsigned)tokens);
+    hipLaunchKernelGGL(router_partial_kernel, pgrid, dim3(HM_WAVE), 0, hm_stream(stream), h, w,
+                       (int)hidden, (int)experts, part, fused ? fused->counters : nullptr,
+                       fused ? fused->n_counters : 0);
+    HM_LAUNCHED();
+#define HM_SELECTP(N, F)                                                                   \
+    hipLaunchKernelGGL((router_select_partial_kernel<N, F>), sgrid, dim3(kBlock), seq_bytes, \
+                       hm_stream(stream), h, w, part, tokens, hidden, experts, top_k, flags, \
+                       logits, ids, scores, status, F ? fused->counters : nullptr,            \
+                       F ? fused->counts : nullptr, F ? fused->offsets : nullptr,            \
+                       F ? fused->perm_tokens : nullptr, F ? fused->perm_weights : nullptr,  \
+                       F ? fused->slots : nullptr)
+#define HM_SELECTP2(N) do { if (fused) HM_SELECTP(N, true); else HM_SELECTP(N, false); } while (0)
+    if (epl <= 1) HM_SELECTP2(1);
+    else if (epl <= 2) HM_SELECTP2(2);
+    else if (epl <= 4) HM_SELECTP2(4);
+    else if (epl <= 8) HM_SELECTP2(8);
+    else HM_SELECTP2(16);
+#undef HM_SELECTP2
+#undef HM_SELECTP
+    HM_LAUNCHED();
+    return HM_OK;
+}
+
+// Routing and grouping of a decode batch (T <= 16) in two launches instead
+// of hm_router_topk + hm_permute's three; same results.  Counter 0 of
+// fused->counters is the select's completion counter; all n_counters are
+// zeroed by the first launch.
+int hm_route_permute_decode(const float* h, const float* w, int64_t tokens, int64_t hidden,
+                            int64_t experts, int32_t top_k, uint32_t flags, uint32_t* ids,
+                            float* scores, int32_t* status, void* route_ws,
+                            const hm_decode_fusion* fused, void* stream) {
+    HM_REQUIRE(experts > 0 && top_k > 0 && top_k <= experts && fused && fused->counters);
+    HM_REQUIRE(h && w && ids && scores && route_ws && tokens > 0 && hidden > 0);
+    if (experts > 1024 || top_k > kMaxTopK || tokens > kDecodeTokens || hidden % kNB != 0 ||
+        tokens * top_k > kSmallPairs || hidden > INT_MAX)
+        return HM_ERR_UNSUPPORTED;
+    return launch_decode_router(h, w, tokens, hidden, experts, top_k, flags,
+                                static_cast<float*>(route_ws), ids, scores, status, route_ws,
+                                fused, stream);
+}
+
+extern "C" {
+
 int hm_router_topk(const float* h, const float* w, int64_t tokens,
                    int64_t hidden, int64_t experts, int32_t top_k,
                    uint32_t flags, uint32_t* ids, float* scores,
@@ -1225,25 +1381,8 @@ int hm_router_topk(const float* h, const float* w, int64_t tokens,
     if (route_ws && tokens <= kDecodeTokens && hidden % kNB == 0 && hidden <= INT_MAX) {
         // decode: certified block partials, then select over the logits
         // formed from them
-        double* part = reinterpret_cast<double*>(static_cast<char*>(route_ws) +
-                                                 route_logits_bytes(tokens, experts));
-        const dim3 pgrid((unsigned)kNB, (unsigned)((experts + HM_WAVE - 1) / HM_WAVE),
-                         (unsigned)tokens);
-        hipLaunchKernelGGL(router_partial_kernel, pgrid, dim3(HM_WAVE), 0, hm_stream(stream), h,
-                           w, (int)hidden, (int)experts, part);
-        HM_LAUNCHED();
-#define HM_SELECTP(N)                                                                     \
-        hipLaunchKernelGGL(router_select_partial_kernel<N>, sgrid, dim3(kBlock), seq_bytes,  \
-                           hm_stream(stream), h, w, part, tokens, hidden, experts, top_k,    \
-                           flags, logits, ids, scores, status)
-        if (epl <= 1) HM_SELECTP(1);
-        else if (epl <= 2) HM_SELECTP(2);
-        else if (epl <= 4) HM_SELECTP(4);
-        else if (epl <= 8) HM_SELECTP(8);
-        else HM_SELECTP(16);
-#undef HM_SELECTP
-        HM_LAUNCHED();
-        return HM_OK;
+        return launch_decode_router(h, w, tokens, hidden, experts, top_k, flags, logits, ids,
+                                    scores, status, route_ws, nullptr, stream);
     }
     const bool aligned = ((uintptr_t)h % 16 == 0) && ((uintptr_t)w % 16 == 0);
     if (route_ws && !(flags & HM_EXEC_ROUTE_SEQUENTIAL) && aligned && experts % kME == 0 &&
