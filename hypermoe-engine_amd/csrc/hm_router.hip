@@ -307,14 +307,37 @@ __global__ __launch_bounds__(256) void router_logits_tile_kernel(
 // the reference's logit.  Otherwise (about one logit in 10^4 - 10^5 for
 // random data, and every non-finite case) the lane runs the reference's
 // sequential chain.  HM_EXEC_ROUTE_SEQUENTIAL sends every logit there.
+//
+// R and P enter the bound only linearly, so each block stores its share
+//   C_j = (2u + 2u^2 H) R_j + 2.02 u^2 (b^2 + H^2) Q_j
+// and the bound is (u (b+1) + 2u^2 H) SA + sum_j C_j, inflated.
 // ---------------------------------------------------------------------------
 constexpr int kNB = 32;  // K blocks per logit (a multiple of 8)
 
-// part[t][j][c][e], c = 0, 1, 2: B_j, R_j, Q_j (expert-minor, so that the
-// select kernel's lanes read consecutive experts); grid (kNB, ceil(E/64), T),
-// one wave, lane = expert.  The block's W rows (64 experts wide) go to LDS
-// in one burst of 16-byte DMA loads (E % 64 == 0, b % 4 == 0, w 16-byte
-// aligned), else per lane.
+__device__ __forceinline__ double block_c_term(double rs, double qs, int64_t hidden) {
+    const double u = 0x1p-53;
+    const double n = (double)hidden, bw = (double)(hidden / kNB);
+    return (2.0 * u + 2.0 * u * u * n) * rs + 2.02 * u * u * (bw * bw + n * n) * qs;
+}
+
+// Whether the bound settles float(s_n), given the block-sum chain's result
+// a, SA (sa) and the sum of the blocks' C_j (sc).
+__device__ __forceinline__ bool block_sums_settle(double a, double sa, double sc,
+                                                  int64_t hidden) {
+    const double u = 0x1p-53;
+    const double n = (double)hidden, bw = (double)(hidden / kNB);
+    const double infl = 1.0 + 4.0 * n * u;  // the magnitude sums' own rounding
+    const double b0 = ((u * (bw + 1.0) + 2.0 * u * u * n) * sa + sc) * infl;
+    const double bc = (b0 * (1.0 + 0x1p-40) + u * fabs(a)) * (1.0 + 0x1p-50);
+    const double lo = a - bc, hi = a + bc;
+    return isfinite(lo) && isfinite(hi) && __float_as_uint((float)lo) == __float_as_uint((float)hi);
+}
+
+// part[t][e][c][j], c = 0, 1: B_j, C_j (block-minor, so that the select
+// kernel's lane reads its logit's blocks as contiguous 16-byte vectors);
+// grid (kNB, ceil(E/64), T), one wave, lane = expert.  The block's W rows
+// (64 experts wide) go to LDS in one burst of 16-byte DMA loads
+// (E % 64 == 0, b % 4 == 0, w 16-byte aligned), else per lane.
 constexpr int kPK = 64;  // k per LDS chunk of a block
 
 __global__ __launch_bounds__(64) void router_partial_kernel(
@@ -359,58 +382,38 @@ __global__ __launch_bounds__(64) void router_partial_kernel(
         }
     }
     if (live) {
-        double* o = part + (((int64_t)t * kNB + j) * 3) * experts + e;
+        double* o = part + ((int64_t)t * experts + e) * 2 * kNB + j;
         o[0] = acc;
-        o[experts] = rs;
-        o[2 * experts] = qs;
+        o[kNB] = block_c_term(rs, qs, hidden);
     }
 }
 
-// Whether the bound above settles float(s_n) given the block-sum chain's
-// result a and the magnitude sums SA (sa), R (sr), P (sp).
-__device__ __forceinline__ bool block_sums_settle(double a, double sa, double sr, double sp,
-                                                  int64_t hidden) {
-    const double u = 0x1p-53;
-    const double n = (double)hidden, bw = (double)(hidden / kNB);
-    const double infl = 1.0 + 4.0 * n * u;  // the magnitude sums' own rounding
-    const double b0 = (u * ((bw + 1.0) * sa + 2.0 * sr) +
-                       2.0 * u * u * (n * (sr + sa) + 1.01 * (bw * bw + n * n) * sp)) * infl;
-    const double bc = (b0 * (1.0 + 0x1p-40) + u * fabs(a)) * (1.0 + 0x1p-50);
-    const double lo = a - bc, hi = a + bc;
-    return isfinite(lo) && isfinite(hi) && __float_as_uint((float)lo) == __float_as_uint((float)hi);
-}
-
 // One logit from its block partials (see above), or from the sequential
-// chain when the bound does not settle the float.
-// pp: this logit's B_0 (part + t*kNB*3*E + e); component c of block j is at
-// pp[(3j + c) * E].
+// chain when the bound does not settle the float.  pp: this logit's
+// [B_0 .. B_31, C_0 .. C_31] (part + (t*E + e) * 2 * kNB).
 __device__ __forceinline__ float certified_logit(const double* __restrict__ pp,
                                                  const float* __restrict__ hrow,
                                                  const float* __restrict__ wcol, int64_t hidden,
                                                  int64_t experts, bool force_seq,
                                                  int32_t* status) {
-    double a = 0.0, sa = 0.0, sr = 0.0, sp = 0.0;
-    // 8 blocks at a time: their 24 loads go out before the dependent chain
-    constexpr int G = 8;
-    const int64_t stride = 3 * experts;
-    for (int j0 = 0; j0 < kNB; j0 += G) {
-        double bv[G], rv[G], qv[G];
-        const double* q = pp + j0 * stride;
+    // all 64 values in 32 vector loads, then the dependent chain
+    double2 bv[kNB / 2], cv[kNB / 2];
 #pragma unroll
-        for (int i = 0; i < G; ++i) {
-            bv[i] = q[i * stride];
-            rv[i] = q[i * stride + experts];
-            qv[i] = q[i * stride + 2 * experts];
-        }
-#pragma unroll
-        for (int i = 0; i < G; ++i) {
-            a += bv[i];
-            sa += fabs(a);
-            sr += rv[i];
-            sp += qv[i];
-        }
+    for (int i = 0; i < kNB / 2; ++i) {
+        bv[i] = reinterpret_cast<const double2*>(pp)[i];
+        cv[i] = reinterpret_cast<const double2*>(pp + kNB)[i];
     }
-    if (!force_seq && block_sums_settle(a, sa, sr, sp, hidden)) return (float)a;
+    double a = 0.0, sa = 0.0, sc = 0.0;
+#pragma unroll
+    for (int i = 0; i < kNB / 2; ++i) {
+        a += bv[i].x;
+        sa += fabs(a);
+        a += bv[i].y;
+        sa += fabs(a);
+        sc += cv[i].x;
+        sc += cv[i].y;
+    }
+    if (!force_seq && block_sums_settle(a, sa, sc, hidden)) return (float)a;
     double acc = 0.0;
     for (int64_t k = 0; k < hidden; ++k)
         acc = __builtin_fma((double)hrow[k], (double)wcol[k * experts], acc);
@@ -628,8 +631,8 @@ __global__ __launch_bounds__(kBlock) void router_select_partial_kernel(
             valid[j] = e < experts;
             v[j] = 0.0f;
             if (valid[j]) {
-                v[j] = certified_logit(part + t * kNB * 3 * experts + e, h + t * hidden, w + e,
-                                       hidden, experts, force_seq, status);
+                v[j] = certified_logit(part + (t * experts + e) * 2 * kNB, h + t * hidden,
+                                       w + e, hidden, experts, force_seq, status);
                 logits[t * experts + e] = v[j];
             }
         }
@@ -948,14 +951,14 @@ __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
                     }
                 }
             }
-            double a = 0.0, sa = 0.0, sr = 0.0, sp = 0.0;
+            const double cj = block_c_term(rs, qs, hidden);
+            double a = 0.0, sa = 0.0, sc = 0.0;
             for (int j = 0; j < kNB; ++j) {
                 a += __shfl(acc, 32 * half + j, HM_WAVE);
                 sa += fabs(a);
-                sr += __shfl(rs, 32 * half + j, HM_WAVE);
-                sp += __shfl(qs, 32 * half + j, HM_WAVE);
+                sc += __shfl(cj, 32 * half + j, HM_WAVE);
             }
-            const bool ok = block_sums_settle(a, sa, sr, sp, hidden);
+            const bool ok = block_sums_settle(a, sa, sc, hidden);
             // the owners of this pass's logits take the settled values
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf) {
@@ -1268,7 +1271,7 @@ int hm_rmsnorm(const float* x, const float* gamma, float* y, int64_t rows,
 
 // Route workspace: the logits [T x E] floats (rounded up to 256 bytes),
 // then for decode batches (T <= kDecodeTokens) the block partials
-// [T x E x kNB x 3] doubles, and for prefill batches with E % 64 == 0 the
+// [T x E x 2 x kNB] doubles, and for prefill batches with E % 64 == 0 the
 // matrix-core range partials [S x T x E] doubles, W transposed [E x H]
 // floats, row norms [S x T] and column norms [S x E] doubles
 // (S = prefill_splits).
@@ -1301,7 +1304,7 @@ size_t hm_route_workspace_bytes(int64_t tokens, int64_t hidden, int64_t experts)
         return b;
     }
     return route_logits_bytes(tokens, experts) +
-           (size_t)tokens * (size_t)experts * kNB * 3 * sizeof(double);
+           (size_t)tokens * (size_t)experts * kNB * 2 * sizeof(double);
 }
 
 }  // extern "C"
