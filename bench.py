@@ -251,11 +251,12 @@ def main():
     log(f"[bench] timed {args.steps} steps: {ms_per_step:.4f} ms/step", q)
 
     # one checked call: routing stats + parity of a token sample
-    res = block.execute_batch(batches[0], d_w)
-    counts = res.counts
-    # distinct experts per step, averaged over the pool
+    # distinct experts per step, averaged over the pool (before the checked
+    # call: each call reuses the block's output buffer)
     unique = float(np.mean([int((block.execute_batch(b, d_w).counts > 0).sum())
                             for b in batches]))
+    res = block.execute_batch(batches[0], d_w)
+    counts = res.counts
     h_host = batches[0].cpu().numpy()
     out = res.output.cpu().numpy()
     tokens_per_s = T / (ms_per_step / 1e3)

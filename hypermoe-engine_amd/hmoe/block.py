@@ -154,7 +154,9 @@ class MoEBlock:
             counts=b["counts"].cpu().numpy(), offsets=b["offsets"].cpu().numpy(),
             perm_tokens=b["perm_tokens"].cpu().numpy(),
             perm_weights=b["perm_weights"].cpu().numpy(), status=status,
-            output=b["out"], expert_out=b["expert_out"])
+            # callee-allocated results (MoERuntime.cpp:134): the next call
+            # reuses the block's buffers
+            output=b["out"].clone(), expert_out=b["expert_out"].clone())
         for e in range(self.layer.experts):
             lo, hi = res.offsets[e], res.offsets[e + 1]
             if hi > lo:
