@@ -42,7 +42,7 @@ KERNEL_SOURCES = ["hm_runtime.hip", "hm_router.hip", "hm_gemm.hip", "hm_gemm_mfm
 # Per-source flags.  The FP64 router MFMAs keep their accumulators in VGPRs
 # (otherwise the compiler copies them to AGPRs and back on every K chunk).
 SOURCE_FLAGS = {"hm_router.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
-HOST_SOURCES = ["hip_backend.cpp", "hip_tensor_backend.cpp", "moe_block.cpp"]
+HOST_SOURCES = ["hip_backend.cpp", "hip_tensor_backend.cpp", "moe_block.cpp", "artefact.cpp"]
 
 KERNELS_SO = LIB / "libhm_kernels.so"
 SYNTH_SO = LIB / "libhm_synth.so"

@@ -13,6 +13,8 @@
 #include "hypermoe/experts/cache_policy.hpp"
 #include "hypermoe/experts/expert_manager.hpp"
 #include "memory/TransferManager.hpp"
+#include "models/ModelManifest.hpp"
+#include "storage/ExpertIndex.hpp"
 #include "models/ExpertWeightMap.hpp"
 #include "backend/CpuBackend.hpp"
 #include "backend/cuda/Int8GemmPlan.hpp"
@@ -285,6 +287,88 @@ int hmref_moe_block(const void* payload, std::int32_t isInt8,
     std::error_code ignored;
     if (!path.empty()) std::filesystem::remove_all(path, ignored);
     return rc;
+}
+
+// ---- packed artefact (experts.index / manifest.json) -----------------------
+
+// storage::ExpertStore::crc32 (ExpertStore.cpp:183-192).
+std::uint32_t hmref_crc32(const void* data, std::size_t bytes) {
+    return storage::ExpertStore::crc32(
+        std::span<const std::byte>(static_cast<const std::byte*>(data), bytes));
+}
+
+// storage::ExpertIndex(records, projections).save(path).  records: 6 u64
+// per record (layer, expert, offset, size, quantization, checksum);
+// projections: 16 u64 per record (layer, expert, type, dtype, rank,
+// reserved, offset, size, shape[4], checksum, trailing, 0, 0).
+int hmref_index_save(const char* path, const std::uint64_t* records, std::size_t nrec,
+                     const std::uint64_t* projections, std::size_t nproj) {
+    return guarded([&] {
+        std::vector<storage::ExpertRecord> rs;
+        for (std::size_t i = 0; i < nrec; ++i) {
+            const auto* r = records + 6 * i;
+            rs.push_back({std::uint32_t(r[0]), std::uint32_t(r[1]), r[2], r[3],
+                          std::uint32_t(r[4]), std::uint32_t(r[5])});
+        }
+        std::vector<storage::ProjectionRecord> ps;
+        for (std::size_t i = 0; i < nproj; ++i) {
+            const auto* p = projections + 16 * i;
+            storage::ProjectionRecord o;
+            o.layer_id = std::uint32_t(p[0]);
+            o.expert_id = std::uint32_t(p[1]);
+            o.projection_type = static_cast<storage::ProjectionType>(p[2]);
+            o.dtype = std::uint32_t(p[3]);
+            o.rank = std::uint32_t(p[4]);
+            o.reserved = std::uint32_t(p[5]);
+            o.offset = p[6];
+            o.size = p[7];
+            for (int d = 0; d < 4; ++d) o.shape[d] = p[8 + d];
+            o.checksum = std::uint32_t(p[12]);
+            o.trailing_reserved = std::uint32_t(p[13]);
+            ps.push_back(o);
+        }
+        storage::ExpertIndex(std::move(rs), std::move(ps)).save(path);
+    });
+}
+
+// storage::ExpertIndex::load(path): counts, and the records in the layout
+// of hmref_index_save (up to the capacities).  -3 on StorageError.
+int hmref_index_load(const char* path, std::uint64_t* records, std::size_t rcap,
+                     std::uint64_t* projections, std::size_t pcap, std::size_t* nrec,
+                     std::size_t* nproj) {
+    return guarded([&] {
+        const auto index = storage::ExpertIndex::load(path);
+        *nrec = index.records().size();
+        *nproj = index.projections().size();
+        for (std::size_t i = 0; i < std::min(rcap, *nrec); ++i) {
+            const auto& r = index.records()[i];
+            const std::uint64_t v[6] = {r.layer_id, r.expert_id, r.offset, r.size,
+                                        r.quantization_type, r.checksum};
+            std::memcpy(records + 6 * i, v, sizeof v);
+        }
+        for (std::size_t i = 0; i < std::min(pcap, *nproj); ++i) {
+            const auto& p = index.projections()[i];
+            const std::uint64_t v[16] = {p.layer_id, p.expert_id,
+                                         static_cast<std::uint64_t>(p.projection_type), p.dtype,
+                                         p.rank, p.reserved, p.offset, p.size, p.shape[0],
+                                         p.shape[1], p.shape[2], p.shape[3], p.checksum,
+                                         p.trailing_reserved, 0, 0};
+            std::memcpy(projections + 16 * i, v, sizeof v);
+        }
+    });
+}
+
+// models::ModelManifest::load(path) (with its validate()), then toJson()
+// into out (NUL-terminated, truncated to cap).
+int hmref_manifest_load(const char* path, char* out, std::size_t cap) {
+    return guarded([&] {
+        const auto json = models::ModelManifest::load(path).toJson();
+        if (out && cap) {
+            const auto n = std::min(cap - 1, json.size());
+            std::memcpy(out, json.data(), n);
+            out[n] = '\0';
+        }
+    });
 }
 
 } // extern "C"
