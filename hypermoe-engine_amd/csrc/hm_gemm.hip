@@ -619,11 +619,27 @@ int hm_launch_down_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int32
     return HM_OK;
 }
 
+bool hm_f32_mfma_gateup_ok(int64_t H, int64_t I);
+bool hm_f32_mfma_down_ok(int64_t H, int64_t I);
+int hm_launch_gateup_f32_mfma(const hm_layer* L, const float* hidden, const int32_t* counts,
+                              const int32_t* offsets, const int32_t* perm_tokens, int64_t R,
+                              int64_t max_tiles, float* z, hipStream_t stream);
+int hm_launch_down_f32_mfma(const hm_layer* L, const float* z, const int32_t* counts,
+                            const int32_t* offsets, int64_t R, int64_t max_tiles, float* y,
+                            hipStream_t stream);
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// FP32 experts: the matrix-core tiles (hm_gemm_f32_mfma.hip) where the
+// shape allows, else the FMA tiles above.
 int hm_launch_gateup_f32(const hm_layer* layer, const float* hidden, const int32_t* counts,
                          const int32_t* offsets, const int32_t* perm_tokens, int64_t R,
                          float* zf, hipStream_t stream) {
     const int64_t H = layer->hidden, I = layer->intermediate, E = layer->experts;
     if (R == 0) return HM_OK;
+    if (hm_f32_mfma_gateup_ok(H, I) && aligned16(hidden) && aligned16(layer->packed))
+        return hm_launch_gateup_f32_mfma(layer, hidden, counts, offsets, perm_tokens, R,
+                                         hm_max_tiles(R, E, 64), zf, stream);
     const dim3 g1((unsigned)hm_max_tiles(R, E, kF32Tile), (unsigned)((I + kF32Tile - 1) / kF32Tile));
     HM_STAGE_LAUNCH(true, true, gateup_f32_kernel, g1, dim3(kBlock), 0, stream, hidden, H, I, E,
                     static_cast<const float*>(layer->packed), counts, offsets, perm_tokens, zf);
@@ -635,6 +651,9 @@ int hm_launch_down_f32(const hm_layer* layer, const int32_t* counts, const int32
                        int64_t R, const float* zf, float* y, hipStream_t stream) {
     const int64_t H = layer->hidden, I = layer->intermediate, E = layer->experts;
     if (R == 0) return HM_OK;
+    if (hm_f32_mfma_down_ok(H, I) && aligned16(zf) && aligned16(layer->packed))
+        return hm_launch_down_f32_mfma(layer, zf, counts, offsets, R, hm_max_tiles(R, E, 64), y,
+                                       stream);
     const dim3 g2((unsigned)hm_max_tiles(R, E, kF32Tile), (unsigned)((H + kF32Tile - 1) / kF32Tile));
     hipLaunchKernelGGL(down_f32_kernel, g2, dim3(kBlock), 0, stream, zf, H, I, E,
                        static_cast<const float*>(layer->packed), counts, offsets, y);

@@ -38,10 +38,11 @@ HIP_FLAGS = [
     f"-I{INCLUDE}", f"-I{CSRC}",
 ]
 KERNEL_SOURCES = ["hm_runtime.hip", "hm_router.hip", "hm_gemm.hip", "hm_gemm_mfma.hip",
-                  "hm_gemv.hip", "hm_block.hip"]
+                  "hm_gemm_f32_mfma.hip", "hm_gemv.hip", "hm_block.hip"]
 # Per-source flags.  The FP64 router MFMAs keep their accumulators in VGPRs
 # (otherwise the compiler copies them to AGPRs and back on every K chunk).
-SOURCE_FLAGS = {"hm_router.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+SOURCE_FLAGS = {"hm_router.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+                "hm_gemm_f32_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 HOST_SOURCES = ["hip_backend.cpp", "hip_tensor_backend.cpp", "moe_block.cpp", "artefact.cpp"]
 
 KERNELS_SO = LIB / "libhm_kernels.so"
