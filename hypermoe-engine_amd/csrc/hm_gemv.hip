@@ -239,6 +239,150 @@ int dispatch_gemv(int64_t K, const float* x_src, const int32_t* perm_tokens, int
     return HM_ERR_UNSUPPORTED;
 }
 
+// ---------------------------------------------------------------------------
+// Decode down projection fused with the combine, column-block major: a
+// workgroup owns kDcCols output columns n0 .. n0+kDcCols-1 for EVERY active
+// expert (its 16 waves take the experts in turn, each streaming the
+// expert's kDcCols down rows into its LDS slot), keeps y[g, n0 ..] of every
+// grouped row g in LDS, and then forms the tokens' outputs for its columns
+// with hm_combine's arithmetic.  No workgroup needs another's results, so
+// there is no device-wide synchronisation, and y goes to memory only when
+// the caller asks for the expert outputs.  Each y is computed with exactly
+// gemv_body's DOWN arithmetic (same lane slices, same reduction), so the
+// results equal the two-kernel path's.  T <= 16, top_k <= 16, I <= 1024.
+// ---------------------------------------------------------------------------
+constexpr int kDcCols = 8;
+constexpr int kDcWaves = 16;
+constexpr int kDcPairs = HM_GEMV_MAX_TOKENS * 16;
+
+__global__ __launch_bounds__(64 * kDcWaves) void gemv_down_combine_kernel(
+    const float* __restrict__ z, int64_t I, int64_t H, int64_t experts,
+    const int8_t* __restrict__ packed, const float* __restrict__ scale,
+    const int32_t* __restrict__ zp, const int32_t* __restrict__ counts,
+    const int32_t* __restrict__ offsets, const uint32_t* __restrict__ ids,
+    const int32_t* __restrict__ slots, const float* __restrict__ scores,
+    const float* __restrict__ residual, int tokens, int top_k, float* __restrict__ y_out,
+    float* __restrict__ out) {
+    __shared__ __attribute__((aligned(1024))) int8_t wl[kDcWaves][kDcCols * 1024];
+    __shared__ float s_y[kDcPairs][kDcCols];
+    __shared__ int s_cnt[1024], s_off[1024], s_act[1024];
+    __shared__ int s_nact;
+    __shared__ uint32_t s_ids[kDcPairs];
+    __shared__ int s_row[HM_GEMV_MAX_TOKENS][16];
+    __shared__ float s_w[HM_GEMV_MAX_TOKENS][16];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t n0 = (int64_t)blockIdx.x * kDcCols;
+    // every routing input the workgroup needs, in one round of loads
+    const int pairs = tokens * top_k;
+    for (int i = tid; i < experts; i += 64 * kDcWaves) {
+        s_cnt[i] = counts[i];
+        s_off[i] = offsets[i];
+    }
+    uint32_t my_id = 0;
+    int my_slot = 0;
+    float my_score = 0.0f;
+    if (tid < pairs) {
+        my_id = ids[tid];
+        my_slot = slots[tid];
+        my_score = scores[tid];
+        s_ids[tid] = my_id;
+    }
+    for (int i = tid; i < HM_GEMV_MAX_TOKENS * 16; i += 64 * kDcWaves) {
+        (&s_row[0][0])[i] = 0;  // (ranks collide only after a routing failure)
+        (&s_w[0][0])[i] = 0.0f;
+    }
+    __syncthreads();
+    // the active experts, ascending (wave 0 compacts the counts); the pairs'
+    // ranks by expert id within their token
+    if (wave == 0) {
+        int seen = 0;
+        for (int64_t base = 0; base < experts; base += 64) {
+            const int64_t e = base + lane;
+            const bool nz = e < experts && s_cnt[e] > 0;
+            const unsigned long long m = __ballot(nz);
+            if (nz) s_act[seen + __popcll(m & ((1ull << lane) - 1))] = (int)e;
+            seen += __popcll(m);
+        }
+        if (lane == 0) s_nact = seen;
+    }
+    if (tid < pairs) {
+        const int t = tid / top_k;
+        int rank = 0;
+        for (int q = 0; q < top_k; ++q) rank += s_ids[t * top_k + q] < my_id;
+        s_row[t][rank & 15] = my_slot;
+        s_w[t][rank & 15] = my_score;
+    }
+    __syncthreads();
+    const int nact = s_nact;
+    const int64_t K = I;
+    int8_t* lds = wl[wave];
+    for (int a = wave; a < nact; a += kDcWaves) {
+        const int e = s_act[a];
+        const int8_t* wrows = packed + (int64_t)e * 3 * H * I + 2 * H * I + n0 * K;
+        const int64_t k = 16 * lane;
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slot's last reads are done
+        if (k < K) {
+#pragma unroll
+            for (int j = 0; j < kDcCols; ++j) dma16(wrows + j * K + k, lds + j * 1024);
+        }
+        const int64_t g0 = s_off[e];
+        const int rows = s_cnt[e];
+        const float sc = scale[e * 3 + 2];
+        const float zc = (float)(128 + zp[e * 3 + 2]);
+        wait_vmcnt<0>();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        for (int r = 0; r < rows; ++r) {
+            const float* xr = z + (g0 + r) * K;
+            float x[16];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 v = k < K ? *reinterpret_cast<const float4*>(xr + k + 4 * i)
+                                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
+            }
+            float xs = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) xs += x[i];
+            float xv[1] = {xs};
+            const float xsum = wave_reduce_many<1>(xv);
+#pragma unroll 1
+            for (int j = 0; j < kDcCols; ++j) {
+                float acc = 0.0f;
+                // lanes without a piece read their own unused slot; x is 0
+                const uint4 wv = *reinterpret_cast<const uint4*>(lds + j * 1024 + 16 * lane);
+                const uint32_t d[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float f[4];
+                    bytes_to_float(d[q], f);
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) acc = __builtin_fmaf(x[4 * q + b], f[b], acc);
+                }
+                float av[1] = {acc};
+                const float tot = wave_reduce_many<1>(av);
+                const float y = __fmul_rn(__fsub_rn(tot, __fmul_rn(zc, xsum)), sc);
+                if (lane == 0) {
+                    s_y[(g0 + r) & (kDcPairs - 1)][j] = y;
+                    if (y_out) y_out[(g0 + r) * H + n0 + j] = y;
+                }
+            }
+        }
+    }
+    // the combine of hm_combine (MoERuntime.cpp:308-325) for these columns
+    __syncthreads();
+    for (int i = tid; i < tokens * kDcCols; i += 64 * kDcWaves) {
+        const int t = i / kDcCols, c = i % kDcCols;
+        float acc = 0.0f;
+        for (int r = 0; r < top_k; ++r)
+            acc = __fadd_rn(acc, __fmul_rn(s_w[t][r], s_y[s_row[t][r] & (kDcPairs - 1)][c]));
+        const int64_t n = n0 + c;
+        if (residual) acc = __fadd_rn(residual[t * H + n], acc);
+        out[t * H + n] = acc;
+    }
+}
+
 // Rows up to 2048 bytes keep a wave's 8 weight rows within 16 KB of LDS.
 bool gemv_k_ok(int64_t K) { return K >= 16 && K % 16 == 0 && K <= 2048; }
 
@@ -258,6 +402,28 @@ int hm_launch_gateup_gemv(const hm_layer* L, const float* hidden, const int32_t*
     const int64_t slots = pairs < L->experts ? pairs : L->experts;
     return dispatch_gemv<true>(L->hidden, hidden, perm_tokens, L->intermediate, L, counts,
                                offsets, slots, z, s);
+}
+
+// The decode down projection fused with the combine (T <= 16, top_k <= 16,
+// I <= 1024, H % 8 == 0); y_out (optional) receives the expert outputs.
+bool hm_gemv_combine_ok(int64_t tokens, int32_t top_k, int64_t H, int64_t I) {
+    return tokens <= HM_GEMV_MAX_TOKENS && top_k <= 16 && I <= 1024 && I % 16 == 0 &&
+           H % kDcCols == 0;
+}
+
+int hm_launch_down_combine_gemv(const hm_layer* L, const float* z, const int32_t* counts,
+                                const int32_t* offsets, const uint32_t* ids,
+                                const int32_t* slots, const float* scores,
+                                const float* residual, int64_t tokens, int32_t top_k,
+                                float* y_out, float* out, hipStream_t s) {
+    if (!hm_gemv_combine_ok(tokens, top_k, L->hidden, L->intermediate) || L->experts > 1024)
+        return HM_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL(gemv_down_combine_kernel, dim3((unsigned)(L->hidden / kDcCols)),
+                       dim3(64 * kDcWaves), 0, s, z, L->intermediate, L->hidden, L->experts,
+                       static_cast<const int8_t*>(L->packed), L->scale, L->zero_point, counts,
+                       offsets, ids, slots, scores, residual, (int)tokens, top_k, y_out, out);
+    HM_LAUNCHED();
+    return HM_OK;
 }
 
 // y[g, n] = z_g . Wd[n] for every grouped row g.
