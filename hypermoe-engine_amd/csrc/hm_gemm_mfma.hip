@@ -367,8 +367,11 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
 
         // ---- epilogue (the next tile's first kS-1 stages are in flight):
         // g and u rows out as floats (SiLU and the Z digits follow in
-        // swiglu_quant_kernel, at full occupancy)
-        {
+        // swiglu_quant_kernel, at full occupancy).  The zero-point
+        // correction is chosen once per tile (zg, zu are uniform), so no
+        // per-element test drags its integer multiplies into the common case.
+        auto epilogue = [&](auto with_zp) {
+            constexpr bool ZP = decltype(with_zp)::value;
             const int e = cur.e, nrows = cur.nrows;
             const float sg = s_sg[e], su = s_su[e];
             const int zg = s_zg[e], zu = s_zu[e];
@@ -380,7 +383,7 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
                     const int rq = acc_row(r0, lane, 4 * q);
                     const float4 sx4 = *reinterpret_cast<const float4*>(&s_xs[m][rq]);
                     int4 ds4[L];
-                    if ((zg | zu) != 0) {
+                    if constexpr (ZP) {
 #pragma unroll
                         for (int l = 0; l < L; ++l) ds4[l] = *reinterpret_cast<const int4*>(&s_xd[m][l][rq]);
                     }
@@ -400,7 +403,7 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
                                 pg[l] = acc[ii][l][j][v];
                                 pu[l] = acc[ii][l][WCP + j][v];
                             }
-                            if ((zg | zu) != 0) {
+                            if constexpr (ZP) {
 #pragma unroll
                                 for (int l = 0; l < L; ++l) {
                                     const int ds = t4 == 0 ? ds4[l].x : t4 == 1 ? ds4[l].y : t4 == 2 ? ds4[l].z : ds4[l].w;
@@ -418,7 +421,9 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
                     }
                 }
             }
-        }
+        };
+        if ((s_zg[cur.e] | s_zu[cur.e]) != 0) epilogue(std::true_type{});
+        else epilogue(std::false_type{});
         // next tile
         slot0 = (slot0 + nk) % kS;
         m = mn;
@@ -621,7 +626,11 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
         // segment |P_l| <= 2^22 (with a zero-point correction), so two
         // limbs combine exactly in int32 and convert with the single
         // rounding of fmaf((float)P_1, 256, (float)P_0).
-        auto fold = [&](int zb) {
+        // The zero-point correction is chosen once per tile (zd is uniform):
+        // a per-element test would let the compiler hoist its integer
+        // multiplies out of the branch into every fold.
+        auto fold = [&](int zb, auto with_zp) {
+            constexpr bool ZP = decltype(with_zp)::value;
 #pragma unroll
             for (int ii = 0; ii < WR; ++ii)
 #pragma unroll
@@ -629,7 +638,7 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
                     const int rq = acc_row(32 * (wr * WR + ii), lane, 4 * q);
                     const float4 zs4 = *reinterpret_cast<const float4*>(&s_zs[m][zb][rq]);
                     int4 dz4[L];
-                    if (zd != 0) {
+                    if constexpr (ZP) {
 #pragma unroll
                         for (int l = 0; l < L; ++l) dz4[l] = *reinterpret_cast<const int4*>(&s_zds[m][l][zb][rq]);
                     }
@@ -638,15 +647,20 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
                         const int v = 4 * q + t4;
                         const float zs = t4 == 0 ? zs4.x : t4 == 1 ? zs4.y : t4 == 2 ? zs4.z : zs4.w;
                         const float alpha = __fmul_rn(zs, sd);
+                        int dzc[L];
+                        if constexpr (ZP) {
+#pragma unroll
+                            for (int l = 0; l < L; ++l)
+                                dzc[l] = zd * (t4 == 0 ? dz4[l].x : t4 == 1 ? dz4[l].y : t4 == 2 ? dz4[l].z : dz4[l].w);
+                        }
 #pragma unroll
                         for (int j = 0; j < WCN; ++j) {
                             int p[L];
 #pragma unroll
                             for (int l = 0; l < L; ++l) p[l] = acc[ii][l][j][v];
-                            if (zd != 0) {
+                            if constexpr (ZP) {
 #pragma unroll
-                                for (int l = 0; l < L; ++l)
-                                    p[l] -= zd * (t4 == 0 ? dz4[l].x : t4 == 1 ? dz4[l].y : t4 == 2 ? dz4[l].z : dz4[l].w);
+                                for (int l = 0; l < L; ++l) p[l] -= dzc[l];
                             }
                             float c;
                             if constexpr (L == 1) c = (float)p[0];
@@ -657,6 +671,10 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
                     }
                 }
         };
+        auto fold_seg = [&](int zb) {
+            if (zd != 0) fold(zb, std::true_type{});
+            else fold(zb, std::false_type{});
+        };
         // nk and kS are even, so a Z segment (two stages) never straddles
         // the two phases
         int ks = 0;
@@ -664,14 +682,14 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
         for (; ks < nk - kS; ks += 2) {
             dstep(ks, std::true_type{}, std::false_type{});
             dstep(ks + 1, std::false_type{}, std::false_type{});
-            fold(ks >> 1);
+            fold_seg(ks >> 1);
         }
         if (has_next) make_src(nxt, src);
 #pragma clang loop unroll(disable)
         for (; ks < nk; ks += 2) {
             dstep(ks, std::true_type{}, std::true_type{});
             dstep(ks + 1, std::false_type{}, std::true_type{});
-            fold(ks >> 1);
+            fold_seg(ks >> 1);
         }
         // ---- epilogue: float rows out (the next tile's stages are in flight)
 #pragma unroll
