@@ -46,7 +46,13 @@ namespace {
 constexpr int kWaves = 8;           // wave64s per workgroup
 constexpr int kThreads = 64 * kWaves;
 constexpr int kKB = 64;             // K bytes per ring stage: two 32-byte MFMA K steps
-constexpr int kS = 4;               // ring stages
+constexpr int kS = 4;               // ring stages (gate/up)
+#ifndef HM_DOWN_STAGES
+#define HM_DOWN_STAGES 5
+#endif
+// ring stages of the down projection (three limbs fill LDS at four)
+template <int L>
+constexpr int down_stages() { return L >= 3 ? 4 : HM_DOWN_STAGES; }
 constexpr int kFragBytes = 32 * kKB;  // one 32-row fragment of a stage
 constexpr int kZBlock = 128;        // Z fixed-point segment (columns of Z = K of down)
 constexpr int kGateUpN = 128;       // columns per projection per gate/up tile
@@ -200,7 +206,7 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
     struct Info {
         int e, nrows, g0, n0;
     };
-    auto info = [&](int i) {
+    auto info = [&](int i) __attribute__((always_inline)) {
         const int j = tr.jbeg + i * tr.step;
         const int gm = j / nbn;
         Info t;
@@ -212,14 +218,14 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
         return t;
     };
     // token ids of the tile rows (rows past nrows repeat the last row)
-    auto fetch_rows = [&](const Info& t, int m) {
+    auto fetch_rows = [&](const Info& t, int m) __attribute__((always_inline)) {
         if (wave < RW) {
             const int r = HM_WAVE * wave + lane;
             dma4(perm_tokens + t.g0 + min(r, t.nrows - 1), &s_rt[m][HM_WAVE * wave]);
         }
     };
     // activation scales and digit sums of those tokens (needs s_rt[m])
-    auto fetch_row_meta = [&](int m) {
+    auto fetch_row_meta = [&](int m) __attribute__((always_inline)) {
         if (wave < RW) {
             const int tok = s_rt[m][HM_WAVE * wave + lane];
             dma4(xscale + tok, &s_xs[m][HM_WAVE * wave]);
@@ -261,7 +267,7 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
 #pragma unroll
     for (int h = 0; h < 2; ++h) rd[h] = frag_read_offset(lane, h);
     v4i fa[2][WR][L], fb[2][2 * WCP];
-    auto read_frags = [&](int slot, int h) {
+    auto read_frags = [&](int slot, int h) __attribute__((always_inline)) {
         const int8_t* st = ring + slot * STAGE;
 #pragma unroll
         for (int ii = 0; ii < WR; ++ii)
@@ -276,7 +282,7 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
     };
     v16i acc[WR][L][2 * WCP];
     // `first`: the tile's first K step starts the accumulators from zero
-    auto mfma_step = [&](int h, auto first) {
+    auto mfma_step = [&](int h, auto first) __attribute__((always_inline)) {
 #pragma unroll
         for (int ii = 0; ii < WR; ++ii)
 #pragma unroll
@@ -288,6 +294,34 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
                     else
                         acc[ii][l][j] = mfma32(fa[h][ii][l], fb[h][j], acc[ii][l][j]);
                 }
+    };
+    // K step h = 0 with the refill of `slot` (stage ksrc of the stream)
+    // spread between its MFMAs: a wave that issues all its loads before its
+    // MFMAs stalls on the load queue while the matrix pipe idles.
+    auto mfma_step_dma = [&](auto first, const int8_t* const (&sp)[LPW], bool do_issue, int slot, int ksrc) {
+        int8_t* st = ring + slot * STAGE;
+        constexpr int NM = WR * L * 2 * WCP;
+        constexpr int PER = NM / LPW > 0 ? NM / LPW : 1;
+#pragma unroll
+        for (int ii = 0; ii < WR; ++ii)
+#pragma unroll
+            for (int l = 0; l < L; ++l)
+#pragma unroll
+                for (int j = 0; j < (2 * WCP); ++j) {
+                    if constexpr (decltype(first)::value)
+                        acc[ii][l][j] = mfma32(fa[0][ii][l], fb[0][j], v16i{});
+                    else
+                        acc[ii][l][j] = mfma32(fa[0][ii][l], fb[0][j], acc[ii][l][j]);
+                    const int idx = (ii * L + l) * (2 * WCP) + j + 1;
+                    if (idx % PER == 0 && idx / PER <= LPW) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (do_issue) dma16(sp[idx / PER - 1] + (int64_t)ksrc * kKB, st + dst[idx / PER - 1]);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+#pragma unroll
+        for (int c = NM / PER; c < LPW; ++c)
+            if (do_issue) dma16(sp[c] + (int64_t)ksrc * kKB, st + dst[c]);
     };
 
     // ---- stream prologue: tile 0's rows, metadata and first kS-1 stages
@@ -322,7 +356,7 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
         // stream, and run stage ks while reading stage ks+1's fragments.
         // Phase A (`next` false) refills with this tile's stages; phase B
         // (the last kS steps) with the next tile's first kS-1 stages.
-        auto kstep = [&](int ks, auto first, auto next) {
+        auto kstep = [&](int ks, auto first, auto next) __attribute__((always_inline)) {
             const int slot = (slot0 + ks) % kS;
             if (ks + 1 < nk) {
                 // the stages after ks+1 still in flight are ks+2 .. ks+kS-1
@@ -331,13 +365,12 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
                 else wait_vmcnt<0>();
             }
             lds_barrier();
-            if constexpr (!decltype(next)::value) {
-                issue(slot, src, ks + kS);
-            } else {
-                if (has_next && ks + kS - nk <= kS - 2) issue(slot, src, ks + kS - nk);
-            }
             const int nslot = (slot + 1) % kS;
-            mfma_step(0, first);
+            if constexpr (!decltype(next)::value) {
+                mfma_step_dma(first, src, true, slot, ks + kS);
+            } else {
+                mfma_step_dma(first, src, has_next && ks + kS - nk <= kS - 2, slot, ks + kS - nk);
+            }
             if (ks + 1 < nk) read_frags(nslot, 0);
             mfma_step(1, std::false_type{});
             if (ks + 1 < nk) read_frags(nslot, 1);
@@ -370,7 +403,7 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
         // swiglu_quant_kernel, at full occupancy).  The zero-point
         // correction is chosen once per tile (zg, zu are uniform), so no
         // per-element test drags its integer multiplies into the common case.
-        auto epilogue = [&](auto with_zp) {
+        auto epilogue = [&](auto with_zp) __attribute__((always_inline)) {
             constexpr bool ZP = decltype(with_zp)::value;
             const int e = cur.e, nrows = cur.nrows;
             const float sg = s_sg[e], su = s_su[e];
@@ -461,10 +494,11 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
     const int32_t* __restrict__ zp, const int32_t* __restrict__ counts,
     const int32_t* __restrict__ offsets, float* __restrict__ y) {
     using T = DownTile<L>;
+    constexpr int kSD = down_stages<L>();
     constexpr int BM = T::BM, BN = T::BN, NA = T::NA, NL = T::NL, LPW = T::LPW, WR = T::WR,
                   WCN = T::WCN, NWC = T::NWC, STAGE = T::STAGE;
     constexpr int RC = BM / HM_WAVE;  // 64-row chunks of a tile
-    __shared__ __attribute__((aligned(1024))) int8_t ring[kS * STAGE];
+    __shared__ __attribute__((aligned(1024))) int8_t ring[kSD * STAGE];
     __shared__ int32_t s_prefix[kMaxExperts + 1];
     __shared__ int32_t s_off[kMaxExperts], s_cnt[kMaxExperts];
     __shared__ float s_sd[kMaxExperts];
@@ -494,7 +528,7 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
     struct Info {
         int e, nrows, g0, n0;
     };
-    auto info = [&](int i) {
+    auto info = [&](int i) __attribute__((always_inline)) {
         const int j = tr.jbeg + i * tr.step;
         const int gm = j / nbn;
         Info t;
@@ -507,7 +541,7 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
     };
     // Z segment scales and digit sums of the tile rows (rows past nrows read
     // the last row); units spread over the waves
-    auto fetch_meta = [&](const Info& t, int m) {
+    auto fetch_meta = [&](const Info& t, int m) __attribute__((always_inline)) {
         for (int u = wave; u < (1 + L) * nbz * RC; u += kWaves) {
             const int kind = u / (nbz * RC), rem = u % (nbz * RC);
             const int b = rem / RC, ch = rem % RC;
@@ -549,7 +583,7 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
 #pragma unroll
     for (int h = 0; h < 2; ++h) rd[h] = frag_read_offset(lane, h);
     v4i fa[2][WR][L], fb[2][WCN];
-    auto read_frags = [&](int slot, int h) {
+    auto read_frags = [&](int slot, int h) __attribute__((always_inline)) {
         const int8_t* st = ring + slot * STAGE;
 #pragma unroll
         for (int ii = 0; ii < WR; ++ii)
@@ -562,7 +596,7 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
     v16i acc[WR][L][WCN];
     float facc[WR][WCN][16];
     // `first`: the first K step of a Z segment starts the partials from zero
-    auto mfma_step = [&](int h, auto first) {
+    auto mfma_step = [&](int h, auto first) __attribute__((always_inline)) {
 #pragma unroll
         for (int ii = 0; ii < WR; ++ii)
 #pragma unroll
@@ -575,24 +609,52 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
                         acc[ii][l][j] = mfma32(fa[h][ii][l], fb[h][j], acc[ii][l][j]);
                 }
     };
+    // K step h = 0 with the refill of `slot` (stage ksrc of the stream)
+    // spread between its MFMAs: a wave that issues all its loads before its
+    // MFMAs stalls on the load queue while the matrix pipe idles.
+    auto mfma_step_dma = [&](auto first, const int8_t* const (&sp)[LPW], bool do_issue, int slot, int ksrc) {
+        int8_t* st = ring + slot * STAGE;
+        constexpr int NM = WR * L * WCN;
+        constexpr int PER = NM / LPW > 0 ? NM / LPW : 1;
+#pragma unroll
+        for (int ii = 0; ii < WR; ++ii)
+#pragma unroll
+            for (int l = 0; l < L; ++l)
+#pragma unroll
+                for (int j = 0; j < WCN; ++j) {
+                    if constexpr (decltype(first)::value)
+                        acc[ii][l][j] = mfma32(fa[0][ii][l], fb[0][j], v16i{});
+                    else
+                        acc[ii][l][j] = mfma32(fa[0][ii][l], fb[0][j], acc[ii][l][j]);
+                    const int idx = (ii * L + l) * WCN + j + 1;
+                    if (idx % PER == 0 && idx / PER <= LPW) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (do_issue) dma16(sp[idx / PER - 1] + (int64_t)ksrc * kKB, st + dst[idx / PER - 1]);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+#pragma unroll
+        for (int c = NM / PER; c < LPW; ++c)
+            if (do_issue) dma16(sp[c] + (int64_t)ksrc * kKB, st + dst[c]);
+    };
 
     Info cur = info(0);
     int m = 0;
     fetch_meta(cur, 0);
-    const int8_t* src[LPW];  // this tile's sources, the next tile's from step nk-kS
+    const int8_t* src[LPW];  // this tile's sources, the next tile's from step nk-kSD
     make_src(cur, src);
     int slot0 = 0;
 #pragma unroll
-    for (int s = 0; s < kS - 1; ++s) issue(s, src, s);
+    for (int s = 0; s < kSD - 1; ++s) issue(s, src, s);
 
     for (int i = 0; i < tr.ntiles; ++i) {
         const bool has_next = i + 1 < tr.ntiles;
         const int mn = m ^ 1;
         Info nxt = cur;
         if (has_next) nxt = info(i + 1);
-        wait_vmcnt<(kS - 2) * LPW>();
+        wait_vmcnt<(kSD - 2) * LPW>();
         lds_barrier();
-        issue((slot0 + kS - 1) % kS, src, kS - 1);
+        issue((slot0 + kSD - 1) % kSD, src, kSD - 1);
         if (has_next) fetch_meta(nxt, mn);
         read_frags(slot0, 0);
         read_frags(slot0, 1);
@@ -604,20 +666,19 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
             for (int j = 0; j < WCN; ++j)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) facc[ii][j][v] = 0.0f;
-        auto dstep = [&](int ks, auto first, auto next) {
-            const int slot = (slot0 + ks) % kS;
+        auto dstep = [&](int ks, auto first, auto next) __attribute__((always_inline)) {
+            const int slot = (slot0 + ks) % kSD;
             if (ks + 1 < nk) {
-                if (has_next || ks + kS - 1 < nk) wait_vmcnt<(kS - 2) * LPW>();
+                if (has_next || ks + kSD - 1 < nk) wait_vmcnt<(kSD - 2) * LPW>();
                 else wait_vmcnt<0>();
             }
             lds_barrier();
+            const int nslot = (slot + 1) % kSD;
             if constexpr (!decltype(next)::value) {
-                issue(slot, src, ks + kS);
+                mfma_step_dma(first, src, true, slot, ks + kSD);
             } else {
-                if (has_next && ks + kS - nk <= kS - 2) issue(slot, src, ks + kS - nk);
+                mfma_step_dma(first, src, has_next && ks + kSD - nk <= kSD - 2, slot, ks + kSD - nk);
             }
-            const int nslot = (slot + 1) % kS;
-            mfma_step(0, first);
             if (ks + 1 < nk) read_frags(nslot, 0);
             mfma_step(1, std::false_type{});
             if (ks + 1 < nk) read_frags(nslot, 1);
@@ -629,7 +690,7 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
         // The zero-point correction is chosen once per tile (zd is uniform):
         // a per-element test would let the compiler hoist its integer
         // multiplies out of the branch into every fold.
-        auto fold = [&](int zb, auto with_zp) {
+        auto fold = [&](int zb, auto with_zp) __attribute__((always_inline)) {
             constexpr bool ZP = decltype(with_zp)::value;
 #pragma unroll
             for (int ii = 0; ii < WR; ++ii)
@@ -671,20 +732,28 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
                     }
                 }
         };
-        auto fold_seg = [&](int zb) {
+        auto fold_seg = [&](int zb) __attribute__((always_inline)) {
             if (zd != 0) fold(zb, std::true_type{});
             else fold(zb, std::false_type{});
         };
-        // nk and kS are even, so a Z segment (two stages) never straddles
-        // the two phases
+        // A Z segment is two stages (nk is even); phase B (the last kSD
+        // steps) may start inside one when kSD is odd.
         int ks = 0;
 #pragma clang loop unroll(disable)
-        for (; ks < nk - kS; ks += 2) {
+        for (; ks + 1 < nk - kSD; ks += 2) {
             dstep(ks, std::true_type{}, std::false_type{});
             dstep(ks + 1, std::false_type{}, std::false_type{});
             fold_seg(ks >> 1);
         }
-        if (has_next) make_src(nxt, src);
+        if (ks < nk - kSD) {
+            dstep(ks, std::true_type{}, std::false_type{});
+            if (has_next) make_src(nxt, src);
+            dstep(ks + 1, std::false_type{}, std::true_type{});
+            fold_seg(ks >> 1);
+            ks += 2;
+        } else if (has_next) {
+            make_src(nxt, src);
+        }
 #pragma clang loop unroll(disable)
         for (; ks < nk; ks += 2) {
             dstep(ks, std::true_type{}, std::true_type{});
@@ -703,7 +772,7 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
                 for (int j = 0; j < WCN; ++j) yr[32 * j] = facc[ii][j][v];
             }
         }
-        slot0 = (slot0 + nk) % kS;
+        slot0 = (slot0 + nk) % kSD;
         m = mn;
         cur = nxt;
     }
@@ -856,7 +925,8 @@ bool hm_mfma_down_ok(int64_t H, int64_t I, int64_t E, int32_t limbs) {
     if (limbs < 1 || limbs > 3 || E < 1 || E > kMaxExperts || H > (1 << 20) || I > (1 << 20))
         return false;
     const int64_t bn = limbs == 1 ? DownTile<1>::BN : limbs == 2 ? DownTile<2>::BN : DownTile<3>::BN;
-    return H % bn == 0 && H >= bn && I % kZBlock == 0 && I / kKB >= kS && I / kZBlock <= kMaxZSeg;
+    const int64_t st = limbs == 1 ? down_stages<1>() : limbs == 2 ? down_stages<2>() : down_stages<3>();
+    return H % bn == 0 && H >= bn && I % kZBlock == 0 && I / kKB >= st && I / kZBlock <= kMaxZSeg;
 }
 
 // gu: scratch for the exact g and u rows, 2 x R x I floats.
