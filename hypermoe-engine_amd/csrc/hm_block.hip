@@ -36,6 +36,10 @@ int hm_launch_down_combine_gemv(const hm_layer* L, const float* z, const int32_t
                                 const int32_t* slots, const float* scores,
                                 const float* residual, int64_t tokens, int32_t top_k,
                                 float* y_out, float* out, hipStream_t s);
+extern "C" int hm_router_topk_quant(const float* h, const float* w, int64_t tokens, int64_t hidden,
+                         int64_t experts, int32_t top_k, uint32_t flags, uint32_t* ids,
+                         float* scores, float* logits_out, int32_t* status, void* route_ws,
+                         const hm_row_quant* xq, bool* quantized, void* stream);
 int hm_route_permute_decode(const float* h, const float* w, int64_t tokens, int64_t hidden,
                             int64_t experts, int32_t top_k, uint32_t flags, uint32_t* ids,
                             float* scores, int32_t* status, void* route_ws,
@@ -199,6 +203,7 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
     // decode: the grouping is fused into the router's select (one launch
     // fewer)
     const bool fuse = gemv && H % 32 == 0 && E <= 1024 && top_k <= 64 && P <= 1024;
+    bool x_quantized = false;
     if (fuse) {
         const hm_decode_fusion f = {p.counters, 1, p.counts, p.offsets, p.perm_tokens,
                                     p.perm_weights, p.slots};
@@ -206,8 +211,13 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
                                      p.scores, status, p.route_ws, &f, stream);
         if (rc || (rc = mark(1)) || (rc = mark(2))) return rc;
     } else {
-        rc = hm_router_topk(hidden, router_w, tokens, H, E, top_k, route_bits, p.ids, p.scores,
-                            nullptr, status, p.route_ws, stream);
+        // the INT8 expert path's activation digits come out of the router's
+        // prefill select kernel when it runs (one launch fewer)
+        const hm_row_quant xq = {p.xdig, p.xscale, p.xdsum, limbs_x};
+        const bool want_q = !gemv && layer->dtype == HM_DTYPE_INT8 && p.xdig;
+        rc = hm_router_topk_quant(hidden, router_w, tokens, H, E, top_k, route_bits, p.ids,
+                                  p.scores, nullptr, status, p.route_ws, want_q ? &xq : nullptr,
+                                  &x_quantized, stream);
         if (rc || (rc = mark(1))) return rc;
         rc = hm_permute(p.ids, p.scores, tokens, top_k, E, p.counts, p.offsets, p.perm_tokens,
                         p.perm_weights, p.slots, p.permute_ws, stream);
@@ -245,8 +255,10 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
         }
         rc = hm_launch_down_gemv(layer, p.zf, counts, p.offsets, P, p.y, s);
     } else if (layer->dtype == HM_DTYPE_INT8) {
-        rc = hm_launch_quantize_rows(hidden, tokens, H, limbs_x, p.xdig, p.xscale, p.xdsum, s);
-        if (rc) return rc;
+        if (!x_quantized) {
+            rc = hm_launch_quantize_rows(hidden, tokens, H, limbs_x, p.xdig, p.xscale, p.xdsum, s);
+            if (rc) return rc;
+        }
         rc = gate_up([&] {
             return hm_launch_gateup_i8(layer, limbs_x, limbs_z, p.xdig, p.xscale, p.xdsum,
                                        tokens, counts, p.offsets, p.perm_tokens, P, p.zdig,

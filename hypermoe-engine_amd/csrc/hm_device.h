@@ -240,6 +240,71 @@ __device__ __forceinline__ float hm_recombine(const int* p, int limbs) {
     return c;
 }
 
+// One wave quantises one FP32 row of n = 256*nv floats (16-byte aligned) to
+// L fixed-point digit planes: the row max gives the step (inv = range /
+// max|x|), every element becomes rint(x * inv) split into L digits.  Plane l
+// of the row goes to digits + l * plane_stride (4 bytes per lane and float4),
+// its digit sum to dsum[l * dsum_stride] (when dsum is set), the scale
+// max|x| / range to *scale.  Shared by the row-quantisation kernel and the
+// prefill router's select kernel, so both write the same bytes.
+constexpr int kHmQuantMaxV = 16;  // n <= 4096
+template <int L>
+__device__ __forceinline__ void hm_quantize_row_wave(const float* __restrict__ xrow, int nv,
+                                                     int8_t* __restrict__ digits,
+                                                     int64_t plane_stride, float* scale,
+                                                     int32_t* __restrict__ dsum,
+                                                     int64_t dsum_stride) {
+    const int lane = threadIdx.x & (HM_WAVE - 1);
+    const float4* xr = reinterpret_cast<const float4*>(xrow);
+    float4 v[kHmQuantMaxV];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kHmQuantMaxV; ++i) {
+        if (i < nv) {
+            v[i] = xr[lane + HM_WAVE * i];
+            amax = fmaxf(fmaxf(amax, fmaxf(fabsf(v[i].x), fabsf(v[i].y))),
+                         fmaxf(fabsf(v[i].z), fabsf(v[i].w)));
+        }
+    }
+    amax = hm_wave_max_dpp(amax);
+    const float range = (float)hm_limb_range(L);
+    const float inv = amax > 0.0f ? __fdiv_rn(range, amax) : 0.0f;
+    int dl[L];
+#pragma unroll
+    for (int l = 0; l < L; ++l) dl[l] = 0;
+#pragma unroll
+    for (int i = 0; i < kHmQuantMaxV; ++i) {
+        if (i < nv) {
+            int d0[L], d1[L], d2[L], d3[L];
+            hm_digits<L>(hm_fixed_point(v[i].x, inv, range), d0);
+            hm_digits<L>(hm_fixed_point(v[i].y, inv, range), d1);
+            hm_digits<L>(hm_fixed_point(v[i].z, inv, range), d2);
+            hm_digits<L>(hm_fixed_point(v[i].w, inv, range), d3);
+#pragma unroll
+            for (int l = 0; l < L; ++l) {
+                const uint32_t word = (uint32_t)(d0[l] & 255) | ((uint32_t)(d1[l] & 255) << 8) |
+                                      ((uint32_t)(d2[l] & 255) << 16) | ((uint32_t)(d3[l] & 255) << 24);
+                reinterpret_cast<uint32_t*>(digits + (int64_t)l * plane_stride)[lane + HM_WAVE * i] = word;
+                dl[l] += d0[l] + d1[l] + d2[l] + d3[l];
+            }
+        }
+    }
+#pragma unroll
+    for (int l = 0; l < L; ++l) {
+        const int sm = hm_wave_sum_dpp(dl[l]);
+        if (lane == 0 && dsum) dsum[(int64_t)l * dsum_stride] = sm;
+    }
+    if (lane == 0) *scale = amax > 0.0f ? __fdiv_rn(amax, range) : 0.0f;
+}
+
+// Where a fused row quantisation writes (digits == nullptr: none).
+struct hm_row_quant {
+    int8_t* digits;    // [limbs][rows][n]
+    float* scales;     // [rows]
+    int32_t* dsum;     // [limbs][rows] or nullptr
+    int32_t limbs;
+};
+
 // Grouped-GEMM tile lookup: tiles of expert e are ceil(counts[e]/tile_m),
 // experts in ascending id.  Which expert, and which tile of it, does linear
 // tile index `tile` name?  False when `tile` is past the last tile.

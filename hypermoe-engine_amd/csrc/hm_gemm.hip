@@ -61,7 +61,7 @@ __global__ __launch_bounds__(kBlock) void limb_quantize_rows_kernel(
 // the row is read once into registers (lane: floats 4*(lane + 64 i) .. +3),
 // reduced with DPP, and each lane stores its four digits of a plane as one
 // 32-bit word.
-constexpr int kQMaxV = 16;
+constexpr int kQMaxV = kHmQuantMaxV;
 
 template <int L>
 __global__ __launch_bounds__(kBlock) void limb_quantize_rows_vec_kernel(
@@ -70,46 +70,8 @@ __global__ __launch_bounds__(kBlock) void limb_quantize_rows_vec_kernel(
     const int lane = threadIdx.x & (HM_WAVE - 1);
     const int64_t r = (int64_t)blockIdx.x * (kBlock / HM_WAVE) + threadIdx.x / HM_WAVE;
     if (r >= rows) return;
-    const float4* xr = reinterpret_cast<const float4*>(x + r * n);
-    float4 v[kQMaxV];
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kQMaxV; ++i) {
-        if (i < nv) {
-            v[i] = xr[lane + HM_WAVE * i];
-            amax = fmaxf(fmaxf(amax, fmaxf(fabsf(v[i].x), fabsf(v[i].y))),
-                         fmaxf(fabsf(v[i].z), fabsf(v[i].w)));
-        }
-    }
-    amax = hm_wave_max_dpp(amax);
-    const float range = (float)hm_limb_range(L);
-    const float inv = amax > 0.0f ? __fdiv_rn(range, amax) : 0.0f;
-    int dl[L];
-#pragma unroll
-    for (int l = 0; l < L; ++l) dl[l] = 0;
-#pragma unroll
-    for (int i = 0; i < kQMaxV; ++i) {
-        if (i < nv) {
-            int d0[L], d1[L], d2[L], d3[L];
-            hm_digits<L>(hm_fixed_point(v[i].x, inv, range), d0);
-            hm_digits<L>(hm_fixed_point(v[i].y, inv, range), d1);
-            hm_digits<L>(hm_fixed_point(v[i].z, inv, range), d2);
-            hm_digits<L>(hm_fixed_point(v[i].w, inv, range), d3);
-#pragma unroll
-            for (int l = 0; l < L; ++l) {
-                const uint32_t word = (uint32_t)(d0[l] & 255) | ((uint32_t)(d1[l] & 255) << 8) |
-                                      ((uint32_t)(d2[l] & 255) << 16) | ((uint32_t)(d3[l] & 255) << 24);
-                reinterpret_cast<uint32_t*>(digits + ((int64_t)l * rows + r) * n)[lane + HM_WAVE * i] = word;
-                dl[l] += d0[l] + d1[l] + d2[l] + d3[l];
-            }
-        }
-    }
-#pragma unroll
-    for (int l = 0; l < L; ++l) {
-        const int s = hm_wave_sum_dpp(dl[l]);
-        if (lane == 0 && dsum) dsum[(int64_t)l * rows + r] = s;
-    }
-    if (lane == 0) scales[r] = amax > 0.0f ? __fdiv_rn(amax, range) : 0.0f;
+    hm_quantize_row_wave<L>(x + r * n, nv, digits + r * n, rows * n, scales + r,
+                            dsum ? dsum + r : nullptr, rows);
 }
 
 // Exact limb partials against a packed [cols x inner] INT8 matrix (test hook

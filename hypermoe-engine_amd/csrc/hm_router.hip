@@ -848,7 +848,7 @@ __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
     const double* __restrict__ hn2, const double* __restrict__ wn2, int64_t tokens,
     int64_t hidden, int64_t experts, int splits, int32_t top_k, uint32_t flags,
     float* __restrict__ logits, uint32_t* __restrict__ ids, float* __restrict__ scores,
-    int32_t* status) {
+    int32_t* status, hm_row_quant xq) {
     // per wave: experts floats for the sequential softmax sum, then two
     // fallback buffers (kFBuf each, 16-byte aligned)
     extern __shared__ __attribute__((aligned(16))) char dyn_lds[];
@@ -1044,6 +1044,19 @@ __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
         if (valid[j] && logits) logits[t * experts + lane + HM_WAVE * j] = v[j];
     select_token<EPL>(v, valid, lane, wave, t, experts, top_k, flags, ids, scores, status,
                       seq_lds);
+    // The token's row in fixed-point digits for the INT8 expert GEMMs (the
+    // block's activation quantisation, fused here: this kernel's time is set
+    // by a few waves' sequential chains, the rest of the machine is idle).
+    if (xq.digits) {
+        const int nv = (int)(hidden / 256);
+        int8_t* d = xq.digits + t * hidden;
+        int32_t* ds = xq.dsum ? xq.dsum + t : nullptr;
+        switch (xq.limbs) {
+        case 1: hm_quantize_row_wave<1>(hrow, nv, d, tokens * hidden, xq.scales + t, ds, tokens); break;
+        case 2: hm_quantize_row_wave<2>(hrow, nv, d, tokens * hidden, xq.scales + t, ds, tokens); break;
+        default: hm_quantize_row_wave<3>(hrow, nv, d, tokens * hidden, xq.scales + t, ds, tokens); break;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1366,11 +1379,29 @@ int hm_route_permute_decode(const float* h, const float* w, int64_t tokens, int6
 
 extern "C" {
 
+int hm_router_topk_quant(const float* h, const float* w, int64_t tokens,
+                         int64_t hidden, int64_t experts, int32_t top_k,
+                         uint32_t flags, uint32_t* ids, float* scores,
+                         float* logits_out, int32_t* status, void* route_ws,
+                         const hm_row_quant* xq, bool* quantized, void* stream);
+
 int hm_router_topk(const float* h, const float* w, int64_t tokens,
                    int64_t hidden, int64_t experts, int32_t top_k,
                    uint32_t flags, uint32_t* ids, float* scores,
                    float* logits_out, int32_t* status, void* route_ws,
                    void* stream) {
+    return hm_router_topk_quant(h, w, tokens, hidden, experts, top_k, flags, ids, scores,
+                                logits_out, status, route_ws, nullptr, nullptr, stream);
+}
+
+// hm_router_topk, and where the prefill select kernel runs, the rows of h
+// quantised into xq's digit planes as well (*quantized tells the caller).
+int hm_router_topk_quant(const float* h, const float* w, int64_t tokens,
+                         int64_t hidden, int64_t experts, int32_t top_k,
+                         uint32_t flags, uint32_t* ids, float* scores,
+                         float* logits_out, int32_t* status, void* route_ws,
+                         const hm_row_quant* xq, bool* quantized, void* stream) {
+    if (quantized) *quantized = false;
     // RouterConfig::validate (src/router/RouterConfig.cpp:9-22)
     HM_REQUIRE(experts > 0 && top_k > 0 && top_k <= experts);
     HM_REQUIRE(h && w && ids && scores && tokens > 0 && hidden > 0);
@@ -1406,10 +1437,17 @@ int hm_router_topk(const float* h, const float* w, int64_t tokens,
         HM_LAUNCHED();
         const size_t split_bytes =
             (kBlock / HM_WAVE) * ((((size_t)experts * 4 + 15) / 16) * 16 + 2 * (size_t)kFBuf);
+        hm_row_quant q = {nullptr, nullptr, nullptr, 0};
+        if (xq && xq->digits && xq->scales && xq->limbs >= 1 && xq->limbs <= 3 &&
+            hidden % 256 == 0 && hidden / 256 <= kHmQuantMaxV &&
+            (uintptr_t)xq->digits % 4 == 0) {
+            q = *xq;
+            if (quantized) *quantized = true;
+        }
 #define HM_SELECTS(N)                                                                     \
         hipLaunchKernelGGL(router_select_split_kernel<N>, sgrid, dim3(kBlock), split_bytes, \
                            hm_stream(stream), h, wt, part, hn2, wn2, tokens, hidden, experts, \
-                           sp, top_k, flags, logits, ids, scores, status)
+                           sp, top_k, flags, logits, ids, scores, status, q)
         if (epl <= 1) HM_SELECTS(1);
         else if (epl <= 2) HM_SELECTS(2);
         else if (epl <= 4) HM_SELECTS(4);
