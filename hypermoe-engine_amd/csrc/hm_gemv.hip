@@ -6,8 +6,8 @@
 // handful of multiply-adds per byte.  These kernels split K across the 64
 // lanes of a wave (each lane owns fixed 16-byte slices of every weight row
 // and the matching activation slices), stream each weight row once from HBM
-// into LDS with coalesced 16-byte direct loads, and reduce each output's
-// per-lane partial dot products across the wave.
+// with coalesced 16-byte loads, and reduce the per-lane partial dot products
+// of all of a wave's outputs across the wave in one butterfly.
 //
 // Arithmetic: the reference computes y = sum_k x_k * (float(q_k - zp) * s)
 // in FP32 (CpuTensorBackend.cpp:173-186).  Here the dequantisation is
@@ -45,6 +45,33 @@ __device__ int hm_active_expert(const int32_t* __restrict__ counts, int64_t expe
         const int c = __popcll(m);
         if (slot < seen + c) {
             // position of the (slot - seen)-th set bit
+            unsigned long long mm = m;
+            for (int i = 0; i < slot - seen; ++i) mm &= mm - 1;
+            return b * 64 + __ffsll((long long)mm) - 1;
+        }
+        seen += c;
+    }
+    return -1;
+}
+
+// The same for E <= 256 with every count load issued at once (one round
+// trip instead of one per 64-expert group).
+__device__ int hm_active_expert_256(const int32_t* __restrict__ counts, int64_t experts,
+                                    int slot) {
+    const int lane = threadIdx.x & 63;
+    int cnt[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const int64_t e = (int64_t)b * 64 + lane;
+        const int c = counts[e < experts ? e : experts - 1];
+        cnt[b] = e < experts ? c : 0;
+    }
+    int seen = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const unsigned long long m = __ballot(cnt[b] > 0);
+        const int c = __popcll(m);
+        if (slot < seen + c) {
             unsigned long long mm = m;
             for (int i = 0; i < slot - seen; ++i) mm &= mm - 1;
             return b * 64 + __ffsll((long long)mm) - 1;
@@ -93,15 +120,12 @@ __device__ __forceinline__ void bytes_to_float(uint32_t d, float* f) {
 // Lane slices of a K-long row (K % 16 == 0, K <= 1024*P): piece p of lane
 // l is the 16 bytes at k = 1024 p + 16 l, present when that is below K.
 //
-// A wave owns kRowsPerWave weight rows.  All of them go straight to the
-// wave's own LDS region with 16-byte global_load_lds (row j, piece p at
-// (j*P + p) KB; lane l's bytes at +16 l), so no registers hold weights and
-// the occupancy stays high; each lane later reads back only the bytes it
-// loaded itself, so a vmcnt wait is the only synchronisation.  Every
-// activation row of the expert's group then sweeps the 8 rows from LDS, one
-// output at a time (a small live register set, so many waves per CU keep
-// many rows in flight): the weights are read from HBM once whatever the
-// group size.
+// A wave owns kRowsPerWave weight rows.  Each lane loads its own 16-byte
+// slices of them straight into registers (the lane later uses only the
+// bytes it loaded, so nothing is shared through LDS and nothing waits on
+// another wave); every activation row of the expert's group then meets
+// them, the rows' partial sums are reduced together, and the weights are
+// read from HBM once whatever the group size.
 //
 // GATEUP: rows j < kNPW are gate rows n0+j, the others the up rows of the
 // same n; the inputs are hidden[perm_tokens[g]]; the output z[g, n] =
@@ -113,7 +137,7 @@ __device__ __forceinline__ void gemv_body(
     int64_t N, const int8_t* __restrict__ packed, int64_t hidden, int64_t inter,
     const float* __restrict__ scale, const int32_t* __restrict__ zp,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
-    float* __restrict__ out, const unsigned long long* s_exp2, int8_t* lds, int e, int lane,
+    float* __restrict__ out, const unsigned long long* s_exp2, int e, int lane,
     int wave) {
     constexpr int kWaves = kGemvThreads / 64;
     const int8_t* ebase = packed + (int64_t)e * 3 * hidden * inter;
@@ -121,7 +145,9 @@ __device__ __forceinline__ void gemv_body(
                               : ((int64_t)blockIdx.x * kWaves + wave) * kRowsPerWave;
     const int64_t g0 = offsets[e];
     const int rows = counts[e];
-    // weights -> LDS
+    // weights -> registers: lane l's own 16-byte slices of every row (all
+    // loads go out before the activations')
+    uint4 wreg[kRowsPerWave][P];
 #pragma unroll
     for (int j = 0; j < kRowsPerWave; ++j) {
         const int proj = GATEUP ? j / kNPW : 2;
@@ -130,7 +156,7 @@ __device__ __forceinline__ void gemv_body(
 #pragma unroll
         for (int p = 0; p < P; ++p) {
             const int64_t k = 1024 * p + 16 * lane;
-            if (k < K) dma16(row + k, lds + (j * P + p) * 1024);
+            wreg[j][p] = k < K ? *reinterpret_cast<const uint4*>(row + k) : make_uint4(0, 0, 0, 0);
         }
     }
     // each row's activations are loaded before the wait: the first row's
@@ -150,7 +176,6 @@ __device__ __forceinline__ void gemv_body(
                 x[p][4 * i + 2] = v.z; x[p][4 * i + 3] = v.w;
             }
         }
-        if (r == 0) wait_vmcnt<0>();  // the weights (and these rows) have landed
         float xs = 0.0f;
 #pragma unroll
         for (int p = 0; p < P; ++p)
@@ -158,40 +183,46 @@ __device__ __forceinline__ void gemv_body(
             for (int i = 0; i < 16; ++i) xs += x[p][i];
         float xv[1] = {xs};
         const float xsum = wave_reduce_many<1>(xv);
-        // one output at a time (gate and up rows of one n together): the
-        // live set stays at one row's 16*P weights
-#pragma unroll 1
-        for (int o = 0; o < (GATEUP ? kNPW : kRowsPerWave); ++o) {
-            float v[GATEUP ? 2 : 1];
+        // the partial dot products of all kRowsPerWave weight rows, then one
+        // reduction for all of them (row j's sum lands in lanes 16j .. 16j+15)
+        float a[kRowsPerWave];
 #pragma unroll
-            for (int h = 0; h < (GATEUP ? 2 : 1); ++h) {
-                const int j = GATEUP ? o + kNPW * h : o;
-                float a = 0.0f;
+        for (int j = 0; j < kRowsPerWave; ++j) {
+            a[j] = 0.0f;
 #pragma unroll
-                for (int p = 0; p < P; ++p) {
-                    // lanes without a piece read their own unused slot; x is 0
-                    const uint4 wv =
-                        *reinterpret_cast<const uint4*>(lds + (j * P + p) * 1024 + 16 * lane);
-                    const uint32_t d[4] = {wv.x, wv.y, wv.z, wv.w};
+            for (int p = 0; p < P; ++p) {
+                // lanes without a piece hold zero weights; x is 0 there too
+                const uint32_t d[4] = {wreg[j][p].x, wreg[j][p].y, wreg[j][p].z, wreg[j][p].w};
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        float f[4];
-                        bytes_to_float(d[q], f);
+                for (int q = 0; q < 4; ++q) {
+                    // converted per row (hoisted out of the row loop, every
+                    // weight row's floats would stay live)
+                    uint32_t dq = d[q];
+                    asm volatile("" : "+v"(dq));
+                    float f[4];
+                    bytes_to_float(dq, f);
 #pragma unroll
-                        for (int b = 0; b < 4; ++b) a = __builtin_fmaf(x[p][4 * q + b], f[b], a);
-                    }
+                    for (int b = 0; b < 4; ++b) a[j] = __builtin_fmaf(x[p][4 * q + b], f[b], a[j]);
                 }
-                float av[1] = {a};
-                const float tot = wave_reduce_many<1>(av);
-                const int proj = GATEUP ? h : 2;
-                const float sc = scale[e * 3 + proj];
-                const float zc = (float)(128 + zp[e * 3 + proj]);
-                v[h] = __fmul_rn(__fsub_rn(tot, __fmul_rn(zc, xsum)), sc);
             }
-            if (lane == 0) {
-                const float y = GATEUP ? __fmul_rn(hm_silu_t(v[0], s_exp2), v[GATEUP ? 1 : 0]) : v[0];
-                out[(g0 + r) * N + n0 + o] = y;
-            }
+        }
+        const float tot = wave_reduce_many<kRowsPerWave>(a);
+        // lane 16j holds row j's sum; each output lane gathers its rows
+        constexpr int kSpan = HM_WAVE / kRowsPerWave;
+        if (GATEUP) {
+            // lanes 0 .. kNPW-1: output o = lane from gate row o and up row kNPW+o
+            const int o = lane < kNPW ? lane : 0;
+            const float tg = __shfl(tot, kSpan * o, HM_WAVE);
+            const float tu = __shfl(tot, kSpan * (kNPW + o), HM_WAVE);
+            const float vg = __fmul_rn(__fsub_rn(tg, __fmul_rn((float)(128 + zp[e * 3 + 0]), xsum)),
+                                       scale[e * 3 + 0]);
+            const float vu = __fmul_rn(__fsub_rn(tu, __fmul_rn((float)(128 + zp[e * 3 + 1]), xsum)),
+                                       scale[e * 3 + 1]);
+            if (lane < kNPW) out[(g0 + r) * N + n0 + o] = __fmul_rn(hm_silu_t(vg, s_exp2), vu);
+        } else {
+            const float v = __fmul_rn(__fsub_rn(tot, __fmul_rn((float)(128 + zp[e * 3 + 2]), xsum)),
+                                      scale[e * 3 + 2]);
+            if (lane % kSpan == 0) out[(g0 + r) * N + n0 + lane / kSpan] = v;
         }
     }
 }
@@ -204,16 +235,16 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_w8_kernel(
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
     float* __restrict__ out) {
     constexpr int kWaves = kGemvThreads / 64;
-    __shared__ __attribute__((aligned(1024))) int8_t wl[kWaves][kRowsPerWave * P * 1024];
     __shared__ unsigned long long s_exp2[32];
     if (GATEUP) hm_load_exp2_table(s_exp2);
     __syncthreads();
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int e = hm_active_expert(counts, experts, (int)blockIdx.y);
+    const int e = experts <= 256 ? hm_active_expert_256(counts, experts, (int)blockIdx.y)
+                                 : hm_active_expert(counts, experts, (int)blockIdx.y);
     if (e < 0) return;
     gemv_body<P, GATEUP>(x_src, perm_tokens, K, N, packed, hidden, inter, scale, zp, counts,
-                         offsets, out, s_exp2, wl[wave], e, lane, wave);
+                         offsets, out, s_exp2, e, lane, wave);
 }
 
 template <int P, bool GATEUP>
@@ -247,9 +278,11 @@ int dispatch_gemv(int64_t K, const float* x_src, const int32_t* perm_tokens, int
 // grouped row g in LDS, and then forms the tokens' outputs for its columns
 // with hm_combine's arithmetic.  No workgroup needs another's results, so
 // there is no device-wide synchronisation, and y goes to memory only when
-// the caller asks for the expert outputs.  Each y is computed with exactly
-// gemv_body's DOWN arithmetic (same lane slices, same reduction), so the
-// results equal the two-kernel path's.  T <= 16, top_k <= 16, I <= 1024.
+// the caller asks for the expert outputs.  Each y uses gemv_body's DOWN
+// lane slices; the 8 columns' partial sums are reduced across the wave
+// together (one butterfly for all of them, not one per column), so y
+// agrees with the two-kernel path to rounding.  T <= 16, top_k <= 16,
+// I <= 1024.
 // ---------------------------------------------------------------------------
 constexpr int kDcCols = 8;
 constexpr int kDcWaves = 16;
@@ -347,26 +380,33 @@ __global__ __launch_bounds__(64 * kDcWaves) void gemv_down_combine_kernel(
             for (int i = 0; i < 16; ++i) xs += x[i];
             float xv[1] = {xs};
             const float xsum = wave_reduce_many<1>(xv);
-#pragma unroll 1
+            // the kDcCols partial dot products of this lane, then one
+            // reduction for all of them (column j ends up in lanes 8j .. 8j+7)
+            float acc[kDcCols];
+#pragma unroll
             for (int j = 0; j < kDcCols; ++j) {
-                float acc = 0.0f;
+                acc[j] = 0.0f;
                 // lanes without a piece read their own unused slot; x is 0
                 const uint4 wv = *reinterpret_cast<const uint4*>(lds + j * 1024 + 16 * lane);
                 const uint32_t d[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
+                    // converted per row (hoisted out of the row loop, the 8
+                    // rows' 128 floats would spill)
+                    uint32_t dq = d[q];
+                    asm volatile("" : "+v"(dq));
                     float f[4];
-                    bytes_to_float(d[q], f);
+                    bytes_to_float(dq, f);
 #pragma unroll
-                    for (int b = 0; b < 4; ++b) acc = __builtin_fmaf(x[4 * q + b], f[b], acc);
+                    for (int b = 0; b < 4; ++b) acc[j] = __builtin_fmaf(x[4 * q + b], f[b], acc[j]);
                 }
-                float av[1] = {acc};
-                const float tot = wave_reduce_many<1>(av);
-                const float y = __fmul_rn(__fsub_rn(tot, __fmul_rn(zc, xsum)), sc);
-                if (lane == 0) {
-                    s_y[(g0 + r) & (kDcPairs - 1)][j] = y;
-                    if (y_out) y_out[(g0 + r) * H + n0 + j] = y;
-                }
+            }
+            const float tot = wave_reduce_many<kDcCols>(acc);
+            const int jl = lane / (HM_WAVE / kDcCols);
+            const float y = __fmul_rn(__fsub_rn(tot, __fmul_rn(zc, xsum)), sc);
+            if (lane % (HM_WAVE / kDcCols) == 0) {
+                s_y[(g0 + r) & (kDcPairs - 1)][jl] = y;
+                if (y_out) y_out[(g0 + r) * H + n0 + jl] = y;
             }
         }
     }
