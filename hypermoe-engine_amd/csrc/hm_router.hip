@@ -802,25 +802,31 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(
 
 // Fallback chains of the split select.  A wave's uncertified logits are
 // taken kFN at a time: lane f < kFN runs the reference's chain (k
-// ascending) for the f-th of them, while the whole wave stages the next
+// ascending) for the f-th of them.  The whole wave stages the next
 // kFK-long piece of their W columns (rows of the transposed copy the
 // matrix-core kernel wrote) and of the token's h row into LDS with 16-byte
-// DMA (double-buffered), so the chains wait on LDS rather than on one
-// global load per step.
-constexpr int kFK = 256;                        // k per staged piece
+// DMA (double-buffered), then forms that piece's exact products
+// double(h_k) * double(w_k) (48-bit, exact in FP64) for both chains in an
+// LDS product buffer, so a chain step is one dependent FP64 add,
+// acc + p_k == fma(h_k, w_k, acc), with no conversions on its path.
+constexpr int kFK = 128;                        // k per staged piece
 constexpr int kFN = 2;                          // chains per round
-constexpr int kFBuf = (kFN + 1) * kFK * 4;      // one buffer: columns + h (3 KB)
-constexpr int kFDma = kFN + 1;                  // 16-byte DMA instructions per piece
-static_assert(kFK == 4 * HM_WAVE, "one 16-byte DMA per staged row piece");
+constexpr int kFBuf = 4 * kFK * 4;              // one buffer: 2 columns, h, pad (2 KB)
+constexpr int kFProd = kFN * kFK * 8;           // products of one piece (2 KB)
+constexpr int kFWave = 2 * kFBuf + kFProd;      // fallback LDS per wave
+constexpr int kFDma = 2;                        // 16-byte DMA instructions per piece
+static_assert(kFK == 2 * HM_WAVE && kFN == 2, "half a wave per staged row piece");
 
 __device__ __forceinline__ void fallback_issue(char* buf, const float* __restrict__ hrow,
                                                const float* __restrict__ wt, int64_t hidden,
                                                int64_t k0, const int (&fe)[kFN], int lane) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this buffer's last reads are done
-    const int64_t k = min(k0 + 4 * lane, hidden - 4);  // past the end: unused
-#pragma unroll
-    for (int f = 0; f < kFN; ++f) dma16(wt + (int64_t)fe[f] * hidden + k, buf + 4 * kFK * f);
-    dma16(hrow + k, buf + 4 * kFK * kFN);
+    const int half = lane >> 5;
+    const int64_t k = min(k0 + 4 * (lane & 31), hidden - 4);  // past the end: unused
+    // lanes 0-31: column 0, lanes 32-63: column 1; then h twice (the second
+    // copy lands in the pad)
+    dma16(wt + (int64_t)fe[half] * hidden + k, buf);
+    dma16(hrow + k, buf + 2 * 4 * kFK);
 }
 
 // The idx-th set bit over the masks need[0..EPL) in (j, lane) order:
@@ -858,7 +864,8 @@ __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
     if (t >= tokens) return;
     const int64_t seq_stride = ((experts * 4 + 15) / 16) * 16;
     float* seq_lds = reinterpret_cast<float*>(dyn_lds);  // indexed by wave * experts
-    char* fb = dyn_lds + (kBlock / HM_WAVE) * seq_stride + (int64_t)wave * 2 * kFBuf;
+    char* fb = dyn_lds + (kBlock / HM_WAVE) * seq_stride + (int64_t)wave * kFWave;
+    double* fprod = reinterpret_cast<double*>(fb + 2 * kFBuf);
     const double u = 0x1p-53;
     const double n = (double)hidden;
     const double gam = n * u / (1.0 - n * u);
@@ -1004,30 +1011,39 @@ __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
             }
             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
             const int kc = (int)min((int64_t)kFK, hidden - c * kFK);  // a multiple of 16
+            {
+                // the piece's products: lane l forms k = 2l, 2l+1 of both chains
+                const float2 hv = reinterpret_cast<const float2*>(cur + 2 * 4 * kFK)[lane];
+                const float2 w0 = reinterpret_cast<const float2*>(cur)[lane];
+                const float2 w1 = reinterpret_cast<const float2*>(cur + 4 * kFK)[lane];
+                const double h0 = (double)hv.x, h1 = (double)hv.y;
+                reinterpret_cast<double2*>(fprod)[lane] = double2{h0 * (double)w0.x, h1 * (double)w0.y};
+                reinterpret_cast<double2*>(fprod + kFK)[lane] = double2{h0 * (double)w1.x, h1 * (double)w1.y};
+            }
+            // (one wave's LDS accesses complete in order: the chain lanes'
+            // reads below see every lane's products)
             if (lane < nf) {
-                // 16 k per step; the next step's LDS reads go out before
-                // this step's dependent chain
-                const float4* c4 = reinterpret_cast<const float4*>(cur) + lane * (kFK / 4);
-                const float4* h4 = reinterpret_cast<const float4*>(cur + 4 * kFN * kFK);
-                float4 ha[4], wa[4];
+                const double2* pp = reinterpret_cast<const double2*>(fprod + lane * kFK);
+                double2 pa[4];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) { ha[q] = h4[q]; wa[q] = c4[q]; }
-                for (int kk = 0; kk < kc; kk += 16) {
-                    const int nx = kk + 16 < kc ? (kk + 16) / 4 : kk / 4;
-                    float4 hb[4], wb[4];
+                for (int q = 0; q < 4; ++q) pa[q] = pp[q];
+                for (int kk = 0; kk < kc; kk += 8) {
+                    const int nx = kk + 8 < kc ? (kk + 8) / 2 : kk / 2;
+                    double2 pb[4];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) { hb[q] = h4[nx + q]; wb[q] = c4[nx + q]; }
+                    for (int q = 0; q < 4; ++q) pb[q] = pp[nx + q];
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
-                        acc = __builtin_fma((double)ha[q].x, (double)wa[q].x, acc);
-                        acc = __builtin_fma((double)ha[q].y, (double)wa[q].y, acc);
-                        acc = __builtin_fma((double)ha[q].z, (double)wa[q].z, acc);
-                        acc = __builtin_fma((double)ha[q].w, (double)wa[q].w, acc);
+                        acc = acc + pa[q].x;
+                        acc = acc + pa[q].y;
                     }
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) { ha[q] = hb[q]; wa[q] = wb[q]; }
+                    for (int q = 0; q < 4; ++q) pa[q] = pb[q];
                 }
             }
+            // the products are rewritten for the next piece only after
+            // the chains have read them
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         }
         if (lane < nf && !isfinite(acc)) hm_status_or(status, HM_STATUS_NONFINITE_SCORE);
 #pragma unroll
@@ -1436,7 +1452,7 @@ int hm_router_topk_quant(const float* h, const float* w, int64_t tokens,
                            (int)(hidden / sp), part, wt, hn2, wn2);
         HM_LAUNCHED();
         const size_t split_bytes =
-            (kBlock / HM_WAVE) * ((((size_t)experts * 4 + 15) / 16) * 16 + 2 * (size_t)kFBuf);
+            (kBlock / HM_WAVE) * ((((size_t)experts * 4 + 15) / 16) * 16 + (size_t)kFWave);
         hm_row_quant q = {nullptr, nullptr, nullptr, 0};
         if (xq && xq->digits && xq->scales && xq->limbs >= 1 && xq->limbs <= 3 &&
             hidden % 256 == 0 && hidden / 256 <= kHmQuantMaxV &&
