@@ -298,8 +298,16 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
     // K step h = 0 with the refill of `slot` (stage ksrc of the stream)
     // spread between its MFMAs: a wave that issues all its loads before its
     // MFMAs stalls on the load queue while the matrix pipe idles.
-    auto mfma_step_dma = [&](auto first, const int8_t* const (&sp)[LPW], bool do_issue, int slot, int ksrc) {
+    auto mfma_step_dma = [&](auto first, const int8_t* const (&sp)[LPW], bool do_issue, int slot,
+                             int ksrc, bool act) __attribute__((always_inline)) {
         int8_t* st = ring + slot * STAGE;
+        if (!act) {
+            // no rows of this wave in the tile: only the loads
+            if (do_issue)
+#pragma unroll
+                for (int c = 0; c < LPW; ++c) dma16(sp[c] + (int64_t)ksrc * kKB, st + dst[c]);
+            return;
+        }
         constexpr int NM = WR * L * 2 * WCP;
         constexpr int PER = NM / LPW > 0 ? NM / LPW : 1;
 #pragma unroll
@@ -349,8 +357,13 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
         lds_barrier();
         issue((slot0 + kS - 1) % kS, src, kS - 1);
         if (has_next) fetch_rows(nxt, mn);
-        read_frags(slot0, 0);
-        read_frags(slot0, 1);
+        // a wave whose rows all lie past the tile's last row (an expert's
+        // partial last tile) skips its fragment reads and MFMAs
+        const bool act = 32 * WR * wr < cur.nrows;
+        if (act) {
+            read_frags(slot0, 0);
+            read_frags(slot0, 1);
+        }
         // One K step: wait for stage ks+1, publish it, refill the slot of
         // stage ks (its fragments are in registers) with stage ks+kS of the
         // stream, and run stage ks while reading stage ks+1's fragments.
@@ -367,13 +380,15 @@ __global__ __launch_bounds__(kThreads) void gateup_mfma_kernel(
             lds_barrier();
             const int nslot = (slot + 1) % kS;
             if constexpr (!decltype(next)::value) {
-                mfma_step_dma(first, src, true, slot, ks + kS);
+                mfma_step_dma(first, src, true, slot, ks + kS, act);
             } else {
-                mfma_step_dma(first, src, has_next && ks + kS - nk <= kS - 2, slot, ks + kS - nk);
+                mfma_step_dma(first, src, has_next && ks + kS - nk <= kS - 2, slot, ks + kS - nk, act);
             }
-            if (ks + 1 < nk) read_frags(nslot, 0);
-            mfma_step(1, std::false_type{});
-            if (ks + 1 < nk) read_frags(nslot, 1);
+            if (act) {
+                if (ks + 1 < nk) read_frags(nslot, 0);
+                mfma_step(1, std::false_type{});
+                if (ks + 1 < nk) read_frags(nslot, 1);
+            }
         };
         int ks = 0;
         if (nk > kS) {
@@ -612,8 +627,16 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
     // K step h = 0 with the refill of `slot` (stage ksrc of the stream)
     // spread between its MFMAs: a wave that issues all its loads before its
     // MFMAs stalls on the load queue while the matrix pipe idles.
-    auto mfma_step_dma = [&](auto first, const int8_t* const (&sp)[LPW], bool do_issue, int slot, int ksrc) {
+    auto mfma_step_dma = [&](auto first, const int8_t* const (&sp)[LPW], bool do_issue, int slot,
+                             int ksrc, bool act) __attribute__((always_inline)) {
         int8_t* st = ring + slot * STAGE;
+        if (!act) {
+            // no rows of this wave in the tile: only the loads
+            if (do_issue)
+#pragma unroll
+                for (int c = 0; c < LPW; ++c) dma16(sp[c] + (int64_t)ksrc * kKB, st + dst[c]);
+            return;
+        }
         constexpr int NM = WR * L * WCN;
         constexpr int PER = NM / LPW > 0 ? NM / LPW : 1;
 #pragma unroll
@@ -656,8 +679,13 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
         lds_barrier();
         issue((slot0 + kSD - 1) % kSD, src, kSD - 1);
         if (has_next) fetch_meta(nxt, mn);
-        read_frags(slot0, 0);
-        read_frags(slot0, 1);
+        // a wave whose rows all lie past the tile's last row (an expert's
+        // partial last tile) skips its fragment reads and MFMAs
+        const bool act = 32 * WR * wr < cur.nrows;
+        if (act) {
+            read_frags(slot0, 0);
+            read_frags(slot0, 1);
+        }
         const float sd = s_sd[cur.e];
         const int zd = s_zd[cur.e];
 #pragma unroll
@@ -675,13 +703,15 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
             lds_barrier();
             const int nslot = (slot + 1) % kSD;
             if constexpr (!decltype(next)::value) {
-                mfma_step_dma(first, src, true, slot, ks + kSD);
+                mfma_step_dma(first, src, true, slot, ks + kSD, act);
             } else {
-                mfma_step_dma(first, src, has_next && ks + kSD - nk <= kSD - 2, slot, ks + kSD - nk);
+                mfma_step_dma(first, src, has_next && ks + kSD - nk <= kSD - 2, slot, ks + kSD - nk, act);
             }
-            if (ks + 1 < nk) read_frags(nslot, 0);
-            mfma_step(1, std::false_type{});
-            if (ks + 1 < nk) read_frags(nslot, 1);
+            if (act) {
+                if (ks + 1 < nk) read_frags(nslot, 0);
+                mfma_step(1, std::false_type{});
+                if (ks + 1 < nk) read_frags(nslot, 1);
+            }
         };
         // end of Z segment zb: exact partials -> float.  Within one 128-wide
         // segment |P_l| <= 2^22 (with a zero-point correction), so two
@@ -733,6 +763,7 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
                 }
         };
         auto fold_seg = [&](int zb) __attribute__((always_inline)) {
+            if (!act) return;
             if (zd != 0) fold(zb, std::true_type{});
             else fold(zb, std::false_type{});
         };

@@ -938,12 +938,21 @@ __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
             const float* hp = hrow + bj * bw;
             const float* wp = wt + e * hidden + bj * bw;
             double acc = 0.0, rs = 0.0, qs = 0.0;
+            // 16 k per step; the next step's loads go out before this step's
+            // chains (the last step loads its own chunk again)
+            float4 hv[4], wv[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                hv[q] = *reinterpret_cast<const float4*>(hp + 4 * q);
+                wv[q] = *reinterpret_cast<const float4*>(wp + 4 * q);
+            }
             for (int64_t k0 = 0; k0 < bw; k0 += 16) {
-                float4 hv[4], wv[4];
+                const int64_t kn = k0 + 16 < bw ? k0 + 16 : k0;
+                float4 hn[4], wn[4];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    hv[q] = *reinterpret_cast<const float4*>(hp + k0 + 4 * q);
-                    wv[q] = *reinterpret_cast<const float4*>(wp + k0 + 4 * q);
+                    hn[q] = *reinterpret_cast<const float4*>(hp + kn + 4 * q);
+                    wn[q] = *reinterpret_cast<const float4*>(wp + kn + 4 * q);
                 }
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -957,6 +966,8 @@ __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
                         qs = __builtin_fma(fabs(hk), fabs(wk), qs);
                     }
                 }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) { hv[q] = hn[q]; wv[q] = wn[q]; }
             }
             const double cj = block_c_term(rs, qs, hidden);
             double a = 0.0, sa = 0.0, sc = 0.0;
