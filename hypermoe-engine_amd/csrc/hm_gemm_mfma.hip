@@ -489,9 +489,12 @@ template <int L>
 struct DownTile {
     static constexpr int WR = 1;                        // 32-row fragments per wave
     static constexpr int WCN = 2;                       // 32-column fragments per wave
-    static constexpr int NWR = 4, NWC = 2;
-    static constexpr int BM = 32 * WR * NWR;            // 128 rows
-    static constexpr int BN = 32 * WCN * NWC;           // 128 columns
+#ifndef HM_DOWN_NWR
+#define HM_DOWN_NWR 2
+#endif
+    static constexpr int NWR = HM_DOWN_NWR, NWC = kWaves / NWR;
+    static constexpr int BM = 32 * WR * NWR;            // 64 rows
+    static constexpr int BN = 32 * WCN * NWC;           // 256 columns
     static constexpr int NA = L * BM / 32;
     static constexpr int NB = BN / 32;
     static constexpr int NF = NA + NB;
