@@ -1225,25 +1225,44 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(
     __syncthreads();
     if ((width & 3) == 0) {
         const int64_t w4 = width >> 2;
-        for (int64_t i = tid; i < w4; i += kBlock) {
-            float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            for (int r0 = 0; r0 < top_k; r0 += 8) {
-                // eight rows' loads in flight, then the adds in ascending order
-                float4 v[8];
+        // two column groups per thread per pass: sixteen rows' float4 loads
+        // in flight before the adds (ascending order per column)
+        for (int64_t i0 = tid; i0 < w4; i0 += 2 * kBlock) {
+          float4 res[2];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) res[h] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          for (int r0 = 0; r0 < top_k; r0 += 8) {
+            float4 v[2][8];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int64_t i = i0 + h * kBlock;
 #pragma unroll
                 for (int q = 0; q < 8; ++q)
-                    if (r0 + q < top_k) v[q] = reinterpret_cast<const float4*>(y + srow[r0 + q] * width)[i];
+                    v[h][q] = r0 + q < top_k && i < w4
+                                  ? reinterpret_cast<const float4*>(y + srow[r0 + q] * width)[i]
+                                  : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                float4 acc = res[h];
 #pragma unroll
                 for (int q = 0; q < 8; ++q) {
                     if (r0 + q < top_k) {
                         const float wv = sw[r0 + q];
-                        acc.x = __fadd_rn(acc.x, __fmul_rn(wv, v[q].x));
-                        acc.y = __fadd_rn(acc.y, __fmul_rn(wv, v[q].y));
-                        acc.z = __fadd_rn(acc.z, __fmul_rn(wv, v[q].z));
-                        acc.w = __fadd_rn(acc.w, __fmul_rn(wv, v[q].w));
+                        acc.x = __fadd_rn(acc.x, __fmul_rn(wv, v[h][q].x));
+                        acc.y = __fadd_rn(acc.y, __fmul_rn(wv, v[h][q].y));
+                        acc.z = __fadd_rn(acc.z, __fmul_rn(wv, v[h][q].z));
+                        acc.w = __fadd_rn(acc.w, __fmul_rn(wv, v[h][q].w));
                     }
                 }
+                res[h] = acc;
             }
+          }
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int64_t i = i0 + h * kBlock;
+            if (i >= w4) break;
+            float4 acc = res[h];
             if (residual) {
                 const float4 rv = reinterpret_cast<const float4*>(residual + t * width)[i];
                 acc.x = __fadd_rn(rv.x, acc.x);
@@ -1252,6 +1271,7 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(
                 acc.w = __fadd_rn(rv.w, acc.w);
             }
             reinterpret_cast<float4*>(out + t * width)[i] = acc;
+          }
         }
         return;
     }
