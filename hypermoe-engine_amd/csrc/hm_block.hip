@@ -109,7 +109,7 @@ size_t plan_block(const hm_layer* L, int64_t T, int32_t k, int32_t lx, int32_t l
     const bool generic = (flags & HM_EXEC_GENERIC) != 0;
     const int64_t H = L->hidden, I = L->intermediate, E = L->experts;
     const int64_t P = T * k;
-    const int64_t nb = (I + kHmZBlock - 1) / kHmZBlock;
+    const int64_t nb = (I + 127) / 128;
     Carve c(base);
     BlockPlan q{};
     q.route_ws = c.take<char>(hm_route_workspace_bytes(T, L->hidden, E));

@@ -305,10 +305,6 @@ struct hm_row_quant {
     int32_t limbs;
 };
 
-// Columns of Z = silu(G)*U per fixed-point segment of the down projection
-// (one scale per segment; the oracle's HMO_ZBLOCK).
-constexpr int kHmZBlock = 256;
-
 // Grouped-GEMM tile lookup: tiles of expert e are ceil(counts[e]/tile_m),
 // experts in ascending id.  Which expert, and which tile of it, does linear
 // tile index `tile` name?  False when `tile` is past the last tile.

@@ -17,7 +17,7 @@
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kZBlock = kHmZBlock;       // columns of Z per fixed-point segment
+constexpr int kZBlock = 128;       // columns of Z per fixed-point segment
 
 // ---------------------------------------------------------------------------
 // Activation rows -> digit planes (one wave per row segment).
@@ -139,7 +139,7 @@ __global__ void gateup_generic_kernel(
     zf[idx] = __fmul_rn(hm_silu(g), u);
 }
 
-// Z [R x I] float -> digit planes per kZBlock-column segment (one wave each).
+// Z [R x I] float -> digit planes per 128-column segment (one wave each).
 template <int L>
 __global__ __launch_bounds__(kBlock) void zquant_generic_kernel(
     const float* __restrict__ zf, int64_t R, int64_t I, int8_t* __restrict__ zdig,

@@ -54,11 +54,11 @@ constexpr int kS = 4;               // ring stages (gate/up)
 template <int L>
 constexpr int down_stages() { return L >= 3 ? 4 : HM_DOWN_STAGES; }
 constexpr int kFragBytes = 32 * kKB;  // one 32-row fragment of a stage
-constexpr int kZBlock = kHmZBlock;  // Z fixed-point segment (columns of Z = K of down)
+constexpr int kZBlock = 128;        // Z fixed-point segment (columns of Z = K of down)
 constexpr int kGateUpN = 128;       // columns per projection per gate/up tile
 constexpr int kXcds = 8;
 constexpr int kMaxExperts = 256;    // expert tables live in LDS
-constexpr int kMaxZSeg = 4;         // down: Z segments per row held in LDS (I <= 1024)
+constexpr int kMaxZSeg = 6;         // down: Z segments per row held in LDS (I <= 768)
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -697,8 +697,7 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
             for (int j = 0; j < WCN; ++j)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) facc[ii][j][v] = 0.0f;
-        // `next`: phase B, the refill is the next tile's stage ks + kSD - nk
-        auto dstep = [&](int ks, auto first, bool next) __attribute__((always_inline)) {
+        auto dstep = [&](int ks, auto first, auto next) __attribute__((always_inline)) {
             const int slot = (slot0 + ks) % kSD;
             if (ks + 1 < nk) {
                 if (has_next || ks + kSD - 1 < nk) wait_vmcnt<(kSD - 2) * LPW>();
@@ -706,18 +705,21 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
             }
             lds_barrier();
             const int nslot = (slot + 1) % kSD;
-            const bool iss = !next || (has_next && ks + kSD - nk <= kSD - 2);
-            mfma_step_dma(first, src, iss, slot, next ? ks + kSD - nk : ks + kSD, act);
+            if constexpr (!decltype(next)::value) {
+                mfma_step_dma(first, src, true, slot, ks + kSD, act);
+            } else {
+                mfma_step_dma(first, src, has_next && ks + kSD - nk <= kSD - 2, slot, ks + kSD - nk, act);
+            }
             if (act) {
                 if (ks + 1 < nk) read_frags(nslot, 0);
                 mfma_step(1, std::false_type{});
                 if (ks + 1 < nk) read_frags(nslot, 1);
             }
         };
-        // end of Z segment zb: exact partials -> float.  Within one segment
-        // |P_l| <= 256*128*255 < 2^24 and the combined digits stay within
-        // +-32639, so two limbs combine exactly in int32 and convert with
-        // the single rounding of fmaf((float)P_1, 256, (float)P_0).
+        // end of Z segment zb: exact partials -> float.  Within one 128-wide
+        // segment |P_l| <= 2^22 (with a zero-point correction), so two
+        // limbs combine exactly in int32 and convert with the single
+        // rounding of fmaf((float)P_1, 256, (float)P_0).
         // The zero-point correction is chosen once per tile (zd is uniform):
         // a per-element test would let the compiler hoist its integer
         // multiplies out of the branch into every fold.
@@ -768,22 +770,29 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
             if (zd != 0) fold(zb, std::true_type{});
             else fold(zb, std::false_type{});
         };
-        // A Z segment is kSeg stages (nk is a multiple of kSeg); phase B
-        // (the last kSD steps, refilling with the next tile's stages) may
-        // start inside one.  `first` (a segment's first step zeroes the
-        // partials) is a template flag, chosen here per step.
-        constexpr int kSeg = kZBlock / kKB;
+        // A Z segment is two stages (nk is even); phase B (the last kSD
+        // steps) may start inside one when kSD is odd.
+        int ks = 0;
 #pragma clang loop unroll(disable)
-        for (int sg = 0; sg < nk / kSeg; ++sg) {
-#pragma unroll
-            for (int i = 0; i < kSeg; ++i) {
-                const int ks = sg * kSeg + i;
-                const bool next = ks >= nk - kSD;
-                if (ks == nk - kSD && has_next) make_src(nxt, src);
-                if (i == 0) dstep(ks, std::true_type{}, next);
-                else dstep(ks, std::false_type{}, next);
-            }
-            fold_seg(sg);
+        for (; ks + 1 < nk - kSD; ks += 2) {
+            dstep(ks, std::true_type{}, std::false_type{});
+            dstep(ks + 1, std::false_type{}, std::false_type{});
+            fold_seg(ks >> 1);
+        }
+        if (ks < nk - kSD) {
+            dstep(ks, std::true_type{}, std::false_type{});
+            if (has_next) make_src(nxt, src);
+            dstep(ks + 1, std::false_type{}, std::true_type{});
+            fold_seg(ks >> 1);
+            ks += 2;
+        } else if (has_next) {
+            make_src(nxt, src);
+        }
+#pragma clang loop unroll(disable)
+        for (; ks < nk; ks += 2) {
+            dstep(ks, std::true_type{}, std::true_type{});
+            dstep(ks + 1, std::false_type{}, std::true_type{});
+            fold_seg(ks >> 1);
         }
         // ---- epilogue: float rows out (the next tile's stages are in flight)
 #pragma unroll
@@ -804,15 +813,33 @@ __global__ __launch_bounds__(kThreads) void down_mfma_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// z = silu(g) * u and its fixed-point digits: one wave per kZBlock-column
-// segment of a grouped row (lane: columns 4*lane .. +3).  The segment max
-// gives the step: inv = range / max|z|, digits of rint(z * inv); the
-// segment scale max|z| / range and the digit sums go out beside them.  The
-// same arithmetic as zquant_generic_kernel over the z of
-// gateup_generic_kernel.
+// z = silu(g) * u and its fixed-point digits: one half-wave per 128-column
+// segment of a grouped row (lane: columns 4*(lane%32) .. +3 of segment
+// 2*wave_id + lane/32).  The segment max gives the step: inv = range /
+// max|z|, digits of rint(z * inv); the segment scale max|z| / range and the
+// digit sums go out beside them.  The same arithmetic as
+// zquant_generic_kernel over the z of gateup_generic_kernel.
 // ---------------------------------------------------------------------------
 constexpr int kSqThreads = 256;
-static_assert(kZBlock == 4 * HM_WAVE, "one wave per Z segment");
+
+// Max / integer sum over each 32-lane half of the wave (both halves at once).
+__device__ __forceinline__ float half_wave_max(float v) {
+    const float r = hm_row16_max(v);
+    const int lane = threadIdx.x & (HM_WAVE - 1);
+    const int b = __builtin_bit_cast(int, r);
+    const float a0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    const float a1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    const float a2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+    const float a3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    return lane < 32 ? fmaxf(a0, a1) : fmaxf(a2, a3);
+}
+__device__ __forceinline__ int half_wave_sum(int v) {
+    const int r = hm_row16_sum(v);
+    const int lane = threadIdx.x & (HM_WAVE - 1);
+    const int s0 = __builtin_amdgcn_readlane(r, 0) + __builtin_amdgcn_readlane(r, 16);
+    const int s1 = __builtin_amdgcn_readlane(r, 32) + __builtin_amdgcn_readlane(r, 48);
+    return lane < 32 ? s0 : s1;
+}
 
 template <int L>
 __global__ __launch_bounds__(kSqThreads) void swiglu_quant_kernel(
@@ -823,10 +850,15 @@ __global__ __launch_bounds__(kSqThreads) void swiglu_quant_kernel(
     __syncthreads();
     const int lane = threadIdx.x & (HM_WAVE - 1);
     const int nbz = I / kZBlock;
-    const int seg = blockIdx.x * (kSqThreads / HM_WAVE) + (int)(threadIdx.x / HM_WAVE);
-    if (seg >= R * nbz) return;
+    const int pair = blockIdx.x * (kSqThreads / HM_WAVE) + (int)(threadIdx.x / HM_WAVE);
+    if (2 * pair >= R * nbz) return;
+    // a wave's two segments; an odd total leaves the last wave's upper half
+    // on a repeat of its lower segment (computed, not stored)
+    const int seg_raw = 2 * pair + (lane >> 5);
+    const bool store = seg_raw < R * nbz;
+    const int seg = store ? seg_raw : 2 * pair;
     const int row = seg / nbz, b = seg % nbz;
-    const int64_t off = (int64_t)row * I + b * kZBlock + 4 * lane;
+    const int64_t off = (int64_t)row * I + b * kZBlock + 4 * (lane & 31);
     const float4 g = *reinterpret_cast<const float4*>(gin + off);
     const float4 u = *reinterpret_cast<const float4*>(uin + off);
     float sv[4];
@@ -840,7 +872,7 @@ __global__ __launch_bounds__(kSqThreads) void swiglu_quant_kernel(
     }
     const float z[4] = {__fmul_rn(sv[0], u.x), __fmul_rn(sv[1], u.y), __fmul_rn(sv[2], u.z),
                         __fmul_rn(sv[3], u.w)};
-    const float amax = hm_wave_max_dpp(fmaxf(fmaxf(fabsf(z[0]), fabsf(z[1])), fmaxf(fabsf(z[2]), fabsf(z[3]))));
+    const float amax = half_wave_max(fmaxf(fmaxf(fabsf(z[0]), fabsf(z[1])), fmaxf(fabsf(z[2]), fabsf(z[3]))));
     const float range = (float)hm_limb_range(L);
     const float inv = amax > 0.0f ? __fdiv_rn(range, amax) : 0.0f;
     int d[4][L];
@@ -850,11 +882,12 @@ __global__ __launch_bounds__(kSqThreads) void swiglu_quant_kernel(
     for (int l = 0; l < L; ++l) {
         const uint32_t word = (uint32_t)(d[0][l] & 255) | ((uint32_t)(d[1][l] & 255) << 8) |
                               ((uint32_t)(d[2][l] & 255) << 16) | ((uint32_t)(d[3][l] & 255) << 24);
-        *reinterpret_cast<uint32_t*>(zdig + (int64_t)l * R * I + off) = word;
-        const int sum = hm_wave_sum_dpp(d[0][l] + d[1][l] + d[2][l] + d[3][l]);
-        if (lane == 0) zdsum[((int64_t)l * R + row) * nbz + b] = sum;
+        if (store) *reinterpret_cast<uint32_t*>(zdig + (int64_t)l * R * I + off) = word;
+        const int sum = half_wave_sum(d[0][l] + d[1][l] + d[2][l] + d[3][l]);
+        if (store && (lane & 31) == 0) zdsum[((int64_t)l * R + row) * nbz + b] = sum;
     }
-    if (lane == 0) zscale[(int64_t)row * nbz + b] = amax > 0.0f ? __fdiv_rn(amax, range) : 0.0f;
+    if (store && (lane & 31) == 0)
+        zscale[(int64_t)row * nbz + b] = amax > 0.0f ? __fdiv_rn(amax, range) : 0.0f;
 }
 
 int persistent_grid() {
@@ -886,10 +919,10 @@ int launch_gateup(const hm_layer* layer, const int8_t* xdig, const float* xscale
                     static_cast<const int8_t*>(layer->packed), layer->scale, layer->zero_point,
                     counts, offsets, perm_tokens, (int)R, gout, uout);
     HM_LAUNCHED();
-    const int64_t segs = R * (I / kZBlock);
+    const int64_t pairs = (R * (I / kZBlock) + 1) / 2;
     const int64_t per_block = kSqThreads / HM_WAVE;
     HM_STAGE_LAUNCH(false, true, swiglu_quant_kernel<L>,
-                    dim3((unsigned)((segs + per_block - 1) / per_block)), dim3(kSqThreads), 0,
+                    dim3((unsigned)((pairs + per_block - 1) / per_block)), dim3(kSqThreads), 0,
                     stream, gout, uout, (int)R, (int)I, zdig, zscale, zdsum);
     HM_LAUNCHED();
     return HM_OK;
@@ -912,15 +945,14 @@ int launch_down(const hm_layer* layer, const int32_t* counts, const int32_t* off
 }  // namespace
 
 // Shape preconditions of the MFMA kernels.  gate/up: K = H in 64-byte
-// stages, at least kS of them; I in 128-column blocks and whole Z segments.
-// down: K = I in 64-byte stages (at least the ring depth), whole kZBlock-wide
-// Z segments (at most kMaxZSeg held per row), H in tiles of the down tile
-// width.  Both keep the expert
+// stages, at least kS of them; I in 128-column blocks.  down: K = I in
+// 64-byte stages (at least kS), 128-wide Z segments (at most kMaxZSeg held
+// per row), H in tiles of the down tile width.  Both keep the expert
 // tables in LDS (E <= kMaxExperts).
 bool hm_mfma_gateup_ok(int64_t H, int64_t I, int64_t E, int32_t limbs) {
     return limbs >= 1 && limbs <= 3 && E >= 1 && E <= kMaxExperts && H <= (1 << 20) &&
            I <= (1 << 20) && H % kKB == 0 &&
-           H / kKB >= kS && I % kGateUpN == 0 && I >= kGateUpN && I % kZBlock == 0;
+           H / kKB >= kS && I % kGateUpN == 0 && I >= kGateUpN;
 }
 
 bool hm_mfma_down_ok(int64_t H, int64_t I, int64_t E, int32_t limbs) {

@@ -128,14 +128,10 @@ int hmo_combine(const float* y_grouped, const int32_t* offsets,
  *   c = (float)P_{L-1}; for l = L-2..0: c = fmaf(c, 256, (float)P_l)
  *   alpha = s * scale_w;  value = c * alpha
  * The gate/up GEMM uses one segment per row (whole H).  The down GEMM uses
- * segments of HMO_ZBLOCK columns of Z = silu(G)*U and accumulates
+ * segments of HM_ZBLOCK columns of Z = silu(G)*U and accumulates
  *   acc = fmaf(c_b, alpha_b, acc)  over blocks b ascending, acc0 = 0.
  * ---------------------------------------------------------------------- */
-/* 256 columns: with two limbs every segment partial |P_l| <= 256*128*255
- * < 2^24 converts to float exactly and 256*P_1 + P_0 (the combined digits
- * n stay within +-32639, so |sum n*(q - zp)| <= 256*32639*255 < 2^31)
- * fits an int32, which the device kernels use. */
-#define HMO_ZBLOCK 256
+#define HMO_ZBLOCK 128
 
 /* Quantise `rows` segments of length n (row stride ld) to L digit planes:
  * digits[(l*rows + r)*n + k]; scales[r] = s. */
