@@ -23,8 +23,10 @@
 namespace {
 
 constexpr int kGemvThreads = 256;
-constexpr int kRowsPerWave = 4;   // weight rows per wave
-constexpr int kNPW = kRowsPerWave / 2;  // gate/up: output columns per wave
+// Weight rows per wave (RW): 4, or 8 for gate/up when the batch selects many
+// experts (more bytes in flight per wave; at one token the extra columns per
+// workgroup only lengthen each wave's critical path).
+constexpr int kRowsPerWave = 4;
 
 // The slot-th expert (ascending id) with a non-zero group; -1 if none.
 // Every wave computes it redundantly from `counts` (E <= 1024); the loads
@@ -120,18 +122,18 @@ __device__ __forceinline__ void bytes_to_float(uint32_t d, float* f) {
 // Lane slices of a K-long row (K % 16 == 0, K <= 1024*P): piece p of lane
 // l is the 16 bytes at k = 1024 p + 16 l, present when that is below K.
 //
-// A wave owns kRowsPerWave weight rows.  Each lane loads its own 16-byte
+// A wave owns RW weight rows.  Each lane loads its own 16-byte
 // slices of them straight into registers (the lane later uses only the
 // bytes it loaded, so nothing is shared through LDS and nothing waits on
 // another wave); every activation row of the expert's group then meets
 // them, the rows' partial sums are reduced together, and the weights are
 // read from HBM once whatever the group size.
 //
-// GATEUP: rows j < kNPW are gate rows n0+j, the others the up rows of the
+// GATEUP: rows j < RW/2 are gate rows n0+j, the others the up rows of the
 // same n; the inputs are hidden[perm_tokens[g]]; the output z[g, n] =
 // silu(g)*u.
 // DOWN: rows j are down rows n0+j; the inputs are z[g, :]; output y[g, n].
-template <int P, bool GATEUP>
+template <int P, bool GATEUP, int RW>
 __device__ __forceinline__ void gemv_body(
     const float* __restrict__ x_src, const int32_t* __restrict__ perm_tokens, int64_t K,
     int64_t N, const int8_t* __restrict__ packed, int64_t hidden, int64_t inter,
@@ -141,15 +143,16 @@ __device__ __forceinline__ void gemv_body(
     int wave) {
     constexpr int kWaves = kGemvThreads / 64;
     const int8_t* ebase = packed + (int64_t)e * 3 * hidden * inter;
+    constexpr int kNPW = RW / 2;  // gate/up: output columns per wave
     const int64_t n0 = GATEUP ? ((int64_t)blockIdx.x * kWaves + wave) * kNPW
-                              : ((int64_t)blockIdx.x * kWaves + wave) * kRowsPerWave;
+                              : ((int64_t)blockIdx.x * kWaves + wave) * RW;
     const int64_t g0 = offsets[e];
     const int rows = counts[e];
     // weights -> registers: lane l's own 16-byte slices of every row (all
     // loads go out before the activations')
-    uint4 wreg[kRowsPerWave][P];
+    uint4 wreg[RW][P];
 #pragma unroll
-    for (int j = 0; j < kRowsPerWave; ++j) {
+    for (int j = 0; j < RW; ++j) {
         const int proj = GATEUP ? j / kNPW : 2;
         const int64_t n = GATEUP ? n0 + j % kNPW : n0 + j;
         const int8_t* row = ebase + proj * hidden * inter + n * K;
@@ -183,11 +186,11 @@ __device__ __forceinline__ void gemv_body(
             for (int i = 0; i < 16; ++i) xs += x[p][i];
         float xv[1] = {xs};
         const float xsum = wave_reduce_many<1>(xv);
-        // the partial dot products of all kRowsPerWave weight rows, then one
+        // the partial dot products of all RW weight rows, then one
         // reduction for all of them (row j's sum lands in lanes 16j .. 16j+15)
-        float a[kRowsPerWave];
+        float a[RW];
 #pragma unroll
-        for (int j = 0; j < kRowsPerWave; ++j) {
+        for (int j = 0; j < RW; ++j) {
             a[j] = 0.0f;
 #pragma unroll
             for (int p = 0; p < P; ++p) {
@@ -206,9 +209,9 @@ __device__ __forceinline__ void gemv_body(
                 }
             }
         }
-        const float tot = wave_reduce_many<kRowsPerWave>(a);
+        const float tot = wave_reduce_many<RW>(a);
         // lane 16j holds row j's sum; each output lane gathers its rows
-        constexpr int kSpan = HM_WAVE / kRowsPerWave;
+        constexpr int kSpan = HM_WAVE / RW;
         if (GATEUP) {
             // lanes 0 .. kNPW-1: output o = lane from gate row o and up row kNPW+o
             const int o = lane < kNPW ? lane : 0;
@@ -227,7 +230,7 @@ __device__ __forceinline__ void gemv_body(
     }
 }
 
-template <int P, bool GATEUP>
+template <int P, bool GATEUP, int RW>
 __global__ __launch_bounds__(kGemvThreads) void gemv_w8_kernel(
     const float* __restrict__ x_src, const int32_t* __restrict__ perm_tokens, int64_t K,
     int64_t N, int64_t experts, const int8_t* __restrict__ packed, int64_t hidden,
@@ -243,18 +246,18 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_w8_kernel(
     const int e = experts <= 256 ? hm_active_expert_256(counts, experts, (int)blockIdx.y)
                                  : hm_active_expert(counts, experts, (int)blockIdx.y);
     if (e < 0) return;
-    gemv_body<P, GATEUP>(x_src, perm_tokens, K, N, packed, hidden, inter, scale, zp, counts,
+    gemv_body<P, GATEUP, RW>(x_src, perm_tokens, K, N, packed, hidden, inter, scale, zp, counts,
                          offsets, out, s_exp2, e, lane, wave);
 }
 
-template <int P, bool GATEUP>
+template <int P, bool GATEUP, int RW>
 int launch_gemv(const float* x_src, const int32_t* perm_tokens, int64_t K, int64_t N,
                 const hm_layer* L, const int32_t* counts, const int32_t* offsets, int64_t slots,
                 float* out, hipStream_t s) {
-    const int64_t per_wg = (kGemvThreads / 64) * (GATEUP ? kNPW : kRowsPerWave);
+    const int64_t per_wg = (kGemvThreads / 64) * (GATEUP ? RW / 2 : RW);
     const dim3 grid((unsigned)(N / per_wg), (unsigned)slots);
     // (the timer, when armed, brackets the gate/up launch)
-    HM_STAGE_LAUNCH(true, true, (gemv_w8_kernel<P, GATEUP>), grid, dim3(kGemvThreads), 0, s,
+    HM_STAGE_LAUNCH(true, true, (gemv_w8_kernel<P, GATEUP, RW>), grid, dim3(kGemvThreads), 0, s,
                     x_src, perm_tokens, K, N, L->experts, static_cast<const int8_t*>(L->packed),
                     L->hidden, L->intermediate, L->scale, L->zero_point, counts, offsets, out);
     HM_LAUNCHED();
@@ -265,8 +268,16 @@ template <bool GATEUP>
 int dispatch_gemv(int64_t K, const float* x_src, const int32_t* perm_tokens, int64_t N,
                   const hm_layer* L, const int32_t* counts, const int32_t* offsets,
                   int64_t slots, float* out, hipStream_t s) {
-    if (K <= 1024) return launch_gemv<1, GATEUP>(x_src, perm_tokens, K, N, L, counts, offsets, slots, out, s);
-    if (K <= 2048) return launch_gemv<2, GATEUP>(x_src, perm_tokens, K, N, L, counts, offsets, slots, out, s);
+    // gate/up of a batch with many selected experts: 8 weight rows per wave
+    // (N must then be a multiple of the 16-column workgroup)
+    if constexpr (GATEUP) {
+        if (slots >= 64 && N % 16 == 0) {
+            if (K <= 1024) return launch_gemv<1, true, 8>(x_src, perm_tokens, K, N, L, counts, offsets, slots, out, s);
+            if (K <= 2048) return launch_gemv<2, true, 8>(x_src, perm_tokens, K, N, L, counts, offsets, slots, out, s);
+        }
+    }
+    if (K <= 1024) return launch_gemv<1, GATEUP, kRowsPerWave>(x_src, perm_tokens, K, N, L, counts, offsets, slots, out, s);
+    if (K <= 2048) return launch_gemv<2, GATEUP, kRowsPerWave>(x_src, perm_tokens, K, N, L, counts, offsets, slots, out, s);
     return HM_ERR_UNSUPPORTED;
 }
 
