@@ -49,6 +49,9 @@ def parse():
     ap.add_argument("--cpu-sample", type=int, default=-1,
                     help="tokens timed on the CPU baseline (-1: per-workload default, 0: skip)")
     ap.add_argument("--quiet", action="store_true")
+    ap.add_argument("--decode-graph", action="store_true",
+                    help="C5: replay the decode step as one captured HIP graph instead of "
+                         "launching its kernels")
     ap.add_argument("--graph", action="store_true",
                     help="replay one captured HIP graph of the block per step instead of "
                          "launching every step from the host")
@@ -405,11 +408,17 @@ def run_stack(args, cfg):
     # the prefill needs its own buffers (the stack re-plans per token count)
     prefill_stack = build_prefill_view(stack)
 
+    def decode_step():
+        if args.decode_graph:
+            g.replay()
+        else:
+            static_in.copy_(stack.launch(static_in))
+
     def job():
         prefill_stack.launch(h_prefill)
         static_in.copy_(h_tok)
         for _ in range(decode_steps):
-            g.replay()
+            decode_step()
 
     for _ in range(args.warmup):
         job()
@@ -426,7 +435,7 @@ def run_stack(args, cfg):
     for _ in range(args.steps):
         static_in.copy_(h_tok)
         for _ in range(decode_steps):
-            g.replay()
+            decode_step()
     ev[2].record()
     torch.cuda.synchronize()
     prefill_ms = ev[0].elapsed_time(ev[1]) / args.steps
@@ -453,7 +462,8 @@ def run_stack(args, cfg):
                    "decode_steps": decode_steps, "hidden": H, "experts": E, "intermediate": I,
                    "top_k": k, "weights": "int8", "limbs": args.limbs,
                    "experts_resident_bytes": int(resident)},
-        "launch": "prefill eager, decode step as one HIP graph (all layers) replayed",
+        "launch": ("prefill eager, decode step as one HIP graph (all layers) replayed"
+                   if args.decode_graph else "prefill and decode steps eager"),
         "prefill_ms": round(prefill_ms, 4),
         "prefill_tokens_per_s": round(T / (prefill_ms / 1e3), 1),
         "decode_ms_per_token": round(decode_ms / decode_steps, 5),
