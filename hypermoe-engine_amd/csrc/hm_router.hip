@@ -1130,7 +1130,8 @@ __global__ __launch_bounds__(kPermThreads) void permute_scatter_kernel(
     const int64_t c = blockIdx.x;
     const int64_t p = c * kPermThreads + tid;
     const int e = p < pairs ? (int)ids[p] : -1;
-    for (int i = tid; i < kPermWaves * 1024; i += kPermThreads) (&wcount[0][0])[i] = 0;
+    for (int i = tid; i < kPermWaves * experts; i += kPermThreads)
+        wcount[i / experts][i % experts] = 0;
     __syncthreads();
     if (e >= 0) atomicAdd(&wcount[wave][e], 1);
     __syncthreads();
@@ -1138,10 +1139,16 @@ __global__ __launch_bounds__(kPermThreads) void permute_scatter_kernel(
     int total = 0, before = 0;
     if (tid < experts) {
         if (hist) {
-            for (int64_t cc = 0; cc < chunks; ++cc) {
-                const int v = hist[cc * experts + tid];
-                total += v;
-                if (cc < c) before += v;
+            // (eight loads in flight per round)
+            for (int64_t c0 = 0; c0 < chunks; c0 += 8) {
+                int v[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) v[q] = c0 + q < chunks ? hist[(c0 + q) * experts + tid] : 0;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    total += v[q];
+                    if (c0 + q < c) before += v[q];
+                }
             }
         } else {
             for (int w = 0; w < kPermWaves; ++w) total += wcount[w][tid];
@@ -1169,13 +1176,19 @@ __global__ __launch_bounds__(kPermThreads) void permute_scatter_kernel(
     }
     __syncthreads();
     if (e < 0) return;
-    // rank among the chunk's earlier pairs of the same expert
+    // rank among the chunk's earlier pairs of the same expert: earlier
+    // waves' counts, then the wave's earlier lanes with the same id (their
+    // mask from one ballot per id bit over the wave's remaining lanes;
+    // pairs past the end have left and come after every live pair)
     int rank = 0;
     for (int w = 0; w < wave; ++w) rank += wcount[w][e];
-    for (int l = 0; l < 64; ++l) {
-        const int other = __shfl(e, l, 64);
-        rank += (l < lane && other == e) ? 1 : 0;
+    unsigned long long same = __ballot(true);
+    for (int b = 0; (1 << b) < experts; ++b) {
+        const bool bit = (e >> b) & 1;
+        const unsigned long long m = __ballot(bit);
+        same &= bit ? m : ~m;
     }
+    rank += __popcll(same & ((1ull << lane) - 1));
     const int pos = base[e] + rank;
     perm_tokens[pos] = (int32_t)(p / top_k);
     perm_weights[pos] = scores[p];
