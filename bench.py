@@ -302,7 +302,7 @@ def main():
                 "work_per_launch": gu_bytes, "launch_ms": round(stage["gate_up"], 5)}
     if not args.no_traffic:
         if gemv:
-            kre = prim = "gemv_w8_kernel<[0-9]+, true>"
+            kre = prim = "gemv_w8_kernel<[0-9]+, true, [0-9]+>"
         elif cfg.int8:
             kre, prim = "gateup_mfma_kernel|swiglu_quant_kernel", "gateup_mfma_kernel"
         else:
