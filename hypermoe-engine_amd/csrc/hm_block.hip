@@ -39,7 +39,12 @@ int hm_launch_down_combine_gemv(const hm_layer* L, const float* z, const int32_t
 extern "C" int hm_router_topk_quant(const float* h, const float* w, int64_t tokens, int64_t hidden,
                          int64_t experts, int32_t top_k, uint32_t flags, uint32_t* ids,
                          float* scores, float* logits_out, int32_t* status, void* route_ws,
-                         const hm_row_quant* xq, bool* quantized, void* stream);
+                         const hm_row_quant* xq, bool* quantized, int32_t* hist,
+                         bool* counted, void* stream);
+extern "C" int hm_permute_counted(const uint32_t* ids, const float* scores, int64_t tokens,
+                       int32_t top_k, int64_t experts, int32_t* counts, int32_t* offsets,
+                       int32_t* perm_tokens, float* perm_weights, int32_t* slots,
+                       void* workspace, bool counted, void* stream);
 int hm_route_permute_decode(const float* h, const float* w, int64_t tokens, int64_t hidden,
                             int64_t experts, int32_t top_k, uint32_t flags, uint32_t* ids,
                             float* scores, int32_t* status, void* route_ws,
@@ -215,12 +220,16 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
         // prefill select kernel when it runs (one launch fewer)
         const hm_row_quant xq = {p.xdig, p.xscale, p.xdsum, limbs_x};
         const bool want_q = !gemv && layer->dtype == HM_DTYPE_INT8 && p.xdig;
+        // and the permutation's chunk histograms (its count pass) as well
+        bool counted = false;
         rc = hm_router_topk_quant(hidden, router_w, tokens, H, E, top_k, route_bits, p.ids,
                                   p.scores, nullptr, status, p.route_ws, want_q ? &xq : nullptr,
-                                  &x_quantized, stream);
+                                  &x_quantized, reinterpret_cast<int32_t*>(p.permute_ws),
+                                  &counted, stream);
         if (rc || (rc = mark(1))) return rc;
-        rc = hm_permute(p.ids, p.scores, tokens, top_k, E, p.counts, p.offsets, p.perm_tokens,
-                        p.perm_weights, p.slots, p.permute_ws, stream);
+        rc = hm_permute_counted(p.ids, p.scores, tokens, top_k, E, p.counts, p.offsets,
+                                p.perm_tokens, p.perm_weights, p.slots, p.permute_ws, counted,
+                                stream);
         if (rc || (rc = mark(2))) return rc;
     }
     const int32_t* counts = p.counts;

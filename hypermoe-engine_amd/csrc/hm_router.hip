@@ -9,6 +9,7 @@
 namespace {
 
 constexpr int kBlock = 256;
+constexpr int kPermChunk = 1024;  // pairs per permutation chunk (kPermThreads)
 
 __device__ __forceinline__ void hm_status_or(int32_t* status, unsigned bits) {
     if (status) atomicOr(reinterpret_cast<unsigned int*>(status), bits);
@@ -437,6 +438,18 @@ __device__ __forceinline__ float certified_logit(const double* __restrict__ pp,
 // ---------------------------------------------------------------------------
 // Softmax, top-k and renormalisation of one token's logits v (one wave; lane
 // holds experts lane + 64 j); writes ids/scores [t, r] in rank order.
+// A token whose selection failed (the status word says so): placeholder ids
+// 0..top_k-1 with zero scores, so that the permutation and expert stages that
+// follow on the stream stay in range.
+__device__ __forceinline__ void select_failed(int lane, int64_t t, int32_t top_k,
+                                              uint32_t* __restrict__ ids,
+                                              float* __restrict__ scores) {
+    if (lane < top_k) {
+        ids[t * top_k + lane] = (uint32_t)lane;
+        scores[t * top_k + lane] = 0.0f;
+    }
+}
+
 template <int EPL>
 __device__ __forceinline__ void select_token(float (&v)[EPL], const bool (&valid)[EPL], int lane,
                                              int wave, int64_t t, int64_t experts, int32_t top_k,
@@ -472,6 +485,7 @@ __device__ __forceinline__ void select_token(float (&v)[EPL], const bool (&valid
         }
         if (!(isfinite(den) && den > 0.0)) {
             if (lane == 0) hm_status_or(status, HM_STATUS_SOFTMAX_FAILED);
+            select_failed(lane, t, top_k, ids, scores);
             return;
         }
 #pragma unroll
@@ -505,6 +519,7 @@ __device__ __forceinline__ void select_token(float (&v)[EPL], const bool (&valid
     if (flags & HM_ROUTE_RENORM) {
         if (!(isfinite(sel_sum) && sel_sum != 0.0)) {
             if (lane == 0) hm_status_or(status, HM_STATUS_RENORM_FAILED);
+            select_failed(lane, t, top_k, ids, scores);
             return;
         }
         my_score = (float)((double)my_score / sel_sum);
@@ -699,8 +714,10 @@ typedef double hm_double4 __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(256) void router_mfma_kernel(
     const float* __restrict__ h, const float* __restrict__ w, int tokens, int hidden,
     int experts, int ksplit, double* __restrict__ part, float* __restrict__ wt,
-    double* __restrict__ hn2, double* __restrict__ wn2) {
+    double* __restrict__ hn2, double* __restrict__ wn2, int32_t* __restrict__ hist, int hist_n) {
     __shared__ __attribute__((aligned(1024))) char ring[kMS][kMW + kMH];
+    // the permutation's chunk histograms, counted by the select kernel
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < hist_n; i += gridDim.x * 256) hist[i] = 0;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, i = lane & 15;
@@ -854,7 +871,7 @@ __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
     const double* __restrict__ hn2, const double* __restrict__ wn2, int64_t tokens,
     int64_t hidden, int64_t experts, int splits, int32_t top_k, uint32_t flags,
     float* __restrict__ logits, uint32_t* __restrict__ ids, float* __restrict__ scores,
-    int32_t* status, hm_row_quant xq) {
+    int32_t* status, hm_row_quant xq, int32_t* __restrict__ hist) {
     // per wave: experts floats for the sequential softmax sum, then two
     // fallback buffers (kFBuf each, 16-byte aligned)
     extern __shared__ __attribute__((aligned(16))) char dyn_lds[];
@@ -1071,6 +1088,13 @@ __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
         if (valid[j] && logits) logits[t * experts + lane + HM_WAVE * j] = v[j];
     select_token<EPL>(v, valid, lane, wave, t, experts, top_k, flags, ids, scores, status,
                       seq_lds);
+    // The permutation's histogram of each 1024-pair chunk (hm_permute's
+    // count pass): each lane re-reads the id it has just written.  Integer
+    // counts, so the atomics' order does not matter.
+    if (hist && lane < top_k) {
+        const int64_t pr = t * top_k + lane;
+        atomicAdd(&hist[(pr / kPermChunk) * experts + ids[pr]], 1);
+    }
     // The token's row in fixed-point digits for the INT8 expert GEMMs (the
     // block's activation quantisation, fused here: this kernel's time is set
     // by a few waves' sequential chains, the rest of the machine is idle).
@@ -1102,7 +1126,7 @@ __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
 // No global atomics; every position is a pure function of the ids.  A single
 // chunk (decode) needs no histogram pass.
 // ---------------------------------------------------------------------------
-constexpr int kPermThreads = 1024;
+constexpr int kPermThreads = kPermChunk;
 constexpr int kPermWaves = kPermThreads / 64;
 
 __global__ __launch_bounds__(kPermThreads) void permute_count_kernel(
@@ -1443,7 +1467,13 @@ int hm_router_topk_quant(const float* h, const float* w, int64_t tokens,
                          int64_t hidden, int64_t experts, int32_t top_k,
                          uint32_t flags, uint32_t* ids, float* scores,
                          float* logits_out, int32_t* status, void* route_ws,
-                         const hm_row_quant* xq, bool* quantized, void* stream);
+                         const hm_row_quant* xq, bool* quantized, int32_t* hist,
+                         bool* counted, void* stream);
+
+int hm_permute_counted(const uint32_t* ids, const float* scores, int64_t tokens,
+                       int32_t top_k, int64_t experts, int32_t* counts, int32_t* offsets,
+                       int32_t* perm_tokens, float* perm_weights, int32_t* slots,
+                       void* workspace, bool counted, void* stream);
 
 int hm_router_topk(const float* h, const float* w, int64_t tokens,
                    int64_t hidden, int64_t experts, int32_t top_k,
@@ -1451,7 +1481,8 @@ int hm_router_topk(const float* h, const float* w, int64_t tokens,
                    float* logits_out, int32_t* status, void* route_ws,
                    void* stream) {
     return hm_router_topk_quant(h, w, tokens, hidden, experts, top_k, flags, ids, scores,
-                                logits_out, status, route_ws, nullptr, nullptr, stream);
+                                logits_out, status, route_ws, nullptr, nullptr, nullptr,
+                                nullptr, stream);
 }
 
 // hm_router_topk, and where the prefill select kernel runs, the rows of h
@@ -1460,8 +1491,10 @@ int hm_router_topk_quant(const float* h, const float* w, int64_t tokens,
                          int64_t hidden, int64_t experts, int32_t top_k,
                          uint32_t flags, uint32_t* ids, float* scores,
                          float* logits_out, int32_t* status, void* route_ws,
-                         const hm_row_quant* xq, bool* quantized, void* stream) {
+                         const hm_row_quant* xq, bool* quantized, int32_t* hist,
+                         bool* counted, void* stream) {
     if (quantized) *quantized = false;
+    if (counted) *counted = false;
     // RouterConfig::validate (src/router/RouterConfig.cpp:9-22)
     HM_REQUIRE(experts > 0 && top_k > 0 && top_k <= experts);
     HM_REQUIRE(h && w && ids && scores && tokens > 0 && hidden > 0);
@@ -1491,9 +1524,14 @@ int hm_router_topk_quant(const float* h, const float* w, int64_t tokens,
         double* hn2 = reinterpret_cast<double*>(wt + experts * hidden);
         double* wn2 = hn2 + (int64_t)sp * tokens;
         const int64_t grid = ((tokens + kMT - 1) / kMT) * (experts / kME) * sp;
+        // the chunk histograms of hm_permute, when the caller passes them
+        const int64_t chunks = (tokens * top_k + kPermChunk - 1) / kPermChunk;
+        int32_t* hc = hist && chunks > 1 && chunks * experts <= INT_MAX ? hist : nullptr;
+        if (hc && counted) *counted = true;
         hipLaunchKernelGGL(router_mfma_kernel, dim3((unsigned)grid), dim3(256), 0,
                            hm_stream(stream), h, w, (int)tokens, (int)hidden, (int)experts,
-                           (int)(hidden / sp), part, wt, hn2, wn2);
+                           (int)(hidden / sp), part, wt, hn2, wn2, hc,
+                           hc ? (int)(chunks * experts) : 0);
         HM_LAUNCHED();
         const size_t split_bytes =
             (kBlock / HM_WAVE) * ((((size_t)experts * 4 + 15) / 16) * 16 + (size_t)kFWave);
@@ -1507,7 +1545,7 @@ int hm_router_topk_quant(const float* h, const float* w, int64_t tokens,
 #define HM_SELECTS(N)                                                                     \
         hipLaunchKernelGGL(router_select_split_kernel<N>, sgrid, dim3(kBlock), split_bytes, \
                            hm_stream(stream), h, wt, part, hn2, wn2, tokens, hidden, experts, \
-                           sp, top_k, flags, logits, ids, scores, status, q)
+                           sp, top_k, flags, logits, ids, scores, status, q, hc)
         if (epl <= 1) HM_SELECTS(1);
         else if (epl <= 2) HM_SELECTS(2);
         else if (epl <= 4) HM_SELECTS(4);
@@ -1554,6 +1592,16 @@ int hm_permute(const uint32_t* ids, const float* scores, int64_t tokens,
                int32_t top_k, int64_t experts, int32_t* counts, int32_t* offsets,
                int32_t* perm_tokens, float* perm_weights, int32_t* slots,
                void* workspace, void* stream) {
+    return hm_permute_counted(ids, scores, tokens, top_k, experts, counts, offsets,
+                              perm_tokens, perm_weights, slots, workspace, false, stream);
+}
+
+// hm_permute; `counted`: the workspace already holds the chunk histograms
+// (the prefill router's select kernel counted them), so only the scatter runs.
+int hm_permute_counted(const uint32_t* ids, const float* scores, int64_t tokens,
+                       int32_t top_k, int64_t experts, int32_t* counts, int32_t* offsets,
+                       int32_t* perm_tokens, float* perm_weights, int32_t* slots,
+                       void* workspace, bool counted, void* stream) {
     HM_REQUIRE(ids && scores && counts && offsets && perm_tokens && perm_weights && slots);
     HM_REQUIRE(tokens > 0 && top_k > 0 && experts > 0 && top_k <= experts);
     if (experts > 1024) return HM_ERR_UNSUPPORTED;
@@ -1564,6 +1612,8 @@ int hm_permute(const uint32_t* ids, const float* scores, int64_t tokens,
     if (chunks > 1) {
         HM_REQUIRE(workspace);
         hist = static_cast<int32_t*>(workspace);
+    }
+    if (chunks > 1 && !counted) {
         hipLaunchKernelGGL(permute_count_kernel, dim3((unsigned)chunks), dim3(kPermThreads), 0,
                            hm_stream(stream), ids, pairs, experts, hist);
         HM_LAUNCHED();
