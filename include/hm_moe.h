@@ -26,7 +26,9 @@
  *     softmax/renormalisation failure) are reported through the device
  *     status word `status` (int32, HM_STATUS_* bits), which the caller reads
  *     back; the reference throws std::runtime_error for them
- *     (src/router/CpuRouterBackend.cpp:47,57-59,83-85).
+ *     (src/router/CpuRouterBackend.cpp:47,57-59,83-85).  A token whose
+ *     softmax or renormalisation failed gets placeholder ids 0..top_k-1 with
+ *     zero scores, so that the launches queued after it stay in range.
  *   - No function throws.
  */
 #ifndef HM_MOE_H

@@ -135,6 +135,8 @@ def test_router_nonfinite_sets_status(dev):
     w = np.array([[np.inf, 1.0], [0.0, 0.0]], np.float32)
     g = run_router(dev, h, w, 1, 3)
     assert g["status"] & 1
+    # a failed token still gets in-range placeholder ids for the stages after it
+    assert (g["ids"] < 2).all()
     rc, _, _ = O.route(h, w, 1, 1, 1)
     assert rc == -3  # HMO_E_RUNTIME
 
@@ -197,6 +199,7 @@ def test_router_parallel_nonfinite_sets_status(dev, T, E):
     w[3, 5] = np.inf
     g = run_router(dev, h, w, 2, 3)
     assert g["status"] & 1
+    assert (g["ids"] < E).all()
 
 
 def test_permute_invariants_large(dev):
