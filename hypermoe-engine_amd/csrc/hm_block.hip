@@ -36,12 +36,12 @@ int hm_launch_down_combine_gemv(const hm_layer* L, const float* z, const int32_t
                                 const int32_t* slots, const float* scores,
                                 const float* residual, int64_t tokens, int32_t top_k,
                                 float* y_out, float* out, hipStream_t s);
-extern "C" int hm_router_topk_quant(const float* h, const float* w, int64_t tokens, int64_t hidden,
+extern "C" __attribute__((visibility("hidden"))) int hm_router_topk_quant(const float* h, const float* w, int64_t tokens, int64_t hidden,
                          int64_t experts, int32_t top_k, uint32_t flags, uint32_t* ids,
                          float* scores, float* logits_out, int32_t* status, void* route_ws,
                          const hm_row_quant* xq, bool* quantized, int32_t* hist,
                          bool* counted, void* stream);
-extern "C" int hm_permute_counted(const uint32_t* ids, const float* scores, int64_t tokens,
+extern "C" __attribute__((visibility("hidden"))) int hm_permute_counted(const uint32_t* ids, const float* scores, int64_t tokens,
                        int32_t top_k, int64_t experts, int32_t* counts, int32_t* offsets,
                        int32_t* perm_tokens, float* perm_weights, int32_t* slots,
                        void* workspace, bool counted, void* stream);

@@ -1463,14 +1463,14 @@ int hm_route_permute_decode(const float* h, const float* w, int64_t tokens, int6
 
 extern "C" {
 
-int hm_router_topk_quant(const float* h, const float* w, int64_t tokens,
+__attribute__((visibility("hidden"))) int hm_router_topk_quant(const float* h, const float* w, int64_t tokens,
                          int64_t hidden, int64_t experts, int32_t top_k,
                          uint32_t flags, uint32_t* ids, float* scores,
                          float* logits_out, int32_t* status, void* route_ws,
                          const hm_row_quant* xq, bool* quantized, int32_t* hist,
                          bool* counted, void* stream);
 
-int hm_permute_counted(const uint32_t* ids, const float* scores, int64_t tokens,
+__attribute__((visibility("hidden"))) int hm_permute_counted(const uint32_t* ids, const float* scores, int64_t tokens,
                        int32_t top_k, int64_t experts, int32_t* counts, int32_t* offsets,
                        int32_t* perm_tokens, float* perm_weights, int32_t* slots,
                        void* workspace, bool counted, void* stream);
@@ -1487,7 +1487,7 @@ int hm_router_topk(const float* h, const float* w, int64_t tokens,
 
 // hm_router_topk, and where the prefill select kernel runs, the rows of h
 // quantised into xq's digit planes as well (*quantized tells the caller).
-int hm_router_topk_quant(const float* h, const float* w, int64_t tokens,
+__attribute__((visibility("hidden"))) int hm_router_topk_quant(const float* h, const float* w, int64_t tokens,
                          int64_t hidden, int64_t experts, int32_t top_k,
                          uint32_t flags, uint32_t* ids, float* scores,
                          float* logits_out, int32_t* status, void* route_ws,
@@ -1598,7 +1598,7 @@ int hm_permute(const uint32_t* ids, const float* scores, int64_t tokens,
 
 // hm_permute; `counted`: the workspace already holds the chunk histograms
 // (the prefill router's select kernel counted them), so only the scatter runs.
-int hm_permute_counted(const uint32_t* ids, const float* scores, int64_t tokens,
+__attribute__((visibility("hidden"))) int hm_permute_counted(const uint32_t* ids, const float* scores, int64_t tokens,
                        int32_t top_k, int64_t experts, int32_t* counts, int32_t* offsets,
                        int32_t* perm_tokens, float* perm_weights, int32_t* slots,
                        void* workspace, bool counted, void* stream) {
