@@ -36,6 +36,20 @@ def test_library_exports_every_declared_symbol():
     assert lib.hm_status_string(1) == b"invalid argument"
 
 
+def test_library_exports_nothing_undeclared():
+    """The kernel library's dynamic symbol table holds no hm_* entry point
+    beyond the header's (internal helpers are hidden)."""
+    import shutil
+    import subprocess
+    if shutil.which("nm") is None:
+        pytest.skip("nm is not installed")
+    out = subprocess.run(["nm", "-D", "--defined-only", str(capi.lib_path())],
+                         capture_output=True, text=True, check=True).stdout
+    exported = {f.split()[-1] for f in out.splitlines() if f.split() and f.split()[-1].startswith("hm_")}
+    extra = sorted(exported - set(declared_functions()))
+    assert not extra, extra
+
+
 def test_plan_known_answers():
     """tests/phase23_tests.cpp:34-46 (mode, partitions, scratch)."""
     def plan(r, k, n, mode=0):
