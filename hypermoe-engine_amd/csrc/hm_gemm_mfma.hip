@@ -950,7 +950,8 @@ int launch_down(const hm_layer* layer, const int32_t* counts, const int32_t* off
 // per row), H in tiles of the down tile width.  Both keep the expert
 // tables in LDS (E <= kMaxExperts).
 bool hm_mfma_gateup_ok(int64_t H, int64_t I, int64_t E, int32_t limbs) {
-    return limbs >= 1 && limbs <= 3 && E >= 1 && E <= kMaxExperts && H <= (1 << 20) &&
+    // |P_l| <= H * 128 * 255 < 2^31 keeps every limb partial exact: H <= 65536
+    return limbs >= 1 && limbs <= 3 && E >= 1 && E <= kMaxExperts && H <= 65536 &&
            I <= (1 << 20) && H % kKB == 0 &&
            H / kKB >= kS && I % kGateUpN == 0 && I >= kGateUpN;
 }

@@ -1129,6 +1129,14 @@ __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
 constexpr int kPermThreads = kPermChunk;
 constexpr int kPermWaves = kPermThreads / 64;
 
+// Ids past the expert count (a caller's bad input, or the placeholders a
+// failed routing leaves for the status word to report) count as the last
+// expert, as in permute_small: every LDS index and grouped position stays in
+// range whatever the ids hold.
+__device__ __forceinline__ int clamp_expert(uint32_t e, int64_t experts) {
+    return e < (uint64_t)experts ? (int)e : (int)experts - 1;
+}
+
 __global__ __launch_bounds__(kPermThreads) void permute_count_kernel(
     const uint32_t* __restrict__ ids, int64_t pairs, int64_t experts, int32_t* __restrict__ hist) {
     __shared__ int h[1024];
@@ -1136,7 +1144,7 @@ __global__ __launch_bounds__(kPermThreads) void permute_count_kernel(
     for (int i = tid; i < experts; i += kPermThreads) h[i] = 0;
     __syncthreads();
     const int64_t p = (int64_t)blockIdx.x * kPermThreads + tid;
-    if (p < pairs) atomicAdd(&h[ids[p]], 1);
+    if (p < pairs) atomicAdd(&h[clamp_expert(ids[p], experts)], 1);
     __syncthreads();
     for (int i = tid; i < experts; i += kPermThreads) hist[(int64_t)blockIdx.x * experts + i] = h[i];
 }
@@ -1153,7 +1161,7 @@ __global__ __launch_bounds__(kPermThreads) void permute_scatter_kernel(
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t c = blockIdx.x;
     const int64_t p = c * kPermThreads + tid;
-    const int e = p < pairs ? (int)ids[p] : -1;
+    const int e = p < pairs ? clamp_expert(ids[p], experts) : -1;
     for (int i = tid; i < kPermWaves * experts; i += kPermThreads)
         wcount[i / experts][i % experts] = 0;
     __syncthreads();

@@ -53,6 +53,31 @@ def assert_compare(actual, expected, atol, rtol, what=""):
                     f"{i.tolist()}: {a[tuple(i)]} vs {b[tuple(i)]}")
 
 
+def oracle_by_token_chunks(fn, hidden, *args, threads=None, chunk=None):
+    """Runs an oracle block function (hm_oracle.moe_block / moe_block_limbs)
+    over token chunks on host threads and concatenates (out, ids, scores).
+
+    Exact, not approximate: routing, each expert row's MLP and the combine
+    are per token in the reference (CpuRouterBackend::routeBatch routes token
+    by token; every GEMM output row depends only on its own input row; the
+    combine sums a token's own expert rows), so a chunk's rows come out with
+    the same bits as in the whole batch.  ctypes releases the GIL for the C
+    call, so the chunks run in parallel."""
+    import os
+    from concurrent.futures import ThreadPoolExecutor
+    hidden = np.ascontiguousarray(hidden, np.float32)
+    T = hidden.shape[0]
+    if threads is None:
+        threads = max(1, min(16, os.cpu_count() or 1))
+    if chunk is None:
+        chunk = max(1, -(-T // (4 * threads)))
+    parts = [slice(i, min(T, i + chunk)) for i in range(0, T, chunk)]
+    with ThreadPoolExecutor(threads) as ex:
+        res = list(ex.map(lambda sl: fn(*args[:3], np.ascontiguousarray(hidden[sl]), *args[3:]),
+                          parts))
+    return tuple(np.concatenate([r[i] for r in res]) for i in range(3))
+
+
 def normwise(actual, expected) -> float:
     a = np.asarray(actual, np.float64)
     b = np.asarray(expected, np.float64)

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import hm_oracle as O
-from conftest import assert_bitexact, assert_compare, normwise
+from conftest import assert_bitexact, assert_compare, normwise, oracle_by_token_chunks
 from hmoe import capi, synth
 from hmoe.block import DeviceExpertLayer, MoEBlock
 
@@ -110,7 +110,11 @@ BLOCK_CASES = [  # (T, H, E, I, k, limbs) -- MFMA shapes and generic shapes
     (1, 2048, 128, 768, 8, 2), (4, 2048, 128, 768, 8, 3), (16, 2048, 128, 768, 8, 2),
     (70, 512, 16, 256, 4, 2), (5, 64, 8, 32, 2, 2), (6, 96, 5, 40, 3, 3), (3, 2, 3, 2, 2, 2),
     # several row tiles per expert (ragged last tile) through the MFMA kernels
-    (300, 512, 4, 256, 2, 2), (203, 1024, 3, 384, 2, 3), (150, 512, 2, 128, 1, 1)]
+    (300, 512, 4, 256, 2, 2), (203, 1024, 3, 384, 2, 3), (150, 512, 2, 128, 1, 1),
+    # more than 1024 pairs with E % 64 == 0: the prefill router's select
+    # kernel counts the permutation's chunk histograms (the count pass is
+    # skipped)
+    (160, 512, 64, 256, 8, 2)]
 
 
 @pytest.mark.parametrize("T,H,E,I,k,L", BLOCK_CASES)
@@ -193,16 +197,22 @@ def test_block_gemv_decode(dev, T, H, E, I, k, skew):
         assert_compare(y[lo:lo + len(b.token_indices)], ref, 1e-4, 1e-4, "expert rows")
 
 
-@pytest.mark.parametrize("T,E", [(16, 64), (40, 8)])
+@pytest.mark.parametrize("T,E", [(16, 64), (40, 8), (300, 4)])
 def test_block_fp32_vs_reference(dev, T, E):
-    """FP32 experts (C1 shape): within 1e-3 of the reference (north star)."""
+    """FP32 experts (C1 shape): within 1e-3 of the reference (north star).
+    T=300 with E=4, k=2 puts about 150 rows on each expert: several 64-row
+    matrix-core tiles per expert with a ragged last tile."""
     H, I, k = 2048, 768, 8 if E >= 8 else 2
+    print(f"[gpu] fp32 block T={T} E={E} k={k}", flush=True)
     payload, scale, zp, h, w = _layer_inputs(3, T, H, E, I, False)
     layer = DeviceExpertLayer(payload, None, None, H, I)
     block = MoEBlock(layer, k)
     res = block.execute_batch(dev.to(h), dev.to(w))
-    rout, rids, _ = O.moe_block(payload, scale, zp, h, w, k, I)
+    rout, rids, rsc = oracle_by_token_chunks(O.moe_block, h, payload, scale, zp, w, k, I)
     assert_bitexact(res.ids, rids, "ids")
+    assert_bitexact(res.scores, rsc, "scores")
+    if T > 64:
+        assert int(np.bincount(rids.ravel(), minlength=E).max()) > 64
     assert_compare(dev.host(res.output), rout, 1e-3, 1e-3, "fp32 block (1e-3)")
     assert normwise(dev.host(res.output), rout) < 1e-5
 
@@ -224,6 +234,13 @@ def test_block_c4_prefill_properties(dev):
     assert np.isfinite(o1).all()
     rc, ids, scores = O.route(h, w, k, 1, 1)
     assert_bitexact(r1.ids, ids, "C4 ids")
+    assert_bitexact(r1.scores, scores, "C4 scores")
+    # the permutation (its chunk histograms counted by the prefill select
+    # kernel at this size) against the oracle's grouping, bit for bit
+    counts, offsets, ptok, pw, _ = O.group(ids, scores, E)
+    assert_bitexact(r1.offsets, offsets, "C4 offsets")
+    assert_bitexact(r1.perm_tokens, ptok, "C4 permutation")
+    assert_bitexact(r1.perm_weights, pw, "C4 permuted weights")
     # a token's output depends only on its own row: a 64-token slice run alone
     # gives the same bits (routing, permutation and tiling are per token/row)
     sub = slice(1000, 1064)
@@ -231,6 +248,12 @@ def test_block_c4_prefill_properties(dev):
     assert_bitexact(dev.host(r3.output), o1[sub], "token-slice invariance")
     lout, _, _ = O.moe_block_limbs(payload, scale, zp, np.ascontiguousarray(h[sub]), w, k, I, 2, 2)
     assert_bitexact(o1[sub], lout, "C4 slice vs limb oracle")
+    # every token against the reference W8A32 block
+    rout, _, _ = oracle_by_token_chunks(O.moe_block, h, payload, scale, zp, w, k, I)
+    assert_compare(o1, rout, 1e-4, 1e-4, "C4 full batch vs reference W8A32 (1e-4)")
+    nw = normwise(o1, rout)
+    print(f"[gpu] C4 full batch normwise error {nw:.3e}", flush=True)
+    assert nw < 1e-4
 
 
 @pytest.mark.parametrize("T", [1, 16, 300])
