@@ -274,6 +274,28 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden,
                          void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/* ---- The block without allocation ------------------------------------
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): hm_moe_block_forward with its workspace in a
+ * library-owned device array of HM_NOALLOC_WORKSPACE_BYTES per GPU (held
+ * from first use until the process ends).  Same arguments and results as
+ * hm_moe_block_forward without the workspace; the caller still passes the
+ * inputs and the outputs in `io`.  Returns HM_ERR_UNSUPPORTED, without
+ * launching anything, when the call needs a larger workspace
+ * (hm_moe_block_workspace_bytes > HM_NOALLOC_WORKSPACE_BYTES: decode
+ * batches always fit, prefill batches up to a few hundred tokens at the
+ * Qwen3-30B-A3B shape).  It allocates nothing and calls no allocating
+ * routine.  All calls on one GPU share the array: calls that overlap on a
+ * GPU (other streams, other host threads) race and must be serialised by
+ * the caller. */
+#define HM_NOALLOC_WORKSPACE_BYTES ((size_t)64 << 20)
+int hm_moe_block_forward_noalloc(const hm_layer* layer, const float* hidden,
+                                 const float* router_w, int64_t tokens,
+                                 int32_t top_k, uint32_t route_flags,
+                                 int32_t limbs_x, int32_t limbs_z,
+                                 const hm_block_io* io, void* stream);
+
 /* ---- Limb arithmetic at op level (build-owned, no reference counterpart):
  * quantise rows to digit planes and return exact int32 partials, so tests
  * can pin "INT8 int32 partials bit-exact" directly.
