@@ -45,7 +45,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="C4")
-    ap.add_argument("--limbs", type=int, default=2)
+    ap.add_argument("--limbs-x", type=int, default=2, help="X (token row) digit planes")
+    ap.add_argument("--limbs-z", type=int, default=3, help="Z (SiLU(G)*U row) digit planes")
     ap.add_argument("--cpu-sample", type=int, default=-1,
                     help="tokens timed on the CPU baseline (-1: per-workload default, 0: skip)")
     ap.add_argument("--quiet", action="store_true")
@@ -70,7 +71,7 @@ def log(msg, quiet=False):
         print(msg, file=sys.stderr, flush=True)
 
 
-def pmc_traffic(workload: str, kernel_re: str, primary_re: str, limbs: int, quiet: bool):
+def pmc_traffic(workload: str, kernel_re: str, primary_re: str, limbs: tuple, quiet: bool):
     """HBM bytes per launch of the dominant stage: two rocprofv3 --pmc runs
     of a short child bench (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch),
     each scaled by what the same counter reads for a plain 256 MiB
@@ -93,7 +94,8 @@ def pmc_traffic(workload: str, kernel_re: str, primary_re: str, limbs: int, quie
             cmd = [exe, "--pmc", counter, "--kernel-include-regex", f"{kernel_re}|copyBuffer",
                    "--output-format", "csv", "-d", d, "-o", "pmc", "--", sys.executable,
                    str(REPO / "bench.py"), "--workload", workload, "--steps", "2", "--warmup",
-                   "1", "--cpu-sample", "0", "--quiet", "--no-traffic", "--limbs", str(limbs),
+                   "1", "--cpu-sample", "0", "--quiet", "--no-traffic", "--limbs-x", str(limbs[0]),
+                   "--limbs-z", str(limbs[1]),
                    "--copy-mb", str(copy_mib)]
             env = dict(os.environ, TMPDIR="/tmp")
             log(f"[bench] traffic: rocprofv3 --pmc {counter}", quiet)
@@ -148,7 +150,7 @@ def main():
     T, H, E, I, k = cfg.tokens, cfg.hidden, cfg.experts, cfg.inter, cfg.top_k
     q = args.quiet
     log(f"[bench] workload {cfg.name}: T={T} H={H} E={E} I={I} k={k} int8={cfg.int8} "
-        f"skew={cfg.skew} limbs={args.limbs}", q)
+        f"skew={cfg.skew} limbs=({args.limbs_x}, {args.limbs_z})", q)
     t0 = time.time()
     payload, scale, zp = synth.expert_layer(cfg.seed, 0, E, H, I, cfg.int8,
                                             threads=min(16, os.cpu_count() or 1))
@@ -175,7 +177,7 @@ def main():
         w[-1, :] = bias
     d_w = torch.from_numpy(w).cuda()
     layer = DeviceExpertLayer(payload, scale, zp, H, I)
-    block = MoEBlock(layer, k, limbs_x=args.limbs, limbs_z=args.limbs)
+    block = MoEBlock(layer, k, limbs_x=args.limbs_x, limbs_z=args.limbs_z)
     torch.cuda.synchronize()
     log(f"[bench] setup {time.time() - t0:.1f}s", q)
 
@@ -274,7 +276,9 @@ def main():
     elif cfg.int8:
         gu_ops = 2 * T * k * 2 * H * I
         dn_ops = 2 * T * k * H * I
-        gu_bytes = unique * 2 * H * I + T * H * args.limbs + T * k * I * args.limbs
+        # X digit planes in, SiLU(G)*U floats out (their Z digits are the
+        # next launch's work)
+        gu_bytes = unique * 2 * H * I + T * H * args.limbs_x + T * k * I * 4
     else:
         gu_ops = 2 * T * k * 2 * H * I
         dn_ops = 2 * T * k * H * I
@@ -285,29 +289,31 @@ def main():
         achieved = gu_ops / gu_s / 1e12
         peak = PEAK_INT8_TOPS if cfg.int8 else PEAK_FP32_TFLOPS
         roof = {"bound": "mfma",
-                "kernel": ("gate/up stage: gateup_mfma_kernel + swiglu_quant_kernel" if cfg.int8
-                           else "gateup_f32_kernel"),
+                "kernel": ("gate/up stage: limb_gemm_kernel<0, Lx, DB> (SiLU(G)*U in its "
+                           "epilogue) + limb_quantize_rows_vec_kernel<Lz> (Z digits)" if cfg.int8
+                           else "expert_f32_mfma_kernel<true>"),
                 "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                 "frac": round(achieved / peak, 4), "traffic": None,
                 "work_per_launch": gu_ops, "launch_ms": round(stage["gate_up"], 5),
-                "hw_mfma_frac_with_limbs": round(achieved * (args.limbs if cfg.int8 else 1) / peak, 4)}
+                "hw_mfma_frac_with_limbs": round(achieved * (args.limbs_x if cfg.int8 else 1) / peak, 4)}
     else:
         achieved = gu_bytes / gu_s / 1e9
         roof = {"bound": "hbm",
-                "kernel": ("gemv_w8_kernel (gate/up)" if gemv else
-                           "gate/up stage: gateup_mfma_kernel + swiglu_quant_kernel" if cfg.int8
-                           else "gateup_f32_kernel"),
+                "kernel": ("gemv_tiles_kernel<true> (gate/up)" if gemv else
+                           "gate/up stage: limb_gemm_kernel<0, Lx, DB> + "
+                           "limb_quantize_rows_vec_kernel<Lz>" if cfg.int8
+                           else "expert_f32_mfma_kernel<true>"),
                 "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
                 "work_per_launch": gu_bytes, "launch_ms": round(stage["gate_up"], 5)}
     if not args.no_traffic:
         if gemv:
-            kre = prim = "gemv_w8_kernel<[0-9]+, true, [0-9]+>"
+            kre = prim = "gemv_tiles_kernel<true>"
         elif cfg.int8:
-            kre, prim = "gateup_mfma_kernel|swiglu_quant_kernel", "gateup_mfma_kernel"
+            kre, prim = "limb_gemm_kernel<0,|limb_quantize_rows_vec_kernel", "limb_gemm_kernel<0,"
         else:
-            kre = prim = "gateup_f32_kernel"
-        tr = pmc_traffic(cfg.name, kre, prim, args.limbs, q)
+            kre = prim = "expert_f32_mfma_kernel<true>"
+        tr = pmc_traffic(cfg.name, kre, prim, (args.limbs_x, args.limbs_z), q)
         if tr is not None:
             roof["traffic"] = tr.pop("bytes")
             roof["traffic_detail"] = tr
@@ -356,7 +362,8 @@ def main():
         "dtype": "int8" if cfg.int8 else "fp32", "data": "synthetic",
         "config": {"workload": cfg.name, "tokens": T, "hidden": H, "experts": E,
                    "intermediate": I, "top_k": k, "weights": "int8" if cfg.int8 else "fp32",
-                   "skewed_routing": cfg.skew, "limbs": args.limbs if cfg.int8 else None,
+                   "skewed_routing": cfg.skew,
+                   "limbs": [args.limbs_x, args.limbs_z] if cfg.int8 else None,
                    "unique_experts": unique, "max_expert_rows": int(counts.max()),
                    "input_batches": pool},
         "launch": "hip_graph_replay" if graph is not None else "eager",
@@ -381,10 +388,10 @@ def run_stack(args, cfg):
     q = args.quiet
     T, H, E, I, k = cfg.tokens, cfg.hidden, cfg.experts, cfg.inter, cfg.top_k
     log(f"[bench] workload {cfg.name}: {cfg.layers} layers, prefill T={T}, {decode_steps} decode "
-        f"steps, H={H} E={E} I={I} k={k} limbs={args.limbs}", q)
+        f"steps, H={H} E={E} I={I} k={k} limbs=({args.limbs_x}, {args.limbs_z})", q)
     torch.cuda.set_device(0)
     t0 = time.time()
-    stack = build_stack(cfg, limbs=args.limbs,
+    stack = build_stack(cfg, limbs_x=args.limbs_x, limbs_z=args.limbs_z,
                         log=lambda l: log(f"[bench] layer {l + 1}/{cfg.layers} resident "
                                           f"({time.time() - t0:.0f}s)", q or (l + 1) % 8))
     resident = sum(l.packed.numel() for l in stack.layers)
@@ -460,7 +467,7 @@ def run_stack(args, cfg):
         "data": "synthetic",
         "config": {"workload": cfg.name, "layers": cfg.layers, "prefill_tokens": T,
                    "decode_steps": decode_steps, "hidden": H, "experts": E, "intermediate": I,
-                   "top_k": k, "weights": "int8", "limbs": args.limbs,
+                   "top_k": k, "weights": "int8", "limbs": [args.limbs_x, args.limbs_z],
                    "experts_resident_bytes": int(resident)},
         "launch": ("prefill eager, decode step as one HIP graph (all layers) replayed"
                    if args.decode_graph else "prefill and decode steps eager"),
@@ -484,7 +491,7 @@ def build_prefill_view(stack):
     the captured decode step's buffers stay untouched)."""
     from hmoe.stack import MoEStack
     return MoEStack(stack.layers, stack.router_w, stack.top_k, eps=stack.eps,
-                    limbs=stack.limbs, flags=stack.flags)
+                    limbs_x=stack.limbs_x, limbs_z=stack.limbs_z, flags=stack.flags)
 
 
 if __name__ == "__main__":

@@ -11,7 +11,7 @@
 int hm_launch_quantize_rows(const float* x, int64_t rows, int64_t n, int32_t limbs,
                             int8_t* digits, float* scales, int32_t* dsum,
                             hipStream_t stream);
-bool hm_use_mfma_gateup(const hm_layer* layer, int32_t lx, int32_t lz, bool force_generic);
+
 int hm_launch_gateup_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int8_t* xdig,
                         const float* xscale, const int32_t* xdsum, int64_t tokens,
                         const int32_t* counts, const int32_t* offsets,
@@ -113,10 +113,8 @@ bool layer_valid(const hm_layer* L) {
 // Lays the workspace out; with base == nullptr only computes the size.
 size_t plan_block(const hm_layer* L, int64_t T, int32_t k, int32_t lx, int32_t lz,
                   uint32_t flags, void* base, BlockPlan* p) {
-    const bool generic = (flags & HM_EXEC_GENERIC) != 0;
     const int64_t H = L->hidden, I = L->intermediate, E = L->experts;
     const int64_t P = T * k;
-    const int64_t nb = (I + 127) / 128;
     Carve c(base);
     BlockPlan q{};
     q.route_ws = c.take<char>(hm_route_workspace_bytes(T, L->hidden, E));
@@ -137,9 +135,9 @@ size_t plan_block(const hm_layer* L, int64_t T, int32_t k, int32_t lx, int32_t l
         q.xscale = c.take<float>((size_t)T);
         q.xdsum = c.take<int32_t>((size_t)lx * T);
         q.zdig = c.take<int8_t>((size_t)lz * P * I);
-        q.zscale = c.take<float>((size_t)P * nb);
-        q.zdsum = c.take<int32_t>((size_t)lz * P * nb);
-        q.zf = c.take<float>((size_t)P * I * (hm_use_mfma_gateup(L, lx, lz, generic) ? 2 : 1));
+        q.zscale = c.take<float>((size_t)P);
+        q.zdsum = c.take<int32_t>((size_t)lz * P);
+        q.zf = c.take<float>((size_t)P * I);
     } else {
         q.zf = c.take<float>((size_t)P * I);
     }

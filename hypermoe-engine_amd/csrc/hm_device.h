@@ -339,6 +339,31 @@ __device__ __forceinline__ bool hm_locate_tile(const int32_t* __restrict__ count
     return false;
 }
 
+// ---------------------------------------------------------------------------
+// INT8 expert weight layout on the device ("tiles"; hm_pack_layer).
+// A projection W [N x K] (N output columns, K inner: gate/up N = I, K = H;
+// down N = H, K = I) is zero-padded to N32 x K32 (multiples of 32) and cut
+// into 32 x 32 tiles; tile (cb, kb) is 1024 contiguous bytes at
+// (cb * K32/32 + kb) * 1024, and inside it the 16 bytes of lane l are
+// W[32 cb + l % 32][32 kb + 16 (l / 32) .. +15] at 16 l.  One wave-wide
+// 16-byte load of a tile is therefore the B operand of
+// v_mfma_i32_32x32x32_i8 for columns 32 cb .. +31 and K step kb, read as one
+// contiguous kilobyte.  Every projection takes H32 * I32 bytes; projection p
+// of expert e starts at (3 e + p) * H32 * I32.
+// ---------------------------------------------------------------------------
+__host__ __device__ __forceinline__ int64_t hm_pad32(int64_t v) { return (v + 31) & ~(int64_t)31; }
+__host__ __device__ __forceinline__ int64_t hm_tile_offset(int64_t n, int64_t k, int64_t K32) {
+    return ((n >> 5) * (K32 >> 5) + (k >> 5)) * 1024 + ((n & 31) + 32 * ((k >> 4) & 1)) * 16 +
+           (k & 15);
+}
+__host__ __device__ __forceinline__ int64_t hm_proj_bytes(int64_t H, int64_t I) {
+    return hm_pad32(H) * hm_pad32(I);
+}
+// Start of projection p (0 gate, 1 up, 2 down) of expert e.
+__host__ __device__ __forceinline__ int64_t hm_proj_offset(int64_t e, int p, int64_t H, int64_t I) {
+    return (3 * e + p) * hm_proj_bytes(H, I);
+}
+
 // Float total order key for top-k: larger score first, equal scores (with
 // -0 == +0) broken by the lower expert id; 0 is never a valid key.
 __device__ __forceinline__ unsigned long long hm_rank_key(float v, unsigned int id) {

@@ -8,8 +8,11 @@
 // loops; they serve shapes the MFMA tiles do not cover and pin the MFMA
 // kernels in tests (bit-for-bit).
 //
-// Packed expert layout (hm_pack_layer): expert e at e*3*H*I elements:
-//   gate^T [I x H] | up^T [I x H] | down^T [H x I]   (K contiguous per row)
+// Packed expert layouts (hm_pack_layer):
+//   INT8: the tile layout of hm_device.h (hm_tile_offset): per projection
+//         32 x 32 tiles, each the kilobyte one MFMA B-operand load reads.
+//   FP32: expert e at e*3*H*I elements, gate^T [I x H] | up^T [I x H] |
+//         down^T [H x I] (K contiguous per row).
 #include "hm_device.h"
 
 #include <limits.h>
@@ -17,7 +20,6 @@
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kZBlock = 128;       // columns of Z per fixed-point segment
 
 // ---------------------------------------------------------------------------
 // Activation rows -> digit planes (one wave per row segment).
@@ -118,8 +120,9 @@ __global__ void gateup_generic_kernel(
     const int64_t row = idx / I, col = idx % I;
     const int64_t e = group_of_row(offsets, experts, row);
     const int64_t t = perm_tokens[row];
-    const int8_t* qg = packed + e * 3 * H * I + col * H;
-    const int8_t* qu = qg + H * I;
+    const int8_t* qg = packed + hm_proj_offset(e, 0, H, I);
+    const int8_t* qu = packed + hm_proj_offset(e, 1, H, I);
+    const int64_t H32 = hm_pad32(H);
     const int zg = zp[e * 3 + 0], zu = zp[e * 3 + 1];
     int pg[L], pu[L];
 #pragma unroll
@@ -127,8 +130,9 @@ __global__ void gateup_generic_kernel(
         const int8_t* d = xdig + ((int64_t)l * tokens + t) * H;
         int ag = 0, au = 0;
         for (int64_t k = 0; k < H; ++k) {
-            ag += (int)d[k] * ((int)qg[k] - zg);
-            au += (int)d[k] * ((int)qu[k] - zu);
+            const int64_t o = hm_tile_offset(col, k, H32);
+            ag += (int)d[k] * ((int)qg[o] - zg);
+            au += (int)d[k] * ((int)qu[o] - zu);
         }
         pg[l] = ag;
         pu[l] = au;
@@ -139,44 +143,9 @@ __global__ void gateup_generic_kernel(
     zf[idx] = __fmul_rn(hm_silu(g), u);
 }
 
-// Z [R x I] float -> digit planes per 128-column segment (one wave each).
-template <int L>
-__global__ __launch_bounds__(kBlock) void zquant_generic_kernel(
-    const float* __restrict__ zf, int64_t R, int64_t I, int8_t* __restrict__ zdig,
-    float* __restrict__ zscale, int32_t* __restrict__ zdsum) {
-    const int lane = threadIdx.x & (HM_WAVE - 1);
-    const int64_t nb = (I + kZBlock - 1) / kZBlock;
-    const int64_t seg = (int64_t)blockIdx.x * (kBlock / HM_WAVE) + threadIdx.x / HM_WAVE;
-    if (seg >= R * nb) return;
-    const int64_t row = seg / nb, b = seg % nb;
-    const int64_t k0 = b * kZBlock;
-    const int64_t kn = (I - k0) < kZBlock ? (I - k0) : kZBlock;
-    const float* zr = zf + row * I + k0;
-    float amax = 0.0f;
-    for (int64_t k = lane; k < kn; k += HM_WAVE) amax = fmaxf(amax, fabsf(zr[k]));
-    amax = hm_wave_max_f32(amax);
-    const float range = (float)hm_limb_range(L);
-    const float inv = amax > 0.0f ? __fdiv_rn(range, amax) : 0.0f;
-    int dl[L];
-#pragma unroll
-    for (int l = 0; l < L; ++l) dl[l] = 0;
-    for (int64_t k = lane; k < kn; k += HM_WAVE) {
-        const int v = hm_fixed_point(zr[k], inv, range);
-#pragma unroll
-        for (int l = 0; l < L; ++l) {
-            const int d = hm_digit(v, l);
-            zdig[((int64_t)l * R + row) * I + k0 + k] = (int8_t)d;
-            dl[l] += d;
-        }
-    }
-#pragma unroll
-    for (int l = 0; l < L; ++l) {
-        const int s = hm_wave_sum_i32(dl[l]);
-        if (lane == 0) zdsum[((int64_t)l * R + row) * nb + b] = s;
-    }
-    if (lane == 0) zscale[row * nb + b] = amax > 0.0f ? __fdiv_rn(amax, range) : 0.0f;
-}
-
+// y[g, n] = recombine(P_l) * (s_z[g] * scale_down), P_l the exact int32
+// partial of Z digit plane l over the whole row (one fixed-point scale per
+// Z row, hm_launch_quantize_rows).
 template <int L>
 __global__ void down_generic_kernel(
     const int8_t* __restrict__ zdig, const float* __restrict__ zscale, int64_t R,
@@ -187,26 +156,18 @@ __global__ void down_generic_kernel(
     if (idx >= R * H) return;
     const int64_t row = idx / H, col = idx % H;
     const int64_t e = group_of_row(offsets, experts, row);
-    const int8_t* qd = packed + e * 3 * H * I + 2 * H * I + col * I;
+    const int8_t* qd = packed + hm_proj_offset(e, 2, H, I);
+    const int64_t I32 = hm_pad32(I);
     const int zd = zp[e * 3 + 2];
-    const float sd = scale[e * 3 + 2];
-    const int64_t nb = (I + kZBlock - 1) / kZBlock;
-    float acc = 0.0f;
-    for (int64_t b = 0; b < nb; ++b) {
-        const int64_t k0 = b * kZBlock;
-        const int64_t k1 = (k0 + kZBlock) < I ? (k0 + kZBlock) : I;
-        int p[L];
+    int p[L];
 #pragma unroll
-        for (int l = 0; l < L; ++l) {
-            const int8_t* d = zdig + ((int64_t)l * R + row) * I;
-            int a = 0;
-            for (int64_t k = k0; k < k1; ++k) a += (int)d[k] * ((int)qd[k] - zd);
-            p[l] = a;
-        }
-        const float alpha = __fmul_rn(zscale[row * nb + b], sd);
-        acc = __builtin_fmaf(hm_recombine(p, L), alpha, acc);
+    for (int l = 0; l < L; ++l) {
+        const int8_t* d = zdig + ((int64_t)l * R + row) * I;
+        int a = 0;
+        for (int64_t k = 0; k < I; ++k) a += (int)d[k] * ((int)qd[hm_tile_offset(col, k, I32)] - zd);
+        p[l] = a;
     }
-    y[idx] = acc;
+    y[idx] = __fmul_rn(hm_recombine(p, L), __fmul_rn(zscale[row], scale[e * 3 + 2]));
 }
 
 // ---------------------------------------------------------------------------
@@ -452,35 +413,92 @@ __global__ void transpose_kernel(const T* __restrict__ src, T* __restrict__ dst,
     }
 }
 
+// INT8 projection [K x N] (row-major, the reference payload) -> tiles
+// (hm_tile_offset), zero-padded to N32 x K32.  One workgroup per tile: the
+// 32 x 32 source block through LDS, then the kilobyte in lane order.
+// blockIdx.x: tile of the projection (cb * K32/32 + kb), blockIdx.y: 3e + p.
+__global__ __launch_bounds__(256) void pack_tiles_i8_kernel(const int8_t* __restrict__ src,
+                                                            int8_t* __restrict__ dst, int64_t H,
+                                                            int64_t I) {
+    __shared__ int8_t t[32][33];
+    const int64_t ep = blockIdx.y;
+    const int p = (int)(ep % 3);
+    const int64_t K = p < 2 ? H : I, N = p < 2 ? I : H;
+    const int64_t K32 = hm_pad32(K);
+    const int64_t cb = blockIdx.x / (K32 >> 5), kb = blockIdx.x % (K32 >> 5);
+    const int8_t* s = src + ep * H * I;
+    const int tid = threadIdx.x;
+    const int kr = tid >> 3, nc = (tid & 7) * 4;
+    const int64_t k = 32 * kb + kr;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t n = 32 * cb + nc + j;
+        t[kr][nc + j] = (k < K && n < N) ? s[k * N + n] : (int8_t)0;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const int nl = tid & 31, k0 = 16 * (tid >> 5);
+        uint32_t w[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            w[q] = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) w[q] |= (uint32_t)(uint8_t)t[k0 + 4 * q + b][nl] << (8 * b);
+        }
+        int8_t* d = dst + hm_proj_offset(ep / 3, p, H, I) + (int64_t)blockIdx.x * 1024 + 16 * tid;
+        *reinterpret_cast<uint4*>(d) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
 }  // namespace
 
 // ===========================================================================
 // Launchers used by the block entry (hm_block.hip) and the C ABI.
 // ===========================================================================
-int hm_launch_quantize_rows(const float* x, int64_t rows, int64_t n, int32_t limbs,
-                            int8_t* digits, float* scales, int32_t* dsum,
-                            hipStream_t stream) {
+// Rows -> digit planes.  `timed`: the launch closes an armed stage timer
+// (the last kernel of the gate/up stage).
+static int quantize_rows(const float* x, int64_t rows, int64_t n, int32_t limbs,
+                         int8_t* digits, float* scales, int32_t* dsum, bool timed,
+                         hipStream_t stream) {
     if (rows == 0) return HM_OK;
     const dim3 grid((unsigned)((rows + 3) / 4));
     const int64_t nv = n / 256;
     if (n % 256 == 0 && nv >= 1 && nv <= kQMaxV && (uintptr_t)x % 16 == 0 && (uintptr_t)digits % 4 == 0) {
+#define HM_QV(LV) HM_STAGE_LAUNCH(false, timed, limb_quantize_rows_vec_kernel<LV>, grid, dim3(kBlock), 0, stream, \
+                                  x, rows, n, (int)nv, digits, scales, dsum)
         switch (limbs) {
-        case 1: hipLaunchKernelGGL(limb_quantize_rows_vec_kernel<1>, grid, dim3(kBlock), 0, stream, x, rows, n, (int)nv, digits, scales, dsum); break;
-        case 2: hipLaunchKernelGGL(limb_quantize_rows_vec_kernel<2>, grid, dim3(kBlock), 0, stream, x, rows, n, (int)nv, digits, scales, dsum); break;
-        case 3: hipLaunchKernelGGL(limb_quantize_rows_vec_kernel<3>, grid, dim3(kBlock), 0, stream, x, rows, n, (int)nv, digits, scales, dsum); break;
+        case 1: HM_QV(1); break;
+        case 2: HM_QV(2); break;
+        case 3: HM_QV(3); break;
         default: return HM_ERR_INVALID;
         }
+#undef HM_QV
         HM_LAUNCHED();
         return HM_OK;
     }
+#define HM_QS(LV) HM_STAGE_LAUNCH(false, timed, limb_quantize_rows_kernel<LV>, grid, dim3(kBlock), 0, stream, \
+                                  x, rows, n, digits, scales, dsum)
     switch (limbs) {
-    case 1: hipLaunchKernelGGL(limb_quantize_rows_kernel<1>, grid, dim3(kBlock), 0, stream, x, rows, n, digits, scales, dsum); break;
-    case 2: hipLaunchKernelGGL(limb_quantize_rows_kernel<2>, grid, dim3(kBlock), 0, stream, x, rows, n, digits, scales, dsum); break;
-    case 3: hipLaunchKernelGGL(limb_quantize_rows_kernel<3>, grid, dim3(kBlock), 0, stream, x, rows, n, digits, scales, dsum); break;
+    case 1: HM_QS(1); break;
+    case 2: HM_QS(2); break;
+    case 3: HM_QS(3); break;
     default: return HM_ERR_INVALID;
     }
+#undef HM_QS
     HM_LAUNCHED();
     return HM_OK;
+}
+
+int hm_launch_quantize_rows(const float* x, int64_t rows, int64_t n, int32_t limbs,
+                            int8_t* digits, float* scales, int32_t* dsum,
+                            hipStream_t stream) {
+    return quantize_rows(x, rows, n, limbs, digits, scales, dsum, false, stream);
+}
+
+static int hm_launch_quantize_rows_timed(const float* x, int64_t rows, int64_t n, int32_t limbs,
+                                         int8_t* digits, float* scales, int32_t* dsum,
+                                         hipStream_t stream) {
+    return quantize_rows(x, rows, n, limbs, digits, scales, dsum, true, stream);
 }
 
 bool hm_mfma_gateup_ok(int64_t H, int64_t I, int64_t E, int32_t limbs);
@@ -488,8 +506,8 @@ bool hm_mfma_down_ok(int64_t H, int64_t I, int64_t E, int32_t limbs);
 int hm_launch_gateup_i8_mfma(const hm_layer* layer, int32_t limbs, const int8_t* xdig,
                              const float* xscale, const int32_t* xdsum, int64_t tokens,
                              const int32_t* counts, const int32_t* offsets,
-                             const int32_t* perm_tokens, int64_t R, float* gu, int8_t* zdig,
-                             float* zscale, int32_t* zdsum, hipStream_t stream);
+                             const int32_t* perm_tokens, int64_t R, float* zf,
+                             hipStream_t stream);
 int hm_launch_down_i8_mfma(const hm_layer* layer, int32_t limbs, const int32_t* counts,
                            const int32_t* offsets, int64_t R, const int8_t* zdig,
                            const float* zscale, const int32_t* zdsum, float* y,
@@ -499,15 +517,15 @@ int64_t hm_max_tiles(int64_t pairs, int64_t experts, int64_t tile_m) {
     return (pairs < experts ? pairs : experts) + pairs / tile_m;
 }
 
-// INT8 expert GEMMs, in two launches (gate/up, then down) so callers can
-// record events between them.  xdig/xscale/xdsum come from
-// hm_launch_quantize_rows over all tokens; zf is scratch: [R x I] floats of
-// z on the generic path, [2 x R x I] floats of g and u on the MFMA path.
-// The MFMA gate/up path quantises Z (swiglu_quant_kernel) with the same
-// digit count as X; down reads Z digits from either gate/up path.
-bool hm_use_mfma_gateup(const hm_layer* layer, int32_t lx, int32_t lz, bool force_generic) {
-    return !force_generic && lx == lz &&
-           hm_mfma_gateup_ok(layer->hidden, layer->intermediate, layer->experts, lx);
+// INT8 expert GEMMs: gate/up (z = silu(g) * u as floats into zf [R x I]),
+// the Z rows' fixed-point digits (one scale per row, the same quantiser as
+// the activations), then down.  xdig/xscale/xdsum: the token rows' digits
+// (hm_launch_quantize_rows over all tokens, or the prefill router's select
+// kernel).  The MFMA kernels (hm_gemm_mfma.hip) where the shape allows, the
+// generic kernels otherwise; both compute the same integers and the same
+// float operation sequence.
+bool hm_use_mfma_gateup(const hm_layer* layer, int32_t lx, bool force_generic) {
+    return !force_generic && hm_mfma_gateup_ok(layer->hidden, layer->intermediate, layer->experts, lx);
 }
 bool hm_use_mfma_down(const hm_layer* layer, int32_t lz, bool force_generic) {
     return !force_generic && hm_mfma_down_ok(layer->hidden, layer->intermediate, layer->experts, lz);
@@ -521,37 +539,31 @@ int hm_launch_gateup_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int
     const int64_t H = layer->hidden, I = layer->intermediate, E = layer->experts;
     const int8_t* packed = static_cast<const int8_t*>(layer->packed);
     if (R == 0) return HM_OK;
-    if (hm_use_mfma_gateup(layer, lx, lz, force_generic)) {
-        return hm_launch_gateup_i8_mfma(layer, lx, xdig, xscale, xdsum, tokens, counts, offsets,
-                                        perm_tokens, R, zf, zdig, zscale, zdsum, stream);
-    }
-    const int64_t nb = (I + kZBlock - 1) / kZBlock;
-    const unsigned g_gu = (unsigned)((R * I + kBlock - 1) / kBlock);
-    const unsigned g_zq = (unsigned)((R * nb + 3) / 4);
-#define HM_GU(LV)                                                                         \
-    HM_STAGE_LAUNCH(true, false, gateup_generic_kernel<LV>, dim3(g_gu), dim3(kBlock), 0, stream, \
-                    xdig, xscale, tokens, H, I, E, packed, layer->scale, layer->zero_point,   \
-                    offsets, perm_tokens, R, zf)
-#define HM_ZQ(LV)                                                                         \
-    HM_STAGE_LAUNCH(false, true, zquant_generic_kernel<LV>, dim3(g_zq), dim3(kBlock), 0, stream, \
-                    zf, R, I, zdig, zscale, zdsum)
-    switch (lx) {
-    case 1: HM_GU(1); break;
-    case 2: HM_GU(2); break;
-    case 3: HM_GU(3); break;
-    default: return HM_ERR_INVALID;
-    }
-    HM_LAUNCHED();
-    switch (lz) {
-    case 1: HM_ZQ(1); break;
-    case 2: HM_ZQ(2); break;
-    case 3: HM_ZQ(3); break;
-    default: return HM_ERR_INVALID;
-    }
+    // the MFMA kernels, or the generic ones where the shape (or a 32-bit
+    // buffer offset) rules them out
+    int rc = hm_use_mfma_gateup(layer, lx, force_generic)
+                 ? hm_launch_gateup_i8_mfma(layer, lx, xdig, xscale, xdsum, tokens, counts,
+                                            offsets, perm_tokens, R, zf, stream)
+                 : HM_ERR_UNSUPPORTED;
+    if (rc == HM_ERR_UNSUPPORTED) {
+        rc = HM_OK;
+        const unsigned g_gu = (unsigned)((R * I + kBlock - 1) / kBlock);
+#define HM_GU(LV)                                                                               \
+        HM_STAGE_LAUNCH(true, false, gateup_generic_kernel<LV>, dim3(g_gu), dim3(kBlock), 0, stream, \
+                        xdig, xscale, tokens, H, I, E, packed, layer->scale, layer->zero_point,   \
+                        offsets, perm_tokens, R, zf)
+        switch (lx) {
+        case 1: HM_GU(1); break;
+        case 2: HM_GU(2); break;
+        case 3: HM_GU(3); break;
+        default: return HM_ERR_INVALID;
+        }
 #undef HM_GU
-#undef HM_ZQ
-    HM_LAUNCHED();
-    return HM_OK;
+        HM_LAUNCHED();
+    }
+    if (rc) return rc;
+    // the stage's last launch (its end closes the timed span when armed)
+    return hm_launch_quantize_rows_timed(zf, R, I, lz, zdig, zscale, zdsum, stream);
 }
 
 int hm_launch_down_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int32_t* counts,
@@ -562,8 +574,9 @@ int hm_launch_down_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int32
     const int8_t* packed = static_cast<const int8_t*>(layer->packed);
     if (R == 0) return HM_OK;
     if (hm_use_mfma_down(layer, lz, force_generic)) {
-        return hm_launch_down_i8_mfma(layer, lz, counts, offsets, R, zdig, zscale, zdsum, y,
-                                      stream);
+        const int rc = hm_launch_down_i8_mfma(layer, lz, counts, offsets, R, zdig, zscale, zdsum,
+                                              y, stream);
+        if (rc != HM_ERR_UNSUPPORTED) return rc;
     }
     const unsigned g_dn = (unsigned)((R * H + kBlock - 1) / kBlock);
 #define HM_DN(LV)                                                                       \
@@ -726,8 +739,9 @@ int hm_matmul_f32(const float* x, const float* w, float* y, int64_t rows, int64_
 size_t hm_packed_layer_bytes(int64_t experts, int64_t hidden, int64_t intermediate,
                              int32_t dtype) {
     if (experts <= 0 || hidden <= 0 || intermediate <= 0) return 0;
-    const size_t elem = dtype == HM_DTYPE_INT8 ? 1 : dtype == HM_DTYPE_FP32 ? 4 : 0;
-    return (size_t)experts * 3 * (size_t)hidden * (size_t)intermediate * elem;
+    if (dtype == HM_DTYPE_INT8) return (size_t)experts * 3 * (size_t)hm_proj_bytes(hidden, intermediate);
+    if (dtype == HM_DTYPE_FP32) return (size_t)experts * 3 * (size_t)hidden * (size_t)intermediate * 4;
+    return 0;
 }
 
 int hm_pack_layer(const void* src, int64_t experts, int64_t hidden, int64_t intermediate,
@@ -736,20 +750,23 @@ int hm_pack_layer(const void* src, int64_t experts, int64_t hidden, int64_t inte
     HM_REQUIRE(dtype == HM_DTYPE_INT8 || dtype == HM_DTYPE_FP32);
     const int64_t H = hidden, I = intermediate;
     hipStream_t s = hm_stream(stream);
+    if (dtype == HM_DTYPE_INT8) {
+        const int64_t tiles = hm_proj_bytes(H, I) / 1024;
+        if (tiles > INT_MAX || 3 * experts > 65535) return HM_ERR_UNSUPPORTED;
+        hipLaunchKernelGGL(pack_tiles_i8_kernel, dim3((unsigned)tiles, (unsigned)(3 * experts)),
+                           dim3(256), 0, s, static_cast<const int8_t*>(src),
+                           static_cast<int8_t*>(dst), H, I);
+        HM_LAUNCHED();
+        return HM_OK;
+    }
     for (int64_t e = 0; e < experts; ++e) {
         for (int p = 0; p < 3; ++p) {
             const int64_t K = p < 2 ? H : I, N = p < 2 ? I : H;
             const int64_t off = e * 3 * H * I + p * H * I;
             const dim3 grid((unsigned)((N + 31) / 32), (unsigned)((K + 31) / 32));
-            if (dtype == HM_DTYPE_INT8) {
-                hipLaunchKernelGGL(transpose_kernel<int8_t>, grid, dim3(kBlock), 0, s,
-                                   static_cast<const int8_t*>(src) + off,
-                                   static_cast<int8_t*>(dst) + off, K, N);
-            } else {
-                hipLaunchKernelGGL(transpose_kernel<float>, grid, dim3(kBlock), 0, s,
-                                   static_cast<const float*>(src) + off,
-                                   static_cast<float*>(dst) + off, K, N);
-            }
+            hipLaunchKernelGGL(transpose_kernel<float>, grid, dim3(kBlock), 0, s,
+                               static_cast<const float*>(src) + off,
+                               static_cast<float*>(dst) + off, K, N);
             HM_LAUNCHED();
         }
     }

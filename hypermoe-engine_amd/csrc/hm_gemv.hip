@@ -3,11 +3,14 @@
 //
 // At decode (a few tokens, each expert sees one or two rows) the expert
 // GEMMs are pure weight streams: 4.5 MiB of INT8 per selected expert and a
-// handful of multiply-adds per byte.  These kernels split K across the 64
-// lanes of a wave (each lane owns fixed 16-byte slices of every weight row
-// and the matching activation slices), stream each weight row once from HBM
-// with coalesced 16-byte loads, and reduce the per-lane partial dot products
-// of all of a wave's outputs across the wave in one butterfly.
+// handful of multiply-adds per byte.  The weights are read in their device
+// layout of 32 x 32 tiles (hm_tile_offset): one wave-wide 16-byte load is a
+// whole kilobyte tile, lane l holding column l % 32 and K bytes
+// 16 (l / 32) .. +15 of it.  A lane's K positions depend only on the K tile,
+// so a wave that walks the column tiles of one K tile keeps the matching 16
+// activations per row in registers and reuses them for every column; the
+// waves of a workgroup split K, and their partial sums meet in LDS in a
+// fixed order.
 //
 // Arithmetic: the reference computes y = sum_k x_k * (float(q_k - zp) * s)
 // in FP32 (CpuTensorBackend.cpp:173-186).  Here the dequantisation is
@@ -18,19 +21,19 @@
 // the reference (rounding of FP32 sums of 2048 terms), not bit-identical to
 // it.  SiLU(G)*U uses the same float operations as the other paths.
 #include "hm_device.h"
-#include "hm_lds_dma.h"
 
 namespace {
 
-constexpr int kGemvThreads = 256;
-// Weight rows per wave (RW): 4, or 8 for gate/up when the batch selects many
-// experts (more bytes in flight per wave; at one token the extra columns per
-// workgroup only lengthen each wave's critical path).
-constexpr int kRowsPerWave = 4;
+constexpr int kGvWaves = 4;                 // waves per workgroup (they split K)
+constexpr int kGvThreads = 64 * kGvWaves;
+constexpr int kGvCols = 8;                  // column tiles (32 columns) per workgroup
+constexpr int kGvRows = 2;                  // activation rows per pass over the weights
+
+typedef int v4i __attribute__((ext_vector_type(4)));
 
 // The slot-th expert (ascending id) with a non-zero group; -1 if none.
 // Every wave computes it redundantly from `counts` (E <= 1024); the loads
-// of all 64-expert groups go out together (two groups at E = 128).
+// of all 64-expert groups go out together.
 __device__ int hm_active_expert(const int32_t* __restrict__ counts, int64_t experts, int slot) {
     const int lane = threadIdx.x & 63;
     constexpr int kGroups = 16;
@@ -56,248 +59,161 @@ __device__ int hm_active_expert(const int32_t* __restrict__ counts, int64_t expe
     return -1;
 }
 
-// The same for E <= 256 with every count load issued at once (one round
-// trip instead of one per 64-expert group).
-__device__ int hm_active_expert_256(const int32_t* __restrict__ counts, int64_t experts,
-                                    int slot) {
-    const int lane = threadIdx.x & 63;
-    int cnt[4];
+// 16 unsigned bytes (after XOR 0x80: u = q + 128) -> 16 floats
+__device__ __forceinline__ void tile_to_float(v4i w, float (&f)[16]) {
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-        const int64_t e = (int64_t)b * 64 + lane;
-        const int c = counts[e < experts ? e : experts - 1];
-        cnt[b] = e < experts ? c : 0;
-    }
-    int seen = 0;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-        const unsigned long long m = __ballot(cnt[b] > 0);
-        const int c = __popcll(m);
-        if (slot < seen + c) {
-            unsigned long long mm = m;
-            for (int i = 0; i < slot - seen; ++i) mm &= mm - 1;
-            return b * 64 + __ffsll((long long)mm) - 1;
-        }
-        seen += c;
-    }
-    return -1;
-}
-
-// Butterfly reduction of N (power of two, <= 64) values across the wave.
-// Afterwards lane l holds the full sum of value index (l >> (6 - log2 N)),
-// i.e. value i sits in lanes [i*64/N, (i+1)*64/N).
-template <int N>
-__device__ __forceinline__ float wave_reduce_many(float (&v)[N]) {
-    const int lane = threadIdx.x & 63;
-    int n = N;
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        if (n > 1) {
-            const bool upper = (lane & m) != 0;
-#pragma unroll
-            for (int i = 0; i < N / 2; ++i) {
-                if (i < n / 2) {
-                    const float send = upper ? v[i] : v[i + n / 2];
-                    const float keep = upper ? v[i + n / 2] : v[i];
-                    v[i] = keep + __shfl_xor(send, m, 64);
-                }
-            }
-            n >>= 1;
-        } else {
-            v[0] += __shfl_xor(v[0], m, 64);
-        }
-    }
-    return v[0];
-}
-
-// 4 unsigned bytes of a dword (after XOR 0x80) -> 4 floats
-__device__ __forceinline__ void bytes_to_float(uint32_t d, float* f) {
-    const uint32_t u = d ^ 0x80808080u;   // v_cvt_f32_ubyte0..3 below
-    f[0] = (float)(u & 0xffu);
-    f[1] = (float)((u >> 8) & 0xffu);
-    f[2] = (float)((u >> 16) & 0xffu);
-    f[3] = (float)(u >> 24);
-}
-
-// Lane slices of a K-long row (K % 16 == 0, K <= 1024*P): piece p of lane
-// l is the 16 bytes at k = 1024 p + 16 l, present when that is below K.
-//
-// A wave owns RW weight rows.  Each lane loads its own 16-byte
-// slices of them straight into registers (the lane later uses only the
-// bytes it loaded, so nothing is shared through LDS and nothing waits on
-// another wave); every activation row of the expert's group then meets
-// them, the rows' partial sums are reduced together, and the weights are
-// read from HBM once whatever the group size.
-//
-// GATEUP: rows j < RW/2 are gate rows n0+j, the others the up rows of the
-// same n; the inputs are hidden[perm_tokens[g]]; the output z[g, n] =
-// silu(g)*u.
-// DOWN: rows j are down rows n0+j; the inputs are z[g, :]; output y[g, n].
-template <int P, bool GATEUP, int RW>
-__device__ __forceinline__ void gemv_body(
-    const float* __restrict__ x_src, const int32_t* __restrict__ perm_tokens, int64_t K,
-    int64_t N, const int8_t* __restrict__ packed, int64_t hidden, int64_t inter,
-    const float* __restrict__ scale, const int32_t* __restrict__ zp,
-    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
-    float* __restrict__ out, const unsigned long long* s_exp2, int e, int lane,
-    int wave) {
-    constexpr int kWaves = kGemvThreads / 64;
-    const int8_t* ebase = packed + (int64_t)e * 3 * hidden * inter;
-    constexpr int kNPW = RW / 2;  // gate/up: output columns per wave
-    const int64_t n0 = GATEUP ? ((int64_t)blockIdx.x * kWaves + wave) * kNPW
-                              : ((int64_t)blockIdx.x * kWaves + wave) * RW;
-    const int64_t g0 = offsets[e];
-    const int rows = counts[e];
-    // weights -> registers: lane l's own 16-byte slices of every row (all
-    // loads go out before the activations')
-    uint4 wreg[RW][P];
-#pragma unroll
-    for (int j = 0; j < RW; ++j) {
-        const int proj = GATEUP ? j / kNPW : 2;
-        const int64_t n = GATEUP ? n0 + j % kNPW : n0 + j;
-        const int8_t* row = ebase + proj * hidden * inter + n * K;
-#pragma unroll
-        for (int p = 0; p < P; ++p) {
-            const int64_t k = 1024 * p + 16 * lane;
-            wreg[j][p] = k < K ? *reinterpret_cast<const uint4*>(row + k) : make_uint4(0, 0, 0, 0);
-        }
-    }
-    // each row's activations are loaded before the wait: the first row's
-    // stream in beside the weights
-    for (int r = 0; r < rows; ++r) {
-        const int64_t src = GATEUP ? (int64_t)perm_tokens[g0 + r] : g0 + r;
-        const float* xr = x_src + src * K;
-        float x[P][16];
-#pragma unroll
-        for (int p = 0; p < P; ++p) {
-            const int64_t k = 1024 * p + 16 * lane;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float4 v = k < K ? *reinterpret_cast<const float4*>(xr + k + 4 * i)
-                                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                x[p][4 * i] = v.x; x[p][4 * i + 1] = v.y;
-                x[p][4 * i + 2] = v.z; x[p][4 * i + 3] = v.w;
-            }
-        }
-        float xs = 0.0f;
-#pragma unroll
-        for (int p = 0; p < P; ++p)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) xs += x[p][i];
-        float xv[1] = {xs};
-        const float xsum = wave_reduce_many<1>(xv);
-        // the partial dot products of all RW weight rows, then one
-        // reduction for all of them (row j's sum lands in lanes 16j .. 16j+15)
-        float a[RW];
-#pragma unroll
-        for (int j = 0; j < RW; ++j) {
-            a[j] = 0.0f;
-#pragma unroll
-            for (int p = 0; p < P; ++p) {
-                // lanes without a piece hold zero weights; x is 0 there too
-                const uint32_t d[4] = {wreg[j][p].x, wreg[j][p].y, wreg[j][p].z, wreg[j][p].w};
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    // converted per row (hoisted out of the row loop, every
-                    // weight row's floats would stay live)
-                    uint32_t dq = d[q];
-                    asm volatile("" : "+v"(dq));
-                    float f[4];
-                    bytes_to_float(dq, f);
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) a[j] = __builtin_fmaf(x[p][4 * q + b], f[b], a[j]);
-                }
-            }
-        }
-        const float tot = wave_reduce_many<RW>(a);
-        // lane 16j holds row j's sum; each output lane gathers its rows
-        constexpr int kSpan = HM_WAVE / RW;
-        if (GATEUP) {
-            // lanes 0 .. kNPW-1: output o = lane from gate row o and up row kNPW+o
-            const int o = lane < kNPW ? lane : 0;
-            const float tg = __shfl(tot, kSpan * o, HM_WAVE);
-            const float tu = __shfl(tot, kSpan * (kNPW + o), HM_WAVE);
-            const float vg = __fmul_rn(__fsub_rn(tg, __fmul_rn((float)(128 + zp[e * 3 + 0]), xsum)),
-                                       scale[e * 3 + 0]);
-            const float vu = __fmul_rn(__fsub_rn(tu, __fmul_rn((float)(128 + zp[e * 3 + 1]), xsum)),
-                                       scale[e * 3 + 1]);
-            if (lane < kNPW) out[(g0 + r) * N + n0 + o] = __fmul_rn(hm_silu_t(vg, s_exp2), vu);
-        } else {
-            const float v = __fmul_rn(__fsub_rn(tot, __fmul_rn((float)(128 + zp[e * 3 + 2]), xsum)),
-                                      scale[e * 3 + 2]);
-            if (lane % kSpan == 0) out[(g0 + r) * N + n0 + lane / kSpan] = v;
-        }
+    for (int q = 0; q < 4; ++q) {
+        uint32_t u = (uint32_t)w[q] ^ 0x80808080u;  // v_cvt_f32_ubyte0..3 below
+        asm volatile("" : "+v"(u));  // converted where used, not hoisted
+        f[4 * q + 0] = (float)(u & 0xffu);
+        f[4 * q + 1] = (float)((u >> 8) & 0xffu);
+        f[4 * q + 2] = (float)((u >> 16) & 0xffu);
+        f[4 * q + 3] = (float)(u >> 24);
     }
 }
 
-template <int P, bool GATEUP, int RW>
-__global__ __launch_bounds__(kGemvThreads) void gemv_w8_kernel(
+// The 16 activations of lane `lane` for K tile kb of row x (0 past K).
+__device__ __forceinline__ void x_slice(const float* __restrict__ x, int64_t K, int kb, int lane,
+                                        float (&v)[16]) {
+    const int64_t k = 32 * (int64_t)kb + 16 * (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 t = k < K ? *reinterpret_cast<const float4*>(x + k + 4 * i)
+                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// GATEUP: z[g, n] = silu(x_g . Wg[n]) * (x_g . Wu[n]), x_g = hidden[perm_tokens[g]]
+// DOWN:   y[g, n] = z_g . Wd[n]
+// Workgroup: one active expert (blockIdx.y-th), kGvCols column tiles from
+// blockIdx.x * kGvCols; wave w takes K tiles [w KT/4, (w+1) KT/4).
+// ---------------------------------------------------------------------------
+template <bool GATEUP>
+__global__ __launch_bounds__(kGvThreads) void gemv_tiles_kernel(
     const float* __restrict__ x_src, const int32_t* __restrict__ perm_tokens, int64_t K,
     int64_t N, int64_t experts, const int8_t* __restrict__ packed, int64_t hidden,
     int64_t inter, const float* __restrict__ scale, const int32_t* __restrict__ zp,
     const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
     float* __restrict__ out) {
-    constexpr int kWaves = kGemvThreads / 64;
+    constexpr int NP = GATEUP ? 2 : 1;  // projections
+    __shared__ float s_red[kGvWaves][kGvRows][NP * kGvCols + 1][32];
     __shared__ unsigned long long s_exp2[32];
     if (GATEUP) hm_load_exp2_table(s_exp2);
-    __syncthreads();
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int e = experts <= 256 ? hm_active_expert_256(counts, experts, (int)blockIdx.y)
-                                 : hm_active_expert(counts, experts, (int)blockIdx.y);
+    const int e = hm_active_expert(counts, experts, (int)blockIdx.y);
+    __syncthreads();
     if (e < 0) return;
-    gemv_body<P, GATEUP, RW>(x_src, perm_tokens, K, N, packed, hidden, inter, scale, zp, counts,
-                         offsets, out, s_exp2, e, lane, wave);
-}
-
-template <int P, bool GATEUP, int RW>
-int launch_gemv(const float* x_src, const int32_t* perm_tokens, int64_t K, int64_t N,
-                const hm_layer* L, const int32_t* counts, const int32_t* offsets, int64_t slots,
-                float* out, hipStream_t s) {
-    const int64_t per_wg = (kGemvThreads / 64) * (GATEUP ? RW / 2 : RW);
-    const dim3 grid((unsigned)(N / per_wg), (unsigned)slots);
-    // (the timer, when armed, brackets the gate/up launch)
-    HM_STAGE_LAUNCH(true, true, (gemv_w8_kernel<P, GATEUP, RW>), grid, dim3(kGemvThreads), 0, s,
-                    x_src, perm_tokens, K, N, L->experts, static_cast<const int8_t*>(L->packed),
-                    L->hidden, L->intermediate, L->scale, L->zero_point, counts, offsets, out);
-    HM_LAUNCHED();
-    return HM_OK;
-}
-
-template <bool GATEUP>
-int dispatch_gemv(int64_t K, const float* x_src, const int32_t* perm_tokens, int64_t N,
-                  const hm_layer* L, const int32_t* counts, const int32_t* offsets,
-                  int64_t slots, float* out, hipStream_t s) {
-    // gate/up of a batch with many selected experts: 8 weight rows per wave
-    // (N must then be a multiple of the 16-column workgroup)
-    if constexpr (GATEUP) {
-        if (slots >= 64 && N % 16 == 0) {
-            if (K <= 1024) return launch_gemv<1, true, 8>(x_src, perm_tokens, K, N, L, counts, offsets, slots, out, s);
-            if (K <= 2048) return launch_gemv<2, true, 8>(x_src, perm_tokens, K, N, L, counts, offsets, slots, out, s);
+    const int64_t K32 = hm_pad32(K), KT = K32 / 32, NT = hm_pad32(N) / 32;
+    const int cb0 = blockIdx.x * kGvCols;
+    const int kb0 = (int)(wave * KT / kGvWaves), kb1 = (int)((wave + 1) * KT / kGvWaves);
+    const int8_t* wbase[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+        wbase[p] = packed + hm_proj_offset(e, GATEUP ? p : 2, hidden, inter) + 16 * lane;
+    const int64_t g0 = offsets[e];
+    const int rows = counts[e];
+    for (int r0 = 0; r0 < rows; r0 += kGvRows) {
+        const int nr = min(kGvRows, rows - r0);
+        const float* xr[kGvRows];
+#pragma unroll
+        for (int r = 0; r < kGvRows; ++r) {
+            const int64_t g = g0 + r0 + min(r, nr - 1);
+            xr[r] = x_src + (GATEUP ? (int64_t)perm_tokens[g] : g) * K;
         }
+        float acc[kGvRows][NP * kGvCols], xs[kGvRows];
+#pragma unroll
+        for (int r = 0; r < kGvRows; ++r) {
+            xs[r] = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NP * kGvCols; ++c) acc[r][c] = 0.0f;
+        }
+        for (int kb = kb0; kb < kb1; ++kb) {
+            // every tile of this K step first (one burst of loads)
+            v4i w[NP * kGvCols];
+#pragma unroll
+            for (int p = 0; p < NP; ++p)
+#pragma unroll
+                for (int c = 0; c < kGvCols; ++c) {
+                    const int cb = min(cb0 + c, (int)NT - 1);
+                    w[p * kGvCols + c] = *reinterpret_cast<const v4i*>(wbase[p] + ((int64_t)cb * KT + kb) * 1024);
+                }
+            float xv[kGvRows][16];
+#pragma unroll
+            for (int r = 0; r < kGvRows; ++r) {
+                x_slice(xr[r], K, kb, lane, xv[r]);
+#pragma unroll
+                for (int j = 0; j < 16; ++j) xs[r] += xv[r][j];
+            }
+#pragma unroll
+            for (int c = 0; c < NP * kGvCols; ++c) {
+                float f[16];
+                tile_to_float(w[c], f);
+#pragma unroll
+                for (int r = 0; r < kGvRows; ++r)
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) acc[r][c] = __builtin_fmaf(xv[r][j], f[j], acc[r][c]);
+            }
+        }
+        // the two K halves of a column (lanes l, l + 32), then the waves in
+        // order through LDS
+#pragma unroll
+        for (int r = 0; r < kGvRows; ++r) {
+#pragma unroll
+            for (int c = 0; c < NP * kGvCols; ++c) {
+                const float v = acc[r][c] + __shfl_xor(acc[r][c], 32, 64);
+                if (lane < 32) s_red[wave][r][c][lane] = v;
+            }
+            const float xv = xs[r] + __shfl_xor(xs[r], 32, 64);
+            if (lane < 32) s_red[wave][r][NP * kGvCols][lane] = xv;
+        }
+        __syncthreads();
+        // wave w finalises rows r = w (of the kGvRows) ... one row per wave
+        for (int r = wave; r < nr; r += kGvWaves) {
+            if (lane < 32) {
+                // the activation sum (every lane of a wave holds its wave's
+                // part), over the waves in order
+                float x_sum = 0.0f;
+                for (int w = 0; w < kGvWaves; ++w) x_sum += s_red[w][r][NP * kGvCols][0];
+                const int64_t g = g0 + r0 + r;
+#pragma unroll
+                for (int c = 0; c < kGvCols; ++c) {
+                    const int64_t n = 32 * (int64_t)(cb0 + c) + lane;
+                    float t[NP];
+#pragma unroll
+                    for (int p = 0; p < NP; ++p) {
+                        float a = 0.0f;
+                        for (int w = 0; w < kGvWaves; ++w) a += s_red[w][r][p * kGvCols + c][lane];
+                        const int pr = GATEUP ? p : 2;
+                        t[p] = __fmul_rn(__fsub_rn(a, __fmul_rn((float)(128 + zp[e * 3 + pr]), x_sum)),
+                                         scale[e * 3 + pr]);
+                    }
+                    if (cb0 + c < NT && n < N) {
+                        if (GATEUP) out[g * N + n] = __fmul_rn(hm_silu_t(t[0], s_exp2), t[NP - 1]);
+                        else out[g * N + n] = t[0];
+                    }
+                }
+            }
+        }
+        __syncthreads();
     }
-    if (K <= 1024) return launch_gemv<1, GATEUP, kRowsPerWave>(x_src, perm_tokens, K, N, L, counts, offsets, slots, out, s);
-    if (K <= 2048) return launch_gemv<2, GATEUP, kRowsPerWave>(x_src, perm_tokens, K, N, L, counts, offsets, slots, out, s);
-    return HM_ERR_UNSUPPORTED;
 }
 
 // ---------------------------------------------------------------------------
-// Decode down projection fused with the combine, column-block major: a
-// workgroup owns kDcCols output columns n0 .. n0+kDcCols-1 for EVERY active
-// expert (its 16 waves take the experts in turn, each streaming the
-// expert's kDcCols down rows into its LDS slot), keeps y[g, n0 ..] of every
-// grouped row g in LDS, and then forms the tokens' outputs for its columns
-// with hm_combine's arithmetic.  No workgroup needs another's results, so
-// there is no device-wide synchronisation, and y goes to memory only when
-// the caller asks for the expert outputs.  Each y uses gemv_body's DOWN
-// lane slices; the 8 columns' partial sums are reduced across the wave
-// together (one butterfly for all of them, not one per column), so y
-// agrees with the two-kernel path to rounding.  T <= 16, top_k <= 16,
-// I <= 1024.
+// Decode down projection fused with the combine, column-tile major: a
+// workgroup owns one 32-column output tile for EVERY active expert (its 16
+// waves take the experts in turn, each streaming the expert's down tiles of
+// that column tile), keeps y[g, those columns] of every grouped row g in
+// LDS, and then forms the tokens' outputs for its columns with hm_combine's
+// arithmetic.  No workgroup needs another's results, so there is no
+// device-wide synchronisation, and y goes to memory only when the caller
+// asks for the expert outputs.  T <= 16, top_k <= 16, I <= 1024.
 // ---------------------------------------------------------------------------
-constexpr int kDcCols = 8;
 constexpr int kDcWaves = 16;
 constexpr int kDcPairs = HM_GEMV_MAX_TOKENS * 16;
+constexpr int kDcMaxKT = 32;  // I <= 1024
 
 __global__ __launch_bounds__(64 * kDcWaves) void gemv_down_combine_kernel(
     const float* __restrict__ z, int64_t I, int64_t H, int64_t experts,
@@ -307,8 +223,7 @@ __global__ __launch_bounds__(64 * kDcWaves) void gemv_down_combine_kernel(
     const int32_t* __restrict__ slots, const float* __restrict__ scores,
     const float* __restrict__ residual, int tokens, int top_k, float* __restrict__ y_out,
     float* __restrict__ out) {
-    __shared__ __attribute__((aligned(1024))) int8_t wl[kDcWaves][kDcCols * 1024];
-    __shared__ float s_y[kDcPairs][kDcCols];
+    __shared__ float s_y[kDcPairs][32];
     __shared__ int s_cnt[1024], s_off[1024], s_act[1024];
     __shared__ int s_nact;
     __shared__ uint32_t s_ids[kDcPairs];
@@ -316,7 +231,7 @@ __global__ __launch_bounds__(64 * kDcWaves) void gemv_down_combine_kernel(
     __shared__ float s_w[HM_GEMV_MAX_TOKENS][16];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int64_t n0 = (int64_t)blockIdx.x * kDcCols;
+    const int cb = blockIdx.x;
     // every routing input the workgroup needs, in one round of loads
     const int pairs = tokens * top_k;
     for (int i = tid; i < experts; i += 64 * kDcWaves) {
@@ -359,90 +274,81 @@ __global__ __launch_bounds__(64 * kDcWaves) void gemv_down_combine_kernel(
     }
     __syncthreads();
     const int nact = s_nact;
-    const int64_t K = I;
-    int8_t* lds = wl[wave];
+    const int64_t KT = hm_pad32(I) / 32;
     for (int a = wave; a < nact; a += kDcWaves) {
         const int e = s_act[a];
-        const int8_t* wrows = packed + (int64_t)e * 3 * H * I + 2 * H * I + n0 * K;
-        const int64_t k = 16 * lane;
-        __builtin_amdgcn_wave_barrier();
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the slot's last reads are done
-        if (k < K) {
+        const int8_t* wt = packed + hm_proj_offset(e, 2, H, I) + (int64_t)cb * KT * 1024 + 16 * lane;
+        // the expert's whole column tile (K <= 1024: at most 32 tiles)
+        v4i w[kDcMaxKT];
 #pragma unroll
-            for (int j = 0; j < kDcCols; ++j) dma16(wrows + j * K + k, lds + j * 1024);
-        }
+        for (int kb = 0; kb < kDcMaxKT; ++kb)
+            if (kb < KT) w[kb] = *reinterpret_cast<const v4i*>(wt + (int64_t)kb * 1024);
         const int64_t g0 = s_off[e];
         const int rows = s_cnt[e];
         const float sc = scale[e * 3 + 2];
         const float zc = (float)(128 + zp[e * 3 + 2]);
-        wait_vmcnt<0>();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
         for (int r = 0; r < rows; ++r) {
-            const float* xr = z + (g0 + r) * K;
-            float x[16];
+            const float* xr = z + (g0 + r) * I;
+            float acc = 0.0f, xs = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float4 v = k < K ? *reinterpret_cast<const float4*>(xr + k + 4 * i)
-                                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
-            }
-            float xs = 0.0f;
+            for (int kb = 0; kb < kDcMaxKT; ++kb) {
+                if (kb < KT) {
+                    float xv[16], f[16];
+                    x_slice(xr, I, kb, lane, xv);
+                    tile_to_float(w[kb], f);
 #pragma unroll
-            for (int i = 0; i < 16; ++i) xs += x[i];
-            float xv[1] = {xs};
-            const float xsum = wave_reduce_many<1>(xv);
-            // the kDcCols partial dot products of this lane, then one
-            // reduction for all of them (column j ends up in lanes 8j .. 8j+7)
-            float acc[kDcCols];
-#pragma unroll
-            for (int j = 0; j < kDcCols; ++j) {
-                acc[j] = 0.0f;
-                // lanes without a piece read their own unused slot; x is 0
-                const uint4 wv = *reinterpret_cast<const uint4*>(lds + j * 1024 + 16 * lane);
-                const uint32_t d[4] = {wv.x, wv.y, wv.z, wv.w};
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    // converted per row (hoisted out of the row loop, the 8
-                    // rows' 128 floats would spill)
-                    uint32_t dq = d[q];
-                    asm volatile("" : "+v"(dq));
-                    float f[4];
-                    bytes_to_float(dq, f);
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) acc[j] = __builtin_fmaf(x[4 * q + b], f[b], acc[j]);
+                    for (int j = 0; j < 16; ++j) {
+                        acc = __builtin_fmaf(xv[j], f[j], acc);
+                        xs += xv[j];
+                    }
                 }
             }
-            const float tot = wave_reduce_many<kDcCols>(acc);
-            const int jl = lane / (HM_WAVE / kDcCols);
-            const float y = __fmul_rn(__fsub_rn(tot, __fmul_rn(zc, xsum)), sc);
-            if (lane % (HM_WAVE / kDcCols) == 0) {
-                s_y[(g0 + r) & (kDcPairs - 1)][jl] = y;
-                if (y_out) y_out[(g0 + r) * H + n0 + jl] = y;
+            acc += __shfl_xor(acc, 32, 64);
+            // the activation sum: lanes l and l + 32 hold the sums of the two
+            // K halves (the same in every column)
+            const float xt = xs + __shfl_xor(xs, 32, 64);
+            const float y = __fmul_rn(__fsub_rn(acc, __fmul_rn(zc, xt)), sc);
+            const int64_t n = 32 * (int64_t)cb + lane;
+            if (lane < 32) {
+                s_y[(g0 + r) & (kDcPairs - 1)][lane] = y;
+                if (y_out && n < H) y_out[(g0 + r) * H + n] = y;
             }
         }
     }
     // the combine of hm_combine (MoERuntime.cpp:308-325) for these columns
     __syncthreads();
-    for (int i = tid; i < tokens * kDcCols; i += 64 * kDcWaves) {
-        const int t = i / kDcCols, c = i % kDcCols;
+    for (int i = tid; i < tokens * 32; i += 64 * kDcWaves) {
+        const int t = i / 32, c = i % 32;
+        const int64_t n = 32 * (int64_t)cb + c;
+        if (n >= H) continue;
         float acc = 0.0f;
         for (int r = 0; r < top_k; ++r)
             acc = __fadd_rn(acc, __fmul_rn(s_w[t][r], s_y[s_row[t][r] & (kDcPairs - 1)][c]));
-        const int64_t n = n0 + c;
         if (residual) acc = __fadd_rn(residual[t * H + n], acc);
         out[t * H + n] = acc;
     }
 }
 
-// Rows up to 2048 bytes keep a wave's 8 weight rows within 16 KB of LDS.
-bool gemv_k_ok(int64_t K) { return K >= 16 && K % 16 == 0 && K <= 2048; }
+template <bool GATEUP>
+int launch_gemv(const float* x_src, const int32_t* perm_tokens, int64_t K, int64_t N,
+                const hm_layer* L, const int32_t* counts, const int32_t* offsets, int64_t slots,
+                float* out, hipStream_t s) {
+    const int64_t nt = hm_pad32(N) / 32;
+    const dim3 grid((unsigned)((nt + kGvCols - 1) / kGvCols), (unsigned)slots);
+    // (the timer, when armed, brackets the gate/up launch)
+    HM_STAGE_LAUNCH(true, true, (gemv_tiles_kernel<GATEUP>), grid, dim3(kGvThreads), 0, s, x_src,
+                    perm_tokens, K, N, L->experts, static_cast<const int8_t*>(L->packed),
+                    L->hidden, L->intermediate, L->scale, L->zero_point, counts, offsets, out);
+    HM_LAUNCHED();
+    return HM_OK;
+}
 
 }  // namespace
 
-// Shapes the GEMV kernels take: H, I multiples of 16 up to 2048 (the
-// tiles: 8 gate/up columns and 16 down rows per workgroup).
+// Shapes the GEMV kernels take: H, I multiples of 16 (whole float4
+// activation slices) up to 65536.
 bool hm_gemv_shape_ok(int64_t H, int64_t I) {
-    return gemv_k_ok(H) && gemv_k_ok(I) && I % 8 == 0 && H % 16 == 0;
+    return H >= 16 && I >= 16 && H % 16 == 0 && I % 16 == 0 && H <= 65536 && I <= 65536;
 }
 
 // z[g, n] = silu(x_g . Wg[n]) * (x_g . Wu[n]) for every grouped row g, with
@@ -450,16 +356,17 @@ bool hm_gemv_shape_ok(int64_t H, int64_t I) {
 int hm_launch_gateup_gemv(const hm_layer* L, const float* hidden, const int32_t* counts,
                           const int32_t* offsets, const int32_t* perm_tokens, int64_t pairs,
                           float* z, hipStream_t s) {
+    if (L->experts > 1024) return HM_ERR_UNSUPPORTED;
     const int64_t slots = pairs < L->experts ? pairs : L->experts;
-    return dispatch_gemv<true>(L->hidden, hidden, perm_tokens, L->intermediate, L, counts,
-                               offsets, slots, z, s);
+    return launch_gemv<true>(hidden, perm_tokens, L->hidden, L->intermediate, L, counts, offsets,
+                             slots, z, s);
 }
 
 // The decode down projection fused with the combine (T <= 16, top_k <= 16,
-// I <= 1024, H % 8 == 0); y_out (optional) receives the expert outputs.
+// I <= 1024); y_out (optional) receives the expert outputs.
 bool hm_gemv_combine_ok(int64_t tokens, int32_t top_k, int64_t H, int64_t I) {
-    return tokens <= HM_GEMV_MAX_TOKENS && top_k <= 16 && I <= 1024 && I % 16 == 0 &&
-           H % kDcCols == 0;
+    return tokens <= HM_GEMV_MAX_TOKENS && top_k <= 16 && I <= 32 * kDcMaxKT && I % 16 == 0 &&
+           H % 16 == 0;
 }
 
 int hm_launch_down_combine_gemv(const hm_layer* L, const float* z, const int32_t* counts,
@@ -469,7 +376,7 @@ int hm_launch_down_combine_gemv(const hm_layer* L, const float* z, const int32_t
                                 float* y_out, float* out, hipStream_t s) {
     if (!hm_gemv_combine_ok(tokens, top_k, L->hidden, L->intermediate) || L->experts > 1024)
         return HM_ERR_UNSUPPORTED;
-    hipLaunchKernelGGL(gemv_down_combine_kernel, dim3((unsigned)(L->hidden / kDcCols)),
+    hipLaunchKernelGGL(gemv_down_combine_kernel, dim3((unsigned)(hm_pad32(L->hidden) / 32)),
                        dim3(64 * kDcWaves), 0, s, z, L->intermediate, L->hidden, L->experts,
                        static_cast<const int8_t*>(L->packed), L->scale, L->zero_point, counts,
                        offsets, ids, slots, scores, residual, (int)tokens, top_k, y_out, out);
@@ -480,7 +387,8 @@ int hm_launch_down_combine_gemv(const hm_layer* L, const float* z, const int32_t
 // y[g, n] = z_g . Wd[n] for every grouped row g.
 int hm_launch_down_gemv(const hm_layer* L, const float* z, const int32_t* counts,
                         const int32_t* offsets, int64_t pairs, float* y, hipStream_t s) {
+    if (L->experts > 1024) return HM_ERR_UNSUPPORTED;
     const int64_t slots = pairs < L->experts ? pairs : L->experts;
-    return dispatch_gemv<false>(L->intermediate, z, nullptr, L->hidden, L, counts, offsets,
-                                slots, y, s);
+    return launch_gemv<false>(z, nullptr, L->intermediate, L->hidden, L, counts, offsets, slots,
+                              y, s);
 }

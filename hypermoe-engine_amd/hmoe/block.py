@@ -44,7 +44,10 @@ class DeviceExpertLayer:
         dtype = capi.HM_DTYPE_INT8 if self.int8 else capi.HM_DTYPE_FP32
         self.dtype = dtype
         src = torch.from_numpy(np.ascontiguousarray(payload)).to("cuda")
-        self.packed = torch.empty_like(src)
+        nbytes = capi.load().hm_packed_layer_bytes(self.experts, hidden, inter, dtype)
+        if nbytes == 0:
+            raise ValueError("invalid expert layer shape")
+        self.packed = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
         s = torch.cuda.current_stream().cuda_stream if stream is None else stream
         capi.call("hm_pack_layer", src.data_ptr(), self.experts, hidden, inter, dtype,
                   self.packed.data_ptr(), s)
@@ -84,7 +87,7 @@ class BlockResult:
 
 class MoEBlock:
     def __init__(self, layer: DeviceExpertLayer, top_k: int, softmax: bool = True,
-                 renorm: bool = True, limbs_x: int = 2, limbs_z: int = 2):
+                 renorm: bool = True, limbs_x: int = 2, limbs_z: int = 3):
         self.layer, self.top_k = layer, top_k
         self.flags = (ROUTE_SOFTMAX if softmax else 0) | (ROUTE_RENORM if renorm else 0)
         self.limbs_x, self.limbs_z = limbs_x, limbs_z

@@ -31,7 +31,8 @@ def _torch():
 
 class MoEStack:
     def __init__(self, layers: list[DeviceExpertLayer], router_w: list, top_k: int,
-                 eps: float = 1e-6, limbs: int = 2, flags: int = capi.HM_ROUTE_SOFTMAX | capi.HM_ROUTE_RENORM):
+                 eps: float = 1e-6, limbs_x: int = 2, limbs_z: int = 3,
+                 flags: int = capi.HM_ROUTE_SOFTMAX | capi.HM_ROUTE_RENORM):
         torch = _torch()
         if not layers or len(layers) != len(router_w):
             raise ValueError("one router matrix per layer")
@@ -39,7 +40,8 @@ class MoEStack:
         if any(l.hidden != h0 for l in layers):
             raise ValueError("all layers share the hidden size")
         self.layers, self.router_w = layers, router_w
-        self.top_k, self.eps, self.limbs, self.flags = top_k, eps, limbs, flags
+        self.top_k, self.eps, self.flags = top_k, eps, flags
+        self.limbs_x, self.limbs_z = limbs_x, limbs_z
         self.hidden = h0
         self.gamma = torch.ones(h0, dtype=torch.float32, device="cuda")
         self.status = torch.zeros(1, dtype=torch.int32, device="cuda")
@@ -52,7 +54,7 @@ class MoEStack:
         need = 0
         for l in self.layers:
             need = max(need, capi.load().hm_moe_block_workspace_bytes(
-                C.byref(l.desc), tokens, self.top_k, self.limbs, self.limbs, 0))
+                C.byref(l.desc), tokens, self.top_k, self.limbs_x, self.limbs_z, 0))
         if need == 0:
             raise ValueError("invalid stack configuration")
         self.ws = torch.empty(need, dtype=torch.uint8, device="cuda")
@@ -81,7 +83,7 @@ class MoEStack:
             io = capi.HmBlockIO(out.data_ptr(), None, None, None, None, None, None, None,
                                 self.status.data_ptr(), cur.data_ptr())
             capi.call("hm_moe_block_forward", C.byref(layer.desc), self.norm.data_ptr(),
-                      w.data_ptr(), tokens, self.top_k, self.flags, self.limbs, self.limbs,
+                      w.data_ptr(), tokens, self.top_k, self.flags, self.limbs_x, self.limbs_z,
                       C.byref(io), self.ws.data_ptr(), self.ws.numel(), s)
             cur = out
             if events is not None:
@@ -100,8 +102,8 @@ class MoEStack:
             raise RuntimeError(f"router failed on the device (status bits {st:#x})")
 
 
-def build_stack(cfg, seed: int | None = None, layers: int | None = None, limbs: int = 2,
-                log=None) -> MoEStack:
+def build_stack(cfg, seed: int | None = None, layers: int | None = None, limbs_x: int = 2,
+                limbs_z: int = 3, log=None) -> MoEStack:
     """The seeded INT8 stack of a configuration (synth.CONFIGS): per layer the
     packed experts and the router matrix, generated on the host by the
     synthetic generator and kept resident on the device."""
@@ -119,4 +121,4 @@ def build_stack(cfg, seed: int | None = None, layers: int | None = None, limbs: 
         routers.append(torch.from_numpy(np.ascontiguousarray(w)).to("cuda"))
         if log is not None:
             log(l)
-    return MoEStack(dev_layers, routers, cfg.top_k, limbs=limbs)
+    return MoEStack(dev_layers, routers, cfg.top_k, limbs_x=limbs_x, limbs_z=limbs_z)

@@ -160,7 +160,7 @@ struct BlockOptions {
     // input).  2 keeps the FP32 result within 1e-4 of the W8A32 reference;
     // 3 within 1e-5.
     int limbsX{2};
-    int limbsZ{2};
+    int limbsZ{3};
     // Run the INT8 expert GEMMs on the scalar kernels (same integers and
     // float operations as the MFMA kernels; for pinning them).
     bool genericKernels{false};

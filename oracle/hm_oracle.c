@@ -504,35 +504,14 @@ int hmo_limb_expert_mlp(const hmo_layer* layer, int64_t expert, const float* x,
     float* g = (float*)malloc(inter * sizeof(float));
     float* u = (float*)malloc(inter * sizeof(float));
     float* z = (float*)malloc(inter * sizeof(float));
-    const int64_t zb = HMO_ZBLOCK;
-    int8_t* dg = (int8_t*)malloc((size_t)(limbs_z * rows * zb));
-    float* s = (float*)malloc((size_t)rows * sizeof(float));
-    int32_t* p = (int32_t*)malloc((size_t)(limbs_z * rows * H) * sizeof(int32_t));
-    int rc = (g && u && z && dg && s && p) ? HMO_OK : HMO_E_RUNTIME;
+    int rc = (g && u && z) ? HMO_OK : HMO_E_RUNTIME;
     if (!rc) rc = hmo_limb_matmul(x, rows, H, base, sc[0], zp[0], I, limbs_x, g);
     if (!rc) rc = hmo_limb_matmul(x, rows, H, base + H * I, sc[1], zp[1], I, limbs_x, u);
     if (!rc) {
         for (size_t i = 0; i < inter; ++i) z[i] = silu1(g[i]) * u[i];
-        for (size_t i = 0; i < (size_t)(rows * H); ++i) y[i] = 0.0F;
-        const int8_t* down = base + 2 * H * I;
-        for (int64_t k0 = 0; k0 < I && rc == HMO_OK; k0 += zb) {
-            const int64_t kn = (I - k0) < zb ? (I - k0) : zb;
-            rc = hmo_limb_quantize(z + k0, rows, kn, I, limbs_z, dg, s);
-            if (!rc) {
-                rc = hmo_limb_partials(dg, rows, kn, limbs_z, down + k0 * H,
-                                       zp[2], H, p);
-            }
-            if (rc) break;
-            for (int64_t r = 0; r < rows; ++r) {
-                const float alpha = s[r] * sc[2];
-                for (int64_t c = 0; c < H; ++c) {
-                    const float cb = recombine(p + r * H + c, rows * H, limbs_z);
-                    y[r * H + c] = fmaf(cb, alpha, y[r * H + c]);
-                }
-            }
-        }
+        rc = hmo_limb_matmul(z, rows, I, base + 2 * H * I, sc[2], zp[2], H, limbs_z, y);
     }
-    free(g); free(u); free(z); free(dg); free(s); free(p);
+    free(g); free(u); free(z);
     return rc;
 }
 

@@ -127,11 +127,11 @@ int hmo_combine(const float* y_grouped, const int32_t* offsets,
  * Recombination (float, explicit fmaf, fixed order):
  *   c = (float)P_{L-1}; for l = L-2..0: c = fmaf(c, 256, (float)P_l)
  *   alpha = s * scale_w;  value = c * alpha
- * The gate/up GEMM uses one segment per row (whole H).  The down GEMM uses
- * segments of HM_ZBLOCK columns of Z = silu(G)*U and accumulates
- *   acc = fmaf(c_b, alpha_b, acc)  over blocks b ascending, acc0 = 0.
+ * Both GEMMs use one segment per row: the gate/up GEMM quantises each
+ * token row of X (whole H), the down GEMM each row of Z = silu(G)*U (whole
+ * I), so every partial is one exact integer per (row, column) and the
+ * recombination above gives the output directly.
  * ---------------------------------------------------------------------- */
-#define HMO_ZBLOCK 128
 
 /* Quantise `rows` segments of length n (row stride ld) to L digit planes:
  * digits[(l*rows + r)*n + k]; scales[r] = s. */
@@ -150,8 +150,9 @@ int hmo_limb_matmul(const float* x, int64_t rows, int64_t inner,
                     const int8_t* q, float scale, int32_t zp, int64_t cols,
                     int32_t limbs, float* y);
 
-/* Expert MLP in limb arithmetic: gate/up with per-row segments, SiLU(G)*U in
- * float, down with HMO_ZBLOCK-column segments. */
+/* Expert MLP in limb arithmetic: G and U with limbs_x digits per X row,
+ * Z = SiLU(G)*U in float (Activation.cpp:44 then CpuTensorBackend::mul),
+ * down with limbs_z digits per Z row. */
 int hmo_limb_expert_mlp(const hmo_layer* layer, int64_t expert, const float* x,
                         int64_t rows, int32_t limbs_x, int32_t limbs_z,
                         float* y);

@@ -387,7 +387,7 @@ void blockTests(const std::shared_ptr<backend::HipBackend>& hip) {
                  L.zp.data()};
     std::vector<float> lout(T * H), lsc(T * k);
     std::vector<uint32_t> lids(T * k);
-    hmo_moe_block_limbs(&ol, h.data(), w.data(), (int64_t)T, (int32_t)k, 1, 1, 2, 2, lout.data(),
+    hmo_moe_block_limbs(&ol, h.data(), w.data(), (int64_t)T, (int32_t)k, 1, 1, 2, 3, lout.data(),
                         lids.data(), lsc.data());
     bool idsOk = res.routing.tokens.size() == T && res.routing.layerId == 7;
     for (std::size_t t = 0; t < T && idsOk; ++t) {

@@ -91,12 +91,16 @@ def test_host_packer_matches_reference_quantiser():
 def test_workspace_and_layer_sizes():
     lib = capi.load()
     assert lib.hm_packed_layer_bytes(128, 2048, 768, capi.HM_DTYPE_INT8) == 128 * 3 * 2048 * 768
+    # INT8 projections are padded to 32 x 32 tiles
+    assert lib.hm_packed_layer_bytes(3, 40, 70, capi.HM_DTYPE_INT8) == 3 * 3 * 64 * 96
     assert lib.hm_packed_layer_bytes(64, 2048, 768, capi.HM_DTYPE_FP32) == 64 * 3 * 2048 * 768 * 4
     layer = capi.HmLayer(128, 2048, 768, capi.HM_DTYPE_INT8, 1, 1, 1)
-    a = lib.hm_moe_block_workspace_bytes(C.byref(layer), 4096, 8, 2, 2, 0)
-    b = lib.hm_moe_block_workspace_bytes(C.byref(layer), 4096, 8, 2, 2, capi.HM_EXEC_GENERIC)
-    # scratch floats: z [P x I] on the generic path, g and u [2 x P x I] on the MFMA path
-    assert a > 0 and a - b == 4096 * 8 * 768 * 4, "MFMA path holds g and u, generic path z"
+    a = lib.hm_moe_block_workspace_bytes(C.byref(layer), 4096, 8, 2, 3, 0)
+    b = lib.hm_moe_block_workspace_bytes(C.byref(layer), 4096, 8, 2, 3, capi.HM_EXEC_GENERIC)
+    # both paths hold the same buffers (z [P x I] floats, then its digits)
+    assert a > 0 and a == b
+    c = lib.hm_moe_block_workspace_bytes(C.byref(layer), 4096, 8, 2, 2, 0)
+    assert a - c == 4096 * 8 * 768 + 4096 * 8 * 4, "one more Z digit plane and its digit sums"
     assert lib.hm_moe_block_workspace_bytes(C.byref(layer), 0, 8, 2, 2, 0) == 0
     # logits, then 4 K ranges of FP64 partials and norms, then W transposed
     assert lib.hm_route_workspace_bytes(4096, 2048, 128) == (

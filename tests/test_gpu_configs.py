@@ -83,7 +83,8 @@ def _layer_by_layer(stack, h, keep_rows):
     for the checked layers, (layer input rows, layer output rows)."""
     cur, saved = h, {}
     for l in range(len(stack.layers)):
-        one = MoEStack([stack.layers[l]], [stack.router_w[l]], stack.top_k, limbs=stack.limbs)
+        one = MoEStack([stack.layers[l]], [stack.router_w[l]], stack.top_k,
+                       limbs_x=stack.limbs_x, limbs_z=stack.limbs_z)
         out = one.launch(cur).clone()
         one.check_status()
         if l in CHECK_LAYERS:
@@ -110,7 +111,7 @@ def _check_layer(stack, host, l, h_in, got, limb_exact):
     assert nw < 1e-4, f"layer {l}"
     if limb_exact:
         lout, _, _ = O.moe_block_limbs(payload, scale, zp, hn, w, C5.top_k, C5.inter,
-                                       stack.limbs, stack.limbs)
+                                       stack.limbs_x, stack.limbs_z)
         assert_bitexact(got, (lout + h_in).astype(np.float32), f"layer {l} vs limb oracle")
 
 

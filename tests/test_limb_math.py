@@ -109,12 +109,13 @@ def test_limb_recombine_is_the_documented_sequence():
 
 
 def test_c4_full_batch_error_budget():
-    """The two-limb block at the full C4 workload (T=4096, E=128, k=8,
-    Zipf-skewed routing) against the reference W8A32 block on every token:
-    the compare form at 1e-4 (CorrectnessOracle.cpp:44-67) and the normwise
-    error max|a-b| / max|b| below 1e-4 with at least 20 % to spare.  The
-    device path is bit-exact against this limb arithmetic, so this bounds
-    the device's error at the benchmark workload, not only on a sample."""
+    """The block's default limb counts (two X digits, three Z digits) at the
+    full C4 workload (T=4096, E=128, k=8, Zipf-skewed routing) against the
+    reference W8A32 block on every token: the compare form at 1e-4
+    (CorrectnessOracle.cpp:44-67) and the normwise error max|a-b| / max|b|
+    below 1e-4 with at least 20 % to spare.  The device path is bit-exact
+    against this limb arithmetic, so this bounds the device's error at the
+    benchmark workload, not only on a sample."""
     from conftest import oracle_by_token_chunks
     from hmoe import synth
     cfg = synth.CONFIGS["C4"]
@@ -124,14 +125,14 @@ def test_c4_full_batch_error_budget():
     w = synth.router_weights(cfg.seed, 0, H, E)
     synth.apply_skew(h, w, synth.zipf_bias(cfg.seed, E))
     ref, rids, _ = oracle_by_token_chunks(O.moe_block, h, payload, scale, zp, w, k, I)
-    out, ids, _ = oracle_by_token_chunks(O.moe_block_limbs, h, payload, scale, zp, w, k, I, 2, 2)
+    out, ids, _ = oracle_by_token_chunks(O.moe_block_limbs, h, payload, scale, zp, w, k, I, 2, 3)
     assert_bitexact(ids, rids, "routing")
     err = np.abs(out.astype(np.float64) - ref.astype(np.float64))
     tok = int(np.argmax(err.max(axis=1)))
     nw = normwise(out, ref)
     per_token = err.max(axis=1) / np.maximum(np.abs(ref).max(axis=1), 1e-30)
-    print(f"C4 L=2: normwise {nw:.3e}, worst token {tok} (abs {err.max():.3e}, "
+    print(f"C4 limbs (2, 3): normwise {nw:.3e}, worst token {tok} (abs {err.max():.3e}, "
           f"its own normwise {per_token[tok]:.3e}), worst per-token normwise "
           f"{per_token.max():.3e} at token {int(np.argmax(per_token))}")
-    assert_compare(out, ref, 1e-4, 1e-4, "C4 L=2 vs reference W8A32")
+    assert_compare(out, ref, 1e-4, 1e-4, "C4 limbs (2, 3) vs reference W8A32")
     assert nw < 0.8e-4, nw
