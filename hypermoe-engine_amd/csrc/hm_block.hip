@@ -16,7 +16,7 @@ int hm_launch_gateup_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int
                         const float* xscale, const int32_t* xdsum, int64_t tokens,
                         const int32_t* counts, const int32_t* offsets,
                         const int32_t* perm_tokens, int64_t R, int8_t* zdig, float* zscale,
-                        int32_t* zdsum, float* zf, bool force_generic, hipStream_t stream);
+                        int32_t* zdsum, float* gu, bool force_generic, hipStream_t stream);
 int hm_launch_down_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int32_t* counts,
                       const int32_t* offsets, int64_t R, const int8_t* zdig,
                       const float* zscale, const int32_t* zdsum, float* y,
@@ -92,6 +92,7 @@ struct BlockPlan {
     float* zscale;
     int32_t* zdsum;
     float* zf;
+    float* gu;  // INT8 limb path: gate | up values [P x 2I], aliasing y
     float* y;
     int32_t* status;
     int32_t* counters;  // decode: the fused select's completion counter
@@ -137,7 +138,12 @@ size_t plan_block(const hm_layer* L, int64_t T, int32_t k, int32_t lx, int32_t l
         q.zdig = c.take<int8_t>((size_t)lz * P * I);
         q.zscale = c.take<float>((size_t)P);
         q.zdsum = c.take<int32_t>((size_t)lz * P);
-        q.zf = c.take<float>((size_t)P * I);
+        // the gate/up values [P x 2I] are dead once the Z digits are cut,
+        // before the down projection writes y: one region serves both
+        q.y = c.take<float>((size_t)P * (H > 2 * I ? H : 2 * I));
+        q.gu = q.y;
+        if (p) *p = q;
+        return c.used;
     } else {
         q.zf = c.take<float>((size_t)P * I);
     }
@@ -271,7 +277,7 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
         rc = gate_up([&] {
             return hm_launch_gateup_i8(layer, limbs_x, limbs_z, p.xdig, p.xscale, p.xdsum,
                                        tokens, counts, p.offsets, p.perm_tokens, P, p.zdig,
-                                       p.zscale, p.zdsum, p.zf, generic, s);
+                                       p.zscale, p.zdsum, p.gu, generic, s);
         });
         if (rc) return rc;
         rc = hm_launch_down_i8(layer, limbs_x, limbs_z, counts, p.offsets, P, p.zdig,

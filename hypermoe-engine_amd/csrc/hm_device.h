@@ -240,31 +240,28 @@ __device__ __forceinline__ float hm_recombine(const int* p, int limbs) {
     return c;
 }
 
-// One wave quantises one FP32 row of n = 256*nv floats (16-byte aligned) to
-// L fixed-point digit planes: the row max gives the step (inv = range /
-// max|x|), every element becomes rint(x * inv) split into L digits.  Plane l
-// of the row goes to digits + l * plane_stride (4 bytes per lane and float4),
-// its digit sum to dsum[l * dsum_stride] (when dsum is set), the scale
-// max|x| / range to *scale.  Shared by the row-quantisation kernel and the
-// prefill router's select kernel, so both write the same bytes.
+// One wave quantises one FP32 row of n = 256*nv floats to L fixed-point
+// digit planes: the row max gives the step (inv = range / max|x|), every
+// element becomes rint(x * inv) split into L digits.  The row is in
+// registers, lane: floats 4*(lane + 64 i) .. +3 in v[i].  Plane l of the row
+// goes to digits + l * plane_stride (4 bytes per lane and float4), its digit
+// sum to dsum[l * dsum_stride] (when dsum is set), the scale max|x| / range
+// to *scale.  Shared by the row-quantisation kernels and the prefill
+// router's select kernel, so all of them write the same bytes.
 constexpr int kHmQuantMaxV = 16;  // n <= 4096
 template <int L>
-__device__ __forceinline__ void hm_quantize_row_wave(const float* __restrict__ xrow, int nv,
-                                                     int8_t* __restrict__ digits,
-                                                     int64_t plane_stride, float* scale,
-                                                     int32_t* __restrict__ dsum,
-                                                     int64_t dsum_stride) {
+__device__ __forceinline__ void hm_quantize_row_values(const float4* v, int nv,
+                                                       int8_t* __restrict__ digits,
+                                                       int64_t plane_stride, float* scale,
+                                                       int32_t* __restrict__ dsum,
+                                                       int64_t dsum_stride) {
     const int lane = threadIdx.x & (HM_WAVE - 1);
-    const float4* xr = reinterpret_cast<const float4*>(xrow);
-    float4 v[kHmQuantMaxV];
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < kHmQuantMaxV; ++i) {
-        if (i < nv) {
-            v[i] = xr[lane + HM_WAVE * i];
+        if (i < nv)
             amax = fmaxf(fmaxf(amax, fmaxf(fabsf(v[i].x), fabsf(v[i].y))),
                          fmaxf(fabsf(v[i].z), fabsf(v[i].w)));
-        }
     }
     amax = hm_wave_max_dpp(amax);
     const float range = (float)hm_limb_range(L);
@@ -295,6 +292,22 @@ __device__ __forceinline__ void hm_quantize_row_wave(const float* __restrict__ x
         if (lane == 0 && dsum) dsum[(int64_t)l * dsum_stride] = sm;
     }
     if (lane == 0) *scale = amax > 0.0f ? __fdiv_rn(amax, range) : 0.0f;
+}
+
+// The same, reading the row (16-byte aligned) from memory.
+template <int L>
+__device__ __forceinline__ void hm_quantize_row_wave(const float* __restrict__ xrow, int nv,
+                                                     int8_t* __restrict__ digits,
+                                                     int64_t plane_stride, float* scale,
+                                                     int32_t* __restrict__ dsum,
+                                                     int64_t dsum_stride) {
+    const int lane = threadIdx.x & (HM_WAVE - 1);
+    const float4* xr = reinterpret_cast<const float4*>(xrow);
+    float4 v[kHmQuantMaxV];
+#pragma unroll
+    for (int i = 0; i < kHmQuantMaxV; ++i)
+        if (i < nv) v[i] = xr[lane + HM_WAVE * i];
+    hm_quantize_row_values<L>(v, nv, digits, plane_stride, scale, dsum, dsum_stride);
 }
 
 // Where a fused row quantisation writes (digits == nullptr: none).

@@ -76,6 +76,100 @@ __global__ __launch_bounds__(kBlock) void limb_quantize_rows_vec_kernel(
                             dsum ? dsum + r : nullptr, rows);
 }
 
+// ---------------------------------------------------------------------------
+// SwiGLU then the Z rows' digit planes: row r of gu [rows x 2n] holds the
+// gate values g (columns 0..n-1) and the up values u (n..2n-1) of one grouped
+// row; z = silu(g) * u (Activation.cpp:44, then the multiply) is quantised
+// like any activation row (one scale per row).  One wave per row.
+// ---------------------------------------------------------------------------
+// rows of n = 256 * NV, 16-byte aligned: the row in registers (NV a
+// template argument, so a wave holds only its own row's values)
+template <int L, int NV>
+__global__ __launch_bounds__(kBlock) void limb_swiglu_quantize_vec_kernel(
+    const float* __restrict__ gu, int64_t rows, int64_t n,
+    int8_t* __restrict__ digits, float* __restrict__ scales, int32_t* __restrict__ dsum) {
+    __shared__ unsigned long long s_exp2[32];
+    hm_load_exp2_table(s_exp2);
+    __syncthreads();
+    const int lane = threadIdx.x & (HM_WAVE - 1);
+    const int64_t r = (int64_t)blockIdx.x * (kBlock / HM_WAVE) + threadIdx.x / HM_WAVE;
+    if (r >= rows) return;
+    const float4* g4 = reinterpret_cast<const float4*>(gu + r * 2 * n);
+    const float4* u4 = reinterpret_cast<const float4*>(gu + r * 2 * n + n);
+    float4 g[NV], u[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        g[i] = g4[lane + HM_WAVE * i];
+        u[i] = u4[lane + HM_WAVE * i];
+    }
+    bool small = true;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+        small = small && fabsf(g[i].x) < 88.0f && fabsf(g[i].y) < 88.0f &&
+                fabsf(g[i].z) < 88.0f && fabsf(g[i].w) < 88.0f;
+    float4 z[NV];
+    // the common path of expf holds for |g| < 88 (hm_expf_small_t); a wave
+    // with any larger gate value takes the full one
+    if (__all(small)) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            z[i].x = __fmul_rn(hm_silu_small_t(g[i].x, s_exp2), u[i].x);
+            z[i].y = __fmul_rn(hm_silu_small_t(g[i].y, s_exp2), u[i].y);
+            z[i].z = __fmul_rn(hm_silu_small_t(g[i].z, s_exp2), u[i].z);
+            z[i].w = __fmul_rn(hm_silu_small_t(g[i].w, s_exp2), u[i].w);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            z[i].x = __fmul_rn(hm_silu_t(g[i].x, s_exp2), u[i].x);
+            z[i].y = __fmul_rn(hm_silu_t(g[i].y, s_exp2), u[i].y);
+            z[i].z = __fmul_rn(hm_silu_t(g[i].z, s_exp2), u[i].z);
+            z[i].w = __fmul_rn(hm_silu_t(g[i].w, s_exp2), u[i].w);
+        }
+    }
+    hm_quantize_row_values<L>(z, NV, digits + r * n, rows * n, scales + r,
+                              dsum ? dsum + r : nullptr, rows);
+}
+
+// any n: z recomputed in the digit pass
+template <int L>
+__global__ __launch_bounds__(kBlock) void limb_swiglu_quantize_kernel(
+    const float* __restrict__ gu, int64_t rows, int64_t n,
+    int8_t* __restrict__ digits, float* __restrict__ scales, int32_t* __restrict__ dsum) {
+    __shared__ unsigned long long s_exp2[32];
+    hm_load_exp2_table(s_exp2);
+    __syncthreads();
+    const int lane = threadIdx.x & (HM_WAVE - 1);
+    const int64_t r = (int64_t)blockIdx.x * (kBlock / HM_WAVE) + threadIdx.x / HM_WAVE;
+    if (r >= rows) return;
+    const float* g = gu + r * 2 * n;
+    const float* u = g + n;
+    float amax = 0.0f;
+    for (int64_t k = lane; k < n; k += HM_WAVE)
+        amax = fmaxf(amax, fabsf(__fmul_rn(hm_silu_t(g[k], s_exp2), u[k])));
+    amax = hm_wave_max_f32(amax);
+    const float range = (float)hm_limb_range(L);
+    const float inv = amax > 0.0f ? __fdiv_rn(range, amax) : 0.0f;
+    int dl[L];
+#pragma unroll
+    for (int l = 0; l < L; ++l) dl[l] = 0;
+    for (int64_t k = lane; k < n; k += HM_WAVE) {
+        const int v = hm_fixed_point(__fmul_rn(hm_silu_t(g[k], s_exp2), u[k]), inv, range);
+#pragma unroll
+        for (int l = 0; l < L; ++l) {
+            const int d = hm_digit(v, l);
+            digits[((int64_t)l * rows + r) * n + k] = (int8_t)d;
+            dl[l] += d;
+        }
+    }
+#pragma unroll
+    for (int l = 0; l < L; ++l) {
+        const int sm = hm_wave_sum_i32(dl[l]);
+        if (lane == 0 && dsum) dsum[(int64_t)l * rows + r] = sm;
+    }
+    if (lane == 0) scales[r] = amax > 0.0f ? __fdiv_rn(amax, range) : 0.0f;
+}
+
 // Exact limb partials against a packed [cols x inner] INT8 matrix (test hook
 // and reference semantics for the MFMA kernels).
 __global__ void limb_partials_kernel(const int8_t* __restrict__ digits,
@@ -114,7 +208,7 @@ __global__ void gateup_generic_kernel(
     int64_t tokens, int64_t H, int64_t I, int64_t experts,
     const int8_t* __restrict__ packed, const float* __restrict__ scale,
     const int32_t* __restrict__ zp, const int32_t* __restrict__ offsets,
-    const int32_t* __restrict__ perm_tokens, int64_t R, float* __restrict__ zf) {
+    const int32_t* __restrict__ perm_tokens, int64_t R, float* __restrict__ gu) {
     const int64_t idx = (int64_t)blockIdx.x * kBlock + threadIdx.x;
     if (idx >= R * I) return;
     const int64_t row = idx / I, col = idx % I;
@@ -138,9 +232,8 @@ __global__ void gateup_generic_kernel(
         pu[l] = au;
     }
     const float sx = xscale[t];
-    const float g = __fmul_rn(hm_recombine(pg, L), __fmul_rn(sx, scale[e * 3 + 0]));
-    const float u = __fmul_rn(hm_recombine(pu, L), __fmul_rn(sx, scale[e * 3 + 1]));
-    zf[idx] = __fmul_rn(hm_silu(g), u);
+    gu[row * 2 * I + col] = __fmul_rn(hm_recombine(pg, L), __fmul_rn(sx, scale[e * 3 + 0]));
+    gu[row * 2 * I + I + col] = __fmul_rn(hm_recombine(pu, L), __fmul_rn(sx, scale[e * 3 + 1]));
 }
 
 // y[g, n] = recombine(P_l) * (s_z[g] * scale_down), P_l the exact int32
@@ -455,16 +548,14 @@ __global__ __launch_bounds__(256) void pack_tiles_i8_kernel(const int8_t* __rest
 // ===========================================================================
 // Launchers used by the block entry (hm_block.hip) and the C ABI.
 // ===========================================================================
-// Rows -> digit planes.  `timed`: the launch closes an armed stage timer
-// (the last kernel of the gate/up stage).
+// Rows -> digit planes.
 static int quantize_rows(const float* x, int64_t rows, int64_t n, int32_t limbs,
-                         int8_t* digits, float* scales, int32_t* dsum, bool timed,
-                         hipStream_t stream) {
+                         int8_t* digits, float* scales, int32_t* dsum, hipStream_t stream) {
     if (rows == 0) return HM_OK;
     const dim3 grid((unsigned)((rows + 3) / 4));
     const int64_t nv = n / 256;
     if (n % 256 == 0 && nv >= 1 && nv <= kQMaxV && (uintptr_t)x % 16 == 0 && (uintptr_t)digits % 4 == 0) {
-#define HM_QV(LV) HM_STAGE_LAUNCH(false, timed, limb_quantize_rows_vec_kernel<LV>, grid, dim3(kBlock), 0, stream, \
+#define HM_QV(LV) HM_STAGE_LAUNCH(false, false, limb_quantize_rows_vec_kernel<LV>, grid, dim3(kBlock), 0, stream, \
                                   x, rows, n, (int)nv, digits, scales, dsum)
         switch (limbs) {
         case 1: HM_QV(1); break;
@@ -476,7 +567,7 @@ static int quantize_rows(const float* x, int64_t rows, int64_t n, int32_t limbs,
         HM_LAUNCHED();
         return HM_OK;
     }
-#define HM_QS(LV) HM_STAGE_LAUNCH(false, timed, limb_quantize_rows_kernel<LV>, grid, dim3(kBlock), 0, stream, \
+#define HM_QS(LV) HM_STAGE_LAUNCH(false, false, limb_quantize_rows_kernel<LV>, grid, dim3(kBlock), 0, stream, \
                                   x, rows, n, digits, scales, dsum)
     switch (limbs) {
     case 1: HM_QS(1); break;
@@ -492,13 +583,45 @@ static int quantize_rows(const float* x, int64_t rows, int64_t n, int32_t limbs,
 int hm_launch_quantize_rows(const float* x, int64_t rows, int64_t n, int32_t limbs,
                             int8_t* digits, float* scales, int32_t* dsum,
                             hipStream_t stream) {
-    return quantize_rows(x, rows, n, limbs, digits, scales, dsum, false, stream);
+    return quantize_rows(x, rows, n, limbs, digits, scales, dsum, stream);
 }
 
-static int hm_launch_quantize_rows_timed(const float* x, int64_t rows, int64_t n, int32_t limbs,
-                                         int8_t* digits, float* scales, int32_t* dsum,
-                                         hipStream_t stream) {
-    return quantize_rows(x, rows, n, limbs, digits, scales, dsum, true, stream);
+// gu [rows x 2n] (g | u per row) -> z = silu(g) * u -> digit planes; the
+// last launch of the gate/up stage (its end closes an armed stage timer).
+static int swiglu_quantize_rows(const float* gu, int64_t rows, int64_t n, int32_t limbs,
+                                int8_t* digits, float* scales, int32_t* dsum,
+                                hipStream_t stream) {
+    if (rows == 0) return HM_OK;
+    if (limbs < 1 || limbs > 3) return HM_ERR_INVALID;
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    const int64_t nv = n / 256;
+    const bool vec = n % 256 == 0 && (uintptr_t)gu % 16 == 0 && (uintptr_t)digits % 4 == 0;
+#define HM_SQ(LV, NV) HM_STAGE_LAUNCH(false, true, (limb_swiglu_quantize_vec_kernel<LV, NV>), grid, \
+                                      dim3(kBlock), 0, stream, gu, rows, n, digits, scales, dsum)
+#define HM_SQL(NV)                                          \
+    do {                                                    \
+        if (limbs == 1) HM_SQ(1, NV);                       \
+        else if (limbs == 2) HM_SQ(2, NV);                  \
+        else HM_SQ(3, NV);                                  \
+    } while (0)
+    if (vec && nv == 1) HM_SQL(1);
+    else if (vec && nv == 2) HM_SQL(2);
+    else if (vec && nv == 3) HM_SQL(3);
+    else if (vec && nv == 4) HM_SQL(4);
+    else if (vec && nv == 6) HM_SQL(6);
+    else if (vec && nv == 8) HM_SQL(8);
+    else {
+#define HM_SG(LV) HM_STAGE_LAUNCH(false, true, limb_swiglu_quantize_kernel<LV>, grid, dim3(kBlock), 0, \
+                                  stream, gu, rows, n, digits, scales, dsum)
+        if (limbs == 1) HM_SG(1);
+        else if (limbs == 2) HM_SG(2);
+        else HM_SG(3);
+#undef HM_SG
+    }
+#undef HM_SQL
+#undef HM_SQ
+    HM_LAUNCHED();
+    return HM_OK;
 }
 
 bool hm_mfma_gateup_ok(int64_t H, int64_t I, int64_t E, int32_t limbs);
@@ -506,7 +629,7 @@ bool hm_mfma_down_ok(int64_t H, int64_t I, int64_t E, int32_t limbs);
 int hm_launch_gateup_i8_mfma(const hm_layer* layer, int32_t limbs, const int8_t* xdig,
                              const float* xscale, const int32_t* xdsum, int64_t tokens,
                              const int32_t* counts, const int32_t* offsets,
-                             const int32_t* perm_tokens, int64_t R, float* zf,
+                             const int32_t* perm_tokens, int64_t R, float* gu,
                              hipStream_t stream);
 int hm_launch_down_i8_mfma(const hm_layer* layer, int32_t limbs, const int32_t* counts,
                            const int32_t* offsets, int64_t R, const int8_t* zdig,
@@ -517,9 +640,10 @@ int64_t hm_max_tiles(int64_t pairs, int64_t experts, int64_t tile_m) {
     return (pairs < experts ? pairs : experts) + pairs / tile_m;
 }
 
-// INT8 expert GEMMs: gate/up (z = silu(g) * u as floats into zf [R x I]),
-// the Z rows' fixed-point digits (one scale per row, the same quantiser as
-// the activations), then down.  xdig/xscale/xdsum: the token rows' digits
+// INT8 expert GEMMs: gate/up (the dequantised gate and up values of every
+// grouped row into gu [R x 2I]), z = silu(g) * u and the Z rows' fixed-point
+// digits (one scale per row, the same quantiser as the activations), then
+// down.  xdig/xscale/xdsum: the token rows' digits
 // (hm_launch_quantize_rows over all tokens, or the prefill router's select
 // kernel).  The MFMA kernels (hm_gemm_mfma.hip) where the shape allows, the
 // generic kernels otherwise; both compute the same integers and the same
@@ -535,7 +659,7 @@ int hm_launch_gateup_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int
                         const float* xscale, const int32_t* xdsum, int64_t tokens,
                         const int32_t* counts, const int32_t* offsets,
                         const int32_t* perm_tokens, int64_t R, int8_t* zdig, float* zscale,
-                        int32_t* zdsum, float* zf, bool force_generic, hipStream_t stream) {
+                        int32_t* zdsum, float* gu, bool force_generic, hipStream_t stream) {
     const int64_t H = layer->hidden, I = layer->intermediate, E = layer->experts;
     const int8_t* packed = static_cast<const int8_t*>(layer->packed);
     if (R == 0) return HM_OK;
@@ -543,7 +667,7 @@ int hm_launch_gateup_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int
     // buffer offset) rules them out
     int rc = hm_use_mfma_gateup(layer, lx, force_generic)
                  ? hm_launch_gateup_i8_mfma(layer, lx, xdig, xscale, xdsum, tokens, counts,
-                                            offsets, perm_tokens, R, zf, stream)
+                                            offsets, perm_tokens, R, gu, stream)
                  : HM_ERR_UNSUPPORTED;
     if (rc == HM_ERR_UNSUPPORTED) {
         rc = HM_OK;
@@ -551,7 +675,7 @@ int hm_launch_gateup_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int
 #define HM_GU(LV)                                                                               \
         HM_STAGE_LAUNCH(true, false, gateup_generic_kernel<LV>, dim3(g_gu), dim3(kBlock), 0, stream, \
                         xdig, xscale, tokens, H, I, E, packed, layer->scale, layer->zero_point,   \
-                        offsets, perm_tokens, R, zf)
+                        offsets, perm_tokens, R, gu)
         switch (lx) {
         case 1: HM_GU(1); break;
         case 2: HM_GU(2); break;
@@ -563,7 +687,7 @@ int hm_launch_gateup_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int
     }
     if (rc) return rc;
     // the stage's last launch (its end closes the timed span when armed)
-    return hm_launch_quantize_rows_timed(zf, R, I, lz, zdig, zscale, zdsum, stream);
+    return swiglu_quantize_rows(gu, R, I, lz, zdig, zscale, zdsum, stream);
 }
 
 int hm_launch_down_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int32_t* counts,

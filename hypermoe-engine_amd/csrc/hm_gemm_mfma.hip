@@ -1,53 +1,54 @@
 // hm_gemm_mfma.hip -- grouped INT8-MFMA expert GEMMs for gfx950.
 //
-// One kernel template serves both projections of the expert MLP:
-//   gate/up  A = the token rows' X digit planes (gathered by perm_tokens),
-//            B = the gate and up tiles; epilogue z = silu(g) * u -> floats.
-//   down     A = the grouped rows' Z digit planes (contiguous),
-//            B = the down tiles; epilogue y -> floats.
 // The activation operand is L fixed-point digit planes with one scale per
 // row (hm_device.h); every plane meets the same weight fragment in one
 // v_mfma_i32_32x32x32_i8, so each plane's int32 partial over the whole row
-// is exact, and the epilogue recombines them (hm_recombine) exactly as the
-// generic kernels and the CPU restatement do.
+// is exact, and the epilogues recombine them (hm_recombine) exactly as the
+// generic kernels and the CPU restatement do.  Weights are 1 KB tiles in
+// MFMA B-operand order (hm_tile_offset): one 16-byte-per-lane load of a
+// contiguous kilobyte is one B fragment.
 //
 // Operand layout of v_mfma_i32_32x32x32_i8: lane l supplies 16 bytes of row
 // l % 32 of A and of column l % 32 of B, K bytes 16 (l / 32) .. +15 of the
 // 32-wide step; its 16 int32 results are column l % 32, rows
 // 8 (v / 4) + 4 (l / 32) + v % 4 (v = 0..15).
 //
-// Workgroup: 4 wave64s (one per SIMD, up to 512 registers each: the
-// accumulators take the AGPRs), persistent, one per CU.  A tile is BM
-// grouped rows of one expert x the workgroup's columns; every wave holds all
-// BM rows and its own two 32-column fragments:
-//   gate/up  wave w: gate and up columns 32 w .. +31 of a 128-column block
-//            of z (the same n, so z = silu(g) * u is lane-local)
-//   down     wave w: output columns 64 w .. +63 of a 256-column block
+// Two persistent kernels, one workgroup per CU:
+//   gate/up  gateup_ring_kernel: 8 wave64s (two per SIMD), A (the token
+//            rows' X digit planes, gathered by perm_tokens) and B both
+//            staged through an LDS ring by DMA; epilogue g and u -> floats
+//            (the SwiGLU runs in the Z quantisation pass, hm_gemm.hip).
+//   down     limb_gemm_kernel: 4 wave64s (one per SIMD, 512 registers: the
+//            accumulators take the AGPRs), A (the grouped rows' Z digit
+//            planes) through an LDS ring by DMA, B straight into a register
+//            ring; epilogue y -> floats.
 //
-// Data movement, per stage of K = 128 bytes (four MFMA K steps):
-//   A  global -> LDS by 16-byte global_load_lds (inline asm), 128-byte row
-//      chunks (whole cache lines), into a ring of kSA stages.  Each row's
+// down, per stage of K = 128 bytes (four MFMA K steps):
+//   A  global -> LDS by 16-byte buffer loads to LDS (inline asm), 128-byte
+//      row chunks (whole cache lines), into a ring of kSA stages.  Each row's
 //      eight 16-byte chunks are stored rotated by (row >> 1) & 7, so the
 //      readers' ds_read_b128 over any 16 lanes hit 16 distinct bank groups.
-//   B  global -> VGPRs: the weights are stored as 1 KB tiles in operand
-//      order (hm_tile_offset), so one 16-byte-per-lane load is one B
-//      fragment, read as one contiguous kilobyte; a ring of DB stages of
-//      registers.
+//   B  global -> VGPRs, a ring of DB stages of registers, loaded DB-1 stages
+//      ahead by loads the compiler does not track (buf_load16).
+// One vmcnt wait per stage completes both operands of the next stage.
 // Every wave issues its share of the loads of later stages between the
 // MFMAs of the current one (a wave that issues its loads in a clump stalls
 // the matrix pipe behind them).  Stages form one stream per workgroup across
-// its tiles, so the next tile's first stages load while the current tile
-// finishes.  The LDS DMA is invisible to the compiler: the kernel waits for
-// it with explicit vmcnt counts (every vector memory instruction between the
-// awaited load and the wait is counted; stores and metadata loads only add
-// to the count, which keeps the wait conservative).
+// its tiles, so the next tile's first stages load during the current tile's
+// last stages and its epilogue.  The kernel waits for its loads with
+// explicit vmcnt counts (every vector memory instruction between the awaited
+// load and the wait is counted; stores and metadata loads only add to the
+// count, which keeps the wait conservative).  A tile is BM grouped rows of
+// one expert x 256 output columns; every wave holds all BM rows and its own
+// two 32-column fragments (output columns 64 w .. +63).
 //
-// Tile order: tiles are numbered m-tile major, column block minor, and split
-// into 8 contiguous ranges, one per XCD (workgroup i runs on XCD i % 8), so
-// the column blocks of an m-tile (sharing A rows) and the m-tiles of one
-// expert (sharing B tiles) meet in one XCD's L2.  In an expert's partial
-// last tile, the 32-row fragments past its last row skip their reads and
-// MFMAs.
+// Tile order (both kernels): tiles are numbered m-tile major, column block
+// minor, and split into 8 contiguous ranges, one per XCD (workgroup i runs
+// on XCD i % 8), so the column blocks of an m-tile (sharing A rows) and the
+// m-tiles of one expert (sharing B tiles) meet in one XCD's L2.  In an
+// expert's partial last tile, the 32-row fragments past its last row skip
+// their MFMAs (down: tiles of two row fragments; gate/up: the waves whose
+// rows all lie past it).
 #include "hm_device.h"
 #include "hm_lds_dma.h"
 
@@ -68,14 +69,12 @@ constexpr int kMaxExperts = 256;    // expert tables live in LDS
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-enum Role { kGateUp = 0, kDown = 1 };
-
-template <int ROLE, int L, int DB>
+template <int L, int DB>
 struct Tile {
     static constexpr int RF = L <= 2 ? 4 : 2;            // 32-row fragments per tile
     static constexpr int BM = 32 * RF;                   // tile rows
     static constexpr int NCF = 2;                        // 32-column fragments per wave
-    static constexpr int BN = ROLE == kGateUp ? 32 * kWaves : 32 * NCF * kWaves;  // output columns
+    static constexpr int BN = 32 * NCF * kWaves;             // output columns
     static constexpr int ASTAGE = L * BM * kKS;          // A bytes per stage
     static constexpr int ALOADS = ASTAGE / 1024;         // wave-wide A loads per stage
     static constexpr int APW = ALOADS / kWaves;          // ... per wave
@@ -84,9 +83,7 @@ struct Tile {
     static constexpr int NG = kKT * RF;                  // (K step, row fragment) groups per stage
     static_assert(ALOADS % kWaves == 0 && APW <= BPW && DB >= 2 && DB <= kSA && kKT % 2 == 0,
                   "tile shape");
-    // A stage's load items: its B loads first (the compiler's waits for the
-    // B registers do not see the DMAs, so a DMA issued after a B load is
-    // only waited for where that B load is), then its A DMAs; item j is
+    // A stage's load items: its B loads first, then its A DMAs; item j is
     // issued before group item_group(j) of the stage.
     static constexpr bool item_is_a(int j) { return j >= BPW; }
     static constexpr int item_a(int j) { return j - BPW; }
@@ -99,12 +96,16 @@ struct Tile {
         for (int j = 0; j < NV; ++j) n += item_group(j) < g ? 1 : 0;
         return n;
     }
-    // loads after the last DMA of a stage, within that stage
-    static constexpr int after_last_a = 0;
-    // At the wait of stage g for A(g+1), whose DMAs stage g+2-kSA issued:
-    // the loads issued since that stage's last DMA.
-    static constexpr int wait_count = after_last_a + (kSA - 3) * NV + items_before(kWaitGroup);
-    static_assert(wait_count <= 63, "vmcnt");
+    static_assert(item_group(BPW - 1) < kWaitGroup, "B items precede the wait");
+    // The one wait of stage g completes both operands of stage g+1:
+    //   A(g+1): DMAs of stage g+2-kSA, the last items of that stage;
+    //   B(g+1): loads of stage g+2-DB, the first BPW items of that stage.
+    // Each count is the number of loads issued after the last awaited one
+    // (vector memory loads complete in issue order).
+    static constexpr int a_count = (kSA - 3) * NV + items_before(kWaitGroup);
+    static constexpr int b_count = (DB - 2) * NV + items_before(kWaitGroup) - BPW;
+    static constexpr int wait_count = a_count < b_count ? a_count : b_count;
+    static_assert(wait_count >= 0 && wait_count <= 63, "vmcnt");
 };
 
 // One wave-wide 16-byte buffer -> LDS load: lane l's 16 bytes from
@@ -120,6 +121,23 @@ __device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t rsrc, uint32_t 
                  ::"v"(voff), "s"(rsrc), "s"(soff), "s"(m0) : "memory", "m0");
 }
 #pragma clang diagnostic pop
+
+// One wave-wide 16-byte buffer -> VGPR load the compiler does not track:
+// it inserts no wait for the result, so the kernel's own vmcnt waits (which
+// count the DMAs too) decide when the registers are complete, and
+// publish() marks that point.  (The compiler's own waits would count only
+// the loads it knows of and so drain loads issued half as long ago as the
+// register ring allows.)  Until its wait the register must not be read,
+// copied or spilled; the build checks this on the compiled code, along every
+// control-flow path (hmoe/isa_check.py), and refuses a library that breaks it.
+__device__ __forceinline__ v4i buf_load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, uint32_t soff) {
+    v4i r;
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(r) : "v"(voff), "s"(rsrc), "s"(soff));
+    return r;
+}
+// After the vmcnt wait that completes a buf_load16: ties the value to that
+// point, so no use of it is scheduled before the wait.
+__device__ __forceinline__ void publish(v4i& r) { asm volatile("" : "+v"(r)); }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
@@ -202,35 +220,28 @@ struct TileInfo {
 };
 
 // ---------------------------------------------------------------------------
-// The grouped limb GEMM.
-//   gate/up: K = H, N = I (z columns), out = zf [R x I]
-//   down:    K = I, N = H, out = y [R x H]
-// A rows: gate/up adig [L][tokens][K] gathered by perm_tokens; down adig
-// [L][R][K] by grouped row.  ascale/adsum: the A rows' fixed-point scales
-// [arows] and digit sums [L][arows] (for non-zero zero points).
+// The down projection: K = I, N = H, out = y [R x H].  A rows: the Z digit
+// planes adig [L][R][K] by grouped row; ascale/adsum: their fixed-point
+// scales [arows] and digit sums [L][arows] (for non-zero zero points).
 // ---------------------------------------------------------------------------
-template <int ROLE, int L, int DB>
+template <int L, int DB>
 __global__ __launch_bounds__(kThreads) void limb_gemm_kernel(
     const int8_t* __restrict__ adig, const float* __restrict__ ascale,
     const int32_t* __restrict__ adsum, int arows, int K, int N, int H, int I, int experts,
     const int8_t* __restrict__ packed, const float* __restrict__ scale,
     const int32_t* __restrict__ zp, const int32_t* __restrict__ counts,
-    const int32_t* __restrict__ offsets, const int32_t* __restrict__ perm_tokens,
-    float* __restrict__ out) {
-    using T = Tile<ROLE, L, DB>;
+    const int32_t* __restrict__ offsets, float* __restrict__ out) {
+    using T = Tile<L, DB>;
     constexpr int RF = T::RF, BM = T::BM, BN = T::BN, NCF = T::NCF, APW = T::APW,
                   BPW = T::BPW, NV = T::NV, ASTAGE = T::ASTAGE;
-    constexpr bool GU = ROLE == kGateUp;
     constexpr int MW = BM / HM_WAVE;  // 64-row metadata chunks of a tile
     __shared__ __attribute__((aligned(1024))) int8_t ring[kSA * ASTAGE];
     __shared__ int32_t s_prefix[kMaxExperts + 1];
     __shared__ int32_t s_off[kMaxExperts], s_cnt[kMaxExperts];
-    __shared__ float s_sa[kMaxExperts], s_sb[kMaxExperts];     // gate (or down), up scale
-    __shared__ int32_t s_za[kMaxExperts], s_zb[kMaxExperts];   // and zero points
-    __shared__ __attribute__((aligned(16))) int32_t s_rt[2][BM];     // gate/up: token of each row
+    __shared__ float s_sa[kMaxExperts];     // down projection scale
+    __shared__ int32_t s_za[kMaxExperts];   // and zero point
     __shared__ __attribute__((aligned(16))) float s_as[2][BM];       // A row scale
     __shared__ __attribute__((aligned(16))) int32_t s_ad[2][L][BM];  // A row digit sums
-    __shared__ unsigned long long s_exp2[32];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -238,12 +249,9 @@ __global__ __launch_bounds__(kThreads) void limb_gemm_kernel(
     for (int e = tid; e < E; e += kThreads) {
         s_cnt[e] = counts[e];
         s_off[e] = offsets[e];
-        s_sa[e] = scale[3 * e + (GU ? 0 : 2)];
-        s_sb[e] = scale[3 * e + 1];
-        s_za[e] = zp[3 * e + (GU ? 0 : 2)];
-        s_zb[e] = zp[3 * e + 1];
+        s_sa[e] = scale[3 * e + 2];
+        s_za[e] = zp[3 * e + 2];
     }
-    if (GU) hm_load_exp2_table(s_exp2);
     __syncthreads();
     if (wave == 0) tile_prefix(s_cnt, E, BM, s_prefix);
     __syncthreads();
@@ -265,22 +273,11 @@ __global__ __launch_bounds__(kThreads) void limb_gemm_kernel(
         t.n0 = (j % nbn) * BN;
         return t;
     };
-    // gate/up: the token ids of a tile's rows (rows past nrows repeat the
-    // last row) into s_rt[m]
-    auto fetch_tokens = [&](const TileInfo& t, int m) __attribute__((always_inline)) {
-        if constexpr (GU) {
-            if (wave < MW) {
-                const int r = HM_WAVE * wave + fresh_lane();
-                dma4(perm_tokens + t.g0 + min(r, t.nrows - 1), &s_rt[m][HM_WAVE * wave]);
-            }
-        }
-    };
-    // the A rows' scales and digit sums into s_as[m], s_ad[m] (gate/up: reads
-    // s_rt[m], which must be visible)
+    // the A rows' scales and digit sums into s_as[m], s_ad[m]
     auto fetch_meta = [&](const TileInfo& t, int m) __attribute__((always_inline)) {
         if (wave < MW) {
             const int r = HM_WAVE * wave + fresh_lane();
-            const int src = GU ? s_rt[m][r] : t.g0 + min(r, t.nrows - 1);
+            const int src = t.g0 + min(r, t.nrows - 1);
             dma4(ascale + src, &s_as[m][HM_WAVE * wave]);
 #pragma unroll
             for (int l = 0; l < L; ++l)
@@ -295,14 +292,14 @@ __global__ __launch_bounds__(kThreads) void limb_gemm_kernel(
     // which holds chunk a_chunk_pos(row, lane%8) of the row.
     const __amdgpu_buffer_rsrc_t arsrc = buffer_rsrc(adig, (uint32_t)((int64_t)L * arows * K));
     uint32_t aoff[APW];
-    auto make_asrc = [&](const TileInfo& t, int m) __attribute__((always_inline)) {
+    auto make_asrc = [&](const TileInfo& t) __attribute__((always_inline)) {
         const int ln = fresh_lane();
 #pragma unroll
         for (int i = 0; i < APW; ++i) {
             const int q = 8 * (wave + kWaves * i) + (ln >> 3);
             const int l = q / BM, r = q % BM;
             const int c = a_chunk_pos(r, ln & 7);
-            const int row = GU ? s_rt[m][r] : t.g0 + min(r, t.nrows - 1);
+            const int row = t.g0 + min(r, t.nrows - 1);
             aoff[i] = (uint32_t)(((int64_t)l * arows + row) * K + 16 * c);
         }
     };
@@ -315,9 +312,8 @@ __global__ __launch_bounds__(kThreads) void limb_gemm_kernel(
         brsrc = buffer_rsrc(packed + hm_proj_offset(t.e, 0, H, I), (uint32_t)(3 * hm_proj_bytes(H, I)));
 #pragma unroll
         for (int f = 0; f < NCF; ++f) {
-            const int p = GU ? f : 2;
-            const int cb = GU ? t.n0 / 32 + wave : t.n0 / 32 + NCF * wave + f;
-            boff[f] = (int)(p * hm_proj_bytes(H, I) + (int64_t)cb * (K32 / 32) * 1024);
+            const int cb = t.n0 / 32 + NCF * wave + f;
+            boff[f] = (int)(2 * hm_proj_bytes(H, I) + (int64_t)cb * (K32 / 32) * 1024);
         }
     };
     auto issue_a = [&](int i, int stage, int ks) __attribute__((always_inline)) {
@@ -325,10 +321,15 @@ __global__ __launch_bounds__(kThreads) void limb_gemm_kernel(
                   ring + (stage % kSA) * ASTAGE + (wave + kWaves * i) * 1024);
     };
     v4i bq[DB][NCF][kKT];
+    auto publish_slot = [&](int slot) __attribute__((always_inline)) {
+#pragma unroll
+        for (int f = 0; f < NCF; ++f)
+#pragma unroll
+            for (int kt = 0; kt < kKT; ++kt) publish(bq[slot][f][kt]);
+    };
     auto load_b = [&](int slot, int j, int ks) __attribute__((always_inline)) {
         const int f = j / kKT, kt = j % kKT;
-        bq[slot][f][kt] = __builtin_amdgcn_raw_buffer_load_b128(brsrc, blane,
-                                                                 boff[f] + (ks * kKT + kt) * 1024, 0);
+        bq[slot][f][kt] = buf_load16(brsrc, blane, (uint32_t)(boff[f] + (ks * kKT + kt) * 1024));
     };
 
     // ---- A fragment reads: the L limb planes of every row fragment of one K
@@ -347,14 +348,11 @@ __global__ __launch_bounds__(kThreads) void limb_gemm_kernel(
 
     v16i acc[L][RF][NCF];
 
-    // ---- stream prologue: tile 0's rows and metadata, the A of stages
-    // 0 .. kSA-2 and the B of stages 0 .. DB-2 (all of tile 0: nk >= kSA)
+    // ---- stream prologue: tile 0's row metadata, the A of stages 0 .. kSA-2
+    // and the B of stages 0 .. DB-2 (all of tile 0: nk >= kSA)
     TileInfo cur = info(0);
-    fetch_tokens(cur, 0);
-    vm_wait<0>();
-    lds_barrier();
     fetch_meta(cur, 0);
-    make_asrc(cur, 0);
+    make_asrc(cur);
     make_bsrc(cur);
 #pragma unroll
     for (int s = 0; s < kSA - 1; ++s)
@@ -367,6 +365,8 @@ __global__ __launch_bounds__(kThreads) void limb_gemm_kernel(
     // A(0) landed and published; its first K step's fragments
     vm_wait<0>();
     lds_barrier();
+#pragma unroll
+    for (int s = 0; s < DB - 1; ++s) publish_slot(s);
     read_a(0, 0, 0);
 
     int m = 0;
@@ -396,20 +396,19 @@ __global__ __launch_bounds__(kThreads) void limb_gemm_kernel(
             const int ksa = ks + kSA - 1 < nk ? ks + kSA - 1 : ks + kSA - 1 - nk;
             const int ksb = ks + DB - 1 < nk ? ks + DB - 1 : ks + DB - 1 - nk;
             if (ks == ka_switch && has_next) {
-                // gate/up: the next tile's tokens, fetched after stage 1 of
-                // this tile, are visible since the barrier of stage 4
-                make_asrc(nxt, mn);
+                make_asrc(nxt);
                 fetch_meta(nxt, mn);
             }
             if (ks == kb_switch && has_next) make_bsrc(nxt);
-            const bool steady = g >= kSA - 2;
 #pragma unroll
             for (int kt = 0; kt < kKT; ++kt) {
                 if (kt == kKT - 1) {
-                    // A(g+1) has landed (stage g+2-kSA issued it); publish it
-                    if (steady) vm_wait<T::wait_count>();
-                    else vm_wait<0>();
+                    // A(g+1) and B(g+1) have landed (issued by stages
+                    // g+2-kSA and g+2-DB, or by the prologue, which ends with
+                    // a full wait); the barrier publishes A(g+1)
+                    vm_wait<T::wait_count>();
                     lds_barrier();
+                    publish_slot((PH + 1) % DB);
                 }
                 const int rb = kt & 1;  // kKT is even: every stage starts on buffer 0
                 // the next K step's fragments (after the last: the next
@@ -429,20 +428,24 @@ __global__ __launch_bounds__(kThreads) void limb_gemm_kernel(
                             __builtin_amdgcn_sched_barrier(0);
                         }
                     }
+                    // row fragments past the tile's last row (an expert's
+                    // partial last tile) skip their MFMAs; the epilogue skips
+                    // their accumulators.  Only with two row fragments: with
+                    // four, the branches split the accumulator ranges and the
+                    // allocator spills them.
+                    if (RF <= 2 ? (rf == 0 || 32 * rf < cur.nrows) : true) {
 #pragma unroll
-                    for (int l = 0; l < L; ++l)
+                        for (int l = 0; l < L; ++l)
 #pragma unroll
-                        for (int f = 0; f < NCF; ++f) {
-                            if (decltype(first)::value && kt == 0)
-                                acc[l][rf][f] = mfma32(fa[rb][l][rf], bq[WS][f][kt], v16i{});
-                            else
-                                acc[l][rf][f] = mfma32(fa[rb][l][rf], bq[WS][f][kt], acc[l][rf][f]);
-                        }
+                            for (int f = 0; f < NCF; ++f) {
+                                if (decltype(first)::value && kt == 0)
+                                    acc[l][rf][f] = mfma32(fa[rb][l][rf], bq[WS][f][kt], v16i{});
+                                else
+                                    acc[l][rf][f] = mfma32(fa[rb][l][rf], bq[WS][f][kt], acc[l][rf][f]);
+                            }
+                    }
                 }
             }
-            // the next tile's tokens, into the buffer the previous tile's
-            // sources were made from (every wave is past that: barriers since)
-            if (ks == 1 && has_next) fetch_tokens(nxt, mn);
             ++g;
         };
 
@@ -466,13 +469,16 @@ __global__ __launch_bounds__(kThreads) void limb_gemm_kernel(
         auto epilogue = [&](auto with_zp) __attribute__((always_inline)) {
             constexpr bool ZP = decltype(with_zp)::value;
             const int e = cur.e;
-            const float sa = s_sa[e], sb = s_sb[e];
-            const int za = s_za[e], zb = s_zb[e];
-            // lane's row within a row quad (0 or 4) and column; everything
-            // else is uniform per (row fragment, quad)
+            const float sa = s_sa[e];
+            const int za = s_za[e];
+            // out [R x N], the wave's two fragments side by side.  The
+            // lane's row within a row quad (0 or 4) and its column;
+            // everything else is uniform per (row fragment, quad).
+            const int64_t ldo = N;
+            const int fstride = 32;
             const int lrow = 4 * (lane >> 5);
-            float* obase = out + (int64_t)cur.g0 * N + cur.n0 + (GU ? 32 : 64) * wave +
-                           (int64_t)lrow * N + (lane & 31);
+            float* obase = out + (int64_t)cur.g0 * ldo + cur.n0 + 64 * wave +
+                           (int64_t)lrow * ldo + (lane & 31);
 #pragma unroll
             for (int rf = 0; rf < RF; ++rf) {
                 if (32 * rf >= cur.nrows) continue;
@@ -486,45 +492,36 @@ __global__ __launch_bounds__(kThreads) void limb_gemm_kernel(
 #pragma unroll
                         for (int l = 0; l < L; ++l) ad4[l] = *reinterpret_cast<const int4*>(&s_ad[m][l][r0 + lrow]);
                     }
-                    float* o = obase + (int64_t)r0 * N;
+                    float* o = obase + (int64_t)r0 * ldo;
 #pragma unroll
                     for (int t4 = 0; t4 < 4; ++t4) {
                         const int v = 4 * q + t4;
                         const float asc = t4 == 0 ? as4.x : t4 == 1 ? as4.y : t4 == 2 ? as4.z : as4.w;
-                        float val[NCF];
+                        if (t4 < nlive) {
 #pragma unroll
-                        for (int f = 0; f < NCF; ++f) {
-                            int p[L];
+                            for (int f = 0; f < NCF; ++f) {
+                                int p[L];
 #pragma unroll
-                            for (int l = 0; l < L; ++l) {
-                                p[l] = acc[l][rf][f][v];
-                                if constexpr (ZP) {
-                                    const int ds = t4 == 0 ? ad4[l].x : t4 == 1 ? ad4[l].y : t4 == 2 ? ad4[l].z : ad4[l].w;
-                                    p[l] -= (GU && f == 1 ? zb : za) * ds;
+                                for (int l = 0; l < L; ++l) {
+                                    p[l] = acc[l][rf][f][v];
+                                    if constexpr (ZP) {
+                                        const int ds = t4 == 0 ? ad4[l].x : t4 == 1 ? ad4[l].y : t4 == 2 ? ad4[l].z : ad4[l].w;
+                                        p[l] -= za * ds;
+                                    }
                                 }
-                            }
-                            const float wsc = __fmul_rn(asc, GU && f == 1 ? sb : sa);
-                            val[f] = __fmul_rn(hm_recombine(p, L), wsc);
-                        }
-                        if constexpr (GU) {
-                            // z = silu(g) * u (Activation.cpp:44, then the multiply)
-                            const float z = __fmul_rn(hm_silu_t(val[0], s_exp2), val[1]);
-                            if (t4 < nlive) o[(int64_t)t4 * N] = z;
-                        } else {
-                            if (t4 < nlive) {
-                                o[(int64_t)t4 * N] = val[0];
-                                o[(int64_t)t4 * N + 32] = val[1];
+                                const float wsc = __fmul_rn(asc, sa);
+                                o[(int64_t)t4 * ldo + fstride * f] = __fmul_rn(hm_recombine(p, L), wsc);
                             }
                         }
                     }
                     // one (row fragment, row quad) at a time: the scheduler
                     // would otherwise start every group's accumulator reads
-                    // and exponentials at once and spill
+                    // at once and spill
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
         };
-        const bool zpt = GU ? ((s_za[cur.e] | s_zb[cur.e]) != 0) : (s_za[cur.e] != 0);
+        const bool zpt = s_za[cur.e] != 0;
         if (zpt) epilogue(std::true_type{});
         else epilogue(std::false_type{});
         m = mn;
@@ -550,47 +547,434 @@ int persistent_grid() {
 // B ring depth for nk stages per tile: the largest of 4, 3, 2 dividing nk.
 int ring_depth(int64_t nk) { return nk % 4 == 0 ? 4 : nk % 3 == 0 ? 3 : nk % 2 == 0 ? 2 : 0; }
 
-bool shape_ok(int role, int64_t K, int64_t N, int64_t E, int32_t limbs) {
+bool shape_ok(int64_t K, int64_t N, int64_t E, int32_t limbs) {
     // |P_l| <= K * 128 * 255 < 2^31 keeps every limb partial exact: K <= 65536
     if (limbs < 1 || limbs > 3 || E < 1 || E > kMaxExperts || K > 65536 || N > (1 << 20))
         return false;
     if (K % kKS != 0) return false;
     const int64_t nk = K / kKS;
-    const int64_t bn = role == kGateUp ? 32 * kWaves : 64 * kWaves;
-    // gate/up reads the next tile's tokens (fetched after stage 1) from
-    // stage 4 on and needs them kSA - 1 stages before the tile ends
-    const int64_t min_nk = role == kGateUp ? 2 * kSA : kSA;
-    return nk >= min_nk && ring_depth(nk) != 0 && N % bn == 0;
+    return nk >= kSA && ring_depth(nk) != 0 && N % (64 * kWaves) == 0;
 }
 
-template <int ROLE, int L, int DB>
+template <int L, int DB>
 int launch(const hm_layer* layer, const int8_t* adig, const float* ascale, const int32_t* adsum,
-           int64_t arows, const int32_t* counts, const int32_t* offsets,
-           const int32_t* perm_tokens, float* out, bool timed, hipStream_t stream) {
+           int64_t arows, const int32_t* counts, const int32_t* offsets, float* out,
+           hipStream_t stream) {
     const int64_t H = layer->hidden, I = layer->intermediate;
-    const int64_t K = ROLE == kGateUp ? H : I, N = ROLE == kGateUp ? I : H;
+    const int64_t K = I, N = H;
     // buffer offsets are 32-bit: the digit planes and one expert's tiles
     if ((int64_t)L * arows * K > INT_MAX || 3 * hm_proj_bytes(H, I) > INT_MAX || arows > INT_MAX)
         return HM_ERR_UNSUPPORTED;
-    HM_STAGE_LAUNCH(timed, false, (limb_gemm_kernel<ROLE, L, DB>), dim3((unsigned)persistent_grid()),
-                    dim3(kThreads), 0, stream, adig, ascale, adsum, (int)arows, (int)K, (int)N,
-                    (int)H, (int)I, (int)layer->experts, static_cast<const int8_t*>(layer->packed),
-                    layer->scale, layer->zero_point, counts, offsets, perm_tokens, out);
+    hipLaunchKernelGGL((limb_gemm_kernel<L, DB>), dim3((unsigned)persistent_grid()), dim3(kThreads), 0,
+                       stream, adig, ascale, adsum, (int)arows, (int)K, (int)N, (int)H, (int)I,
+                       (int)layer->experts, static_cast<const int8_t*>(layer->packed), layer->scale,
+                       layer->zero_point, counts, offsets, out);
     HM_LAUNCHED();
     return HM_OK;
 }
 
-template <int ROLE, int L>
+template <int L>
 int launch_l(const hm_layer* layer, const int8_t* adig, const float* ascale,
              const int32_t* adsum, int64_t arows, const int32_t* counts, const int32_t* offsets,
-             const int32_t* perm_tokens, float* out, bool timed, hipStream_t stream) {
-    const int64_t K = ROLE == kGateUp ? layer->hidden : layer->intermediate;
-    switch (ring_depth(K / kKS)) {
-    case 4: return launch<ROLE, L, 4>(layer, adig, ascale, adsum, arows, counts, offsets, perm_tokens, out, timed, stream);
-    case 3: return launch<ROLE, L, 3>(layer, adig, ascale, adsum, arows, counts, offsets, perm_tokens, out, timed, stream);
-    case 2: return launch<ROLE, L, 2>(layer, adig, ascale, adsum, arows, counts, offsets, perm_tokens, out, timed, stream);
+             float* out, hipStream_t stream) {
+    switch (ring_depth(layer->intermediate / kKS)) {
+    case 4: return launch<L, 4>(layer, adig, ascale, adsum, arows, counts, offsets, out, stream);
+    case 3: return launch<L, 3>(layer, adig, ascale, adsum, arows, counts, offsets, out, stream);
+    case 2: return launch<L, 2>(layer, adig, ascale, adsum, arows, counts, offsets, out, stream);
     default: return HM_ERR_UNSUPPORTED;
     }
+}
+
+// ===========================================================================
+// gate/up: a ring kernel of its own.  8 wave64s per workgroup (two per
+// SIMD, 256 registers each), both operands staged through LDS by DMA, so
+// while one wave of a SIMD waits (for a stage, or in its epilogue) the other
+// keeps the matrix pipe busy.  Tile = BM grouped rows x (128 gate + 128 up)
+// weight columns; wave (wr, wc) owns rows [32 WR wr, +32 WR) and gate and up
+// columns [32 WCP wc, +32 WCP).  Per ring stage of 64 K bytes:
+//   A  the L digit planes of the tile rows (gathered by perm_tokens), in
+//      fragments of 32 rows x 64 bytes, two wave-wide 16-byte DMAs each
+//      (lane: row 16 h + lane/4, chunk (lane%4) ^ ((lane/16)%4)), read back
+//      bank-conflict free with the swizzle of gu_frag_read_offset;
+//   B  the 8 weight fragments (4 gate, 4 up column blocks of 32), each the
+//      two 1 KB operand-order tiles (hm_tile_offset) of the stage's K steps,
+//      one contiguous DMA each and read back at 16 lane.
+// Epilogue: the dequantised g and u values (z = silu(g) * u and the Z digits
+// follow in one pass over the rows at full occupancy, hm_gemm.hip).
+// ===========================================================================
+constexpr int kGuWaves = 8;
+constexpr int kGuThreads = 64 * kGuWaves;
+constexpr int kGuKB = 64;                   // K bytes per ring stage: two MFMA K steps
+constexpr int kGuStages = 4;                // ring stages
+constexpr int kGuFrag = 32 * kGuKB;         // bytes of one fragment of a stage
+constexpr int kGuN = 128;                   // columns per projection per tile
+
+__device__ __forceinline__ int gu_frag_load_row(int lane, int hf) { return 16 * hf + (lane >> 2); }
+__device__ __forceinline__ int gu_frag_load_chunk(int lane) { return (lane & 3) ^ ((lane >> 4) & 3); }
+// A fragment reader of K step h: lane m (row r = m%32, chunk c = 2h + m/32)
+// at 1024 (r/16) + 16 (4 (r%16) + (c ^ ((r/4)%4))); over any 16 consecutive
+// lanes these are 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int gu_frag_read_offset(int lane, int h) {
+    const int r = lane & 31, c = 2 * h + (lane >> 5);
+    return 1024 * (r >> 4) + 16 * (4 * (r & 15) + (c ^ ((r >> 2) & 3)));
+}
+__device__ __forceinline__ v4i lds16(const int8_t* p) { return *reinterpret_cast<const v4i*>(p); }
+
+template <int L>
+struct GateUpTile {
+    static constexpr int WR = 1;                        // 32-row fragments per wave
+    static constexpr int WCP = L >= 3 ? 1 : 2;          // gate (and up) fragments per wave
+    static constexpr int NWC = kGuN / 32 / WCP;         // waves across the columns
+    static constexpr int NWR = kGuWaves / NWC;          // waves across the rows
+    static constexpr int BM = 32 * WR * NWR;            // 128 rows (64 at three limbs)
+    static constexpr int NA = L * BM / 32;              // A fragments per stage
+    static constexpr int NB = 2 * kGuN / 32;            // 8 B fragments (4 gate, 4 up)
+    static constexpr int NF = NA + NB;
+    static constexpr int NL = 2 * NF;                   // wave-wide loads per stage
+    static constexpr int LPW = (NL + kGuWaves - 1) / kGuWaves;
+    static constexpr int STAGE = NF * kGuFrag;
+};
+
+template <int L>
+__global__ __launch_bounds__(kGuThreads) void gateup_ring_kernel(
+    const int8_t* __restrict__ xdig, const float* __restrict__ xscale,
+    const int32_t* __restrict__ xdsum, int tokens, int H, int I, int experts,
+    const int8_t* __restrict__ packed, const float* __restrict__ scale,
+    const int32_t* __restrict__ zp, const int32_t* __restrict__ counts,
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ perm_tokens,
+    float* __restrict__ gu) {
+    using T = GateUpTile<L>;
+    constexpr int BM = T::BM, NA = T::NA, NL = T::NL, LPW = T::LPW, WR = T::WR, WCP = T::WCP,
+                  NWC = T::NWC, STAGE = T::STAGE;
+    constexpr int RW = BM / HM_WAVE;  // waves that move one value per tile row
+    constexpr int kS = kGuStages;
+    __shared__ __attribute__((aligned(1024))) int8_t ring[kS * STAGE];
+    __shared__ int32_t s_prefix[kMaxExperts + 1];
+    __shared__ int32_t s_off[kMaxExperts], s_cnt[kMaxExperts];
+    __shared__ float s_sg[kMaxExperts], s_su[kMaxExperts];
+    __shared__ int32_t s_zg[kMaxExperts], s_zu[kMaxExperts];
+    __shared__ __attribute__((aligned(16))) int32_t s_rt[2][BM];     // token of each tile row
+    __shared__ __attribute__((aligned(16))) float s_xs[2][BM];       // its activation scale
+    __shared__ __attribute__((aligned(16))) int32_t s_xd[2][L][BM];  // its digit sums
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wr = wave / NWC, wc = wave % NWC;
+    const int E = experts;
+    for (int e = tid; e < E; e += kGuThreads) {
+        s_cnt[e] = counts[e];
+        s_off[e] = offsets[e];
+        s_sg[e] = scale[3 * e + 0];
+        s_su[e] = scale[3 * e + 1];
+        s_zg[e] = zp[3 * e + 0];
+        s_zu[e] = zp[3 * e + 1];
+    }
+    __syncthreads();
+    if (wave == 0) tile_prefix(s_cnt, E, BM, s_prefix);
+    __syncthreads();
+    const int nbn = I / kGuN;
+    const TileRange tr = tile_range(s_prefix[E] * nbn);
+    if (tr.ntiles == 0) return;
+    const int nk = H / kGuKB;
+    const int64_t tiles_k = hm_pad32(H) / 32;  // K tiles of one 32-column block
+
+    auto info = [&](int i) __attribute__((always_inline)) {
+        const int j = tr.jbeg + i * tr.step;
+        const int gm = j / nbn;
+        TileInfo t;
+        t.e = locate_expert(s_prefix, E, gm);
+        const int mt = gm - s_prefix[t.e];
+        t.g0 = s_off[t.e] + mt * BM;
+        t.nrows = min(BM, s_cnt[t.e] - mt * BM);
+        t.n0 = (j % nbn) * kGuN;
+        return t;
+    };
+    // token ids of the tile rows (rows past nrows repeat the last row)
+    auto fetch_rows = [&](const TileInfo& t, int m) __attribute__((always_inline)) {
+        if (wave < RW) {
+            const int r = HM_WAVE * wave + lane;
+            dma4(perm_tokens + t.g0 + min(r, t.nrows - 1), &s_rt[m][HM_WAVE * wave]);
+        }
+    };
+    // activation scales and digit sums of those tokens (needs s_rt[m])
+    auto fetch_row_meta = [&](int m) __attribute__((always_inline)) {
+        if (wave < RW) {
+            const int tok = s_rt[m][HM_WAVE * wave + lane];
+            dma4(xscale + tok, &s_xs[m][HM_WAVE * wave]);
+#pragma unroll
+            for (int l = 0; l < L; ++l) dma4(xdsum + (int64_t)l * tokens + tok, &s_xd[m][l][HM_WAVE * wave]);
+        }
+    };
+    // this wave's load units: unit u = fragment u/2, half (K step) u%2
+    int dst[LPW];
+#pragma unroll
+    for (int c = 0; c < LPW; ++c) {
+        const int u = (wave + kGuWaves * c) % NL;
+        dst[c] = (u >> 1) * kGuFrag + 1024 * (u & 1);
+    }
+    // per-lane sources at stage 0 and their advance per stage (A: 64 bytes
+    // of the row; B: two 1 KB tiles)
+    int sstep[LPW];
+#pragma unroll
+    for (int c = 0; c < LPW; ++c) sstep[c] = ((wave + kGuWaves * c) % NL) / 2 < NA ? kGuKB : 2048;
+    auto make_src = [&](const TileInfo& t, int m, const int8_t* (&src)[LPW]) {
+        const int ch = gu_frag_load_chunk(lane);
+#pragma unroll
+        for (int c = 0; c < LPW; ++c) {
+            const int u = (wave + kGuWaves * c) % NL;
+            const int f = u >> 1, h = u & 1;
+            if (f < NA) {
+                const int l = f / (BM / 32), i = f % (BM / 32);
+                const int tok = s_rt[m][32 * i + gu_frag_load_row(lane, h)];
+                src[c] = xdig + ((int64_t)l * tokens + tok) * H + 16 * ch;
+            } else {
+                const int fb = f - NA;
+                const int64_t cb = t.n0 / 32 + (fb & 3);
+                src[c] = packed + hm_proj_offset(t.e, fb >> 2, H, I) + (cb * tiles_k + h) * 1024 + 16 * lane;
+            }
+        }
+    };
+    auto issue = [&](int slot, const int8_t* const (&src)[LPW], int ks) {
+        int8_t* st = ring + slot * STAGE;
+#pragma unroll
+        for (int c = 0; c < LPW; ++c) dma16(src[c] + (int64_t)ks * sstep[c], st + dst[c]);
+    };
+
+    int rd[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) rd[h] = gu_frag_read_offset(lane, h);
+    v4i fa[2][WR][L], fb[2][2 * WCP];
+    auto read_frags = [&](int slot, int h) __attribute__((always_inline)) {
+        const int8_t* st = ring + slot * STAGE;
+#pragma unroll
+        for (int ii = 0; ii < WR; ++ii)
+#pragma unroll
+            for (int l = 0; l < L; ++l)
+                fa[h][ii][l] = lds16(st + (l * (BM / 32) + wr * WR + ii) * kGuFrag + rd[h]);
+#pragma unroll
+        for (int j = 0; j < 2 * WCP; ++j) {
+            const int fbi = j < WCP ? wc * WCP + j : 4 + wc * WCP + (j - WCP);
+            fb[h][j] = lds16(st + (NA + fbi) * kGuFrag + 1024 * h + 16 * lane);
+        }
+    };
+    v16i acc[WR][L][2 * WCP];
+    auto mfma_step = [&](int h, auto first) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ii = 0; ii < WR; ++ii)
+#pragma unroll
+            for (int l = 0; l < L; ++l)
+#pragma unroll
+                for (int j = 0; j < 2 * WCP; ++j) {
+                    if constexpr (decltype(first)::value)
+                        acc[ii][l][j] = mfma32(fa[h][ii][l], fb[h][j], v16i{});
+                    else
+                        acc[ii][l][j] = mfma32(fa[h][ii][l], fb[h][j], acc[ii][l][j]);
+                }
+    };
+    // K step h = 0 with the refill of `slot` (stage ksrc of the stream)
+    // spread between its MFMAs: a wave that issues all its loads before its
+    // MFMAs stalls on the load queue while the matrix pipe idles.
+    auto mfma_step_dma = [&](auto first, const int8_t* const (&sp)[LPW], bool do_issue, int slot,
+                             int ksrc, bool act) __attribute__((always_inline)) {
+        int8_t* st = ring + slot * STAGE;
+        if (!act) {
+            // no rows of this wave in the tile: only the loads
+            if (do_issue)
+#pragma unroll
+                for (int c = 0; c < LPW; ++c) dma16(sp[c] + (int64_t)ksrc * sstep[c], st + dst[c]);
+            return;
+        }
+        constexpr int NM = WR * L * 2 * WCP;
+        constexpr int PER = NM / LPW > 0 ? NM / LPW : 1;
+#pragma unroll
+        for (int ii = 0; ii < WR; ++ii)
+#pragma unroll
+            for (int l = 0; l < L; ++l)
+#pragma unroll
+                for (int j = 0; j < (2 * WCP); ++j) {
+                    if constexpr (decltype(first)::value)
+                        acc[ii][l][j] = mfma32(fa[0][ii][l], fb[0][j], v16i{});
+                    else
+                        acc[ii][l][j] = mfma32(fa[0][ii][l], fb[0][j], acc[ii][l][j]);
+                    const int idx = (ii * L + l) * (2 * WCP) + j + 1;
+                    if (idx % PER == 0 && idx / PER <= LPW) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (do_issue)
+                            dma16(sp[idx / PER - 1] + (int64_t)ksrc * sstep[idx / PER - 1], st + dst[idx / PER - 1]);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
+#pragma unroll
+        for (int c = NM / PER; c < LPW; ++c)
+            if (do_issue) dma16(sp[c] + (int64_t)ksrc * sstep[c], st + dst[c]);
+    };
+
+    // ---- stream prologue: tile 0's rows, metadata and first kS-1 stages
+    TileInfo cur = info(0);
+    int m = 0;
+    fetch_rows(cur, 0);
+    vm_wait<0>();
+    lds_barrier();
+    fetch_row_meta(0);
+    // per-lane sources of this wave's loads; from step nk-kS on (when this
+    // tile has issued its last stage) they hold the next tile's
+    const int8_t* src[LPW];
+    make_src(cur, 0, src);
+    int slot0 = 0;  // ring slot of the current tile's stage 0
+#pragma unroll
+    for (int s = 0; s < kS - 1; ++s) issue(s, src, s);
+
+    for (int i = 0; i < tr.ntiles; ++i) {
+        const bool has_next = i + 1 < tr.ntiles;
+        const int mn = m ^ 1;
+        TileInfo nxt = cur;
+        if (has_next) nxt = info(i + 1);
+        // stage 0 has landed once at most the kS-2 later stages are in flight
+        vm_wait<(kS - 2) * LPW>();
+        lds_barrier();
+        issue((slot0 + kS - 1) % kS, src, kS - 1);
+        if (has_next) fetch_rows(nxt, mn);
+        // a wave whose rows all lie past the tile's last row (an expert's
+        // partial last tile) skips its fragment reads and MFMAs
+        const bool act = 32 * WR * wr < cur.nrows;
+        if (act) {
+            read_frags(slot0, 0);
+            read_frags(slot0, 1);
+        }
+        // One K step: wait for stage ks+1, publish it, refill the slot of
+        // stage ks (its fragments are in registers) with stage ks+kS of the
+        // stream, and run stage ks while reading stage ks+1's fragments.
+        // Phase A (`next` false) refills with this tile's stages; phase B
+        // (the last kS steps) with the next tile's first kS-1 stages.
+        auto kstep = [&](int ks, auto first, auto next) __attribute__((always_inline)) {
+            const int slot = (slot0 + ks) % kS;
+            if (ks + 1 < nk) {
+                // the stages after ks+1 still in flight are ks+2 .. ks+kS-1
+                // of the stream (fewer at the stream's end)
+                if (has_next || ks + kS - 1 < nk) vm_wait<(kS - 2) * LPW>();
+                else vm_wait<0>();
+            }
+            lds_barrier();
+            const int nslot = (slot + 1) % kS;
+            if constexpr (!decltype(next)::value) {
+                mfma_step_dma(first, src, true, slot, ks + kS, act);
+            } else {
+                mfma_step_dma(first, src, has_next && ks + kS - nk <= kS - 2, slot, ks + kS - nk, act);
+            }
+            if (act) {
+                if (ks + 1 < nk) read_frags(nslot, 0);
+                mfma_step(1, std::false_type{});
+                if (ks + 1 < nk) read_frags(nslot, 1);
+            }
+        };
+        int ks = 0;
+        if (nk > kS) {
+            kstep(0, std::true_type{}, std::false_type{});
+#pragma clang loop unroll(disable)
+            for (ks = 1; ks < nk - kS; ++ks) kstep(ks, std::false_type{}, std::false_type{});
+        }
+        if (has_next) {
+            // the next tile's row tokens (fetched at this tile's start) have
+            // landed once a stage issued after them has
+            if (nk < 2 * kS) {
+                vm_wait<0>();
+                lds_barrier();
+            }
+            make_src(nxt, mn, src);
+            fetch_row_meta(mn);
+        }
+        if (ks == 0) {
+            kstep(0, std::true_type{}, std::true_type{});
+            ks = 1;
+        }
+#pragma clang loop unroll(disable)
+        for (; ks < nk; ++ks) kstep(ks, std::false_type{}, std::true_type{});
+
+        // ---- epilogue (the next tile's first kS-1 stages are in flight):
+        // g and u into the row's two halves of gu.  The zero-point
+        // correction is chosen once per tile (zg, zu are uniform), so no
+        // per-element test drags its integer multiplies into the common case.
+        auto epilogue = [&](auto with_zp) __attribute__((always_inline)) {
+            constexpr bool ZP = decltype(with_zp)::value;
+            const int e = cur.e, nrows = cur.nrows;
+            const float sg = s_sg[e], su = s_su[e];
+            const int zg = s_zg[e], zu = s_zu[e];
+#pragma unroll
+            for (int ii = 0; ii < WR; ++ii) {
+                const int r0 = 32 * (wr * WR + ii);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int rq = r0 + 8 * q + 4 * (lane >> 5);  // rows rq .. rq+3
+                    const float4 sx4 = *reinterpret_cast<const float4*>(&s_xs[m][rq]);
+                    int4 ds4[L];
+                    if constexpr (ZP) {
+#pragma unroll
+                        for (int l = 0; l < L; ++l) ds4[l] = *reinterpret_cast<const int4*>(&s_xd[m][l][rq]);
+                    }
+#pragma unroll
+                    for (int t4 = 0; t4 < 4; ++t4) {
+                        const int v = 4 * q + t4;
+                        const float sx = t4 == 0 ? sx4.x : t4 == 1 ? sx4.y : t4 == 2 ? sx4.z : sx4.w;
+                        const float fg = __fmul_rn(sx, sg), fu = __fmul_rn(sx, su);
+                        const bool live = rq + t4 < nrows;
+                        float* grow = gu + (int64_t)(cur.g0 + rq + t4) * (2 * (int64_t)I) + cur.n0 +
+                                      32 * wc * WCP + (lane & 31);
+#pragma unroll
+                        for (int j = 0; j < WCP; ++j) {
+                            int pg[L], pu[L];
+#pragma unroll
+                            for (int l = 0; l < L; ++l) {
+                                pg[l] = acc[ii][l][j][v];
+                                pu[l] = acc[ii][l][WCP + j][v];
+                            }
+                            if constexpr (ZP) {
+#pragma unroll
+                                for (int l = 0; l < L; ++l) {
+                                    const int ds = t4 == 0 ? ds4[l].x : t4 == 1 ? ds4[l].y : t4 == 2 ? ds4[l].z : ds4[l].w;
+                                    pg[l] -= zg * ds;
+                                    pu[l] -= zu * ds;
+                                }
+                            }
+                            const float g = __fmul_rn(hm_recombine(pg, L), fg);
+                            const float u = __fmul_rn(hm_recombine(pu, L), fu);
+                            if (live) {
+                                grow[32 * j] = g;
+                                grow[I + 32 * j] = u;
+                            }
+                        }
+                    }
+                }
+            }
+        };
+        if (act) {
+            if ((s_zg[cur.e] | s_zu[cur.e]) != 0) epilogue(std::true_type{});
+            else epilogue(std::false_type{});
+        }
+        // next tile
+        slot0 = (slot0 + nk) % kS;
+        m = mn;
+        cur = nxt;
+    }
+}
+
+bool gateup_shape_ok(int64_t H, int64_t I, int64_t E, int32_t limbs) {
+    // |P_l| <= H * 128 * 255 < 2^31 keeps every limb partial exact: H <= 65536
+    return limbs >= 1 && limbs <= 3 && E >= 1 && E <= kMaxExperts && H <= 65536 &&
+           I <= (1 << 20) && H % kGuKB == 0 && H / kGuKB >= kGuStages && I % kGuN == 0;
+}
+
+template <int L>
+int launch_gateup(const hm_layer* layer, const int8_t* xdig, const float* xscale,
+                  const int32_t* xdsum, int64_t tokens, const int32_t* counts,
+                  const int32_t* offsets, const int32_t* perm_tokens, float* gu,
+                  hipStream_t stream) {
+    HM_STAGE_LAUNCH(true, false, gateup_ring_kernel<L>, dim3((unsigned)persistent_grid()),
+                    dim3(kGuThreads), 0, stream, xdig, xscale, xdsum, (int)tokens,
+                    (int)layer->hidden, (int)layer->intermediate, (int)layer->experts,
+                    static_cast<const int8_t*>(layer->packed), layer->scale, layer->zero_point,
+                    counts, offsets, perm_tokens, gu);
+    HM_LAUNCHED();
+    return HM_OK;
 }
 
 }  // namespace
@@ -599,25 +983,25 @@ int launch_l(const hm_layer* layer, const int8_t* adig, const float* ascale,
 // them for the stream's look-ahead, a count the B register ring divides),
 // N in whole workgroup column blocks, E <= 256 (tables in LDS).
 bool hm_mfma_gateup_ok(int64_t H, int64_t I, int64_t E, int32_t limbs) {
-    return shape_ok(kGateUp, H, I, E, limbs);
+    return gateup_shape_ok(H, I, E, limbs);
 }
 
 bool hm_mfma_down_ok(int64_t H, int64_t I, int64_t E, int32_t limbs) {
-    return shape_ok(kDown, I, H, E, limbs);
+    return shape_ok(I, H, E, limbs);
 }
 
-// zf [R x I]: z = silu(g) * u of every grouped row.  The first kernel of the
+// gu [R x 2I]: the gate and up values of every grouped row.  The first kernel of the
 // gate/up stage (its start opens an armed stage timer).
 int hm_launch_gateup_i8_mfma(const hm_layer* layer, int32_t limbs, const int8_t* xdig,
                              const float* xscale, const int32_t* xdsum, int64_t tokens,
                              const int32_t* counts, const int32_t* offsets,
-                             const int32_t* perm_tokens, int64_t R, float* zf,
+                             const int32_t* perm_tokens, int64_t R, float* gu,
                              hipStream_t stream) {
     if (tokens > INT_MAX || R > INT_MAX) return HM_ERR_OVERFLOW;
     switch (limbs) {
-    case 1: return launch_l<kGateUp, 1>(layer, xdig, xscale, xdsum, tokens, counts, offsets, perm_tokens, zf, true, stream);
-    case 2: return launch_l<kGateUp, 2>(layer, xdig, xscale, xdsum, tokens, counts, offsets, perm_tokens, zf, true, stream);
-    case 3: return launch_l<kGateUp, 3>(layer, xdig, xscale, xdsum, tokens, counts, offsets, perm_tokens, zf, true, stream);
+    case 1: return launch_gateup<1>(layer, xdig, xscale, xdsum, tokens, counts, offsets, perm_tokens, gu, stream);
+    case 2: return launch_gateup<2>(layer, xdig, xscale, xdsum, tokens, counts, offsets, perm_tokens, gu, stream);
+    case 3: return launch_gateup<3>(layer, xdig, xscale, xdsum, tokens, counts, offsets, perm_tokens, gu, stream);
     default: return HM_ERR_INVALID;
     }
 }
@@ -629,9 +1013,9 @@ int hm_launch_down_i8_mfma(const hm_layer* layer, int32_t limbs, const int32_t* 
                            hipStream_t stream) {
     if (R > INT_MAX) return HM_ERR_OVERFLOW;
     switch (limbs) {
-    case 1: return launch_l<kDown, 1>(layer, zdig, zscale, zdsum, R, counts, offsets, nullptr, y, false, stream);
-    case 2: return launch_l<kDown, 2>(layer, zdig, zscale, zdsum, R, counts, offsets, nullptr, y, false, stream);
-    case 3: return launch_l<kDown, 3>(layer, zdig, zscale, zdsum, R, counts, offsets, nullptr, y, false, stream);
+    case 1: return launch_l<1>(layer, zdig, zscale, zdsum, R, counts, offsets, y, stream);
+    case 2: return launch_l<2>(layer, zdig, zscale, zdsum, R, counts, offsets, y, stream);
+    case 3: return launch_l<3>(layer, zdig, zscale, zdsum, R, counts, offsets, y, stream);
     default: return HM_ERR_INVALID;
     }
 }

@@ -10,6 +10,9 @@ tree is mounted) oracle/_ref/libhm_ref.so.
 
 Every HIP translation unit is built with -ffp-contract=off (FMAs only where a
 kernel asks for one explicitly) and with packed FP32 instructions disabled.
+Sources with loads the compiler does not track (UNTRACKED_LOAD_SOURCES) are
+assembled from a saved listing that hmoe.isa_check verifies first: no
+register of such a load may be touched before a wait completes it.
 """
 from __future__ import annotations
 
@@ -43,6 +46,8 @@ KERNEL_SOURCES = ["hm_runtime.hip", "hm_router.hip", "hm_gemm.hip", "hm_gemm_mfm
 # (otherwise the compiler copies them to AGPRs and back on every K chunk).
 SOURCE_FLAGS = {"hm_router.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
                 "hm_gemm_f32_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+# Sources whose kernels issue register loads the compiler does not track.
+UNTRACKED_LOAD_SOURCES = {"hm_gemm_mfma.hip"}
 HOST_SOURCES = ["hip_backend.cpp", "hip_tensor_backend.cpp", "moe_block.cpp", "artefact.cpp"]
 
 KERNELS_SO = LIB / "libhm_kernels.so"
@@ -59,14 +64,39 @@ def _run(cmd: list[str], cwd: Path | None = None) -> None:
 
 
 def _quiet_filter(text: str) -> str:
-    return "\n".join(l for l in text.splitlines() if "packed-fp32-ops" not in l)
+    # the feature warning of the host pass, and the note on the M0 clobber of
+    # the LDS-DMA statements (the kernels keep nothing else in M0)
+    return "\n".join(l for l in text.splitlines()
+                     if "packed-fp32-ops" not in l and "Reserved registers on the clobber list" not in l
+                     and "clobber list contains reserved registers" not in l
+                     and not l.endswith("warnings generated."))
+
+
+def _device_listing(obj: Path) -> Path:
+    return obj.with_name(f"{obj.stem}-hip-amdgcn-amd-amdhsa-{ARCH}.s")
 
 
 def _compile_hip(src: Path, obj: Path) -> str:
-    cmd = [HIPCC, *HIP_FLAGS, *SOURCE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
+    checked = src.name in UNTRACKED_LOAD_SOURCES
+    # -save-temps=obj: the object is assembled from the listing that is checked
+    extra = ["-save-temps=obj"] if checked else []
+    cmd = [HIPCC, *HIP_FLAGS, *SOURCE_FLAGS.get(src.name, []), *extra, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}")
+    if checked:
+        from hmoe import isa_check
+        listing = _device_listing(obj)
+        for tmp in obj.parent.glob(f"{obj.stem}-*"):
+            if tmp != listing:
+                tmp.unlink()
+        for tmp in obj.parent.glob(f"{obj.stem}.hip-*"):
+            tmp.unlink()
+        problems = isa_check.check_file(listing)
+        if problems:
+            obj.unlink(missing_ok=True)
+            raise RuntimeError(f"{src.name}: untracked load registers used before their wait:\n"
+                               + "\n".join(problems[:20]))
     return _quiet_filter(res.stdout)
 
 
