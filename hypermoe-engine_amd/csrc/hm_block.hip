@@ -32,12 +32,6 @@ int hm_launch_gateup_gemv(const hm_layer* L, const float* hidden, const int32_t*
                           float* z, hipStream_t s);
 int hm_launch_down_gemv(const hm_layer* L, const float* z, const int32_t* counts,
                         const int32_t* offsets, int64_t pairs, float* y, hipStream_t s);
-bool hm_gemv_combine_ok(int64_t tokens, int32_t top_k, int64_t H, int64_t I);
-int hm_launch_down_combine_gemv(const hm_layer* L, const float* z, const int32_t* counts,
-                                const int32_t* offsets, const uint32_t* ids,
-                                const int32_t* slots, const float* scores,
-                                const float* residual, int64_t tokens, int32_t top_k,
-                                float* y_out, float* out, hipStream_t s);
 extern "C" __attribute__((visibility("hidden"))) int hm_router_topk_quant(const float* h, const float* w, int64_t tokens, int64_t hidden,
                          int64_t experts, int32_t top_k, uint32_t flags, uint32_t* ids,
                          float* scores, float* logits_out, int32_t* status, void* route_ws,
@@ -259,15 +253,6 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
                                          p.zf, s);
         });
         if (rc) return rc;
-        if (hm_gemv_combine_ok(tokens, top_k, H, layer->intermediate) && E <= 1024) {
-            // down projection and combine in one launch; the expert outputs
-            // are written only when the caller asks for them
-            rc = hm_launch_down_combine_gemv(layer, p.zf, counts, p.offsets, p.ids, p.slots,
-                                             p.scores, io->residual, tokens, top_k,
-                                             io->expert_out, io->out, s);
-            if (rc || (rc = mark(5))) return rc;
-            return mark(6);
-        }
         rc = hm_launch_down_gemv(layer, p.zf, counts, p.offsets, P, p.y, s);
     } else if (layer->dtype == HM_DTYPE_INT8) {
         if (!x_quantized) {
