@@ -131,6 +131,55 @@ def pmc_traffic(workload: str, kernel_re: str, primary_re: str, limbs: tuple, qu
                            f"WRITE_SIZE {wcal:.0f} KiB"}
 
 
+def pmc_mfma(workload: str, kernels: dict, limbs: tuple, quiet: bool):
+    """Matrix-core utilisation of the prefill GEMMs from hardware counters:
+    one rocprofv3 --pmc run of a short child bench with
+    SQ_VALU_MFMA_BUSY_CYCLES (summed over the SIMDs), SQ_BUSY_CU_CYCLES
+    (summed over the CUs) and SQ_INSTS_MFMA.  Per kernel (name -> regex):
+    mfma_busy_frac = MFMA busy cycles / (4 SIMDs x CU busy cycles), averaged
+    over its dispatches.  None when rocprofv3 is missing or the run fails."""
+    import csv
+    import re
+    import shutil
+    import subprocess
+    import tempfile
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None
+    counters = ["SQ_VALU_MFMA_BUSY_CYCLES", "SQ_BUSY_CU_CYCLES", "SQ_INSTS_MFMA"]
+    with tempfile.TemporaryDirectory(dir="/tmp") as d:
+        cmd = [exe, "--pmc", *counters, "--kernel-include-regex", "|".join(kernels.values()),
+               "--output-format", "csv", "-d", d, "-o", "pmc", "--", sys.executable,
+               str(REPO / "bench.py"), "--workload", workload, "--steps", "2", "--warmup", "1",
+               "--cpu-sample", "0", "--quiet", "--no-traffic", "--limbs-x", str(limbs[0]),
+               "--limbs-z", str(limbs[1])]
+        log("[bench] counters: rocprofv3 --pmc " + " ".join(counters), quiet)
+        try:
+            subprocess.run(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"),
+                           stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, timeout=240)
+        except subprocess.TimeoutExpired:
+            return None
+        files = list(Path(d).rglob("*counter_collection.csv"))
+        if not files:
+            return None
+        vals = {name: {c: [] for c in counters} for name in kernels}
+        with open(files[0]) as f:
+            for r in csv.DictReader(f):
+                for name, rx in kernels.items():
+                    if re.search(rx, r["Kernel_Name"]) and r["Counter_Name"] in counters:
+                        vals[name][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    out = {"counters": "SQ_VALU_MFMA_BUSY_CYCLES / (4 x SQ_BUSY_CU_CYCLES), per dispatch"}
+    for name, v in vals.items():
+        if not v["SQ_BUSY_CU_CYCLES"]:
+            return None
+        busy = sum(v["SQ_VALU_MFMA_BUSY_CYCLES"]) / len(v["SQ_VALU_MFMA_BUSY_CYCLES"])
+        cu = sum(v["SQ_BUSY_CU_CYCLES"]) / len(v["SQ_BUSY_CU_CYCLES"])
+        out[name] = {"mfma_busy_frac": round(busy / (4.0 * cu), 4),
+                     "mfma_busy_cycles": busy, "busy_cu_cycles": cu,
+                     "mfma_insts": sum(v["SQ_INSTS_MFMA"]) / max(1, len(v["SQ_INSTS_MFMA"]))}
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -278,7 +327,7 @@ def main():
         dn_ops = 2 * T * k * H * I
         # X digit planes in, SiLU(G)*U floats out (their Z digits are the
         # next launch's work)
-        gu_bytes = unique * 2 * H * I + T * H * args.limbs_x + T * k * I * 4
+        gu_bytes = unique * 2 * H * I + T * H * args.limbs_x + T * k * I * args.limbs_z
     else:
         gu_ops = 2 * T * k * 2 * H * I
         dn_ops = 2 * T * k * H * I
@@ -289,9 +338,9 @@ def main():
         achieved = gu_ops / gu_s / 1e12
         peak = PEAK_INT8_TOPS if cfg.int8 else PEAK_FP32_TFLOPS
         roof = {"bound": "mfma",
-                "kernel": ("gate/up stage: limb_gemm_kernel<0, Lx, DB> (SiLU(G)*U in its "
-                           "epilogue) + limb_quantize_rows_vec_kernel<Lz> (Z digits)" if cfg.int8
-                           else "expert_f32_mfma_kernel<true>"),
+                "kernel": ("gate/up stage: gateup_ring_kernel<Lx> (G, U) + "
+                           "limb_swiglu_quantize_vec_kernel<Lz, I/256> (SiLU(G)*U, Z digits)"
+                           if cfg.int8 else "expert_f32_mfma_kernel<true>"),
                 "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                 "frac": round(achieved / peak, 4), "traffic": None,
                 "work_per_launch": gu_ops, "launch_ms": round(stage["gate_up"], 5),
@@ -299,24 +348,29 @@ def main():
     else:
         achieved = gu_bytes / gu_s / 1e9
         roof = {"bound": "hbm",
-                "kernel": ("gemv_tiles_kernel<true> (gate/up)" if gemv else
-                           "gate/up stage: limb_gemm_kernel<0, Lx, DB> + "
-                           "limb_quantize_rows_vec_kernel<Lz>" if cfg.int8
+                "kernel": ("gemv_kernel<true, 1> (gate/up)" if gemv else
+                           "gate/up stage: gateup_ring_kernel<Lx> + "
+                           "limb_swiglu_quantize_vec_kernel<Lz, I/256>" if cfg.int8
                            else "expert_f32_mfma_kernel<true>"),
                 "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
                 "work_per_launch": gu_bytes, "launch_ms": round(stage["gate_up"], 5)}
     if not args.no_traffic:
         if gemv:
-            kre = prim = "gemv_tiles_kernel<true>"
+            kre = prim = "gemv_kernel<true"
         elif cfg.int8:
-            kre, prim = "limb_gemm_kernel<0,|limb_quantize_rows_vec_kernel", "limb_gemm_kernel<0,"
+            kre, prim = "gateup_ring_kernel|limb_swiglu_quantize", "gateup_ring_kernel"
         else:
             kre = prim = "expert_f32_mfma_kernel<true>"
         tr = pmc_traffic(cfg.name, kre, prim, (args.limbs_x, args.limbs_z), q)
         if tr is not None:
             roof["traffic"] = tr.pop("bytes")
             roof["traffic_detail"] = tr
+        if prefill and cfg.int8:
+            hw = pmc_mfma(cfg.name, {"gate_up": "gateup_ring_kernel", "down": "limb_gemm_kernel"},
+                          (args.limbs_x, args.limbs_z), q)
+            if hw is not None:
+                roof["hw_mfma"] = hw
     layer_bytes = synth.algorithmic_bytes(cfg, unique)
     layer_ops = synth.algorithmic_ops(cfg)
     layer = {"hbm_frac": round(layer_bytes / (ms_per_step / 1e3) / 1e9 / PEAK_HBM_GBS, 4),
