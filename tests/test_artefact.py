@@ -19,8 +19,9 @@ import numpy as np
 import pytest
 
 import hm_oracle as O
-from conftest import assert_bitexact
+from conftest import assert_bitexact, assert_compare
 from hmoe import artefact as A
+from hmoe import capi
 from hmoe import synth
 
 HAVE_REF = O.ref_available()
@@ -312,6 +313,17 @@ def test_loaded_layer_runs_like_the_generated_one(tmp_path, dev):
         b = MoEBlock(ref_layer, k).execute_batch(h, w0)
         assert_bitexact(a.ids, b.ids, "ids")
         assert_bitexact(a.output.cpu().numpy(), b.output.cpu().numpy(), "outputs")
+        # and the loaded layer against the oracles: the reference block
+        # (ids bit-exact, output within 1e-4) and, on the integer-limb path,
+        # the limb restatement bit for bit
+        hn, wn = h.cpu().numpy(), w0.cpu().numpy()
+        rout, rids, _ = O.moe_block(p, s, z, hn, wn, k, I)
+        assert_bitexact(a.ids, rids, "ids vs reference")
+        assert_compare(a.output.cpu().numpy(), rout, 1e-4, 1e-4, "loaded layer vs reference block")
+        la = MoEBlock(layer, m.top_k, limbs_x=2, limbs_z=3).execute_batch(
+            h, w, exec_flags=capi.HM_EXEC_LIMBS)
+        lout, _, _ = O.moe_block_limbs(p, s, z, hn, wn, k, I, 2, 3)
+        assert_bitexact(la.output.cpu().numpy(), lout, "loaded layer vs limb oracle")
 
 
 def test_host_library_exports_the_artefact_abi():

@@ -7,6 +7,7 @@ import math
 
 import numpy as np
 
+import hm_oracle as O
 from hmoe import synth
 
 
@@ -76,3 +77,23 @@ def test_zipf_skew_makes_a_hot_expert():
     counts = np.bincount(ids.ravel(), minlength=E)
     assert 9.5 * counts.mean() <= counts.max() <= 10.5 * counts.mean()
     assert counts.min() > 0
+
+
+def test_int8_payload_is_the_pinned_quantiser():
+    """The generator's INT8 projections are the reference packer's symmetric
+    quantisation (Quantization.cpp:45-79) of the float draws: every chosen
+    projection regenerated from its tag and quantised by the oracle (and by
+    the reference build where present) gives the payload bytes, scale and
+    zero point bit for bit."""
+    E, H, I = 3, 96, 64
+    p, s, z = synth.expert_layer(5, 2, E, H, I, True, threads=2)
+    for e in range(E):
+        for proj in range(3):
+            w = synth.normal(5, synth.tag_expert(2, e, proj), H * I, 0.0, 0.02)
+            q, sc, zp, _ = O.quantize_int8(w)
+            assert np.array_equal(q, p[e, proj]), (e, proj)
+            assert np.float32(sc).view(np.uint32) == s[e, proj].view(np.uint32)
+            assert zp == z[e, proj] == 0
+            if O.ref_available():
+                rq, rs, rz, _ = O.ref_quantize_int8(w)
+                assert np.array_equal(rq, q) and rs == sc and rz == zp
