@@ -28,10 +28,15 @@ int hm_launch_down_f32(const hm_layer* layer, const int32_t* counts, const int32
                        int64_t R, const float* zf, float* y, hipStream_t stream);
 bool hm_gemv_shape_ok(int64_t H, int64_t I);
 int hm_launch_gateup_gemv(const hm_layer* L, const float* hidden, const int32_t* counts,
-                          const int32_t* offsets, const int32_t* perm_tokens, int64_t pairs,
-                          float* z, hipStream_t s);
+                          const int32_t* perm_tokens, int64_t tokens, int64_t pairs, float* z,
+                          hipStream_t s);
 int hm_launch_down_gemv(const hm_layer* L, const float* z, const int32_t* counts,
-                        const int32_t* offsets, int64_t pairs, float* y, hipStream_t s);
+                        int64_t pairs, float* y, hipStream_t s);
+bool hm_gemv_combine_ok(int64_t tokens, int32_t top_k, int64_t H, int64_t I);
+int hm_launch_down_combine_gemv(const hm_layer* L, const float* z, const int32_t* counts,
+                                const uint32_t* ids, const int32_t* slots, const float* scores,
+                                const float* residual, int64_t tokens, int32_t top_k,
+                                float* y_out, float* out, hipStream_t s);
 extern "C" __attribute__((visibility("hidden"))) int hm_router_topk_quant(const float* h, const float* w, int64_t tokens, int64_t hidden,
                          int64_t experts, int32_t top_k, uint32_t flags, uint32_t* ids,
                          float* scores, float* logits_out, int32_t* status, void* route_ws,
@@ -249,11 +254,20 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
     };
     if (gemv) {
         rc = gate_up([&] {
-            return hm_launch_gateup_gemv(layer, hidden, counts, p.offsets, p.perm_tokens, P,
+            return hm_launch_gateup_gemv(layer, hidden, counts, p.perm_tokens, tokens, P,
                                          p.zf, s);
         });
         if (rc) return rc;
-        rc = hm_launch_down_gemv(layer, p.zf, counts, p.offsets, P, p.y, s);
+        // one or two tokens: the down projection and the combine in one
+        // launch (the combine's events mark its end)
+        if (E <= 1024 && hm_gemv_combine_ok(tokens, top_k, H, layer->intermediate)) {
+            rc = hm_launch_down_combine_gemv(layer, p.zf, counts, p.ids, p.slots, p.scores,
+                                             io->residual, tokens, top_k, io->expert_out,
+                                             io->out, s);
+            if (rc || (rc = mark(5)) || (rc = mark(6))) return rc;
+            return HM_OK;
+        }
+        rc = hm_launch_down_gemv(layer, p.zf, counts, P, p.y, s);
     } else if (layer->dtype == HM_DTYPE_INT8) {
         if (!x_quantized) {
             rc = hm_launch_quantize_rows(hidden, tokens, H, limbs_x, p.xdig, p.xscale, p.xdsum, s);

@@ -28,35 +28,79 @@ constexpr int kGvWaves = 8;                 // waves per workgroup
 constexpr int kGvThreads = 64 * kGvWaves;
 constexpr int kGvRows = 4;                  // activation rows per pass (weights stay in registers)
 constexpr int kGvMaxTiles = 16;             // K tiles per wave: K <= 32 * 16 * (waves per projection)
+constexpr int kGvXPer = 2;                  // float4 of a row per thread: K <= 4 * 2 * kGvThreads
+constexpr int kGvAllFloats = 16384;         // s_x of every token's row: T * K32 <= this
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-// The slot-th expert (ascending id) with a non-zero group; -1 if none.
-// Every wave computes it redundantly from `counts` (E <= 1024); the loads
-// of all 64-expert groups go out together.
-__device__ int hm_active_expert(const int32_t* __restrict__ counts, int64_t experts, int slot) {
+// The slot-th expert (ascending id) with a non-zero group (e = -1 if
+// none), its group's first grouped row (the exclusive prefix sum of counts,
+// i.e. offsets[e]) and its row count, from the counts hm_load_counts read
+// (E <= 64 NG).  Every group is reduced before the search, so no load is
+// left in flight past this point (a later wait for its register would also
+// wait for every load issued after it).  Every wave computes it
+// redundantly.
+struct hm_active { int e, g0, rows; };
+
+__device__ __forceinline__ int hm_wave_sum(int v) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+    return v;
+}
+
+// The counts of the NG 64-expert groups (lane l of group b: expert 64 b + l;
+// zero past E), loads only: issue them before other loads, so that their
+// wait (in hm_active_expert) does not also wait for those.
+template <int NG>
+__device__ __forceinline__ void hm_load_counts(const int32_t* __restrict__ counts,
+                                               int64_t experts, int (&cnt)[NG]) {
     const int lane = threadIdx.x & 63;
-    constexpr int kGroups = 16;
-    int cnt[kGroups];
 #pragma unroll
-    for (int b = 0; b < kGroups; ++b) {
+    for (int b = 0; b < NG; ++b) {
         const int64_t e = (int64_t)b * 64 + lane;
-        cnt[b] = e < experts ? counts[e] : 0;
+        cnt[b] = counts[e < experts ? e : experts - 1];  // (clamped: no branch per load)
     }
-    int seen = 0;
+}
+
+template <int NG>
+__device__ __forceinline__ hm_active hm_active_expert(int (&cnt)[NG], int64_t experts, int slot) {
+    const int lane = threadIdx.x & 63;
+    unsigned long long m[NG];
+    int tot[NG];
 #pragma unroll
-    for (int b = 0; b < kGroups; ++b) {
-        const unsigned long long m = __ballot(cnt[b] > 0);
-        const int c = __popcll(m);
-        if (slot < seen + c) {
+    for (int b = 0; b < NG; ++b) {
+        if ((int64_t)b * 64 + lane >= experts) cnt[b] = 0;
+        m[b] = __ballot(cnt[b] > 0);
+        tot[b] = hm_wave_sum(cnt[b]);
+    }
+    hm_active r{-1, 0, 0};
+    int seen = 0, before = 0;
+#pragma unroll
+    for (int b = 0; b < NG; ++b) {
+        const int c = __popcll(m[b]);
+        if (r.e < 0 && slot < seen + c) {
             // position of the (slot - seen)-th set bit
-            unsigned long long mm = m;
+            unsigned long long mm = m[b];
             for (int i = 0; i < slot - seen; ++i) mm &= mm - 1;
-            return b * 64 + __ffsll((long long)mm) - 1;
+            const int pos = __ffsll((long long)mm) - 1;
+            r.e = b * 64 + pos;
+            // (uniform values: read from lane 0, so that they live in SGPRs)
+            r.rows = __builtin_amdgcn_readfirstlane(__shfl(cnt[b], pos, 64));
+            r.g0 = __builtin_amdgcn_readfirstlane(before + hm_wave_sum(lane < pos ? cnt[b] : 0));
         }
         seen += c;
+        before += __builtin_amdgcn_readfirstlane(tot[b]);
     }
-    return -1;
+    return r;
+}
+
+// v where keep, else +0 (bitwise: a select between v and a zero vector
+// would be turned into a select between their addresses, which puts v in
+// scratch memory)
+__device__ __forceinline__ float4 hm_keep_if(float4 v, bool keep) {
+    const int m = keep ? -1 : 0;
+    return make_float4(__int_as_float(__float_as_int(v.x) & m), __int_as_float(__float_as_int(v.y) & m),
+                       __int_as_float(__float_as_int(v.z) & m), __int_as_float(__float_as_int(v.w) & m));
 }
 
 // 16 unsigned bytes (after XOR 0x80: u = q + 128) -> 16 floats
@@ -82,14 +126,21 @@ __device__ __forceinline__ void tile_to_float(v4i w, float (&f)[16]) {
 // kGvRows at a time, from an LDS copy of the rows.  Partial sums meet in LDS
 // in a fixed order (the two K halves of a tile, then the K ranges in
 // ascending order).  Dynamic LDS: kGvRows * K32 floats.
+//
+// Issue order: the expf table, counts, the first row block and only then
+// the weights, so that the rows reach LDS while the weights stream; the
+// first block runs as straight-line code, so that each tile is used as it
+// arrives (a loop around it would wait for every load at its entry).  With
+// ALL (gate/up of a few tokens: T * K32 <= kGvAllFloats) s_x holds every
+// token's row, loaded before anything else, and grouped row g reads row
+// perm_tokens[g] of it.
 // ---------------------------------------------------------------------------
-template <bool GATEUP, int CT>
+template <bool GATEUP, int CT, int NG, bool ALL>
 __global__ __launch_bounds__(kGvThreads) void gemv_kernel(
     const float* __restrict__ x_src, const int32_t* __restrict__ perm_tokens, int64_t K,
     int64_t N, int64_t experts, const int8_t* __restrict__ packed, int64_t hidden,
     int64_t inter, const float* __restrict__ scale, const int32_t* __restrict__ zp,
-    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
-    float* __restrict__ out) {
+    const int32_t* __restrict__ counts, int64_t n_tokens, float* __restrict__ out) {
     constexpr int NP = GATEUP ? 2 : 1;           // projections
     constexpr int NQ = kGvWaves / (NP * CT);     // K ranges per (projection, column tile)
     static_assert(NQ >= 1 && NP * CT * NQ == kGvWaves, "wave split");
@@ -97,41 +148,95 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(
     __shared__ float s_red[NP][CT][NQ][kGvRows][32];
     __shared__ float s_xs[NQ][kGvRows];
     __shared__ unsigned long long s_exp2[32];
-    if (GATEUP) hm_load_exp2_table(s_exp2);
+    __shared__ float4 s_dump;
     const int tid = threadIdx.x, lane = tid & 63;
+    const unsigned long long tab = GATEUP && tid < 32 ? kHmExp2Table[tid] : 0ull;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int p = wave / (CT * NQ), c = (wave / NQ) % CT, q = wave % NQ;
-    const int e = hm_active_expert(counts, experts, (int)blockIdx.y);
+    int cnt[NG];
+    hm_load_counts<NG>(counts, experts, cnt);
+    // ALL: every token's row, right after the counts (it needs no routing
+    // result)
+    constexpr int kAllX = ALL ? kGvAllFloats / 4 / kGvThreads : 1;
+    float4 xa[kAllX];
+    const int64_t K32 = hm_pad32(K), k4 = K32 / 4;
+    // (loads from clamped in-range addresses, no branch: a load under a
+    // branch is merged with its alternative at the join, which waits for it;
+    // the range is applied where the values are stored)
+    const uint32_t k4u = (uint32_t)k4;
+    if (ALL) {
+#pragma unroll
+        for (int u = 0; u < kAllX; ++u) {
+            const uint32_t i = (uint32_t)tid + (uint32_t)u * kGvThreads;
+            const uint32_t t = min(i / k4u, (uint32_t)n_tokens - 1), k = min(4 * (i % k4u), (uint32_t)K - 4);
+            xa[u] = *reinterpret_cast<const float4*>(x_src + (int64_t)t * K + k);
+        }
+    }
+    const hm_active act = hm_active_expert<NG>(cnt, experts, (int)blockIdx.y);
+    const int e = act.e;
     if (e < 0) return;  // uniform: every wave computes the same e
-    const int64_t K32 = hm_pad32(K), KT = K32 / 32;
+    const int64_t KT = K32 / 32;
     const int64_t NT = hm_pad32(N) / 32;
     const int cb = min((int)(CT * blockIdx.x) + c, (int)NT - 1);  // past the last tile: repeats it
     const int kb0 = (int)(q * KT / NQ), nkb = (int)((q + 1) * KT / NQ) - kb0;
-    // the wave's weight tiles, all loads in flight together
+    const int64_t g0 = act.g0;
+    const int rows = act.rows;
+    // the first row block's activations (zero past K)
+    const int nr0 = min(kGvRows, rows);
+    constexpr int kRowX = ALL ? 1 : kGvRows;
+    float4 xr[kRowX][kGvXPer];
+#pragma unroll
+    for (int r = 0; r < kRowX && !ALL; ++r) {
+        const int64_t g = g0 + min(r, nr0 - 1);
+        const float* src = x_src + (GATEUP ? (int64_t)perm_tokens[g] : g) * K;
+#pragma unroll
+        for (int v = 0; v < kGvXPer; ++v) {
+            const int64_t k = min(4 * ((int64_t)tid + (int64_t)v * kGvThreads), K - 4);
+            xr[r][v] = *reinterpret_cast<const float4*>(src + k);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // (keeps the row loads ahead of the weight loads)
+    // the wave's weight tiles, all loads in flight together (tiles past the
+    // wave's range re-read its last one, or tile 0 of the column: no branch)
     const int8_t* wt = packed + hm_proj_offset(e, GATEUP ? p : 2, hidden, inter) +
-                       ((int64_t)cb * KT + kb0) * 1024 + 16 * lane;
+                       (int64_t)cb * KT * 1024 + 16 * lane;
     v4i w[kGvMaxTiles];
 #pragma unroll
-    for (int t = 0; t < kGvMaxTiles; ++t)
-        if (t < nkb) w[t] = *reinterpret_cast<const v4i*>(wt + (int64_t)t * 1024);
-    const int64_t g0 = offsets[e];
-    const int rows = counts[e];
-    for (int r0 = 0; r0 < rows; r0 += kGvRows) {
-        const int nr = min(kGvRows, rows - r0);
-        // the rows into LDS (zero past K: the padded K tiles hold zeros too)
-        const int64_t k4 = K32 / 4;
-        for (int64_t i = tid; i < (int64_t)nr * k4; i += kGvThreads) {
-            const int r = (int)(i / k4);
-            const int64_t k = 4 * (i % k4);
-            const int64_t g = g0 + r0 + r;
-            const float* xr = x_src + (GATEUP ? (int64_t)perm_tokens[g] : g) * K;
-            const float4 v = k < K ? *reinterpret_cast<const float4*>(xr + k) : make_float4(0.f, 0.f, 0.f, 0.f);
-            *reinterpret_cast<float4*>(&s_x[r * K32 + k]) = v;
-        }
-        __syncthreads();
-        float acc[kGvRows], xs[kGvRows];
+    for (int t = 0; t < kGvMaxTiles; ++t) {
+        const int kb = nkb > 0 ? kb0 + min(t, nkb - 1) : 0;
+        w[t] = *reinterpret_cast<const v4i*>(wt + (int64_t)kb * 1024);
+    }
+    if (ALL) {
 #pragma unroll
-        for (int r = 0; r < kGvRows; ++r) acc[r] = xs[r] = 0.0f;
+        for (int u = 0; u < kAllX; ++u) {
+            const uint32_t i = (uint32_t)tid + (uint32_t)u * kGvThreads;
+            if (i < n_tokens * k4)  // (zero past K)
+                *reinterpret_cast<float4*>(&s_x[4 * i]) = hm_keep_if(xa[u], 4 * (i % k4u) < K);
+        }
+    } else {
+        // (unconditional stores, so that no load is sunk into a branch behind
+        // the weights: slices past the row go to a dummy slot, rows past nr0
+        // are not read)
+#pragma unroll
+        for (int r = 0; r < kRowX; ++r)
+#pragma unroll
+            for (int v = 0; v < kGvXPer; ++v) {
+                const int64_t i = (int64_t)tid + (int64_t)v * kGvThreads;
+                float4* dst = i < k4 ? reinterpret_cast<float4*>(&s_x[r * K32 + 4 * i]) : &s_dump;
+                *dst = hm_keep_if(xr[r][v], r < nr0 && 4 * i < K);
+            }
+    }
+    if (GATEUP && tid < 32) s_exp2[tid] = tab;
+    // one row block: rows r0 .. r0 + nr - 1, already in s_x
+    auto block = [&](int r0, int nr) {
+        // the block's rows in s_x
+        int64_t xoff[kGvRows];
+#pragma unroll
+        for (int r = 0; r < kGvRows; ++r)
+            xoff[r] = (ALL ? (r < nr ? (int64_t)perm_tokens[g0 + r0 + r] : 0) : r) * K32;
+        float acc[kGvRows];
+#pragma unroll
+        for (int r = 0; r < kGvRows; ++r) acc[r] = 0.0f;
 #pragma unroll
         for (int t = 0; t < kGvMaxTiles; ++t) {
             if (t < nkb) {
@@ -141,7 +246,7 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(
 #pragma unroll
                 for (int r = 0; r < kGvRows; ++r) {
                     if (r < nr) {
-                        const float4* xv = reinterpret_cast<const float4*>(&s_x[r * K32 + k]);
+                        const float4* xv = reinterpret_cast<const float4*>(&s_x[xoff[r] + k]);
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             const float4 v = xv[i];
@@ -149,7 +254,6 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(
                             acc[r] = __builtin_fmaf(v.y, f[4 * i + 1], acc[r]);
                             acc[r] = __builtin_fmaf(v.z, f[4 * i + 2], acc[r]);
                             acc[r] = __builtin_fmaf(v.w, f[4 * i + 3], acc[r]);
-                            xs[r] += (v.x + v.y) + (v.z + v.w);
                         }
                     }
                 }
@@ -159,9 +263,19 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(
 #pragma unroll
         for (int r = 0; r < kGvRows; ++r) {
             const float a = acc[r] + __shfl_xor(acc[r], 32, 64);
-            const float x = xs[r] + __shfl_xor(xs[r], 32, 64);
             if (lane < 32) s_red[p][c][q][r][lane] = a;
-            if (p == 0 && c == 0 && lane == 0) s_xs[q][r] = x;
+        }
+        // the rows' sums over this K range (one wave per range)
+        if (p == 0 && c == 0) {
+#pragma unroll
+            for (int r = 0; r < kGvRows; ++r) {
+                if (r >= nr) break;
+                float x = 0.0f;
+                for (int k = 32 * kb0 + lane; k < 32 * (kb0 + nkb); k += 64) x += s_x[xoff[r] + k];
+#pragma unroll
+                for (int d = 32; d >= 1; d >>= 1) x += __shfl_xor(x, d, 64);
+                if (lane == 0) s_xs[q][r] = x;
+            }
         }
         __syncthreads();
         // one half-wave per (row, column tile) finishes its 32 columns
@@ -188,24 +302,432 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(
                 else out[g * N + n] = v[0];
             }
         }
+    };
+    __syncthreads();
+    block(0, nr0);
+    // further row blocks (more than kGvRows rows on the expert)
+    for (int r0 = kGvRows; r0 < rows; r0 += kGvRows) {
+        const int nr = min(kGvRows, rows - r0);
+        __syncthreads();  // the previous block's reads of s_x and s_red are done
+        for (int64_t i = tid; !ALL && i < (int64_t)nr * k4; i += kGvThreads) {
+            const int r = (int)(i / k4);
+            const int64_t k = 4 * (i % k4);
+            const int64_t g = g0 + r0 + r;
+            const float* xrow = x_src + (GATEUP ? (int64_t)perm_tokens[g] : g) * K;
+            const float4 v = k < K ? *reinterpret_cast<const float4*>(xrow + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+            *reinterpret_cast<float4*>(&s_x[r * K32 + k]) = v;
+        }
         __syncthreads();
+        block(r0, nr);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Gate/up of a few tokens (T * K32 <= kGvAllFloats) on 8-column slices:
+//   z[g, n] = silu(x_g . Wg[n]) * (x_g . Wu[n]),  x_g = hidden[perm_tokens[g]]
+// Workgroup: one active expert (the blockIdx.y-th) x 8 columns (slice
+// blockIdx.x: N/8 x slots workgroups, three or more per CU at decode, so
+// the weight stream and its dequantising arithmetic spread over every CU).
+// As in the fused down kernel, one wave-wide 16-byte load covers four K
+// tiles of the slice (lane l: tile l / 16, K half (l / 8) % 2, column
+// l % 8); wave (p, q) takes projection p and K quarter q, holds its LJ
+// loads in registers and runs the expert's rows past them.  Every token's
+// row is in LDS (loaded first, with the counts), grouped row g reads row
+// perm_tokens[g].  Sums: per lane in K order, the eight lanes of a column
+// in a fixed tree, the quarters in order; then the factored dequantisation
+// and SiLU(G)*U as in gemv_kernel.
+// ---------------------------------------------------------------------------
+constexpr int kGsQ = 4;  // K quarters (waves per projection)
+
+template <int NG, int LJ>
+__global__ __launch_bounds__(kGvThreads) void gateup_slice_kernel(
+    const float* __restrict__ x_src, const int32_t* __restrict__ perm_tokens, int64_t K,
+    int64_t N, int64_t experts, const int8_t* __restrict__ packed, const float* __restrict__ scale,
+    const int32_t* __restrict__ zp, const int32_t* __restrict__ counts, int n_tokens,
+    float* __restrict__ out) {
+    extern __shared__ __attribute__((aligned(16))) float s_x[];      // [T][K32]
+    __shared__ float s_red[2][kGsQ][kGvRows][8];
+    __shared__ float s_xs[kGsQ][kGvRows];
+    __shared__ unsigned long long s_exp2[32];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int p = wave / kGsQ, q = wave % kGsQ;
+    const unsigned long long tab = tid < 32 ? kHmExp2Table[tid] : 0ull;
+    // counts, then the token rows (only the slices that exist: a uniform
+    // bound per load, no data merged at a join)
+    int cnt[NG];
+    hm_load_counts<NG>(counts, experts, cnt);
+    const int64_t K32 = hm_pad32(K), KT = K32 / 32;
+    const uint32_t k4 = (uint32_t)(K32 / 4), nx = (uint32_t)n_tokens * k4;
+    constexpr int kX = kGvAllFloats / 4 / kGvThreads;
+    float4 xa[kX];
+#pragma unroll
+    for (int u = 0; u < kX; ++u) {
+        if ((uint32_t)u * kGvThreads < nx) {
+            const uint32_t i = min((uint32_t)tid + (uint32_t)u * kGvThreads, nx - 1);
+            const uint32_t t = i / k4, k = min(4 * (i % k4), (uint32_t)K - 4);
+            xa[u] = *reinterpret_cast<const float4*>(x_src + (int64_t)t * K + k);
+        }
+    }
+    const hm_active act = hm_active_expert<NG>(cnt, experts, (int)blockIdx.y);
+    const int e = act.e;
+    if (e < 0) return;  // uniform: every wave computes the same e
+    const int64_t n0 = 8 * (int64_t)blockIdx.x;
+    const int64_t cb = n0 >> 5;
+    const int sl = (int)(n0 & 31) >> 3;
+    const int kb0 = (int)(q * KT / kGsQ), nkb = (int)((q + 1) * KT / kGsQ) - kb0;
+    const int tq = lane >> 4, kh = (lane >> 3) & 1, col = lane & 7;
+    // the x rows to LDS (zero past K) before the weights go out
+#pragma unroll
+    for (int u = 0; u < kX; ++u) {
+        const uint32_t i = (uint32_t)tid + (uint32_t)u * kGvThreads;
+        if ((uint32_t)u * kGvThreads < nx && i < nx)
+            *reinterpret_cast<float4*>(&s_x[4 * i]) = hm_keep_if(xa[u], 4 * (i % k4) < K);
+    }
+    if (tid < 32) s_exp2[tid] = tab;
+    __builtin_amdgcn_sched_barrier(0);
+    // the weights: LJ loads of four K tiles (tiles past the quarter re-read
+    // its last one and are skipped below)
+    const int8_t* wsrc = packed + hm_proj_offset(e, p, K, N) + cb * KT * 1024 + 512 * kh +
+                         128 * sl + 16 * col;
+    v4i w[LJ];
+#pragma unroll
+    for (int j = 0; j < LJ; ++j)
+        w[j] = *reinterpret_cast<const v4i*>(wsrc + (int64_t)(kb0 + min(4 * j + tq, max(nkb - 1, 0))) * 1024);
+    __syncthreads();
+    const int64_t g0 = act.g0;
+    const int rows = act.rows;
+    for (int r0 = 0; r0 < rows; r0 += kGvRows) {
+        const int nr = min(kGvRows, rows - r0);
+        int64_t xoff[kGvRows];
+#pragma unroll
+        for (int r = 0; r < kGvRows; ++r)
+            xoff[r] = (r < nr ? (int64_t)perm_tokens[g0 + r0 + r] : 0) * K32 + 32 * (kb0 + tq) + 16 * kh;
+        float acc[kGvRows];
+#pragma unroll
+        for (int r = 0; r < kGvRows; ++r) acc[r] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < LJ; ++j) {
+            if (4 * j + tq < nkb) {
+                float f[16];
+                tile_to_float(w[j], f);
+#pragma unroll
+                for (int r = 0; r < kGvRows; ++r) {
+                    if (r < nr) {
+                        const float4* xv = reinterpret_cast<const float4*>(&s_x[xoff[r] + 128 * j]);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const float4 v = xv[i];
+                            acc[r] = __builtin_fmaf(v.x, f[4 * i], acc[r]);
+                            acc[r] = __builtin_fmaf(v.y, f[4 * i + 1], acc[r]);
+                            acc[r] = __builtin_fmaf(v.z, f[4 * i + 2], acc[r]);
+                            acc[r] = __builtin_fmaf(v.w, f[4 * i + 3], acc[r]);
+                        }
+                    }
+                }
+            }
+        }
+        // the eight lanes of each column: K halves, then the four tiles
+#pragma unroll
+        for (int r = 0; r < kGvRows; ++r) {
+            float a = acc[r];
+            a += __shfl_xor(a, 8, 64);
+            a += __shfl_xor(a, 16, 64);
+            a += __shfl_xor(a, 32, 64);
+            if (lane < 8) s_red[p][q][r][lane] = a;
+        }
+        // the rows' sums over this K quarter (the gate waves)
+        if (p == 0) {
+#pragma unroll
+            for (int r = 0; r < kGvRows; ++r) {
+                if (r >= nr) break;
+                const int64_t xr0 = (int64_t)perm_tokens[g0 + r0 + r] * K32;
+                float xs = 0.0f;
+                for (int k = 32 * kb0 + lane; k < 32 * (kb0 + nkb); k += 64) xs += s_x[xr0 + k];
+#pragma unroll
+                for (int d = 32; d >= 1; d >>= 1) xs += __shfl_xor(xs, d, 64);
+                if (lane == 0) s_xs[q][r] = xs;
+            }
+        }
+        __syncthreads();
+        if (tid < nr * 8) {
+            const int r = tid >> 3, c = tid & 7;
+            float x_sum = 0.0f, a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kGsQ; ++j) {
+                x_sum += s_xs[j][r];
+                a0 += s_red[0][j][r][c];
+                a1 += s_red[1][j][r][c];
+            }
+            const float g = __fmul_rn(__fsub_rn(a0, __fmul_rn((float)(128 + zp[e * 3]), x_sum)), scale[e * 3]);
+            const float uu = __fmul_rn(__fsub_rn(a1, __fmul_rn((float)(128 + zp[e * 3 + 1]), x_sum)),
+                                       scale[e * 3 + 1]);
+            const int64_t n = n0 + c;
+            if (n < N) out[(g0 + r0 + r) * N + n] = __fmul_rn(hm_silu_t(g, s_exp2), uu);
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Decode down projection fused with the combine, for few (token, expert)
+// pairs (P = T*k <= kDcPairs), with no workgroup waiting for another: the
+// workgroup owns kDcCols = 8 output columns for every active expert (H/8
+// workgroups, enough to keep every CU streaming) and forms the tokens'
+// outputs for them itself.
+//
+// Eight columns of a tile are two 128-byte pieces of it (K halves 0 and 1:
+// bytes 128 s .. +127 and 512 + 128 s .. +127 for slice s), so one
+// wave-wide 16-byte load covers four K tiles: lane l takes tile l / 16, K
+// half (l / 8) % 2, column l % 8.  The waves split (active expert, K range):
+// with nact < 8 active experts 8 / nact waves share an expert's K, with
+// nact >= 8 a wave takes experts wave and wave + 8 whole.  Each wave holds
+// its expert's pieces in registers and runs the expert's z rows (staged in
+// LDS) past them; the eight lanes of a column sum in a fixed tree, the waves
+// of an expert in K order, and
+//   y[g, n] = s (sum_k z_k u_k - (128 + zp) sum_k z_k),  u = q + 128,
+// as in gemv_kernel.  The combine follows hm_combine's arithmetic (pairs by
+// ascending expert id from 0, residual added last).  Every load that needs
+// no routing result (z, the residual, counts) is issued first.
+// ---------------------------------------------------------------------------
+constexpr int kDcWaves = 8;
+constexpr int kDcThreads = 64 * kDcWaves;
+constexpr int kDcPairs = 16;                    // P = T * k
+constexpr int kDcCols = 8;                      // output columns per workgroup
+constexpr int kDcMaxTiles = 24;                 // K tiles of down: I <= 32 * 24
+constexpr int kDcLoads = kDcMaxTiles / 4;       // wave loads per expert (four K tiles each)
+constexpr int kDcZ = (kDcPairs * 32 * kDcMaxTiles / 4 + kDcThreads - 1) / kDcThreads;  // z float4 per thread
+
+// NG: 64-expert groups (E <= 64 NG)
+template <int NG>
+__global__ __launch_bounds__(kDcThreads) void gemv_down_combine_kernel(
+    const float* __restrict__ z, int64_t I, int64_t H, int64_t experts,
+    const int8_t* __restrict__ packed, const float* __restrict__ scale,
+    const int32_t* __restrict__ zp, const int32_t* __restrict__ counts,
+    const uint32_t* __restrict__ ids, const int32_t* __restrict__ slots,
+    const float* __restrict__ scores, const float* __restrict__ residual, int tokens,
+    int top_k, float* __restrict__ y_out, float* __restrict__ out) {
+    extern __shared__ __attribute__((aligned(16))) float s_z[];      // [P][I32]
+    __shared__ float s_part[kDcWaves][2][kDcPairs][kDcCols];         // per wave, unit, row
+    __shared__ float s_zs[kDcWaves][2][kDcPairs];                    // the rows' z sums
+    __shared__ float s_y[kDcPairs][kDcCols];
+    __shared__ int s_act[kDcPairs], s_off[kDcPairs];
+    __shared__ uint32_t s_ids[kDcPairs];
+    __shared__ int32_t s_row[kDcPairs];
+    __shared__ float s_w[kDcPairs];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int P = tokens * top_k;
+    const int64_t I32 = hm_pad32(I), KT = I32 / 32;
+    const int64_t n0 = (int64_t)kDcCols * blockIdx.x;
+    const int64_t cb = n0 >> 5;
+    const int sl = (int)(n0 & 31) / kDcCols;
+    // loads first, none under a branch (clamped in-range addresses; the
+    // ranges are applied where the values are used): counts, then what
+    // needs no routing result -- z rows, the residual, the pairs
+    int cnt[NG];
+    hm_load_counts<NG>(counts, experts, cnt);
+    const uint32_t q4 = (uint32_t)(I32 / 4);
+    float4 zv[kDcZ];
+#pragma unroll
+    for (int u = 0; u < kDcZ; ++u) {
+        const uint32_t i = (uint32_t)tid + (uint32_t)u * kDcThreads;
+        const uint32_t g = min(i / q4, (uint32_t)P - 1), k = min(4 * (i % q4), (uint32_t)I - 4);
+        zv[u] = *reinterpret_cast<const float4*>(z + (int64_t)g * I + k);
+    }
+    const int ct = tid / kDcCols, cc = tid % kDcCols;  // combine: token ct, column n0 + cc
+    const bool comb = ct < tokens && n0 + cc < H;
+    float res = 0.0f;
+    if (residual) res = residual[(int64_t)min(ct, tokens - 1) * H + min(n0 + cc, H - 1)];
+    const int pt = min(tid, P - 1);
+    const uint32_t pid = ids[pt];
+    const int32_t prow = slots[pt];
+    const float psc = scores[pt];
+    // the active experts (ascending id), every wave: lane j < nact holds the
+    // j-th, its row count and its group's first row (an exclusive prefix
+    // sum, i.e. offsets[e])
+    unsigned long long m[NG];
+    int nact = 0;
+#pragma unroll
+    for (int b = 0; b < NG; ++b) {
+        if ((int64_t)b * 64 + lane >= experts) cnt[b] = 0;
+        m[b] = __ballot(cnt[b] > 0);
+        nact += __popcll(m[b]);
+    }
+    nact = min(nact, kDcPairs);
+    int my_act = 0, my_rows = 0;
+    {
+        int seen = 0;
+#pragma unroll
+        for (int b = 0; b < NG; ++b) {
+            const int c = __popcll(m[b]);
+            const int k = lane - seen;  // this lane's rank within the group
+            unsigned long long mm = m[b];
+            for (int i = 0; i < k && i < c; ++i) mm &= mm - 1;
+            const int pos = mm ? __ffsll((long long)mm) - 1 : 0;
+            const int rb = __shfl(cnt[b], pos, 64);
+            if (k >= 0 && k < c) {
+                my_act = b * 64 + pos;
+                my_rows = rb;
+            }
+            seen += c;
+        }
+    }
+    if (lane >= nact) my_rows = 0;
+    int incl = my_rows;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int t = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += t;
+    }
+    const int my_off = incl - my_rows;
+    // this wave's units: (expert slot, K range) -- two whole experts, or one
+    // K range of 8 / nact
+    const int wpe = nact >= kDcWaves ? 1 : kDcWaves / max(nact, 1);
+    const int q = wave % wpe;
+    const int kb0 = (int)(q * KT / wpe), nkb = (int)((q + 1) * KT / wpe) - kb0;
+    const int unit_slot[2] = {nact >= kDcWaves ? wave : wave / wpe, wave + kDcWaves};
+    const bool unit_on[2] = {unit_slot[0] < nact, nact >= kDcWaves && unit_slot[1] < nact};
+    int unit_e[2], unit_g0[2], unit_rows[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        const int sl_ = min(unit_slot[s], 63);
+        unit_e[s] = __builtin_amdgcn_readfirstlane(__shfl(my_act, sl_, 64));
+        unit_g0[s] = __builtin_amdgcn_readfirstlane(__shfl(my_off, sl_, 64));
+        unit_rows[s] = min(__builtin_amdgcn_readfirstlane(__shfl(my_rows, sl_, 64)), kDcPairs);
+    }
+    // z to LDS (zero past I); the pairs' ids; the active list -- before the
+    // weights are issued, so that no wait for these loads (which complete
+    // in issue order) also waits for weights
+#pragma unroll
+    for (int u = 0; u < kDcZ; ++u) {
+        const uint32_t i = (uint32_t)tid + (uint32_t)u * kDcThreads;
+        if (i < (uint32_t)P * q4) *reinterpret_cast<float4*>(&s_z[4 * i]) = hm_keep_if(zv[u], 4 * (i % q4) < I);
+    }
+    if (tid < P) s_ids[tid] = pid;
+    if (wave == 0 && lane < nact) {
+        s_act[lane] = my_act;
+        s_off[lane] = my_off;
+    }
+    __builtin_amdgcn_sched_barrier(0);  // (keeps the stores above the weight loads)
+    // the weights: four K tiles per load, no branch for the first unit
+    // (tiles past the K range re-read its last one, an idle wave reads
+    // expert 0's; both are skipped below)
+    const int tq = lane >> 4, kh = (lane >> 3) & 1, col = lane & 7;
+    v4i w[2][kDcLoads];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        if (s == 1 && !unit_on[1]) continue;
+        const int8_t* src = packed + hm_proj_offset(unit_e[s], 2, H, I) + cb * KT * 1024 +
+                            512 * kh + 128 * sl + 16 * col;
+#pragma unroll
+        for (int j = 0; j < kDcLoads; ++j)
+            w[s][j] = *reinterpret_cast<const v4i*>(src + (int64_t)(kb0 + min(4 * j + tq, max(nkb - 1, 0))) * 1024);
+    }
+    __syncthreads();
+    if (tid < P) {  // hm_combine's order: the token's pairs by ascending id
+        const int t = tid / top_k;
+        int rank = 0;
+        for (int r = 0; r < top_k; ++r) rank += s_ids[t * top_k + r] < pid;
+        s_row[t * top_k + rank] = prow & (kDcPairs - 1);
+        s_w[t * top_k + rank] = psc;
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        if (!unit_on[s]) continue;
+        const int g0 = unit_g0[s], rows = unit_rows[s];
+        for (int r = 0; r < rows; ++r) {
+            float acc = 0.0f, xs = 0.0f;
+            const float* zr = &s_z[(int64_t)(g0 + r) * I32 + 32 * (kb0 + tq) + 16 * kh];
+#pragma unroll
+            for (int j = 0; j < kDcLoads; ++j) {
+                if (4 * j + tq < nkb) {
+                    float f[16];
+                    tile_to_float(w[s][j], f);
+                    const float4* xv = reinterpret_cast<const float4*>(zr + 128 * j);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float4 v = xv[i];
+                        acc = __builtin_fmaf(v.x, f[4 * i], acc);
+                        acc = __builtin_fmaf(v.y, f[4 * i + 1], acc);
+                        acc = __builtin_fmaf(v.z, f[4 * i + 2], acc);
+                        acc = __builtin_fmaf(v.w, f[4 * i + 3], acc);
+                        xs += (v.x + v.y) + (v.z + v.w);
+                    }
+                }
+            }
+            // the eight lanes of each column: K halves, then the four tiles
+            acc += __shfl_xor(acc, 8, 64);
+            xs += __shfl_xor(xs, 8, 64);
+            acc += __shfl_xor(acc, 16, 64);
+            xs += __shfl_xor(xs, 16, 64);
+            acc += __shfl_xor(acc, 32, 64);
+            xs += __shfl_xor(xs, 32, 64);
+            if (lane < kDcCols) s_part[wave][s][r][lane] = acc;
+            if (lane == 0) s_zs[wave][s][r] = xs;
+        }
+    }
+    __syncthreads();
+    // y of every grouped row for these columns: its expert's units in K order
+    if (tid < P * kDcCols) {
+        const int g = tid / kDcCols, c = tid % kDcCols;
+        float y = 0.0f;  // no routed rows: never after a successful routing
+        if (nact > 0) {
+            int a = 0;
+            for (int j = 1; j < nact; ++j)
+                if (s_off[j] <= g) a = j;
+            const int e = s_act[a], r = (g - s_off[a]) & (kDcPairs - 1);
+            const int w0 = nact >= kDcWaves ? a % kDcWaves : a * wpe;
+            const int su = nact >= kDcWaves ? a / kDcWaves : 0;
+            float acc = 0.0f, zs = 0.0f;
+            for (int j = 0; j < wpe; ++j) {
+                acc += s_part[w0 + j][su][r][c];
+                zs += s_zs[w0 + j][su][r];
+            }
+            y = __fmul_rn(__fsub_rn(acc, __fmul_rn((float)(128 + zp[e * 3 + 2]), zs)), scale[e * 3 + 2]);
+        }
+        s_y[g][c] = y;
+        if (y_out && n0 + c < H) y_out[(int64_t)g * H + n0 + c] = y;
+    }
+    __syncthreads();
+    // the combine of hm_combine (MoERuntime.cpp:308-325) for these columns
+    if (comb) {
+        float acc = 0.0f;
+        for (int r = 0; r < top_k; ++r)
+            acc = __fadd_rn(acc, __fmul_rn(s_w[ct * top_k + r], s_y[s_row[ct * top_k + r]][cc]));
+        if (residual) acc = __fadd_rn(res, acc);
+        out[(int64_t)ct * H + n0 + cc] = acc;
     }
 }
 
 template <bool GATEUP, int CT>
 int launch_gemv(const float* x_src, const int32_t* perm_tokens, int64_t K, int64_t N,
-                const hm_layer* L, const int32_t* counts, const int32_t* offsets, int64_t slots,
+                const hm_layer* L, const int32_t* counts, int64_t slots, int64_t tokens,
                 float* out, hipStream_t s) {
     constexpr int NQ = kGvWaves / ((GATEUP ? 2 : 1) * CT);
     const int64_t nt = hm_pad32(N) / 32, kt = hm_pad32(K) / 32;
     // every wave's K range within its register tiles
     if ((kt + NQ - 1) / NQ > kGvMaxTiles) return HM_ERR_UNSUPPORTED;
     const dim3 grid((unsigned)((nt + CT - 1) / CT), (unsigned)slots);
-    const size_t lds = (size_t)kGvRows * hm_pad32(K) * sizeof(float);
+    // gate/up of a few tokens: every token's row in LDS
+    const bool all = GATEUP && CT == 1 && tokens * hm_pad32(K) <= kGvAllFloats;
+    const size_t lds = (size_t)(all ? tokens : kGvRows) * hm_pad32(K) * sizeof(float);
     // (the timer, when armed, brackets the gate/up launch)
-    HM_STAGE_LAUNCH(true, true, (gemv_kernel<GATEUP, CT>), grid, dim3(kGvThreads), lds, s, x_src,
-                    perm_tokens, K, N, L->experts, static_cast<const int8_t*>(L->packed),
-                    L->hidden, L->intermediate, L->scale, L->zero_point, counts, offsets, out);
+#define HM_GV(NG, ALL)                                                                         \
+    HM_STAGE_LAUNCH(true, true, (gemv_kernel<GATEUP, CT, NG, ALL>), grid, dim3(kGvThreads), lds, \
+                    s, x_src, perm_tokens, K, N, L->experts,                                    \
+                    static_cast<const int8_t*>(L->packed), L->hidden, L->intermediate,          \
+                    L->scale, L->zero_point, counts, tokens, out)
+#define HM_GV2(NG)                                                                             \
+    do {                                                                                       \
+        if (GATEUP && CT == 1 && all) HM_GV(NG, GATEUP && CT == 1);                             \
+        else HM_GV(NG, false);                                                                 \
+    } while (0)
+    if (L->experts <= 128) HM_GV2(2);
+    else if (L->experts <= 256) HM_GV2(4);
+    else HM_GV2(16);
+#undef HM_GV2
+#undef HM_GV
     HM_LAUNCHED();
     return HM_OK;
 }
@@ -224,25 +746,77 @@ bool hm_gemv_shape_ok(int64_t H, int64_t I) {
 // z[g, n] = silu(x_g . Wg[n]) * (x_g . Wu[n]) for every grouped row g, with
 // x_g = hidden[perm_tokens[g]]; `pairs` = T*k bounds the active experts.
 int hm_launch_gateup_gemv(const hm_layer* L, const float* hidden, const int32_t* counts,
-                          const int32_t* offsets, const int32_t* perm_tokens, int64_t pairs,
-                          float* z, hipStream_t s) {
+                          const int32_t* perm_tokens, int64_t tokens, int64_t pairs, float* z,
+                          hipStream_t s) {
     if (L->experts > 1024) return HM_ERR_UNSUPPORTED;
     const int64_t slots = pairs < L->experts ? pairs : L->experts;
-    return launch_gemv<true, 1>(hidden, perm_tokens, L->hidden, L->intermediate, L, counts,
-                                offsets, slots, z, s);
+    const int64_t K = L->hidden, N = L->intermediate, KT = hm_pad32(K) / 32;
+    if (tokens * hm_pad32(K) <= kGvAllFloats && KT <= 32 * kGsQ) {
+        // a few tokens: every row in LDS, 8-column slices
+        const dim3 grid((unsigned)((N + 7) / 8), (unsigned)slots);
+        const size_t lds = (size_t)tokens * hm_pad32(K) * sizeof(float);
+        const int lj = (int)((KT + kGsQ - 1) / kGsQ + 3) / 4;  // loads per wave
+#define HM_GS(NG, LJ)                                                                          \
+    HM_STAGE_LAUNCH(true, true, (gateup_slice_kernel<NG, LJ>), grid, dim3(kGvThreads), lds, s,   \
+                    hidden, perm_tokens, K, N, L->experts,                                      \
+                    static_cast<const int8_t*>(L->packed), L->scale, L->zero_point, counts,     \
+                    (int)tokens, z)
+#define HM_GS2(NG)                                                                             \
+    do {                                                                                       \
+        if (lj <= 1) HM_GS(NG, 1);                                                             \
+        else if (lj <= 2) HM_GS(NG, 2);                                                        \
+        else if (lj <= 4) HM_GS(NG, 4);                                                        \
+        else HM_GS(NG, 8);                                                                     \
+    } while (0)
+        if (L->experts <= 128) HM_GS2(2);
+        else if (L->experts <= 256) HM_GS2(4);
+        else HM_GS2(16);
+#undef HM_GS2
+#undef HM_GS
+        HM_LAUNCHED();
+        return HM_OK;
+    }
+    return launch_gemv<true, 1>(hidden, perm_tokens, K, N, L, counts, slots, tokens, z, s);
+}
+
+// The decode down projection fused with the combine (P = T * k <= 16 pairs,
+// I <= 768): y_out (optional) receives the expert outputs, out the block's.
+bool hm_gemv_combine_ok(int64_t tokens, int32_t top_k, int64_t H, int64_t I) {
+    return tokens * top_k <= kDcPairs && hm_pad32(I) / 32 <= kDcMaxTiles && I % 16 == 0 &&
+           H % kDcCols == 0;
+}
+
+int hm_launch_down_combine_gemv(const hm_layer* L, const float* z, const int32_t* counts,
+                                const uint32_t* ids, const int32_t* slots, const float* scores,
+                                const float* residual, int64_t tokens, int32_t top_k,
+                                float* y_out, float* out, hipStream_t s) {
+    if (!hm_gemv_combine_ok(tokens, top_k, L->hidden, L->intermediate) || L->experts > 1024)
+        return HM_ERR_UNSUPPORTED;
+    const size_t lds = (size_t)tokens * top_k * hm_pad32(L->intermediate) * sizeof(float);
+#define HM_DC(NG)                                                                            \
+    hipLaunchKernelGGL(gemv_down_combine_kernel<NG>, dim3((unsigned)(L->hidden / kDcCols)),  \
+                       dim3(kDcThreads), lds, s, z, L->intermediate, L->hidden, L->experts,  \
+                       static_cast<const int8_t*>(L->packed), L->scale, L->zero_point,       \
+                       counts, ids, slots, scores, residual, (int)tokens, top_k, y_out, out)
+    if (L->experts <= 128) HM_DC(2);
+    else if (L->experts <= 256) HM_DC(4);
+    else HM_DC(16);
+#undef HM_DC
+    HM_LAUNCHED();
+    return HM_OK;
 }
 
 // y[g, n] = z_g . Wd[n] for every grouped row g.
 int hm_launch_down_gemv(const hm_layer* L, const float* z, const int32_t* counts,
-                        const int32_t* offsets, int64_t pairs, float* y, hipStream_t s) {
+                        int64_t pairs, float* y, hipStream_t s) {
     if (L->experts > 1024) return HM_ERR_UNSUPPORTED;
     const int64_t slots = pairs < L->experts ? pairs : L->experts;
     // few experts: one column tile per workgroup (more workgroups in
     // flight); many: four (a workgroup's setup spread over four times the
     // weights)
     if (slots >= 32 && hm_pad32(L->intermediate) / 32 <= 2 * kGvMaxTiles)
-        return launch_gemv<false, 4>(z, nullptr, L->intermediate, L->hidden, L, counts, offsets,
-                                     slots, y, s);
-    return launch_gemv<false, 1>(z, nullptr, L->intermediate, L->hidden, L, counts, offsets, slots,
-                                 y, s);
+        return launch_gemv<false, 4>(z, nullptr, L->intermediate, L->hidden, L, counts, slots, 0,
+                                     y, s);
+    return launch_gemv<false, 1>(z, nullptr, L->intermediate, L->hidden, L, counts, slots, 0, y,
+                                 s);
 }
