@@ -5,6 +5,9 @@ Workloads (hmoe.synth.CONFIGS):
   C4     (default) INT8 Qwen3-30B-A3B-shape block, 4096-token prefill,
          128 experts, top-8, Zipf(1.1)-skewed routing
   C3-1, C3-4, C3-16   decode shapes (1/4/16 tokens)
+  M256   (not a BASELINE config) 256-token INT8 prefill of the C4 layer:
+         mostly groups of at most 32 rows (with --split-k: the bounded
+         split-K GEMM for those)
   C1, C2 FP32 64-expert blocks
 
 One step = one MoE-block call (route -> permute -> INT8 SwiGLU experts:
@@ -56,6 +59,9 @@ def parse():
     ap.add_argument("--graph", action="store_true",
                     help="replay one captured HIP graph of the block per step instead of "
                          "launching every step from the host")
+    ap.add_argument("--split-k", action="store_true",
+                    help="INT8 prefill: groups of at most 32 rows take the bounded split-K GEMM "
+                         "(HM_EXEC_SPLIT_K) instead of the tile GEMMs' partial tiles")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 --pmc child runs that measure the dominant "
                          "kernel's HBM bytes per launch (roofline.traffic = null)")
@@ -227,6 +233,8 @@ def main():
     d_w = torch.from_numpy(w).cuda()
     layer = DeviceExpertLayer(payload, scale, zp, H, I)
     block = MoEBlock(layer, k, limbs_x=args.limbs_x, limbs_z=args.limbs_z)
+    if args.split_k:
+        block.flags |= capi.HM_EXEC_SPLIT_K
     torch.cuda.synchronize()
     log(f"[bench] setup {time.time() - t0:.1f}s", q)
 

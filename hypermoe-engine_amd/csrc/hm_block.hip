@@ -16,11 +16,12 @@ int hm_launch_gateup_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int
                         const float* xscale, const int32_t* xdsum, int64_t tokens,
                         const int32_t* counts, const int32_t* offsets,
                         const int32_t* perm_tokens, int64_t R, int8_t* zdig, float* zscale,
-                        int32_t* zdsum, float* gu, bool force_generic, hipStream_t stream);
+                        int32_t* zdsum, float* gu, bool force_generic, bool split_k,
+                        hipStream_t stream);
 int hm_launch_down_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int32_t* counts,
                       const int32_t* offsets, int64_t R, const int8_t* zdig,
                       const float* zscale, const int32_t* zdsum, float* y,
-                      bool force_generic, hipStream_t stream);
+                      bool force_generic, bool split_k, hipStream_t stream);
 int hm_launch_gateup_f32(const hm_layer* layer, const float* hidden, const int32_t* counts,
                          const int32_t* offsets, const int32_t* perm_tokens, int64_t R,
                          float* zf, hipStream_t stream);
@@ -175,6 +176,7 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
     }
     if (tokens > INT_MAX / top_k) return HM_ERR_OVERFLOW;
     const bool generic = (route_flags & HM_EXEC_GENERIC) != 0;
+    const bool split_k = (route_flags & HM_EXEC_SPLIT_K) != 0;
     void* base = reinterpret_cast<void*>(
         (reinterpret_cast<uintptr_t>(workspace) + kAlign - 1) & ~(uintptr_t)(kAlign - 1));
     const size_t need =
@@ -276,11 +278,11 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
         rc = gate_up([&] {
             return hm_launch_gateup_i8(layer, limbs_x, limbs_z, p.xdig, p.xscale, p.xdsum,
                                        tokens, counts, p.offsets, p.perm_tokens, P, p.zdig,
-                                       p.zscale, p.zdsum, p.gu, generic, s);
+                                       p.zscale, p.zdsum, p.gu, generic, split_k, s);
         });
         if (rc) return rc;
         rc = hm_launch_down_i8(layer, limbs_x, limbs_z, counts, p.offsets, P, p.zdig,
-                               p.zscale, p.zdsum, p.y, generic, s);
+                               p.zscale, p.zdsum, p.y, generic, split_k, s);
     } else {
         rc = gate_up([&] {
             return hm_launch_gateup_f32(layer, hidden, counts, p.offsets, p.perm_tokens, P,

@@ -629,11 +629,11 @@ bool hm_mfma_down_ok(int64_t H, int64_t I, int64_t E, int32_t limbs);
 int hm_launch_gateup_i8_mfma(const hm_layer* layer, int32_t limbs, const int8_t* xdig,
                              const float* xscale, const int32_t* xdsum, int64_t tokens,
                              const int32_t* counts, const int32_t* offsets,
-                             const int32_t* perm_tokens, int64_t R, float* gu,
+                             const int32_t* perm_tokens, int64_t R, float* gu, bool split_k,
                              hipStream_t stream);
 int hm_launch_down_i8_mfma(const hm_layer* layer, int32_t limbs, const int32_t* counts,
                            const int32_t* offsets, int64_t R, const int8_t* zdig,
-                           const float* zscale, const int32_t* zdsum, float* y,
+                           const float* zscale, const int32_t* zdsum, float* y, bool split_k,
                            hipStream_t stream);
 
 int64_t hm_max_tiles(int64_t pairs, int64_t experts, int64_t tile_m) {
@@ -659,7 +659,8 @@ int hm_launch_gateup_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int
                         const float* xscale, const int32_t* xdsum, int64_t tokens,
                         const int32_t* counts, const int32_t* offsets,
                         const int32_t* perm_tokens, int64_t R, int8_t* zdig, float* zscale,
-                        int32_t* zdsum, float* gu, bool force_generic, hipStream_t stream) {
+                        int32_t* zdsum, float* gu, bool force_generic, bool split_k,
+                        hipStream_t stream) {
     const int64_t H = layer->hidden, I = layer->intermediate, E = layer->experts;
     const int8_t* packed = static_cast<const int8_t*>(layer->packed);
     if (R == 0) return HM_OK;
@@ -667,7 +668,7 @@ int hm_launch_gateup_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int
     // buffer offset) rules them out
     int rc = hm_use_mfma_gateup(layer, lx, force_generic)
                  ? hm_launch_gateup_i8_mfma(layer, lx, xdig, xscale, xdsum, tokens, counts,
-                                            offsets, perm_tokens, R, gu, stream)
+                                            offsets, perm_tokens, R, gu, split_k, stream)
                  : HM_ERR_UNSUPPORTED;
     if (rc == HM_ERR_UNSUPPORTED) {
         rc = HM_OK;
@@ -693,13 +694,13 @@ int hm_launch_gateup_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int
 int hm_launch_down_i8(const hm_layer* layer, int32_t lx, int32_t lz, const int32_t* counts,
                       const int32_t* offsets, int64_t R, const int8_t* zdig,
                       const float* zscale, const int32_t* zdsum, float* y,
-                      bool force_generic, hipStream_t stream) {
+                      bool force_generic, bool split_k, hipStream_t stream) {
     const int64_t H = layer->hidden, I = layer->intermediate, E = layer->experts;
     const int8_t* packed = static_cast<const int8_t*>(layer->packed);
     if (R == 0) return HM_OK;
     if (hm_use_mfma_down(layer, lz, force_generic)) {
         const int rc = hm_launch_down_i8_mfma(layer, lz, counts, offsets, R, zdig, zscale, zdsum,
-                                              y, stream);
+                                              y, split_k, stream);
         if (rc != HM_ERR_UNSUPPORTED) return rc;
     }
     const unsigned g_dn = (unsigned)((R * H + kBlock - 1) / kBlock);

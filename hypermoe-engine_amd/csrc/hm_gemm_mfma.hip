@@ -169,12 +169,15 @@ __device__ __forceinline__ int a_chunk_pos(int r, int c) { return c ^ ((r >> 1) 
 
 // Exclusive prefix of the m-tiles of every expert (ceil(count / bm)) into
 // prefix[0..E], prefix[E] = total.  One full wave.
-__device__ __forceinline__ void tile_prefix(const int32_t* cnt, int E, int bm, int32_t* prefix) {
+// Experts with at most `skinny` rows get no tiles (skinny_split_kernel
+// takes them).
+__device__ __forceinline__ void tile_prefix(const int32_t* cnt, int E, int bm, int skinny,
+                                            int32_t* prefix) {
     const int lane = threadIdx.x & (HM_WAVE - 1);
     int base = 0;
     for (int c0 = 0; c0 < E; c0 += HM_WAVE) {
         const int e = c0 + lane;
-        const int n = e < E ? (cnt[e] + bm - 1) / bm : 0;
+        const int n = e < E && cnt[e] > skinny ? (cnt[e] + bm - 1) / bm : 0;
         int incl = n;
 #pragma unroll
         for (int sft = 1; sft < HM_WAVE; sft <<= 1) {
@@ -230,7 +233,7 @@ __global__ __launch_bounds__(kThreads) void limb_gemm_kernel(
     const int32_t* __restrict__ adsum, int arows, int K, int N, int H, int I, int experts,
     const int8_t* __restrict__ packed, const float* __restrict__ scale,
     const int32_t* __restrict__ zp, const int32_t* __restrict__ counts,
-    const int32_t* __restrict__ offsets, float* __restrict__ out) {
+    const int32_t* __restrict__ offsets, int skinny, float* __restrict__ out) {
     using T = Tile<L, DB>;
     constexpr int RF = T::RF, BM = T::BM, BN = T::BN, NCF = T::NCF, APW = T::APW,
                   BPW = T::BPW, NV = T::NV, ASTAGE = T::ASTAGE;
@@ -253,7 +256,7 @@ __global__ __launch_bounds__(kThreads) void limb_gemm_kernel(
         s_za[e] = zp[3 * e + 2];
     }
     __syncthreads();
-    if (wave == 0) tile_prefix(s_cnt, E, BM, s_prefix);
+    if (wave == 0) tile_prefix(s_cnt, E, BM, skinny, s_prefix);
     __syncthreads();
     const int nbn = N / BN;
     const TileRange tr = tile_range(s_prefix[E] * nbn);
@@ -530,6 +533,203 @@ __global__ __launch_bounds__(kThreads) void limb_gemm_kernel(
     vm_wait<0>();
 }
 
+// ===========================================================================
+// Skinny groups: bounded split-K.  An expert with at most kSkinnyRows = 32
+// grouped rows (a cold expert; most experts of a mid-size batch) would
+// fill a tile of BM rows mostly with padding, and the tile still streams
+// every row of its A stages.  Such experts skip the tile kernels
+// (tile_prefix) and come here: one workgroup per (expert, kSkCB column
+// blocks of 32); its A rows (all K, the L digit planes) go to LDS once, in
+// MFMA operand order, and its 8 waves are kSkCB column blocks x kSkP K
+// parts.  Each wave streams its block's weight tiles over its K part and
+// runs v_mfma_i32_32x32x32_i8 on its own accumulators; the parts' int32
+// limb partials meet in LDS in part order (integer addition: exact, so the
+// partials, and hence the epilogue's floats, equal the tile kernels' bit
+// for bit).  K is split into a bounded number of parts as the reference's
+// split-K does (P = min(8, ceil(K/512)), Int8GemmPlan.cpp:29-53, reduced in
+// a fixed order, CudaKernels.cu:53-107), here kSkP = 2 within a workgroup.
+//   GU    gate and up (NP = 2): A = the X digit planes of the rows' tokens
+//         (perm_tokens), out = gu [R x 2I];
+//   down  (NP = 1): A = the Z digit planes of the grouped rows, out = y.
+// LDS: the A rows, L x 32 x K bytes, reused for the partials (skinny_lds).
+// ===========================================================================
+constexpr int kSkinnyRows = 32;   // one 32-row fragment
+constexpr int kSkWaves = 8;
+constexpr int kSkThreads = 64 * kSkWaves;
+constexpr int kSkP = 2;           // K parts
+constexpr int kSkCB = kSkWaves / kSkP;  // column blocks per workgroup
+constexpr int kSkLds = 131072;    // A bytes in LDS: L * 32 * K
+constexpr int kSkDepth = 4;       // K steps of weights in flight per wave
+
+template <int L, bool GU>
+__global__ __launch_bounds__(kSkThreads) void skinny_split_kernel(
+    const int8_t* __restrict__ adig, const float* __restrict__ ascale,
+    const int32_t* __restrict__ adsum, int arows, const int32_t* __restrict__ perm_tokens,
+    int K, int N, int H, int I, const int8_t* __restrict__ packed,
+    const float* __restrict__ scale, const int32_t* __restrict__ zp,
+    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
+    float* __restrict__ out) {
+    constexpr int NP = GU ? 2 : 1;
+    extern __shared__ __attribute__((aligned(1024))) int8_t s_a[];   // [L][KT][32 rows][32 B]
+    __shared__ int32_t s_arow[32];
+    const int e = blockIdx.y;
+    const int nrows = counts[e];
+    if (nrows == 0 || nrows > kSkinnyRows) return;          // (uniform)
+    const int g0 = offsets[e];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int KT = K / 32;
+    if (tid < 32) {
+        const int g = g0 + min(tid, nrows - 1);  // rows past the group repeat its last
+        s_arow[tid] = GU ? perm_tokens[g] : g;
+    }
+    __syncthreads();
+    // the A rows into LDS: one wave-wide 16-byte load per (plane, K step):
+    // lane -> row lane/2, half lane%2 (32 rows x 32 bytes, MFMA order)
+    {
+        const int arow = s_arow[lane >> 1];
+        for (int q = wave; q < L * KT; q += kSkWaves) {
+            const int l = q / KT, kt = q - l * KT;
+            dma16(adig + ((int64_t)l * arows + arow) * K + 32 * kt + 16 * (lane & 1),
+                  s_a + 1024 * q);
+        }
+    }
+    // this wave's column block and K part
+    const int cbl = wave % kSkCB, part = wave / kSkCB;
+    const int cb = blockIdx.x * kSkCB + cbl;                // output columns 32 cb .. +31
+    const int kt0 = part * KT / kSkP, kt1 = (part + 1) * KT / kSkP;
+    const bool live = 32 * cb < N;                          // (uniform per wave)
+    const int8_t* bsrc[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+        bsrc[p] = packed + hm_proj_offset(e, GU ? p : 2, H, I) +
+                  (int64_t)min(cb, N / 32 - 1) * KT * 1024 + 16 * lane;
+    // weights kSkDepth steps ahead (a step past the part re-reads its last)
+    v4i fb[kSkDepth][NP];
+#pragma unroll
+    for (int d = 0; d < kSkDepth; ++d)
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+            fb[d][p] = *reinterpret_cast<const v4i*>(bsrc[p] + (int64_t)min(kt0 + d, kt1 - 1) * 1024);
+    vm_wait<0>();   // this wave's A loads (the first weights land about as soon)
+    lds_barrier();  // every wave's
+    v16i acc[L][NP];
+#pragma unroll
+    for (int l = 0; l < L; ++l)
+#pragma unroll
+        for (int p = 0; p < NP; ++p) acc[l][p] = v16i{};
+    const int aoff = 32 * (lane & 31) + 16 * (lane >> 5);
+    for (int kt = kt0; kt < kt1; kt += kSkDepth) {
+#pragma unroll
+        for (int d = 0; d < kSkDepth; ++d) {
+            if (kt + d < kt1) {
+                v4i fa[L];
+#pragma unroll
+                for (int l = 0; l < L; ++l)
+                    fa[l] = *reinterpret_cast<const v4i*>(s_a + 1024 * (l * KT + kt + d) + aoff);
+#pragma unroll
+                for (int l = 0; l < L; ++l)
+#pragma unroll
+                    for (int p = 0; p < NP; ++p) acc[l][p] = mfma32(fa[l], fb[d][p], acc[l][p]);
+            }
+#pragma unroll
+            for (int p = 0; p < NP; ++p)
+                fb[d][p] = *reinterpret_cast<const v4i*>(
+                    bsrc[p] + (int64_t)min(kt + d + kSkDepth, kt1 - 1) * 1024);
+        }
+    }
+    // the parts' partials meet in LDS (the A copy is no longer read)
+    __syncthreads();
+    int32_t* s_p = reinterpret_cast<int32_t*>(s_a);          // [part-1][cbl][L][NP][16][64]
+    constexpr int PW = L * NP * 16 * HM_WAVE;                // ints per wave
+    if (part > 0) {
+#pragma unroll
+        for (int l = 0; l < L; ++l)
+#pragma unroll
+            for (int p = 0; p < NP; ++p)
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+                    s_p[((part - 1) * kSkCB + cbl) * PW + ((l * NP + p) * 16 + v) * HM_WAVE + lane] = acc[l][p][v];
+    }
+    __syncthreads();
+    if (part > 0 || !live) return;
+#pragma unroll
+    for (int q = 1; q < kSkP; ++q)
+#pragma unroll
+        for (int l = 0; l < L; ++l)
+#pragma unroll
+            for (int p = 0; p < NP; ++p)
+#pragma unroll
+                for (int v = 0; v < 16; ++v)
+                    acc[l][p][v] += s_p[((q - 1) * kSkCB + cbl) * PW + ((l * NP + p) * 16 + v) * HM_WAVE + lane];
+    // epilogue, as the tile kernels': result register v of lane m is row
+    // 8 (v/4) + 4 (m/32) + v%4, column m%32
+    const int zpa = zp[3 * e + (GU ? 0 : 2)], zpb = GU ? zp[3 * e + 1] : 0;
+    const float sa = scale[3 * e + (GU ? 0 : 2)], sb = GU ? scale[3 * e + 1] : 0.0f;
+    const int64_t n = 32 * (int64_t)cb + (lane & 31);
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const int row = 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        if (row >= nrows) continue;
+        const int arow = s_arow[row];
+        const float asc = ascale[arow];
+        int pa[L], pb[L];
+#pragma unroll
+        for (int l = 0; l < L; ++l) {
+            pa[l] = acc[l][0][v];
+            pb[l] = acc[l][NP - 1][v];
+        }
+        if (zpa != 0 || zpb != 0) {
+#pragma unroll
+            for (int l = 0; l < L; ++l) {
+                const int ds = adsum[(int64_t)l * arows + arow];
+                pa[l] -= zpa * ds;
+                pb[l] -= zpb * ds;
+            }
+        }
+        if (GU) {
+            const float fg = __fmul_rn(asc, sa), fu = __fmul_rn(asc, sb);
+            float* grow = out + (int64_t)(g0 + row) * (2 * (int64_t)I) + n;
+            grow[0] = __fmul_rn(hm_recombine(pa, L), fg);
+            grow[I] = __fmul_rn(hm_recombine(pb, L), fu);
+        } else {
+            out[(int64_t)(g0 + row) * N + n] = __fmul_rn(hm_recombine(pa, L), __fmul_rn(asc, sa));
+        }
+    }
+}
+
+// Dynamic LDS of the skinny kernel: the A rows, or the K parts' partials
+// (parts 1 .. kSkP-1, 16 ints per lane per accumulator) if larger.
+size_t skinny_lds(int64_t K, int32_t limbs, bool gu) {
+    const size_t a = (size_t)limbs * 32 * K;
+    const size_t p = (size_t)(kSkP - 1) * kSkCB * limbs * (gu ? 2 : 1) * 16 * HM_WAVE * sizeof(int32_t);
+    return a > p ? a : p;
+}
+
+// Whether the skinny kernel takes this projection: its LDS fits and K
+// splits into whole K steps.
+bool skinny_ok(int64_t K, int64_t N, int32_t limbs, bool gu) {
+    return skinny_lds(K, limbs, gu) <= (size_t)kSkLds && K % 32 == 0 && K / 32 >= kSkP &&
+           N % 32 == 0;
+}
+
+template <int L, bool GU>
+int launch_skinny(const hm_layer* layer, const int8_t* adig, const float* ascale,
+                  const int32_t* adsum, int64_t arows, const int32_t* perm_tokens,
+                  const int32_t* counts, const int32_t* offsets, float* out, hipStream_t stream,
+                  bool timed_first) {
+    const int64_t H = layer->hidden, I = layer->intermediate;
+    const int64_t K = GU ? H : I, N = GU ? I : H;
+    const dim3 grid((unsigned)((N / 32 + kSkCB - 1) / kSkCB), (unsigned)layer->experts);
+    const size_t lds = skinny_lds(K, L, GU);
+    HM_STAGE_LAUNCH(timed_first, false, (skinny_split_kernel<L, GU>), grid, dim3(kSkThreads), lds,
+                    stream, adig, ascale, adsum, (int)arows, perm_tokens, (int)K, (int)N, (int)H,
+                    (int)I, static_cast<const int8_t*>(layer->packed), layer->scale,
+                    layer->zero_point, counts, offsets, out);
+    HM_LAUNCHED();
+    return HM_OK;
+}
+
 int persistent_grid() {
     static int cached[64];
     int dev = 0;
@@ -558,7 +758,7 @@ bool shape_ok(int64_t K, int64_t N, int64_t E, int32_t limbs) {
 
 template <int L, int DB>
 int launch(const hm_layer* layer, const int8_t* adig, const float* ascale, const int32_t* adsum,
-           int64_t arows, const int32_t* counts, const int32_t* offsets, float* out,
+           int64_t arows, const int32_t* counts, const int32_t* offsets, int skinny, float* out,
            hipStream_t stream) {
     const int64_t H = layer->hidden, I = layer->intermediate;
     const int64_t K = I, N = H;
@@ -568,7 +768,7 @@ int launch(const hm_layer* layer, const int8_t* adig, const float* ascale, const
     hipLaunchKernelGGL((limb_gemm_kernel<L, DB>), dim3((unsigned)persistent_grid()), dim3(kThreads), 0,
                        stream, adig, ascale, adsum, (int)arows, (int)K, (int)N, (int)H, (int)I,
                        (int)layer->experts, static_cast<const int8_t*>(layer->packed), layer->scale,
-                       layer->zero_point, counts, offsets, out);
+                       layer->zero_point, counts, offsets, skinny, out);
     HM_LAUNCHED();
     return HM_OK;
 }
@@ -576,11 +776,20 @@ int launch(const hm_layer* layer, const int8_t* adig, const float* ascale, const
 template <int L>
 int launch_l(const hm_layer* layer, const int8_t* adig, const float* ascale,
              const int32_t* adsum, int64_t arows, const int32_t* counts, const int32_t* offsets,
-             float* out, hipStream_t stream) {
+             float* out, bool split_k, hipStream_t stream) {
+    if (ring_depth(layer->intermediate / kKS) == 0) return HM_ERR_UNSUPPORTED;
+    // skinny groups (split K, when asked for), then the tiles of the others
+    const bool sk = split_k && skinny_ok(layer->intermediate, layer->hidden, L, false);
+    if (sk) {
+        const int rc = launch_skinny<L, false>(layer, adig, ascale, adsum, arows, nullptr, counts,
+                                               offsets, out, stream, false);
+        if (rc) return rc;
+    }
+    const int skinny = sk ? kSkinnyRows : 0;
     switch (ring_depth(layer->intermediate / kKS)) {
-    case 4: return launch<L, 4>(layer, adig, ascale, adsum, arows, counts, offsets, out, stream);
-    case 3: return launch<L, 3>(layer, adig, ascale, adsum, arows, counts, offsets, out, stream);
-    case 2: return launch<L, 2>(layer, adig, ascale, adsum, arows, counts, offsets, out, stream);
+    case 4: return launch<L, 4>(layer, adig, ascale, adsum, arows, counts, offsets, skinny, out, stream);
+    case 3: return launch<L, 3>(layer, adig, ascale, adsum, arows, counts, offsets, skinny, out, stream);
+    case 2: return launch<L, 2>(layer, adig, ascale, adsum, arows, counts, offsets, skinny, out, stream);
     default: return HM_ERR_UNSUPPORTED;
     }
 }
@@ -641,7 +850,7 @@ __global__ __launch_bounds__(kGuThreads) void gateup_ring_kernel(
     const int32_t* __restrict__ xdsum, int tokens, int H, int I, int experts,
     const int8_t* __restrict__ packed, const float* __restrict__ scale,
     const int32_t* __restrict__ zp, const int32_t* __restrict__ counts,
-    const int32_t* __restrict__ offsets, const int32_t* __restrict__ perm_tokens,
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ perm_tokens, int skinny,
     float* __restrict__ gu) {
     using T = GateUpTile<L>;
     constexpr int BM = T::BM, NA = T::NA, NL = T::NL, LPW = T::LPW, WR = T::WR, WCP = T::WCP,
@@ -670,7 +879,7 @@ __global__ __launch_bounds__(kGuThreads) void gateup_ring_kernel(
         s_zu[e] = zp[3 * e + 1];
     }
     __syncthreads();
-    if (wave == 0) tile_prefix(s_cnt, E, BM, s_prefix);
+    if (wave == 0) tile_prefix(s_cnt, E, BM, skinny, s_prefix);
     __syncthreads();
     const int nbn = I / kGuN;
     const TileRange tr = tile_range(s_prefix[E] * nbn);
@@ -966,13 +1175,21 @@ bool gateup_shape_ok(int64_t H, int64_t I, int64_t E, int32_t limbs) {
 template <int L>
 int launch_gateup(const hm_layer* layer, const int8_t* xdig, const float* xscale,
                   const int32_t* xdsum, int64_t tokens, const int32_t* counts,
-                  const int32_t* offsets, const int32_t* perm_tokens, float* gu,
+                  const int32_t* offsets, const int32_t* perm_tokens, float* gu, bool split_k,
                   hipStream_t stream) {
-    HM_STAGE_LAUNCH(true, false, gateup_ring_kernel<L>, dim3((unsigned)persistent_grid()),
+    // skinny groups (split K, when asked for; its start opens an armed stage
+    // timer), then the tiles of the others
+    const bool sk = split_k && skinny_ok(layer->hidden, layer->intermediate, L, true);
+    if (sk) {
+        const int rc = launch_skinny<L, true>(layer, xdig, xscale, xdsum, tokens, perm_tokens,
+                                              counts, offsets, gu, stream, true);
+        if (rc) return rc;
+    }
+    HM_STAGE_LAUNCH(!sk, false, gateup_ring_kernel<L>, dim3((unsigned)persistent_grid()),
                     dim3(kGuThreads), 0, stream, xdig, xscale, xdsum, (int)tokens,
                     (int)layer->hidden, (int)layer->intermediate, (int)layer->experts,
                     static_cast<const int8_t*>(layer->packed), layer->scale, layer->zero_point,
-                    counts, offsets, perm_tokens, gu);
+                    counts, offsets, perm_tokens, sk ? kSkinnyRows : 0, gu);
     HM_LAUNCHED();
     return HM_OK;
 }
@@ -995,13 +1212,13 @@ bool hm_mfma_down_ok(int64_t H, int64_t I, int64_t E, int32_t limbs) {
 int hm_launch_gateup_i8_mfma(const hm_layer* layer, int32_t limbs, const int8_t* xdig,
                              const float* xscale, const int32_t* xdsum, int64_t tokens,
                              const int32_t* counts, const int32_t* offsets,
-                             const int32_t* perm_tokens, int64_t R, float* gu,
+                             const int32_t* perm_tokens, int64_t R, float* gu, bool split_k,
                              hipStream_t stream) {
     if (tokens > INT_MAX || R > INT_MAX) return HM_ERR_OVERFLOW;
     switch (limbs) {
-    case 1: return launch_gateup<1>(layer, xdig, xscale, xdsum, tokens, counts, offsets, perm_tokens, gu, stream);
-    case 2: return launch_gateup<2>(layer, xdig, xscale, xdsum, tokens, counts, offsets, perm_tokens, gu, stream);
-    case 3: return launch_gateup<3>(layer, xdig, xscale, xdsum, tokens, counts, offsets, perm_tokens, gu, stream);
+    case 1: return launch_gateup<1>(layer, xdig, xscale, xdsum, tokens, counts, offsets, perm_tokens, gu, split_k, stream);
+    case 2: return launch_gateup<2>(layer, xdig, xscale, xdsum, tokens, counts, offsets, perm_tokens, gu, split_k, stream);
+    case 3: return launch_gateup<3>(layer, xdig, xscale, xdsum, tokens, counts, offsets, perm_tokens, gu, split_k, stream);
     default: return HM_ERR_INVALID;
     }
 }
@@ -1009,13 +1226,13 @@ int hm_launch_gateup_i8_mfma(const hm_layer* layer, int32_t limbs, const int8_t*
 // y [R x H] from the Z digit planes [L][R][I] (one scale per row).
 int hm_launch_down_i8_mfma(const hm_layer* layer, int32_t limbs, const int32_t* counts,
                            const int32_t* offsets, int64_t R, const int8_t* zdig,
-                           const float* zscale, const int32_t* zdsum, float* y,
+                           const float* zscale, const int32_t* zdsum, float* y, bool split_k,
                            hipStream_t stream) {
     if (R > INT_MAX) return HM_ERR_OVERFLOW;
     switch (limbs) {
-    case 1: return launch_l<1>(layer, zdig, zscale, zdsum, R, counts, offsets, y, stream);
-    case 2: return launch_l<2>(layer, zdig, zscale, zdsum, R, counts, offsets, y, stream);
-    case 3: return launch_l<3>(layer, zdig, zscale, zdsum, R, counts, offsets, y, stream);
+    case 1: return launch_l<1>(layer, zdig, zscale, zdsum, R, counts, offsets, y, split_k, stream);
+    case 2: return launch_l<2>(layer, zdig, zscale, zdsum, R, counts, offsets, y, split_k, stream);
+    case 3: return launch_l<3>(layer, zdig, zscale, zdsum, R, counts, offsets, y, split_k, stream);
     default: return HM_ERR_INVALID;
     }
 }

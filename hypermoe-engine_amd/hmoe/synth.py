@@ -142,6 +142,9 @@ CONFIGS = {
     "C3-4": Config("C3-4", tokens=4),
     "C3-16": Config("C3-16", tokens=16),
     "C4": Config("C4", tokens=4096, skew=True),
+    # not a BASELINE config: a mid-size INT8 prefill (16 rows per expert on
+    # average), where most groups are skinny (the split-K comparison)
+    "M256": Config("M256", tokens=256, skew=True),
     "C5": Config("C5", tokens=2048, layers=48),
 }
 

@@ -75,6 +75,12 @@ typedef enum hm_status {
  * certifying the parallel sums (the results are identical; the flag
  * exercises the fallback). */
 #define HM_EXEC_ROUTE_SEQUENTIAL 0x400u
+/* Execution flag for hm_moe_block_forward: INT8 prefill experts with at most
+ * 32 grouped rows take the bounded split-K GEMM (K split over a workgroup's
+ * waves, exact integer partials; the same bits as without it) instead of
+ * the tile GEMMs' partial tiles.  Off by default: on this GPU it is slower
+ * at every batch size measured (the tiles stream the same weights faster). */
+#define HM_EXEC_SPLIT_K 0x800u
 
 /* Expert weight dtypes (src/tensor/DType.hpp:9-14 numbering). */
 #define HM_DTYPE_FP32 0

@@ -189,6 +189,35 @@ def test_block_int8_bitexact_vs_limb_oracle(dev, T, H, E, I, k, LX, LZ):
         assert nw < 3e-4
 
 
+@pytest.mark.parametrize("T,H,E,I,k,LX,LZ,skew", [
+    (400, 1024, 16, 512, 4, 2, 3, True), (256, 2048, 128, 768, 8, 3, 3, False),
+    (256, 512, 32, 256, 8, 1, 2, True)])
+def test_block_skinny_split_k(dev, T, H, E, I, k, LX, LZ, skew):
+    """With HM_EXEC_SPLIT_K, experts of at most 32 grouped rows run the
+    bounded split-K kernel (K split over the workgroup's waves, int32 limb
+    partials summed exactly), the others the tile kernels, in one block: a
+    skewed batch with both kinds, a mid-size batch where most experts are
+    skinny, one to three digit planes.  Bit-exact against the limb oracle,
+    against the generic kernels and against the tile kernels alone."""
+    print(f"[gpu] skinny split-K T={T} H={H} E={E} I={I} k={k} limbs=({LX}, {LZ})", flush=True)
+    payload, scale, zp, h, w = _layer_inputs(41 + T, T, H, E, I, True, skew=skew)
+    block = MoEBlock(DeviceExpertLayer(payload, scale, zp, H, I), k, limbs_x=LX, limbs_z=LZ)
+    res = block.execute_batch(dev.to(h), dev.to(w),
+                              exec_flags=capi.HM_EXEC_LIMBS | capi.HM_EXEC_SPLIT_K)
+    counts = np.asarray(res.counts)
+    assert ((counts > 0) & (counts <= 32)).any(), "no skinny group in this batch"
+    if skew:
+        assert (counts > 32).any(), "no tiled group in this batch"
+    out = dev.host(res.output)
+    lout, lids, _ = O.moe_block_limbs(payload, scale, zp, h, w, k, I, LX, LZ)
+    assert_bitexact(res.ids, lids, "ids")
+    assert_bitexact(out, lout, "split-K block vs limb oracle")
+    gen = block.execute_batch(dev.to(h), dev.to(w), exec_flags=capi.HM_EXEC_GENERIC)
+    assert_bitexact(dev.host(gen.output), out, "split-K kernels vs generic kernels")
+    tiles = block.execute_batch(dev.to(h), dev.to(w), exec_flags=capi.HM_EXEC_LIMBS)
+    assert_bitexact(dev.host(tiles.output), out, "split-K kernels vs tile kernels")
+
+
 def test_block_int8_nonzero_zero_points(dev):
     """Zero points other than 0 (validateParameters allows [-128, 127])."""
     T, H, E, I, k = 24, 2048, 8, 768, 2

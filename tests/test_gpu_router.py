@@ -100,11 +100,13 @@ def test_router_reference_closed_forms(dev):
     assert groups == [[0, 2], [0, 1, 2], [1]]
 
 
-def test_router_wide_spread_uses_sequential_denominator(dev):
+@pytest.mark.parametrize("T", [2, 64])
+def test_router_wide_spread_uses_sequential_denominator(dev, T):
     """Logits spread > 12: some softmax terms fall below 2^-17, so the select
-    kernel takes its sequential double-sum path."""
+    kernel takes its sequential double-sum path (T = 2: the one-workgroup
+    select, every thread on one token)."""
     rng = np.random.default_rng(5)
-    T, H, E, k = 64, 256, 128, 8
+    H, E, k = 256, 128, 8
     h = O.rmsnorm(rng.standard_normal((T, H)).astype(np.float32), np.ones(H, np.float32))
     w = (1.5 * rng.standard_normal((H, E))).astype(np.float32)
     g = run_router(dev, h, w, k, 3)
@@ -114,10 +116,12 @@ def test_router_wide_spread_uses_sequential_denominator(dev):
     assert_bitexact(g["scores"], scores, "scores")
 
 
-def test_router_ties_and_duplicates(dev):
-    """Many exactly equal logits (duplicated router columns)."""
+@pytest.mark.parametrize("T", [3, 40])
+def test_router_ties_and_duplicates(dev, T):
+    """Many exactly equal logits (duplicated router columns): ranks by key
+    (T = 3) and rounds of argmax (T = 40) break ties by ascending id."""
     rng = np.random.default_rng(9)
-    T, H, E, k = 40, 64, 64, 8
+    H, E, k = 64, 64, 8
     h = rng.standard_normal((T, H)).astype(np.float32)
     base = (0.02 * rng.standard_normal((H, 8))).astype(np.float32)
     w = np.tile(base, (1, E // 8))
