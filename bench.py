@@ -356,7 +356,8 @@ def main():
     else:
         achieved = gu_bytes / gu_s / 1e9
         roof = {"bound": "hbm",
-                "kernel": ("gemv_kernel<true, 1> (gate/up)" if gemv else
+                "kernel": ("gate/up GEMV: gateup_slice_kernel<NG, LJ> (every token row in LDS) "
+                           "or gemv_kernel<true, 1, NG, ALL>" if gemv else
                            "gate/up stage: gateup_ring_kernel<Lx> + "
                            "limb_swiglu_quantize_vec_kernel<Lz, I/256>" if cfg.int8
                            else "expert_f32_mfma_kernel<true>"),
@@ -365,7 +366,7 @@ def main():
                 "work_per_launch": gu_bytes, "launch_ms": round(stage["gate_up"], 5)}
     if not args.no_traffic:
         if gemv:
-            kre = prim = "gemv_kernel<true"
+            kre = prim = "gateup_slice_kernel|gemv_kernel<true"
         elif cfg.int8:
             kre, prim = "gateup_ring_kernel|limb_swiglu_quantize", "gateup_ring_kernel"
         else:

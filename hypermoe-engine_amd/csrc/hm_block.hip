@@ -29,10 +29,10 @@ int hm_launch_down_f32(const hm_layer* layer, const int32_t* counts, const int32
                        int64_t R, const float* zf, float* y, hipStream_t stream);
 bool hm_gemv_shape_ok(int64_t H, int64_t I);
 int hm_launch_gateup_gemv(const hm_layer* L, const float* hidden, const int32_t* counts,
-                          const int32_t* perm_tokens, int64_t tokens, int64_t pairs, float* z,
-                          hipStream_t s);
+                          const int32_t* offsets, const int32_t* perm_tokens, int64_t tokens,
+                          int64_t pairs, float* z, hipStream_t s);
 int hm_launch_down_gemv(const hm_layer* L, const float* z, const int32_t* counts,
-                        int64_t pairs, float* y, hipStream_t s);
+                        const int32_t* offsets, int64_t pairs, float* y, hipStream_t s);
 bool hm_gemv_combine_ok(int64_t tokens, int32_t top_k, int64_t H, int64_t I);
 int hm_launch_down_combine_gemv(const hm_layer* L, const float* z, const int32_t* counts,
                                 const uint32_t* ids, const int32_t* slots, const float* scores,
@@ -256,7 +256,7 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
     };
     if (gemv) {
         rc = gate_up([&] {
-            return hm_launch_gateup_gemv(layer, hidden, counts, p.perm_tokens, tokens, P,
+            return hm_launch_gateup_gemv(layer, hidden, counts, p.offsets, p.perm_tokens, tokens, P,
                                          p.zf, s);
         });
         if (rc) return rc;
@@ -269,7 +269,7 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
             if (rc || (rc = mark(5)) || (rc = mark(6))) return rc;
             return HM_OK;
         }
-        rc = hm_launch_down_gemv(layer, p.zf, counts, P, p.y, s);
+        rc = hm_launch_down_gemv(layer, p.zf, counts, p.offsets, P, p.y, s);
     } else if (layer->dtype == HM_DTYPE_INT8) {
         if (!x_quantized) {
             rc = hm_launch_quantize_rows(hidden, tokens, H, limbs_x, p.xdig, p.xscale, p.xdsum, s);

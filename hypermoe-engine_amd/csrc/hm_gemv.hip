@@ -28,7 +28,6 @@ constexpr int kGvWaves = 8;                 // waves per workgroup
 constexpr int kGvThreads = 64 * kGvWaves;
 constexpr int kGvRows = 4;                  // activation rows per pass (weights stay in registers)
 constexpr int kGvMaxTiles = 16;             // K tiles per wave: K <= 32 * 16 * (waves per projection)
-constexpr int kGvXPer = 2;                  // float4 of a row per thread: K <= 4 * 2 * kGvThreads
 constexpr int kGvAllFloats = 16384;         // s_x of every token's row: T * K32 <= this
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -116,6 +115,36 @@ __device__ __forceinline__ void tile_to_float(v4i w, float (&f)[16]) {
     }
 }
 
+// The slot-th expert (ascending id) with a non-zero group; -1 if none
+// (gemv_kernel's scan).
+// Every wave computes it redundantly from `counts` (E <= 1024); the loads
+// of all 64-expert groups go out together.
+__device__ int hm_active_expert_scan(const int32_t* __restrict__ counts, int64_t experts, int slot) {
+    const int lane = threadIdx.x & 63;
+    constexpr int kGroups = 16;
+    int cnt[kGroups];
+#pragma unroll
+    for (int b = 0; b < kGroups; ++b) {
+        const int64_t e = (int64_t)b * 64 + lane;
+        cnt[b] = e < experts ? counts[e] : 0;
+    }
+    int seen = 0;
+#pragma unroll
+    for (int b = 0; b < kGroups; ++b) {
+        const unsigned long long m = __ballot(cnt[b] > 0);
+        const int c = __popcll(m);
+        if (slot < seen + c) {
+            // position of the (slot - seen)-th set bit
+            unsigned long long mm = m;
+            for (int i = 0; i < slot - seen; ++i) mm &= mm - 1;
+            return b * 64 + __ffsll((long long)mm) - 1;
+        }
+        seen += c;
+    }
+    return -1;
+}
+
+
 // ---------------------------------------------------------------------------
 // GATEUP: z[g, n] = silu(x_g . Wg[n]) * (x_g . Wu[n]), x_g = hidden[perm_tokens[g]]
 // DOWN:   y[g, n] = z_g . Wd[n]
@@ -126,21 +155,14 @@ __device__ __forceinline__ void tile_to_float(v4i w, float (&f)[16]) {
 // kGvRows at a time, from an LDS copy of the rows.  Partial sums meet in LDS
 // in a fixed order (the two K halves of a tile, then the K ranges in
 // ascending order).  Dynamic LDS: kGvRows * K32 floats.
-//
-// Issue order: the expf table, counts, the first row block and only then
-// the weights, so that the rows reach LDS while the weights stream; the
-// first block runs as straight-line code, so that each tile is used as it
-// arrives (a loop around it would wait for every load at its entry).  With
-// ALL (gate/up of a few tokens: T * K32 <= kGvAllFloats) s_x holds every
-// token's row, loaded before anything else, and grouped row g reads row
-// perm_tokens[g] of it.
 // ---------------------------------------------------------------------------
-template <bool GATEUP, int CT, int NG, bool ALL>
+template <bool GATEUP, int CT>
 __global__ __launch_bounds__(kGvThreads) void gemv_kernel(
     const float* __restrict__ x_src, const int32_t* __restrict__ perm_tokens, int64_t K,
     int64_t N, int64_t experts, const int8_t* __restrict__ packed, int64_t hidden,
     int64_t inter, const float* __restrict__ scale, const int32_t* __restrict__ zp,
-    const int32_t* __restrict__ counts, int64_t n_tokens, float* __restrict__ out) {
+    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
+    float* __restrict__ out) {
     constexpr int NP = GATEUP ? 2 : 1;           // projections
     constexpr int NQ = kGvWaves / (NP * CT);     // K ranges per (projection, column tile)
     static_assert(NQ >= 1 && NP * CT * NQ == kGvWaves, "wave split");
@@ -148,95 +170,41 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(
     __shared__ float s_red[NP][CT][NQ][kGvRows][32];
     __shared__ float s_xs[NQ][kGvRows];
     __shared__ unsigned long long s_exp2[32];
-    __shared__ float4 s_dump;
+    if (GATEUP) hm_load_exp2_table(s_exp2);
     const int tid = threadIdx.x, lane = tid & 63;
-    const unsigned long long tab = GATEUP && tid < 32 ? kHmExp2Table[tid] : 0ull;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int p = wave / (CT * NQ), c = (wave / NQ) % CT, q = wave % NQ;
-    int cnt[NG];
-    hm_load_counts<NG>(counts, experts, cnt);
-    // ALL: every token's row, right after the counts (it needs no routing
-    // result)
-    constexpr int kAllX = ALL ? kGvAllFloats / 4 / kGvThreads : 1;
-    float4 xa[kAllX];
-    const int64_t K32 = hm_pad32(K), k4 = K32 / 4;
-    // (loads from clamped in-range addresses, no branch: a load under a
-    // branch is merged with its alternative at the join, which waits for it;
-    // the range is applied where the values are stored)
-    const uint32_t k4u = (uint32_t)k4;
-    if (ALL) {
-#pragma unroll
-        for (int u = 0; u < kAllX; ++u) {
-            const uint32_t i = (uint32_t)tid + (uint32_t)u * kGvThreads;
-            const uint32_t t = min(i / k4u, (uint32_t)n_tokens - 1), k = min(4 * (i % k4u), (uint32_t)K - 4);
-            xa[u] = *reinterpret_cast<const float4*>(x_src + (int64_t)t * K + k);
-        }
-    }
-    const hm_active act = hm_active_expert<NG>(cnt, experts, (int)blockIdx.y);
-    const int e = act.e;
+    const int e = hm_active_expert_scan(counts, experts, (int)blockIdx.y);
     if (e < 0) return;  // uniform: every wave computes the same e
-    const int64_t KT = K32 / 32;
+    const int64_t K32 = hm_pad32(K), KT = K32 / 32;
     const int64_t NT = hm_pad32(N) / 32;
     const int cb = min((int)(CT * blockIdx.x) + c, (int)NT - 1);  // past the last tile: repeats it
     const int kb0 = (int)(q * KT / NQ), nkb = (int)((q + 1) * KT / NQ) - kb0;
-    const int64_t g0 = act.g0;
-    const int rows = act.rows;
-    // the first row block's activations (zero past K)
-    const int nr0 = min(kGvRows, rows);
-    constexpr int kRowX = ALL ? 1 : kGvRows;
-    float4 xr[kRowX][kGvXPer];
-#pragma unroll
-    for (int r = 0; r < kRowX && !ALL; ++r) {
-        const int64_t g = g0 + min(r, nr0 - 1);
-        const float* src = x_src + (GATEUP ? (int64_t)perm_tokens[g] : g) * K;
-#pragma unroll
-        for (int v = 0; v < kGvXPer; ++v) {
-            const int64_t k = min(4 * ((int64_t)tid + (int64_t)v * kGvThreads), K - 4);
-            xr[r][v] = *reinterpret_cast<const float4*>(src + k);
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);  // (keeps the row loads ahead of the weight loads)
-    // the wave's weight tiles, all loads in flight together (tiles past the
-    // wave's range re-read its last one, or tile 0 of the column: no branch)
+    // the wave's weight tiles, all loads in flight together
     const int8_t* wt = packed + hm_proj_offset(e, GATEUP ? p : 2, hidden, inter) +
-                       (int64_t)cb * KT * 1024 + 16 * lane;
+                       ((int64_t)cb * KT + kb0) * 1024 + 16 * lane;
     v4i w[kGvMaxTiles];
 #pragma unroll
-    for (int t = 0; t < kGvMaxTiles; ++t) {
-        const int kb = nkb > 0 ? kb0 + min(t, nkb - 1) : 0;
-        w[t] = *reinterpret_cast<const v4i*>(wt + (int64_t)kb * 1024);
-    }
-    if (ALL) {
-#pragma unroll
-        for (int u = 0; u < kAllX; ++u) {
-            const uint32_t i = (uint32_t)tid + (uint32_t)u * kGvThreads;
-            if (i < n_tokens * k4)  // (zero past K)
-                *reinterpret_cast<float4*>(&s_x[4 * i]) = hm_keep_if(xa[u], 4 * (i % k4u) < K);
+    for (int t = 0; t < kGvMaxTiles; ++t)
+        if (t < nkb) w[t] = *reinterpret_cast<const v4i*>(wt + (int64_t)t * 1024);
+    const int64_t g0 = offsets[e];
+    const int rows = counts[e];
+    for (int r0 = 0; r0 < rows; r0 += kGvRows) {
+        const int nr = min(kGvRows, rows - r0);
+        // the rows into LDS (zero past K: the padded K tiles hold zeros too)
+        const int64_t k4 = K32 / 4;
+        for (int64_t i = tid; i < (int64_t)nr * k4; i += kGvThreads) {
+            const int r = (int)(i / k4);
+            const int64_t k = 4 * (i % k4);
+            const int64_t g = g0 + r0 + r;
+            const float* xr = x_src + (GATEUP ? (int64_t)perm_tokens[g] : g) * K;
+            const float4 v = k < K ? *reinterpret_cast<const float4*>(xr + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+            *reinterpret_cast<float4*>(&s_x[r * K32 + k]) = v;
         }
-    } else {
-        // (unconditional stores, so that no load is sunk into a branch behind
-        // the weights: slices past the row go to a dummy slot, rows past nr0
-        // are not read)
+        __syncthreads();
+        float acc[kGvRows], xs[kGvRows];
 #pragma unroll
-        for (int r = 0; r < kRowX; ++r)
-#pragma unroll
-            for (int v = 0; v < kGvXPer; ++v) {
-                const int64_t i = (int64_t)tid + (int64_t)v * kGvThreads;
-                float4* dst = i < k4 ? reinterpret_cast<float4*>(&s_x[r * K32 + 4 * i]) : &s_dump;
-                *dst = hm_keep_if(xr[r][v], r < nr0 && 4 * i < K);
-            }
-    }
-    if (GATEUP && tid < 32) s_exp2[tid] = tab;
-    // one row block: rows r0 .. r0 + nr - 1, already in s_x
-    auto block = [&](int r0, int nr) {
-        // the block's rows in s_x
-        int64_t xoff[kGvRows];
-#pragma unroll
-        for (int r = 0; r < kGvRows; ++r)
-            xoff[r] = (ALL ? (r < nr ? (int64_t)perm_tokens[g0 + r0 + r] : 0) : r) * K32;
-        float acc[kGvRows];
-#pragma unroll
-        for (int r = 0; r < kGvRows; ++r) acc[r] = 0.0f;
+        for (int r = 0; r < kGvRows; ++r) acc[r] = xs[r] = 0.0f;
 #pragma unroll
         for (int t = 0; t < kGvMaxTiles; ++t) {
             if (t < nkb) {
@@ -246,7 +214,7 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(
 #pragma unroll
                 for (int r = 0; r < kGvRows; ++r) {
                     if (r < nr) {
-                        const float4* xv = reinterpret_cast<const float4*>(&s_x[xoff[r] + k]);
+                        const float4* xv = reinterpret_cast<const float4*>(&s_x[r * K32 + k]);
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             const float4 v = xv[i];
@@ -254,6 +222,7 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(
                             acc[r] = __builtin_fmaf(v.y, f[4 * i + 1], acc[r]);
                             acc[r] = __builtin_fmaf(v.z, f[4 * i + 2], acc[r]);
                             acc[r] = __builtin_fmaf(v.w, f[4 * i + 3], acc[r]);
+                            xs[r] += (v.x + v.y) + (v.z + v.w);
                         }
                     }
                 }
@@ -263,19 +232,9 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(
 #pragma unroll
         for (int r = 0; r < kGvRows; ++r) {
             const float a = acc[r] + __shfl_xor(acc[r], 32, 64);
+            const float x = xs[r] + __shfl_xor(xs[r], 32, 64);
             if (lane < 32) s_red[p][c][q][r][lane] = a;
-        }
-        // the rows' sums over this K range (one wave per range)
-        if (p == 0 && c == 0) {
-#pragma unroll
-            for (int r = 0; r < kGvRows; ++r) {
-                if (r >= nr) break;
-                float x = 0.0f;
-                for (int k = 32 * kb0 + lane; k < 32 * (kb0 + nkb); k += 64) x += s_x[xoff[r] + k];
-#pragma unroll
-                for (int d = 32; d >= 1; d >>= 1) x += __shfl_xor(x, d, 64);
-                if (lane == 0) s_xs[q][r] = x;
-            }
+            if (p == 0 && c == 0 && lane == 0) s_xs[q][r] = x;
         }
         __syncthreads();
         // one half-wave per (row, column tile) finishes its 32 columns
@@ -302,25 +261,10 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(
                 else out[g * N + n] = v[0];
             }
         }
-    };
-    __syncthreads();
-    block(0, nr0);
-    // further row blocks (more than kGvRows rows on the expert)
-    for (int r0 = kGvRows; r0 < rows; r0 += kGvRows) {
-        const int nr = min(kGvRows, rows - r0);
-        __syncthreads();  // the previous block's reads of s_x and s_red are done
-        for (int64_t i = tid; !ALL && i < (int64_t)nr * k4; i += kGvThreads) {
-            const int r = (int)(i / k4);
-            const int64_t k = 4 * (i % k4);
-            const int64_t g = g0 + r0 + r;
-            const float* xrow = x_src + (GATEUP ? (int64_t)perm_tokens[g] : g) * K;
-            const float4 v = k < K ? *reinterpret_cast<const float4*>(xrow + k) : make_float4(0.f, 0.f, 0.f, 0.f);
-            *reinterpret_cast<float4*>(&s_x[r * K32 + k]) = v;
-        }
         __syncthreads();
-        block(r0, nr);
     }
 }
+
 
 // ---------------------------------------------------------------------------
 // Gate/up of a few tokens (T * K32 <= kGvAllFloats) on 8-column slices:
@@ -702,35 +646,22 @@ __global__ __launch_bounds__(kDcThreads) void gemv_down_combine_kernel(
 
 template <bool GATEUP, int CT>
 int launch_gemv(const float* x_src, const int32_t* perm_tokens, int64_t K, int64_t N,
-                const hm_layer* L, const int32_t* counts, int64_t slots, int64_t tokens,
+                const hm_layer* L, const int32_t* counts, const int32_t* offsets, int64_t slots,
                 float* out, hipStream_t s) {
     constexpr int NQ = kGvWaves / ((GATEUP ? 2 : 1) * CT);
     const int64_t nt = hm_pad32(N) / 32, kt = hm_pad32(K) / 32;
     // every wave's K range within its register tiles
     if ((kt + NQ - 1) / NQ > kGvMaxTiles) return HM_ERR_UNSUPPORTED;
     const dim3 grid((unsigned)((nt + CT - 1) / CT), (unsigned)slots);
-    // gate/up of a few tokens: every token's row in LDS
-    const bool all = GATEUP && CT == 1 && tokens * hm_pad32(K) <= kGvAllFloats;
-    const size_t lds = (size_t)(all ? tokens : kGvRows) * hm_pad32(K) * sizeof(float);
+    const size_t lds = (size_t)kGvRows * hm_pad32(K) * sizeof(float);
     // (the timer, when armed, brackets the gate/up launch)
-#define HM_GV(NG, ALL)                                                                         \
-    HM_STAGE_LAUNCH(true, true, (gemv_kernel<GATEUP, CT, NG, ALL>), grid, dim3(kGvThreads), lds, \
-                    s, x_src, perm_tokens, K, N, L->experts,                                    \
-                    static_cast<const int8_t*>(L->packed), L->hidden, L->intermediate,          \
-                    L->scale, L->zero_point, counts, tokens, out)
-#define HM_GV2(NG)                                                                             \
-    do {                                                                                       \
-        if (GATEUP && CT == 1 && all) HM_GV(NG, GATEUP && CT == 1);                             \
-        else HM_GV(NG, false);                                                                 \
-    } while (0)
-    if (L->experts <= 128) HM_GV2(2);
-    else if (L->experts <= 256) HM_GV2(4);
-    else HM_GV2(16);
-#undef HM_GV2
-#undef HM_GV
+    HM_STAGE_LAUNCH(true, true, (gemv_kernel<GATEUP, CT>), grid, dim3(kGvThreads), lds, s, x_src,
+                    perm_tokens, K, N, L->experts, static_cast<const int8_t*>(L->packed),
+                    L->hidden, L->intermediate, L->scale, L->zero_point, counts, offsets, out);
     HM_LAUNCHED();
     return HM_OK;
 }
+
 
 }  // namespace
 
@@ -746,13 +677,15 @@ bool hm_gemv_shape_ok(int64_t H, int64_t I) {
 // z[g, n] = silu(x_g . Wg[n]) * (x_g . Wu[n]) for every grouped row g, with
 // x_g = hidden[perm_tokens[g]]; `pairs` = T*k bounds the active experts.
 int hm_launch_gateup_gemv(const hm_layer* L, const float* hidden, const int32_t* counts,
-                          const int32_t* perm_tokens, int64_t tokens, int64_t pairs, float* z,
-                          hipStream_t s) {
+                          const int32_t* offsets, const int32_t* perm_tokens, int64_t tokens,
+                          int64_t pairs, float* z, hipStream_t s) {
     if (L->experts > 1024) return HM_ERR_UNSUPPORTED;
     const int64_t slots = pairs < L->experts ? pairs : L->experts;
     const int64_t K = L->hidden, N = L->intermediate, KT = hm_pad32(K) / 32;
-    if (tokens * hm_pad32(K) <= kGvAllFloats && KT <= 32 * kGsQ) {
-        // a few tokens: every row in LDS, 8-column slices
+    if (tokens <= 2 && tokens * hm_pad32(K) <= kGvAllFloats && KT <= 32 * kGsQ) {
+        // one or two tokens: every row in LDS, 8-column slices (C3-1 29.0
+        // against 31.1 us per step for gemv_kernel; from four tokens on the
+        // slices re-stage too many rows: C3-4 68.6 against 64.1 us)
         const dim3 grid((unsigned)((N + 7) / 8), (unsigned)slots);
         const size_t lds = (size_t)tokens * hm_pad32(K) * sizeof(float);
         const int lj = (int)((KT + kGsQ - 1) / kGsQ + 3) / 4;  // loads per wave
@@ -776,7 +709,7 @@ int hm_launch_gateup_gemv(const hm_layer* L, const float* hidden, const int32_t*
         HM_LAUNCHED();
         return HM_OK;
     }
-    return launch_gemv<true, 1>(hidden, perm_tokens, K, N, L, counts, slots, tokens, z, s);
+    return launch_gemv<true, 1>(hidden, perm_tokens, K, N, L, counts, offsets, slots, z, s);
 }
 
 // The decode down projection fused with the combine (P = T * k <= 16 pairs,
@@ -808,15 +741,15 @@ int hm_launch_down_combine_gemv(const hm_layer* L, const float* z, const int32_t
 
 // y[g, n] = z_g . Wd[n] for every grouped row g.
 int hm_launch_down_gemv(const hm_layer* L, const float* z, const int32_t* counts,
-                        int64_t pairs, float* y, hipStream_t s) {
+                        const int32_t* offsets, int64_t pairs, float* y, hipStream_t s) {
     if (L->experts > 1024) return HM_ERR_UNSUPPORTED;
     const int64_t slots = pairs < L->experts ? pairs : L->experts;
     // few experts: one column tile per workgroup (more workgroups in
     // flight); many: four (a workgroup's setup spread over four times the
     // weights)
     if (slots >= 32 && hm_pad32(L->intermediate) / 32 <= 2 * kGvMaxTiles)
-        return launch_gemv<false, 4>(z, nullptr, L->intermediate, L->hidden, L, counts, slots, 0,
-                                     y, s);
-    return launch_gemv<false, 1>(z, nullptr, L->intermediate, L->hidden, L, counts, slots, 0, y,
-                                 s);
+        return launch_gemv<false, 4>(z, nullptr, L->intermediate, L->hidden, L, counts, offsets,
+                                     slots, y, s);
+    return launch_gemv<false, 1>(z, nullptr, L->intermediate, L->hidden, L, counts, offsets, slots,
+                                 y, s);
 }
