@@ -357,7 +357,7 @@ def main():
         achieved = gu_bytes / gu_s / 1e9
         roof = {"bound": "hbm",
                 "kernel": ("gate/up GEMV: gateup_slice_kernel<NG, LJ> (every token row in LDS) "
-                           "or gemv_kernel<true, 1, NG, ALL>" if gemv else
+                           "or gemv_kernel<true, 1> (more than two tokens)" if gemv else
                            "gate/up stage: gateup_ring_kernel<Lx> + "
                            "limb_swiglu_quantize_vec_kernel<Lz, I/256>" if cfg.int8
                            else "expert_f32_mfma_kernel<true>"),
