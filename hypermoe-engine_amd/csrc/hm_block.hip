@@ -6,6 +6,8 @@
 #include <limits.h>
 #include <math.h>
 
+#include <cmath>
+
 #include <mutex>
 
 int hm_launch_quantize_rows(const float* x, int64_t rows, int64_t n, int32_t limbs,
@@ -50,7 +52,8 @@ extern "C" __attribute__((visibility("hidden"))) int hm_permute_counted(const ui
 int hm_route_permute_decode(const float* h, const float* w, int64_t tokens, int64_t hidden,
                             int64_t experts, int32_t top_k, uint32_t flags, uint32_t* ids,
                             float* scores, int32_t* status, void* route_ws,
-                            const hm_decode_fusion* fused, void* stream);
+                            const hm_decode_fusion* fused, const hm_norm_fold* norm,
+                            void* stream);
 
 namespace {
 
@@ -164,11 +167,41 @@ size_t hm_moe_block_workspace_bytes(const hm_layer* layer, int64_t tokens, int32
            kAlign;
 }
 
-int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float* router_w,
-                         int64_t tokens, int32_t top_k, uint32_t route_flags,
-                         int32_t limbs_x, int32_t limbs_z, const hm_block_io* io,
-                         void* workspace, size_t workspace_bytes, void* stream) {
-    HM_REQUIRE(layer_valid(layer) && hidden && router_w && io && io->out && workspace);
+}  // extern "C"
+
+namespace {
+
+// The layer's RMSNorm ahead of the block (hm_moe_layer_forward): h is the
+// layer input and the residual, normed receives RMSNorm(h).
+struct LayerNorm {
+    const float* gamma;
+    float eps;
+    float* normed;
+};
+
+// hm_moe_block_forward, and with `ln` the RMSNorm before it (folded into
+// the decode router's first kernel, else its own launch).
+int block_forward(const hm_layer* layer, const float* hidden, const float* router_w,
+                  int64_t tokens, int32_t top_k, uint32_t route_flags, int32_t limbs_x,
+                  int32_t limbs_z, const hm_block_io* io_in, void* workspace,
+                  size_t workspace_bytes, void* stream, const LayerNorm* ln) {
+    HM_REQUIRE(layer_valid(layer) && hidden && router_w && io_in && io_in->out && workspace);
+    hm_block_io io_ln;
+    const hm_block_io* io = io_in;
+    if (ln) {
+        // h is the residual; normed is read by every kernel after the norm
+        // while h is still read, so the two must not overlap
+        HM_REQUIRE(ln->gamma && ln->normed && std::isfinite(ln->eps) && ln->eps > 0.0f);
+        HM_REQUIRE(!io_in->residual || io_in->residual == hidden);
+        const size_t row_bytes = (size_t)layer->hidden * sizeof(float);
+        const uintptr_t a0 = reinterpret_cast<uintptr_t>(hidden),
+                        b0 = reinterpret_cast<uintptr_t>(ln->normed);
+        HM_REQUIRE(tokens <= 0 || a0 + (size_t)tokens * row_bytes <= b0 ||
+                   b0 + (size_t)tokens * row_bytes <= a0);
+        io_ln = *io_in;
+        io_ln.residual = hidden;
+        io = &io_ln;
+    }
     HM_REQUIRE(tokens > 0 && top_k > 0 && top_k <= layer->experts);
     if (layer->dtype == HM_DTYPE_INT8) {
         HM_REQUIRE(limbs_x >= 1 && limbs_x <= 3 && limbs_z >= 1 && limbs_z <= 3);
@@ -219,10 +252,20 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
     if (fuse) {
         const hm_decode_fusion f = {p.counters, 1, p.counts, p.offsets, p.perm_tokens,
                                     p.perm_weights, p.slots};
+        const hm_norm_fold nf = {ln ? ln->gamma : nullptr, ln ? ln->normed : nullptr,
+                                 ln ? ln->eps : 0.0f,
+                                 (route_flags & HM_EXEC_ROUTE_SEQUENTIAL) ? 1 : 0};
         rc = hm_route_permute_decode(hidden, router_w, tokens, H, E, top_k, route_bits, p.ids,
-                                     p.scores, status, p.route_ws, &f, stream);
+                                     p.scores, status, p.route_ws, &f, ln ? &nf : nullptr,
+                                     stream);
+        if (ln) hidden = ln->normed;
         if (rc || (rc = mark(1)) || (rc = mark(2))) return rc;
     } else {
+        if (ln) {
+            rc = hm_rmsnorm(hidden, ln->gamma, ln->normed, tokens, H, ln->eps, stream);
+            if (rc) return rc;
+            hidden = ln->normed;
+        }
         // the INT8 expert path's activation digits come out of the router's
         // prefill select kernel when it runs (one launch fewer)
         const hm_row_quant xq = {p.xdig, p.xscale, p.xdsum, limbs_x};
@@ -296,6 +339,28 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float
                     stream);
     if (rc || (rc = mark(6))) return rc;
     return HM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hm_moe_block_forward(const hm_layer* layer, const float* hidden, const float* router_w,
+                         int64_t tokens, int32_t top_k, uint32_t route_flags,
+                         int32_t limbs_x, int32_t limbs_z, const hm_block_io* io,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+    return block_forward(layer, hidden, router_w, tokens, top_k, route_flags, limbs_x, limbs_z,
+                         io, workspace, workspace_bytes, stream, nullptr);
+}
+
+int hm_moe_layer_forward(const hm_layer* layer, const float* h, const float* gamma, float eps,
+                         float* normed, const float* router_w, int64_t tokens, int32_t top_k,
+                         uint32_t route_flags, int32_t limbs_x, int32_t limbs_z,
+                         const hm_block_io* io, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+    const LayerNorm ln = {gamma, eps, normed};
+    return block_forward(layer, h, router_w, tokens, top_k, route_flags, limbs_x, limbs_z, io,
+                         workspace, workspace_bytes, stream, &ln);
 }
 
 }  // extern "C"

@@ -60,6 +60,18 @@ struct hm_decode_fusion {
     int32_t* slots;
 };
 
+// RMSNorm folded into the decode router's first kernel: the rows it reads
+// are the layer input h, normalised with gamma and eps on the fly; x_out
+// [T x H] receives RMSNorm(h), the rows every later kernel of the block
+// reads.  force_seq: every row takes the reference's sequential sum of
+// squares (the certified interval is skipped).  gamma == nullptr: no norm.
+struct hm_norm_fold {
+    const float* gamma;
+    float* x_out;
+    float eps;
+    int force_seq;
+};
+
 // ---------------------------------------------------------------------------
 // Wave64 reductions (all 64 lanes must be active).
 // ---------------------------------------------------------------------------

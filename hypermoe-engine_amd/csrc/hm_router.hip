@@ -33,6 +33,24 @@ __device__ __forceinline__ double hm_inv_rms(double s, double width, double eps)
     return 1.0 / sqrt(s / width + eps);
 }
 
+// The relative half-width d of the interval around a tree sum of `width`
+// squares that holds the sequential sum (above).
+__device__ __forceinline__ double hm_rms_sum_slack(int64_t width) {
+    const double u = 0x1p-53;
+    const double gam = (double)(width - 1) * u / (1.0 - (double)(width - 1) * u);
+    return 4.0 * gam / (1.0 - gam);
+}
+
+// The reference's own sum: double(x_k)^2 added in ascending k from +0.
+__device__ __forceinline__ double hm_rms_sum_seq(const float* __restrict__ xr, int64_t width) {
+    double s = 0.0;
+    for (int64_t i = 0; i < width; ++i) {
+        const float v = xr[i];
+        s += (double)v * v;
+    }
+    return s;
+}
+
 __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(
     const float* __restrict__ x, const float* __restrict__ gamma,
     float* __restrict__ y, int64_t width, float eps) {
@@ -56,9 +74,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(
     __syncthreads();
     double s_fast = 0.0;
     for (int w = 0; w < kBlock / HM_WAVE; ++w) s_fast += red[w];
-    const double u = 0x1p-53;
-    const double gam = (double)(width - 1) * u / (1.0 - (double)(width - 1) * u);
-    const double d = 4.0 * gam / (1.0 - gam);
+    const double d = hm_rms_sum_slack(width);
     const double wd = (double)width, ed = (double)eps;
     const double inv_lo = hm_inv_rms(s_fast * (1.0 + d), wd, ed);
     const double inv_hi = hm_inv_rms(s_fast * (1.0 - d), wd, ed);
@@ -74,14 +90,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(
     }
     __syncthreads();
     if (!ambiguous) return;
-    if (tid == 0) {
-        double s = 0.0;
-        for (int64_t i = 0; i < width; ++i) {
-            const float v = row_lds[i];
-            s += (double)v * v;
-        }
-        inv_seq = hm_inv_rms(s, wd, ed);
-    }
+    if (tid == 0) inv_seq = hm_inv_rms(hm_rms_sum_seq(row_lds, width), wd, ed);
     __syncthreads();
     const double inv = inv_seq;
     for (int64_t i = tid; i < width; i += kBlock) {
@@ -339,11 +348,20 @@ __device__ __forceinline__ bool block_sums_settle(double a, double sa, double sc
 // grid (kNB, ceil(E/64), T), one wave, lane = expert.  The block's W rows
 // (64 experts wide) go to LDS in one burst of 16-byte DMA loads
 // (E % 64 == 0, b % 4 == 0, w 16-byte aligned), else per lane.
+//
+// With norm.gamma the kernel also is A1 RMSNorm (RMSNorm.cpp:65-77; the
+// transformer block runs it on the router's input, TransformerBlock.cpp:
+// 88-104): every wave of a token forms the row's tree sum of squares,
+// brackets the reference's sequential sum by it as rmsnorm_kernel does, and
+// normalises the elements of its own K block; an element the bracket does
+// not settle makes the wave take the sequential sum itself, which gives the
+// reference's value for every element.  The waves of expert group 0 write
+// their blocks to norm.x_out.
 constexpr int kPK = 64;  // k per LDS chunk of a block
 
 __global__ __launch_bounds__(64) void router_partial_kernel(
     const float* __restrict__ h, const float* __restrict__ w, int hidden, int experts,
-    double* __restrict__ part, int32_t* __restrict__ zero_ctr, int n_zero) {
+    double* __restrict__ part, int32_t* __restrict__ zero_ctr, int n_zero, hm_norm_fold norm) {
     __shared__ double s_h[kPK];                                        // broadcast reads
     __shared__ __attribute__((aligned(1024))) float s_w[kPK][HM_WAVE];  // [k][lane]
     const int lane = threadIdx.x;
@@ -358,16 +376,68 @@ __global__ __launch_bounds__(64) void router_partial_kernel(
     const int b = hidden / kNB;
     const bool full = experts % HM_WAVE == 0 && b % 4 == 0 && (uintptr_t)w % 16 == 0;
     const int k0 = j * b;
-    const float* hp = h + (int64_t)t * hidden + k0;
+    const float* hrow = h + (int64_t)t * hidden;
+    const float* hp = hrow + k0;
+    const bool fold = norm.gamma != nullptr;
+    // the whole row in one burst of 16-byte loads (at most 16 per lane)
+    const bool row4 = hidden % 256 == 0 && hidden <= 16 * 256 && (uintptr_t)h % 16 == 0;
+    double inv_lo = 0.0, inv_hi = 0.0, inv_seq = 0.0;
+    bool have_seq = false;
     double acc = 0.0, rs = 0.0, qs = 0.0;
     for (int c0 = 0; c0 < b; c0 += kPK) {
         const int kc = min(kPK, b - c0);
         __builtin_amdgcn_wave_barrier();
-        s_h[lane] = lane < kc ? (double)hp[c0 + lane] : 0.0;
+        // unconditional loads from clamped addresses (a load under a branch
+        // is waited for at the branch's end), masked once they are in
+        const int lc = min(lane, kc - 1);
+        float hv = hp[c0 + lc];
+        const float gv = (fold ? norm.gamma + k0 : hp)[c0 + lc];
         if (full) {
             // lane l: row 4i + l/16, floats 4*(l%16) .. +3 of the 64-expert row
             const float* src = w + (int64_t)(k0 + c0 + (lane >> 4)) * experts + e0 + 4 * (lane & 15);
             for (int i = 0; i < kc / 4; ++i) dma16(src + (int64_t)4 * i * experts, &s_w[4 * i][0]);
+        }
+        if (fold) {
+            if (c0 == 0) {
+                // the row's squares, in any order (their loads overlap the
+                // block's W burst)
+                double ss = 0.0;
+                if (row4) {
+                    const float4* r4 = reinterpret_cast<const float4*>(hrow);
+                    const int n4 = hidden >> 8;
+                    float4 v[16];
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) v[i] = r4[lane + HM_WAVE * min(i, n4 - 1)];
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const double q = ((double)v[i].x * v[i].x + (double)v[i].y * v[i].y) +
+                                         ((double)v[i].z * v[i].z + (double)v[i].w * v[i].w);
+                        ss += i < n4 ? q : 0.0;
+                    }
+                } else {
+                    for (int i = lane; i < hidden; i += HM_WAVE) {
+                        const float v = hrow[i];
+                        ss += (double)v * v;
+                    }
+                }
+                const double s_fast = hm_wave_sum_f64(ss);
+                const double d = hm_rms_sum_slack(hidden);
+                inv_lo = hm_inv_rms(s_fast * (1.0 + d), (double)hidden, (double)norm.eps);
+                inv_hi = hm_inv_rms(s_fast * (1.0 - d), (double)hidden, (double)norm.eps);
+            }
+            hv = lane < kc ? hv : 0.0f;
+            const double g = lane < kc ? (double)gv : 0.0;
+            const float a = (float)((double)hv * inv_lo * g);
+            const float bb = (float)((double)hv * inv_hi * g);
+            if (!have_seq && (norm.force_seq || __any(__float_as_uint(a) != __float_as_uint(bb)))) {
+                inv_seq = hm_inv_rms(hm_rms_sum_seq(hrow, hidden), (double)hidden, (double)norm.eps);
+                have_seq = true;
+            }
+            hv = have_seq ? (float)((double)hv * inv_seq * g) : a;
+            if (blockIdx.y == 0 && lane < kc) norm.x_out[(int64_t)t * hidden + k0 + c0 + lane] = hv;
+        }
+        s_h[lane] = lane < kc ? (double)hv : 0.0;
+        if (full) {
             wait_vmcnt<0>();
         } else {
             for (int i = 0; i < kc; ++i) s_w[i][lane] = live ? w[(int64_t)(k0 + c0 + i) * experts + e] : 0.0f;
@@ -1420,7 +1490,8 @@ size_t hm_route_workspace_bytes(int64_t tokens, int64_t hidden, int64_t experts)
 static int launch_decode_router(const float* h, const float* w, int64_t tokens, int64_t hidden,
                                 int64_t experts, int32_t top_k, uint32_t flags, float* logits,
                                 uint32_t* ids, float* scores, int32_t* status, void* route_ws,
-                                const hm_decode_fusion* fused, void* stream) {
+                                const hm_decode_fusion* fused, const hm_norm_fold* norm,
+                                void* stream) {
     const int epl = (int)((experts + HM_WAVE - 1) / HM_WAVE);
     const dim3 sgrid((unsigned)((tokens + 3) / 4));
     const size_t seq_bytes = (size_t)(kBlock / HM_WAVE) * experts * sizeof(float);
@@ -1428,10 +1499,13 @@ static int launch_decode_router(const float* h, const float* w, int64_t tokens, 
                                              route_logits_bytes(tokens, experts));
     const dim3 pgrid((unsigned)kNB, (unsigned)((experts + HM_WAVE - 1) / HM_WAVE),
                      (unsigned)tokens);
+    const hm_norm_fold nf = norm ? *norm : hm_norm_fold{nullptr, nullptr, 0.0f, 0};
     hipLaunchKernelGGL(router_partial_kernel, pgrid, dim3(HM_WAVE), 0, hm_stream(stream), h, w,
                        (int)hidden, (int)experts, part, fused ? fused->counters : nullptr,
-                       fused ? fused->n_counters : 0);
+                       fused ? fused->n_counters : 0, nf);
     HM_LAUNCHED();
+    // the select kernel's fallback chains read the normalised rows
+    if (norm) h = norm->x_out;
 #define HM_SELECTP(N, F)                                                                   \
     hipLaunchKernelGGL((router_select_partial_kernel<N, F>), sgrid, dim3(kBlock), seq_bytes, \
                        hm_stream(stream), h, w, part, tokens, hidden, experts, top_k, flags, \
@@ -1454,19 +1528,23 @@ static int launch_decode_router(const float* h, const float* w, int64_t tokens, 
 // Routing and grouping of a decode batch (T <= 16) in two launches instead
 // of hm_router_topk + hm_permute's three; same results.  Counter 0 of
 // fused->counters is the select's completion counter; all n_counters are
-// zeroed by the first launch.
+// zeroed by the first launch.  With `norm`, h is the layer input and the
+// router (and norm->x_out) get RMSNorm(h) (hm_rmsnorm's results).
 int hm_route_permute_decode(const float* h, const float* w, int64_t tokens, int64_t hidden,
                             int64_t experts, int32_t top_k, uint32_t flags, uint32_t* ids,
                             float* scores, int32_t* status, void* route_ws,
-                            const hm_decode_fusion* fused, void* stream) {
+                            const hm_decode_fusion* fused, const hm_norm_fold* norm,
+                            void* stream) {
     HM_REQUIRE(experts > 0 && top_k > 0 && top_k <= experts && fused && fused->counters);
     HM_REQUIRE(h && w && ids && scores && route_ws && tokens > 0 && hidden > 0);
+    HM_REQUIRE(!norm || (norm->gamma && norm->x_out && std::isfinite(norm->eps) &&
+                         norm->eps > 0.0f));
     if (experts > 1024 || top_k > kMaxTopK || tokens > kDecodeTokens || hidden % kNB != 0 ||
         tokens * top_k > kSmallPairs || hidden > INT_MAX)
         return HM_ERR_UNSUPPORTED;
     return launch_decode_router(h, w, tokens, hidden, experts, top_k, flags,
                                 static_cast<float*>(route_ws), ids, scores, status, route_ws,
-                                fused, stream);
+                                fused, norm, stream);
 }
 
 extern "C" {
@@ -1517,7 +1595,7 @@ __attribute__((visibility("hidden"))) int hm_router_topk_quant(const float* h, c
         // decode: certified block partials, then select over the logits
         // formed from them
         return launch_decode_router(h, w, tokens, hidden, experts, top_k, flags, logits, ids,
-                                    scores, status, route_ws, nullptr, stream);
+                                    scores, status, route_ws, nullptr, nullptr, stream);
     }
     const bool aligned = ((uintptr_t)h % 16 == 0) && ((uintptr_t)w % 16 == 0);
     if (route_ws && !(flags & HM_EXEC_ROUTE_SEQUENTIAL) && aligned && experts % kME == 0 &&

@@ -88,6 +88,8 @@ SIGNATURES = {
                                      c_i32, C.POINTER(HmBlockIO), vp, c_sz, vp]),
     "hm_moe_block_forward_noalloc": (c_i32, [C.POINTER(HmLayer), vp, vp, c_i64, c_i32, c_u32,
                                              c_i32, c_i32, C.POINTER(HmBlockIO), vp]),
+    "hm_moe_layer_forward": (c_i32, [C.POINTER(HmLayer), vp, vp, c_f32, vp, vp, c_i64, c_i32,
+                                     c_u32, c_i32, c_i32, C.POINTER(HmBlockIO), vp, c_sz, vp]),
     "hm_limb_quantize_rows": (c_i32, [vp, c_i64, c_i64, c_i32, vp, vp, vp]),
     "hm_limb_partials": (c_i32, [vp, c_i64, c_i64, c_i32, vp, c_i32, c_i64, vp, vp]),
     "hm_debug_expf": (c_i32, [vp, vp, c_i64, vp]),

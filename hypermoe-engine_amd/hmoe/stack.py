@@ -5,8 +5,9 @@ Each layer is TransformerBlock::execute with attention omitted
     h' = h + MoE(RMSNorm(h))
 with RMSNorm as RMSNorm::execute (src/transformer/norm/RMSNorm.cpp:65-77)
 and the MoE block as MoERuntime::executeBatch.  Everything runs through the
-C ABI on one stream: hm_rmsnorm, then hm_moe_block_forward with the
-residual folded into its combine.  The layers share one block workspace and
+C ABI on one stream: one hm_moe_layer_forward per layer (the RMSNorm
+folded into the router's first kernel for decode batches, launched ahead of
+the block otherwise; the residual folded into the combine).  The layers share one block workspace and
 one device status word; the residual stream ping-pongs between two buffers
 so that a layer's output never aliases its residual input.  A decode step
 issues no allocation and no synchronisation, so it can be captured in a HIP
@@ -77,14 +78,15 @@ class MoEStack:
         if events is not None:
             events[0].record()
         for i, (layer, w) in enumerate(zip(self.layers, self.router_w)):
-            capi.call("hm_rmsnorm", cur.data_ptr(), self.gamma.data_ptr(), self.norm.data_ptr(),
-                      tokens, self.hidden, self.eps, s)
             out = self.ping[i & 1]
             io = capi.HmBlockIO(out.data_ptr(), None, None, None, None, None, None, None,
-                                self.status.data_ptr(), cur.data_ptr())
-            capi.call("hm_moe_block_forward", C.byref(layer.desc), self.norm.data_ptr(),
-                      w.data_ptr(), tokens, self.top_k, self.flags, self.limbs_x, self.limbs_z,
-                      C.byref(io), self.ws.data_ptr(), self.ws.numel(), s)
+                                self.status.data_ptr(), None)
+            # RMSNorm, the block and the residual in one call (the norm runs
+            # inside the router's first kernel for decode batches)
+            capi.call("hm_moe_layer_forward", C.byref(layer.desc), cur.data_ptr(),
+                      self.gamma.data_ptr(), self.eps, self.norm.data_ptr(), w.data_ptr(),
+                      tokens, self.top_k, self.flags, self.limbs_x, self.limbs_z, C.byref(io),
+                      self.ws.data_ptr(), self.ws.numel(), s)
             cur = out
             if events is not None:
                 events[i + 1].record()

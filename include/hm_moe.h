@@ -280,6 +280,23 @@ int hm_moe_block_forward(const hm_layer* layer, const float* hidden,
                          void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/* One MoE sub-layer of the transformer block
+ * (src/transformer/runtime/TransformerBlock.cpp:88-104: RMSNorm.cpp:65-77
+ * on the layer input, the MoE block on the normalised rows, the input added
+ * back): io->out = h + MoE(RMSNorm(h; gamma, eps)).  normed [tokens x
+ * hidden] receives RMSNorm(h) (hm_rmsnorm's values); it must not overlap h.
+ * io->residual must be NULL or h.  Decode batches normalise inside the
+ * router's first kernel (one launch fewer than hm_rmsnorm followed by
+ * hm_moe_block_forward); other batches launch hm_rmsnorm first.  Same
+ * workspace as hm_moe_block_forward. */
+int hm_moe_layer_forward(const hm_layer* layer, const float* h,
+                         const float* gamma, float eps, float* normed,
+                         const float* router_w, int64_t tokens, int32_t top_k,
+                         uint32_t route_flags, int32_t limbs_x,
+                         int32_t limbs_z, const hm_block_io* io,
+                         void* workspace, size_t workspace_bytes,
+                         void* stream);
+
 /* ---- The block without allocation ------------------------------------
  * No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that

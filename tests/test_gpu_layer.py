@@ -1,0 +1,145 @@
+"""hm_moe_layer_forward: the MoE sub-layer of the transformer block,
+out = h + MoE(RMSNorm(h)) (src/transformer/runtime/TransformerBlock.cpp:
+88-104), with the RMSNorm (src/transformer/norm/RMSNorm.cpp:65-77) folded
+into the decode router's first kernel.  Called through the C ABI and
+checked bit for bit: its normalised rows against the oracle's RMSNorm, its
+routing and output against hm_rmsnorm followed by hm_moe_block_forward with
+h as the residual.  Decode sizes take the folded norm, prefill sizes the
+separate launch; gamma is not all ones; HM_EXEC_ROUTE_SEQUENTIAL makes every
+row take the sequential sum of squares; and row 0 is built so that some
+elements are not settled by the bracket around the tree sum, which sends
+their K blocks to the sequential sum."""
+from __future__ import annotations
+
+import ctypes as C
+import math
+
+import numpy as np
+import pytest
+
+import hm_oracle as O
+from conftest import assert_bitexact
+from hmoe import capi, synth
+from hmoe.block import DeviceExpertLayer, MoEBlock
+
+pytestmark = pytest.mark.gpu
+
+H, E, I, K = 2048, 32, 256, 4
+EPS = 1e-5
+
+
+def _slack(width):
+    """The kernels' relative bracket half-width around the tree sum of
+    `width` squares (the same double operations in the same order)."""
+    u = 2.0 ** -53
+    gam = (width - 1) * u / (1.0 - (width - 1) * u)
+    return 4.0 * gam / (1.0 - gam)
+
+
+def _unsettled_row(rng, eps):
+    """A row whose squares add exactly in any order (powers of two), and a
+    gamma with 32 elements (one per router K block) where float(x * inv * g)
+    differs at the two ends of the bracket, so the kernels must take the
+    sequential sum there.  Returns (row, gamma, unsettled indices)."""
+    row = (rng.choice([-2.0, -1.0, -0.5, 0.5, 1.0, 2.0], H)).astype(np.float32)
+    gamma = (0.5 + rng.random(H)).astype(np.float32)
+    s = float(np.sum(row.astype(np.float64) ** 2))  # exact
+    d = _slack(H)
+    inv_lo = 1.0 / math.sqrt(s * (1.0 + d) / H + float(np.float32(eps)))
+    inv_hi = 1.0 / math.sqrt(s * (1.0 - d) / H + float(np.float32(eps)))
+    # candidate gammas: every float in [1, 2).  Every x here is a power of
+    # two, so x * inv * g scales inv * g exactly and rounds like it.
+    g = 1.0 + np.arange(1 << 23, dtype=np.float64) * 2.0 ** -23
+    hits = np.nonzero((inv_lo * g).astype(np.float32) != (inv_hi * g).astype(np.float32))[0]
+    assert hits.size >= 32, "too few unsettled gammas for this row"
+    picked = []
+    for blk in range(32):
+        i = blk * (H // 32) + int(rng.integers(H // 32))
+        gamma[i] = np.float32(g[hits[int(rng.integers(hits.size))]])
+        picked.append(i)
+    return row, gamma, picked
+
+
+@pytest.fixture(scope="module")
+def layer():
+    payload, scale, zp = synth.expert_layer(91, 0, E, H, I, True)
+    return DeviceExpertLayer(payload, scale, zp, H, I)
+
+
+def _layer_forward(block, h, gamma, w, flags):
+    import torch
+    T = h.shape[0]
+    P = T * block.top_k
+    normed = torch.full((T, H), float("nan"), dtype=torch.float32, device="cuda")
+    out = torch.full((T, H), float("nan"), dtype=torch.float32, device="cuda")
+    ids = torch.full((T, block.top_k), -1, dtype=torch.int32, device="cuda")
+    scores = torch.empty((T, block.top_k), dtype=torch.float32, device="cuda")
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    need = capi.load().hm_moe_block_workspace_bytes(C.byref(block.layer.desc), T, block.top_k,
+                                                    block.limbs_x, block.limbs_z,
+                                                    block.flags | flags)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    io = capi.HmBlockIO(out.data_ptr(), ids.data_ptr(), scores.data_ptr(), None, None, None,
+                        None, None, status.data_ptr(), None)
+    capi.call("hm_moe_layer_forward", C.byref(block.layer.desc), h.data_ptr(), gamma.data_ptr(),
+              EPS, normed.data_ptr(), w.data_ptr(), T, block.top_k, block.flags | flags,
+              block.limbs_x, block.limbs_z, C.byref(io), ws.data_ptr(), ws.numel(),
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    assert P == ids.numel()
+    return normed.cpu().numpy(), ids.cpu().numpy().view(np.uint32), out.cpu().numpy()
+
+
+@pytest.mark.parametrize("T", [1, 2, 5, 16, 40])
+@pytest.mark.parametrize("seq", [False, True])
+def test_layer_forward_matches_norm_then_block(dev, layer, T, seq):
+    import torch
+    print(f"[gpu] layer forward T={T} seq={seq}", flush=True)
+    rng = np.random.default_rng(1000 + T)
+    row0, gamma, picked = _unsettled_row(rng, EPS)
+    h = rng.standard_normal((T, H)).astype(np.float32)
+    h[0] = row0
+    w = synth.router_weights(91, 0, H, E)
+    dh, dg, dw = (torch.from_numpy(a).cuda() for a in (h, gamma, w))
+    block = MoEBlock(layer, K)
+    flags = capi.HM_EXEC_ROUTE_SEQUENTIAL if seq else 0
+    normed, ids, out = _layer_forward(block, dh, dg, dw, flags)
+    # the normalised rows: the oracle's RMSNorm, bit for bit (row 0's
+    # unsettled elements included)
+    ref_norm = O.rmsnorm(h, gamma, EPS)
+    assert_bitexact(normed, ref_norm, f"T={T} RMSNorm")
+    assert_bitexact(normed[0, picked], ref_norm[0, picked], f"T={T} unsettled elements")
+    # hm_rmsnorm on the device, then the block with h as the residual
+    dn = torch.empty_like(dh)
+    capi.call("hm_rmsnorm", dh.data_ptr(), dg.data_ptr(), dn.data_ptr(), T, H, EPS,
+              torch.cuda.current_stream().cuda_stream)
+    ref = block.execute_batch(dn, dw, residual=dh, exec_flags=flags)
+    assert_bitexact(dn.cpu().numpy(), ref_norm, f"T={T} hm_rmsnorm")
+    assert_bitexact(ids, ref.ids, f"T={T} routing")
+    assert_bitexact(out, ref.output.cpu().numpy(), f"T={T} output")
+
+
+def test_layer_forward_rejects_overlap(dev, layer):
+    """normed overlapping h, or a residual other than h, is refused before
+    anything runs."""
+    import torch
+    block = MoEBlock(layer, K)
+    T = 2
+    h = torch.randn((T, H), dtype=torch.float32, device="cuda")
+    g = torch.ones(H, dtype=torch.float32, device="cuda")
+    w = torch.from_numpy(synth.router_weights(91, 0, H, E)).cuda()
+    out = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    other = torch.empty((T, H), dtype=torch.float32, device="cuda")
+    need = capi.load().hm_moe_block_workspace_bytes(C.byref(layer.desc), T, K, 2, 3, 0)
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    lib = capi.load()
+    s = torch.cuda.current_stream().cuda_stream
+    for normed_ptr, residual in ((h.data_ptr() + 4 * H, None), (other.data_ptr(), out.data_ptr())):
+        io = capi.HmBlockIO(out.data_ptr(), None, None, None, None, None, None, None, None,
+                            residual)
+        rc = lib.hm_moe_layer_forward(C.byref(layer.desc), h.data_ptr(), g.data_ptr(), EPS,
+                                      normed_ptr, w.data_ptr(), T, K, 0, 2, 3, C.byref(io),
+                                      ws.data_ptr(), ws.numel(), s)
+        assert rc == capi.HM_ERR_INVALID
+    torch.cuda.synchronize()
