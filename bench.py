@@ -346,7 +346,7 @@ def main():
         achieved = gu_ops / gu_s / 1e12
         peak = PEAK_INT8_TOPS if cfg.int8 else PEAK_FP32_TFLOPS
         roof = {"bound": "mfma",
-                "kernel": ("gate/up stage: gateup_ring_kernel<Lx> (G, U) + "
+                "kernel": ("gate/up stage: ring_gemm_kernel<Lx, false> (G, U) + "
                            "limb_swiglu_quantize_vec_kernel<Lz, I/256> (SiLU(G)*U, Z digits)"
                            if cfg.int8 else "expert_f32_mfma_kernel<true>"),
                 "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
@@ -358,7 +358,7 @@ def main():
         roof = {"bound": "hbm",
                 "kernel": ("gate/up GEMV: gateup_slice_kernel<NG, LJ> (every token row in LDS) "
                            "or gemv_kernel<true, 1> (more than two tokens)" if gemv else
-                           "gate/up stage: gateup_ring_kernel<Lx> + "
+                           "gate/up stage: ring_gemm_kernel<Lx, false> + "
                            "limb_swiglu_quantize_vec_kernel<Lz, I/256>" if cfg.int8
                            else "expert_f32_mfma_kernel<true>"),
                 "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
@@ -368,7 +368,8 @@ def main():
         if gemv:
             kre = prim = "gateup_slice_kernel|gemv_kernel<true"
         elif cfg.int8:
-            kre, prim = "gateup_ring_kernel|limb_swiglu_quantize", "gateup_ring_kernel"
+            kre, prim = ("ring_gemm_kernel<[0-9], false>|limb_swiglu_quantize",
+                         "ring_gemm_kernel<[0-9], false>")
         else:
             kre = prim = "expert_f32_mfma_kernel<true>"
         tr = pmc_traffic(cfg.name, kre, prim, (args.limbs_x, args.limbs_z), q)
@@ -376,7 +377,8 @@ def main():
             roof["traffic"] = tr.pop("bytes")
             roof["traffic_detail"] = tr
         if prefill and cfg.int8:
-            hw = pmc_mfma(cfg.name, {"gate_up": "gateup_ring_kernel", "down": "limb_gemm_kernel"},
+            hw = pmc_mfma(cfg.name, {"gate_up": "ring_gemm_kernel<[0-9], false>",
+                                     "down": "ring_gemm_kernel<[0-9], true>|limb_gemm_kernel"},
                           (args.limbs_x, args.limbs_z), q)
             if hw is not None:
                 roof["hw_mfma"] = hw

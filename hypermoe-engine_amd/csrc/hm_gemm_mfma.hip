@@ -13,17 +13,19 @@
 // 32-wide step; its 16 int32 results are column l % 32, rows
 // 8 (v / 4) + 4 (l / 32) + v % 4 (v = 0..15).
 //
-// Two persistent kernels, one workgroup per CU:
-//   gate/up  gateup_ring_kernel: 8 wave64s (two per SIMD), A (the token
-//            rows' X digit planes, gathered by perm_tokens) and B both
+// Persistent kernels, one workgroup per CU:
+//   ring_gemm_kernel<L, false> (gate/up): 8 wave64s (two per SIMD), A (the
+//            token rows' X digit planes, gathered by perm_tokens) and B both
 //            staged through an LDS ring by DMA; epilogue g and u -> floats
 //            (the SwiGLU runs in the Z quantisation pass, hm_gemm.hip).
-//   down     limb_gemm_kernel: 4 wave64s (one per SIMD, 512 registers: the
-//            accumulators take the AGPRs), A (the grouped rows' Z digit
-//            planes) through an LDS ring by DMA, B straight into a register
-//            ring; epilogue y -> floats.
+//   ring_gemm_kernel<L, true> (down): the same kernel on the grouped rows'
+//            Z digit planes and the down tiles; epilogue y -> floats.
+//   limb_gemm_kernel (down, for shapes the ring does not take): 4 wave64s
+//            (one per SIMD, 512 registers: the accumulators take the
+//            AGPRs), A through an LDS ring by DMA, B straight into a
+//            register ring.
 //
-// down, per stage of K = 128 bytes (four MFMA K steps):
+// limb_gemm_kernel, per stage of K = 128 bytes (four MFMA K steps):
 //   A  global -> LDS by 16-byte buffer loads to LDS (inline asm), 128-byte
 //      row chunks (whole cache lines), into a ring of kSA stages.  Each row's
 //      eight 16-byte chunks are stored rotated by (row >> 1) & 7, so the
@@ -777,7 +779,9 @@ template <int L>
 int launch_l(const hm_layer* layer, const int8_t* adig, const float* ascale,
              const int32_t* adsum, int64_t arows, const int32_t* counts, const int32_t* offsets,
              float* out, bool split_k, hipStream_t stream) {
-    if (ring_depth(layer->intermediate / kKS) == 0) return HM_ERR_UNSUPPORTED;
+    if (!shape_ok(layer->intermediate, layer->hidden, layer->experts, L) ||
+        ring_depth(layer->intermediate / kKS) == 0)
+        return HM_ERR_UNSUPPORTED;
     // skinny groups (split K, when asked for), then the tiles of the others
     const bool sk = split_k && skinny_ok(layer->intermediate, layer->hidden, L, false);
     if (sk) {
@@ -844,8 +848,13 @@ struct GateUpTile {
     static constexpr int STAGE = NF * kGuFrag;
 };
 
-template <int L>
-__global__ __launch_bounds__(kGuThreads) void gateup_ring_kernel(
+// DN = false: gate/up, A = X digit planes [L][arows = T][K = H] gathered
+// by perm_tokens, out = gu [R x 2I] (tile: 128 gate + 128 up columns).
+// DN = true: down, A = Z digit planes [L][arows = R][K = I] of the grouped
+// rows themselves, out = y [R x H] (tile: 256 down columns; the "gate" half
+// of the gate/up tile is its first 128 columns, the "up" half the next).
+template <int L, bool DN>
+__global__ __launch_bounds__(kGuThreads) void ring_gemm_kernel(
     const int8_t* __restrict__ xdig, const float* __restrict__ xscale,
     const int32_t* __restrict__ xdsum, int tokens, int H, int I, int experts,
     const int8_t* __restrict__ packed, const float* __restrict__ scale,
@@ -853,6 +862,13 @@ __global__ __launch_bounds__(kGuThreads) void gateup_ring_kernel(
     const int32_t* __restrict__ offsets, const int32_t* __restrict__ perm_tokens, int skinny,
     float* __restrict__ gu) {
     using T = GateUpTile<L>;
+    // inner and output dimensions of the projection(s), output columns per
+    // tile, the out row stride and the offset of the tile's second half
+    const int K = DN ? I : H, N = DN ? H : I;
+    constexpr int TN = DN ? 2 * kGuN : kGuN;
+    const int64_t ldo = DN ? (int64_t)N : 2 * (int64_t)N;
+    const int half = DN ? kGuN : N;
+    constexpr int PG = DN ? 2 : 0, PU = DN ? 2 : 1;  // the halves' projections
     constexpr int BM = T::BM, NA = T::NA, NL = T::NL, LPW = T::LPW, WR = T::WR, WCP = T::WCP,
                   NWC = T::NWC, STAGE = T::STAGE;
     constexpr int RW = BM / HM_WAVE;  // waves that move one value per tile row
@@ -873,19 +889,19 @@ __global__ __launch_bounds__(kGuThreads) void gateup_ring_kernel(
     for (int e = tid; e < E; e += kGuThreads) {
         s_cnt[e] = counts[e];
         s_off[e] = offsets[e];
-        s_sg[e] = scale[3 * e + 0];
-        s_su[e] = scale[3 * e + 1];
-        s_zg[e] = zp[3 * e + 0];
-        s_zu[e] = zp[3 * e + 1];
+        s_sg[e] = scale[3 * e + PG];
+        s_su[e] = scale[3 * e + PU];
+        s_zg[e] = zp[3 * e + PG];
+        s_zu[e] = zp[3 * e + PU];
     }
     __syncthreads();
     if (wave == 0) tile_prefix(s_cnt, E, BM, skinny, s_prefix);
     __syncthreads();
-    const int nbn = I / kGuN;
+    const int nbn = N / TN;
     const TileRange tr = tile_range(s_prefix[E] * nbn);
     if (tr.ntiles == 0) return;
-    const int nk = H / kGuKB;
-    const int64_t tiles_k = hm_pad32(H) / 32;  // K tiles of one 32-column block
+    const int nk = K / kGuKB;
+    const int64_t tiles_k = hm_pad32(K) / 32;  // K tiles of one 32-column block
 
     auto info = [&](int i) __attribute__((always_inline)) {
         const int j = tr.jbeg + i * tr.step;
@@ -895,14 +911,16 @@ __global__ __launch_bounds__(kGuThreads) void gateup_ring_kernel(
         const int mt = gm - s_prefix[t.e];
         t.g0 = s_off[t.e] + mt * BM;
         t.nrows = min(BM, s_cnt[t.e] - mt * BM);
-        t.n0 = (j % nbn) * kGuN;
+        t.n0 = (j % nbn) * TN;
         return t;
     };
-    // token ids of the tile rows (rows past nrows repeat the last row)
+    // A rows of the tile rows: their tokens (gate/up) or the grouped rows
+    // themselves (down); rows past nrows repeat the last row
     auto fetch_rows = [&](const TileInfo& t, int m) __attribute__((always_inline)) {
         if (wave < RW) {
             const int r = HM_WAVE * wave + lane;
-            dma4(perm_tokens + t.g0 + min(r, t.nrows - 1), &s_rt[m][HM_WAVE * wave]);
+            if constexpr (DN) s_rt[m][r] = t.g0 + min(r, t.nrows - 1);
+            else dma4(perm_tokens + t.g0 + min(r, t.nrows - 1), &s_rt[m][HM_WAVE * wave]);
         }
     };
     // activation scales and digit sums of those tokens (needs s_rt[m])
@@ -935,11 +953,12 @@ __global__ __launch_bounds__(kGuThreads) void gateup_ring_kernel(
             if (f < NA) {
                 const int l = f / (BM / 32), i = f % (BM / 32);
                 const int tok = s_rt[m][32 * i + gu_frag_load_row(lane, h)];
-                src[c] = xdig + ((int64_t)l * tokens + tok) * H + 16 * ch;
+                src[c] = xdig + ((int64_t)l * tokens + tok) * K + 16 * ch;
             } else {
                 const int fb = f - NA;
-                const int64_t cb = t.n0 / 32 + (fb & 3);
-                src[c] = packed + hm_proj_offset(t.e, fb >> 2, H, I) + (cb * tiles_k + h) * 1024 + 16 * lane;
+                const int64_t cb = t.n0 / 32 + (DN ? fb : (fb & 3));
+                src[c] = packed + hm_proj_offset(t.e, DN ? 2 : fb >> 2, H, I) +
+                         (cb * tiles_k + h) * 1024 + 16 * lane;
             }
         }
     };
@@ -1126,7 +1145,7 @@ __global__ __launch_bounds__(kGuThreads) void gateup_ring_kernel(
                         const float sx = t4 == 0 ? sx4.x : t4 == 1 ? sx4.y : t4 == 2 ? sx4.z : sx4.w;
                         const float fg = __fmul_rn(sx, sg), fu = __fmul_rn(sx, su);
                         const bool live = rq + t4 < nrows;
-                        float* grow = gu + (int64_t)(cur.g0 + rq + t4) * (2 * (int64_t)I) + cur.n0 +
+                        float* grow = gu + (int64_t)(cur.g0 + rq + t4) * ldo + cur.n0 +
                                       32 * wc * WCP + (lane & 31);
 #pragma unroll
                         for (int j = 0; j < WCP; ++j) {
@@ -1148,7 +1167,7 @@ __global__ __launch_bounds__(kGuThreads) void gateup_ring_kernel(
                             const float u = __fmul_rn(hm_recombine(pu, L), fu);
                             if (live) {
                                 grow[32 * j] = g;
-                                grow[I + 32 * j] = u;
+                                grow[half + 32 * j] = u;
                             }
                         }
                     }
@@ -1172,6 +1191,37 @@ bool gateup_shape_ok(int64_t H, int64_t I, int64_t E, int32_t limbs) {
            I <= (1 << 20) && H % kGuKB == 0 && H / kGuKB >= kGuStages && I % kGuN == 0;
 }
 
+// The down projection on the ring kernel: K = I in 64-byte stages, N = H in
+// 256-column tiles.
+bool down_ring_ok(int64_t H, int64_t I, int64_t E, int32_t limbs) {
+    return limbs >= 1 && limbs <= 3 && E >= 1 && E <= kMaxExperts && I <= 65536 &&
+           H <= (1 << 20) && I % kGuKB == 0 && I / kGuKB >= kGuStages && H % (2 * kGuN) == 0;
+}
+
+// Down: skinny groups (split K, when asked for), then the tiles of the
+// others on the ring kernel, or on limb_gemm_kernel where the ring's shape
+// conditions do not hold.
+template <int L>
+int launch_down(const hm_layer* layer, const int8_t* zdig, const float* zscale,
+                const int32_t* zdsum, int64_t R, const int32_t* counts, const int32_t* offsets,
+                float* y, bool split_k, hipStream_t stream) {
+    if (!down_ring_ok(layer->hidden, layer->intermediate, layer->experts, L))
+        return launch_l<L>(layer, zdig, zscale, zdsum, R, counts, offsets, y, split_k, stream);
+    const bool sk = split_k && skinny_ok(layer->intermediate, layer->hidden, L, false);
+    if (sk) {
+        const int rc = launch_skinny<L, false>(layer, zdig, zscale, zdsum, R, nullptr, counts,
+                                               offsets, y, stream, false);
+        if (rc) return rc;
+    }
+    hipLaunchKernelGGL((ring_gemm_kernel<L, true>), dim3((unsigned)persistent_grid()),
+                       dim3(kGuThreads), 0, stream, zdig, zscale, zdsum, (int)R,
+                       (int)layer->hidden, (int)layer->intermediate, (int)layer->experts,
+                       static_cast<const int8_t*>(layer->packed), layer->scale,
+                       layer->zero_point, counts, offsets, nullptr, sk ? kSkinnyRows : 0, y);
+    HM_LAUNCHED();
+    return HM_OK;
+}
+
 template <int L>
 int launch_gateup(const hm_layer* layer, const int8_t* xdig, const float* xscale,
                   const int32_t* xdsum, int64_t tokens, const int32_t* counts,
@@ -1185,7 +1235,7 @@ int launch_gateup(const hm_layer* layer, const int8_t* xdig, const float* xscale
                                               counts, offsets, gu, stream, true);
         if (rc) return rc;
     }
-    HM_STAGE_LAUNCH(!sk, false, gateup_ring_kernel<L>, dim3((unsigned)persistent_grid()),
+    HM_STAGE_LAUNCH(!sk, false, (ring_gemm_kernel<L, false>), dim3((unsigned)persistent_grid()),
                     dim3(kGuThreads), 0, stream, xdig, xscale, xdsum, (int)tokens,
                     (int)layer->hidden, (int)layer->intermediate, (int)layer->experts,
                     static_cast<const int8_t*>(layer->packed), layer->scale, layer->zero_point,
@@ -1204,7 +1254,7 @@ bool hm_mfma_gateup_ok(int64_t H, int64_t I, int64_t E, int32_t limbs) {
 }
 
 bool hm_mfma_down_ok(int64_t H, int64_t I, int64_t E, int32_t limbs) {
-    return shape_ok(I, H, E, limbs);
+    return down_ring_ok(H, I, E, limbs) || shape_ok(I, H, E, limbs);
 }
 
 // gu [R x 2I]: the gate and up values of every grouped row.  The first kernel of the
@@ -1230,9 +1280,9 @@ int hm_launch_down_i8_mfma(const hm_layer* layer, int32_t limbs, const int32_t* 
                            hipStream_t stream) {
     if (R > INT_MAX) return HM_ERR_OVERFLOW;
     switch (limbs) {
-    case 1: return launch_l<1>(layer, zdig, zscale, zdsum, R, counts, offsets, y, split_k, stream);
-    case 2: return launch_l<2>(layer, zdig, zscale, zdsum, R, counts, offsets, y, split_k, stream);
-    case 3: return launch_l<3>(layer, zdig, zscale, zdsum, R, counts, offsets, y, split_k, stream);
+    case 1: return launch_down<1>(layer, zdig, zscale, zdsum, R, counts, offsets, y, split_k, stream);
+    case 2: return launch_down<2>(layer, zdig, zscale, zdsum, R, counts, offsets, y, split_k, stream);
+    case 3: return launch_down<3>(layer, zdig, zscale, zdsum, R, counts, offsets, y, split_k, stream);
     default: return HM_ERR_INVALID;
     }
 }
