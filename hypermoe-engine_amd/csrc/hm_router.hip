@@ -623,36 +623,38 @@ __global__ __launch_bounds__(kBlock) void router_select_kernel(
 }
 
 // The stable counting sort of permute_count/scatter for at most
-// kSmallPairs pairs, by one workgroup (kBlock threads): counts and offsets
+// kSmallPairs pairs, by one workgroup (NT threads): counts and offsets
 // from an LDS histogram and a block scan, each pair's rank among the
 // earlier pairs of its expert by a scan of the ids in LDS.  Ids past the
 // expert count (left behind by a routing failure the status word reports)
 // are treated as the last expert so that every position stays in range.
 constexpr int kSmallPairs = 1024;
 
+template <int NT>
 __device__ void permute_small(const uint32_t* __restrict__ ids, const float* __restrict__ scores,
                               int pairs, int top_k, int experts, int32_t* __restrict__ counts,
                               int32_t* __restrict__ offsets, int32_t* __restrict__ perm_tokens,
                               float* __restrict__ perm_weights, int32_t* __restrict__ slots) {
+    constexpr int EPT = 1024 / NT;  // experts per thread in the scan (E <= 1024)
     __shared__ int s_cnt[1024];
     __shared__ int s_off[1024];
     __shared__ int s_ids[kSmallPairs];
-    __shared__ int s_wsum[kBlock / HM_WAVE];
+    __shared__ int s_wsum[NT / HM_WAVE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int i = tid; i < experts; i += kBlock) s_cnt[i] = 0;
+    for (int i = tid; i < experts; i += NT) s_cnt[i] = 0;
     __syncthreads();
-    for (int p = tid; p < pairs; p += kBlock) {
+    for (int p = tid; p < pairs; p += NT) {
         const uint32_t e = ids[p];
         const int ec = e < (uint32_t)experts ? (int)e : experts - 1;
         s_ids[p] = ec;
         atomicAdd(&s_cnt[ec], 1);
     }
     __syncthreads();
-    // exclusive scan over experts: thread tid owns experts 4*tid .. +3
-    int v[4], tot = 0;
+    // exclusive scan over experts: thread tid owns experts EPT*tid .. +EPT-1
+    int v[EPT], tot = 0;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int e = 4 * tid + q;
+    for (int q = 0; q < EPT; ++q) {
+        const int e = EPT * tid + q;
         v[q] = e < experts ? s_cnt[e] : 0;
         tot += v[q];
     }
@@ -667,8 +669,8 @@ __device__ void permute_small(const uint32_t* __restrict__ ids, const float* __r
     int base = incl - tot;
     for (int wv = 0; wv < wave; ++wv) base += s_wsum[wv];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int e = 4 * tid + q;
+    for (int q = 0; q < EPT; ++q) {
+        const int e = EPT * tid + q;
         if (e < experts) {
             s_off[e] = base;
             counts[e] = v[q];
@@ -678,7 +680,7 @@ __device__ void permute_small(const uint32_t* __restrict__ ids, const float* __r
         base += v[q];
     }
     __syncthreads();
-    for (int p = tid; p < pairs; p += kBlock) {
+    for (int p = tid; p < pairs; p += NT) {
         const int e = s_ids[p];
         int rank = 0;
         for (int q = 0; q < p; ++q) rank += s_ids[q] == e;
@@ -690,22 +692,25 @@ __device__ void permute_small(const uint32_t* __restrict__ ids, const float* __r
 }
 
 // Select over logits formed from the decode partials (and written to
-// `logits` too).  With PERMUTE the workgroup that finishes last (a device
-// counter, zeroed by router_partial_kernel) also sorts the pairs into
-// expert groups, which is hm_permute's result: one launch fewer per decode
-// step.
-template <int EPL, bool PERMUTE>
-__global__ __launch_bounds__(kBlock) void router_select_partial_kernel(
+// `logits` too), NW waves (tokens) per workgroup.  With PERMUTE the
+// workgroup that finishes last (a device counter, zeroed by
+// router_partial_kernel) also sorts the pairs into expert groups, which is
+// hm_permute's result: one launch fewer per decode step.  Each token reads
+// 2 kNB doubles per logit (64 KB at E = 128) that other CUs wrote, at the
+// few tens of GB/s one CU draws: the fused step gives every token a
+// workgroup (a CU) of its own once there are several.
+template <int EPL, bool PERMUTE, int NW>
+__global__ __launch_bounds__(NW * HM_WAVE) void router_select_partial_kernel(
     const float* __restrict__ h, const float* __restrict__ w, const double* __restrict__ part,
     int64_t tokens, int64_t hidden, int64_t experts, int32_t top_k, uint32_t flags,
     float* __restrict__ logits, uint32_t* __restrict__ ids, float* __restrict__ scores,
     int32_t* status, int32_t* __restrict__ done_ctr, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ perm_tokens,
     float* __restrict__ perm_weights, int32_t* __restrict__ slots) {
-    extern __shared__ float seq_lds[];  // (kBlock/64) * experts floats
+    extern __shared__ float seq_lds[];  // NW * experts floats
     const int lane = threadIdx.x & (HM_WAVE - 1);
     const int wave = threadIdx.x / HM_WAVE;
-    const int64_t t = (int64_t)blockIdx.x * (kBlock / HM_WAVE) + wave;
+    const int64_t t = (int64_t)blockIdx.x * NW + wave;
     const bool force_seq = (flags & HM_EXEC_ROUTE_SEQUENTIAL) != 0;
     if (t < tokens) {
         float v[EPL];
@@ -740,8 +745,8 @@ __global__ __launch_bounds__(kBlock) void router_select_partial_kernel(
         } else {
             __syncthreads();  // one workgroup: its own ids and scores
         }
-        permute_small(ids, scores, (int)(tokens * top_k), top_k, (int)experts, counts, offsets,
-                      perm_tokens, perm_weights, slots);
+        permute_small<NW * HM_WAVE>(ids, scores, (int)(tokens * top_k), top_k, (int)experts,
+                                    counts, offsets, perm_tokens, perm_weights, slots);
     }
 }
 
@@ -1493,8 +1498,10 @@ static int launch_decode_router(const float* h, const float* w, int64_t tokens, 
                                 const hm_decode_fusion* fused, const hm_norm_fold* norm,
                                 void* stream) {
     const int epl = (int)((experts + HM_WAVE - 1) / HM_WAVE);
-    const dim3 sgrid((unsigned)((tokens + 3) / 4));
-    const size_t seq_bytes = (size_t)(kBlock / HM_WAVE) * experts * sizeof(float);
+    // fused with several tokens: one wave (token) per workgroup; else four
+    const int nw = fused && tokens > 1 ? 1 : 4;
+    const dim3 sgrid((unsigned)((tokens + nw - 1) / nw));
+    const size_t seq_bytes = (size_t)nw * experts * sizeof(float);
     double* part = reinterpret_cast<double*>(static_cast<char*>(route_ws) +
                                              route_logits_bytes(tokens, experts));
     const dim3 pgrid((unsigned)kNB, (unsigned)((experts + HM_WAVE - 1) / HM_WAVE),
@@ -1506,14 +1513,19 @@ static int launch_decode_router(const float* h, const float* w, int64_t tokens, 
     HM_LAUNCHED();
     // the select kernel's fallback chains read the normalised rows
     if (norm) h = norm->x_out;
-#define HM_SELECTP(N, F)                                                                   \
-    hipLaunchKernelGGL((router_select_partial_kernel<N, F>), sgrid, dim3(kBlock), seq_bytes, \
-                       hm_stream(stream), h, w, part, tokens, hidden, experts, top_k, flags, \
-                       logits, ids, scores, status, F ? fused->counters : nullptr,            \
-                       F ? fused->counts : nullptr, F ? fused->offsets : nullptr,            \
-                       F ? fused->perm_tokens : nullptr, F ? fused->perm_weights : nullptr,  \
-                       F ? fused->slots : nullptr)
-#define HM_SELECTP2(N) do { if (fused) HM_SELECTP(N, true); else HM_SELECTP(N, false); } while (0)
+#define HM_SELECTP(N, F, W)                                                                \
+    hipLaunchKernelGGL((router_select_partial_kernel<N, F, W>), sgrid, dim3(W * HM_WAVE),    \
+                       seq_bytes, hm_stream(stream), h, w, part, tokens, hidden, experts,    \
+                       top_k, flags, logits, ids, scores, status,                            \
+                       F ? fused->counters : nullptr, F ? fused->counts : nullptr,           \
+                       F ? fused->offsets : nullptr, F ? fused->perm_tokens : nullptr,       \
+                       F ? fused->perm_weights : nullptr, F ? fused->slots : nullptr)
+#define HM_SELECTP2(N)                                  \
+    do {                                                \
+        if (!fused) HM_SELECTP(N, false, 4);            \
+        else if (nw == 1) HM_SELECTP(N, true, 1);       \
+        else HM_SELECTP(N, true, 4);                    \
+    } while (0)
     if (epl <= 1) HM_SELECTP2(1);
     else if (epl <= 2) HM_SELECTP2(2);
     else if (epl <= 4) HM_SELECTP2(4);
