@@ -41,10 +41,19 @@ __device__ __forceinline__ double hm_rms_sum_slack(int64_t width) {
     return 4.0 * gam / (1.0 - gam);
 }
 
-// The reference's own sum: double(x_k)^2 added in ascending k from +0.
+// The reference's own sum: double(x_k)^2 added in ascending k from +0
+// (the values read 16 at a time, so that the reads overlap the additions).
 __device__ __forceinline__ double hm_rms_sum_seq(const float* __restrict__ xr, int64_t width) {
     double s = 0.0;
-    for (int64_t i = 0; i < width; ++i) {
+    int64_t i = 0;
+    for (; i + 16 <= width; i += 16) {
+        float r[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) r[u] = xr[i + u];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) s += (double)r[u] * r[u];
+    }
+    for (; i < width; ++i) {
         const float v = xr[i];
         s += (double)v * v;
     }
@@ -362,6 +371,7 @@ constexpr int kPK = 64;  // k per LDS chunk of a block
 __global__ __launch_bounds__(64) void router_partial_kernel(
     const float* __restrict__ h, const float* __restrict__ w, int hidden, int experts,
     double* __restrict__ part, int32_t* __restrict__ zero_ctr, int n_zero, hm_norm_fold norm) {
+    extern __shared__ float s_row[];  // with the norm: the row (hidden floats)
     __shared__ double s_h[kPK];                                        // broadcast reads
     __shared__ __attribute__((aligned(1024))) float s_w[kPK][HM_WAVE];  // [k][lane]
     const int lane = threadIdx.x;
@@ -383,6 +393,7 @@ __global__ __launch_bounds__(64) void router_partial_kernel(
     const bool row4 = hidden % 256 == 0 && hidden <= 16 * 256 && (uintptr_t)h % 16 == 0;
     double inv_lo = 0.0, inv_hi = 0.0, inv_seq = 0.0;
     bool have_seq = false;
+    float4 v[16];  // the row (row4): kept for an LDS copy if the sequential sum is needed
     double acc = 0.0, rs = 0.0, qs = 0.0;
     for (int c0 = 0; c0 < b; c0 += kPK) {
         const int kc = min(kPK, b - c0);
@@ -405,7 +416,6 @@ __global__ __launch_bounds__(64) void router_partial_kernel(
                 if (row4) {
                     const float4* r4 = reinterpret_cast<const float4*>(hrow);
                     const int n4 = hidden >> 8;
-                    float4 v[16];
 #pragma unroll
                     for (int i = 0; i < 16; ++i) v[i] = r4[lane + HM_WAVE * min(i, n4 - 1)];
 #pragma unroll
@@ -418,6 +428,7 @@ __global__ __launch_bounds__(64) void router_partial_kernel(
                     for (int i = lane; i < hidden; i += HM_WAVE) {
                         const float v = hrow[i];
                         ss += (double)v * v;
+                        s_row[i] = v;
                     }
                 }
                 const double s_fast = hm_wave_sum_f64(ss);
@@ -430,7 +441,16 @@ __global__ __launch_bounds__(64) void router_partial_kernel(
             const float a = (float)((double)hv * inv_lo * g);
             const float bb = (float)((double)hv * inv_hi * g);
             if (!have_seq && (norm.force_seq || __any(__float_as_uint(a) != __float_as_uint(bb)))) {
-                inv_seq = hm_inv_rms(hm_rms_sum_seq(hrow, hidden), (double)hidden, (double)norm.eps);
+                // the sequential sum over the row's LDS copy (every lane
+                // the same, broadcast reads)
+                if (row4) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        if (i < (hidden >> 8)) reinterpret_cast<float4*>(s_row)[lane + HM_WAVE * i] = v[i];
+                }
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                inv_seq = hm_inv_rms(hm_rms_sum_seq(s_row, hidden), (double)hidden, (double)norm.eps);
                 have_seq = true;
             }
             hv = have_seq ? (float)((double)hv * inv_seq * g) : a;
@@ -459,14 +479,12 @@ __global__ __launch_bounds__(64) void router_partial_kernel(
     }
 }
 
-// One logit from its block partials (see above), or from the sequential
-// chain when the bound does not settle the float.  pp: this logit's
-// [B_0 .. B_31, C_0 .. C_31] (part + (t*E + e) * 2 * kNB).
-__device__ __forceinline__ float certified_logit(const double* __restrict__ pp,
-                                                 const float* __restrict__ hrow,
-                                                 const float* __restrict__ wcol, int64_t hidden,
-                                                 int64_t experts, bool force_seq,
-                                                 int32_t* status) {
+// One logit from its block partials (see above); *settled is false when
+// the bound does not settle the float (the caller then runs the sequential
+// chain).  pp: this logit's [B_0 .. B_31, C_0 .. C_31] (part + (t*E + e) *
+// 2 * kNB).
+__device__ __forceinline__ float block_logit(const double* __restrict__ pp, int64_t hidden,
+                                             bool force_seq, bool* settled) {
     // all 64 values in 32 vector loads, then the dependent chain
     double2 bv[kNB / 2], cv[kNB / 2];
 #pragma unroll
@@ -484,12 +502,50 @@ __device__ __forceinline__ float certified_logit(const double* __restrict__ pp,
         sc += cv[i].x;
         sc += cv[i].y;
     }
-    if (!force_seq && block_sums_settle(a, sa, sc, hidden)) return (float)a;
-    double acc = 0.0;
-    for (int64_t k = 0; k < hidden; ++k)
-        acc = __builtin_fma((double)hrow[k], (double)wcol[k * experts], acc);
-    if (!isfinite(acc)) hm_status_or(status, HM_STATUS_NONFINITE_SCORE);
-    return (float)acc;
+    *settled = !force_seq && block_sums_settle(a, sa, sc, hidden);
+    return (float)a;
+}
+
+// The reference's sequential chain s_k = fl(s_{k-1} + h_k w_k) (the
+// product is exact in double, so fl(s + p) = fma(h, w, s)) for the logit of
+// expert e0 + lane of every lane whose bit is set in `need`, one logit at a time:
+// the whole wave forms 64 exact products at once into LDS (prod: 64
+// doubles of this wave) and the owning lane adds them in order, 16 reads
+// ahead of its additions.  hidden % 16 == 0.  Returns the owning lane's
+// float logit (others: v unchanged).
+__device__ __forceinline__ float chain_logits(unsigned long long need, int lane, float v, int64_t e0,
+                                              const float* __restrict__ hrow,
+                                              const float* __restrict__ w, int64_t hidden,
+                                              int64_t experts, double* prod, int32_t* status) {
+    while (need) {
+        const int owner = __ffsll((long long)need) - 1;
+        need &= need - 1;
+        const int64_t eo = e0 + owner;
+        double acc = 0.0;
+        for (int64_t c0 = 0; c0 < hidden; c0 += HM_WAVE) {
+            const int64_t k = min(c0 + lane, hidden - 1);
+            const double p = (double)hrow[k] * (double)w[k * experts + eo];
+            __builtin_amdgcn_wave_barrier();
+            prod[lane] = p;
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            if (lane == owner) {
+                const int n = (int)min((int64_t)HM_WAVE, hidden - c0);
+                for (int i = 0; i < n; i += 16) {
+                    double r[16];
+#pragma unroll
+                    for (int u = 0; u < 16; ++u) r[u] = prod[i + u];
+#pragma unroll
+                    for (int u = 0; u < 16; ++u) acc += r[u];
+                }
+            }
+        }
+        if (lane == owner) {
+            if (!isfinite(acc)) hm_status_or(status, HM_STATUS_NONFINITE_SCORE);
+            v = (float)acc;
+        }
+    }
+    return v;
 }
 
 // ---------------------------------------------------------------------------
@@ -708,6 +764,7 @@ __global__ __launch_bounds__(NW * HM_WAVE) void router_select_partial_kernel(
     int32_t* __restrict__ offsets, int32_t* __restrict__ perm_tokens,
     float* __restrict__ perm_weights, int32_t* __restrict__ slots) {
     extern __shared__ float seq_lds[];  // NW * experts floats
+    __shared__ double s_prod[NW][HM_WAVE];
     const int lane = threadIdx.x & (HM_WAVE - 1);
     const int wave = threadIdx.x / HM_WAVE;
     const int64_t t = (int64_t)blockIdx.x * NW + wave;
@@ -720,11 +777,13 @@ __global__ __launch_bounds__(NW * HM_WAVE) void router_select_partial_kernel(
             const int64_t e = lane + (int64_t)HM_WAVE * j;
             valid[j] = e < experts;
             v[j] = 0.0f;
-            if (valid[j]) {
-                v[j] = certified_logit(part + (t * experts + e) * 2 * kNB, h + t * hidden,
-                                       w + e, hidden, experts, force_seq, status);
-                logits[t * experts + e] = v[j];
-            }
+            bool settled = true;
+            if (valid[j]) v[j] = block_logit(part + (t * experts + e) * 2 * kNB, hidden, force_seq, &settled);
+            // the logits the bound leaves open: the reference's chain
+            v[j] = chain_logits(__ballot(valid[j] && !settled), lane, v[j], (int64_t)HM_WAVE * j,
+                                h + t * hidden, w,
+                                hidden, experts, s_prod[wave], status);
+            if (valid[j]) logits[t * experts + e] = v[j];
         }
         select_token<EPL>(v, valid, lane, wave, t, experts, top_k, flags, ids, scores, status,
                           seq_lds);
@@ -1507,7 +1566,8 @@ static int launch_decode_router(const float* h, const float* w, int64_t tokens, 
     const dim3 pgrid((unsigned)kNB, (unsigned)((experts + HM_WAVE - 1) / HM_WAVE),
                      (unsigned)tokens);
     const hm_norm_fold nf = norm ? *norm : hm_norm_fold{nullptr, nullptr, 0.0f, 0};
-    hipLaunchKernelGGL(router_partial_kernel, pgrid, dim3(HM_WAVE), 0, hm_stream(stream), h, w,
+    hipLaunchKernelGGL(router_partial_kernel, pgrid, dim3(HM_WAVE),
+                       norm ? (size_t)hidden * sizeof(float) : 0, hm_stream(stream), h, w,
                        (int)hidden, (int)experts, part, fused ? fused->counters : nullptr,
                        fused ? fused->n_counters : 0, nf);
     HM_LAUNCHED();
