@@ -1609,8 +1609,9 @@ int hm_route_permute_decode(const float* h, const float* w, int64_t tokens, int6
                             void* stream) {
     HM_REQUIRE(experts > 0 && top_k > 0 && top_k <= experts && fused && fused->counters);
     HM_REQUIRE(h && w && ids && scores && route_ws && tokens > 0 && hidden > 0);
+    // (the norm's row copy is hidden floats of LDS, as in hm_rmsnorm)
     HM_REQUIRE(!norm || (norm->gamma && norm->x_out && std::isfinite(norm->eps) &&
-                         norm->eps > 0.0f));
+                         norm->eps > 0.0f && hidden <= 16384));
     if (experts > 1024 || top_k > kMaxTopK || tokens > kDecodeTokens || hidden % kNB != 0 ||
         tokens * top_k > kSmallPairs || hidden > INT_MAX)
         return HM_ERR_UNSUPPORTED;
