@@ -352,8 +352,9 @@ __device__ __forceinline__ bool block_sums_settle(double a, double sa, double sc
     return isfinite(lo) && isfinite(hi) && __float_as_uint((float)lo) == __float_as_uint((float)hi);
 }
 
-// part[t][e][c][j], c = 0, 1: B_j, C_j (block-minor, so that the select
-// kernel's lane reads its logit's blocks as contiguous 16-byte vectors);
+// part[t][e][j][c], c = 0, 1: B_j, C_j (block-minor, so that the select
+// kernel's lane reads its logit's blocks as contiguous 16-byte vectors,
+// one block's pair in each);
 // grid (kNB, ceil(E/64), T), one wave, lane = expert.  The block's W rows
 // (64 experts wide) go to LDS in one burst of 16-byte DMA loads
 // (E % 64 == 0, b % 4 == 0, w 16-byte aligned), else per lane.
@@ -473,34 +474,35 @@ __global__ __launch_bounds__(64) void router_partial_kernel(
         }
     }
     if (live) {
-        double* o = part + ((int64_t)t * experts + e) * 2 * kNB + j;
-        o[0] = acc;
-        o[kNB] = block_c_term(rs, qs, hidden);
+        double2* o = reinterpret_cast<double2*>(part + ((int64_t)t * experts + e) * 2 * kNB) + j;
+        *o = make_double2(acc, block_c_term(rs, qs, hidden));
     }
 }
 
 // One logit from its block partials (see above); *settled is false when
 // the bound does not settle the float (the caller then runs the sequential
-// chain).  pp: this logit's [B_0 .. B_31, C_0 .. C_31] (part + (t*E + e) *
+// chain).  pp: this logit's [B_0, C_0, B_1, C_1 .. B_31, C_31] (part + (t*E + e) *
 // 2 * kNB).
 __device__ __forceinline__ float block_logit(const double* __restrict__ pp, int64_t hidden,
                                              bool force_seq, bool* settled) {
-    // all 64 values in 32 vector loads, then the dependent chain
-    double2 bv[kNB / 2], cv[kNB / 2];
+    // all 64 values in 32 vector loads (each block's B_j and C_j in one,
+    // so that both sums need every load), then the dependent chain
+    typedef int hm_i4 __attribute__((ext_vector_type(4)));
+    hm_i4 raw[kNB];
 #pragma unroll
-    for (int i = 0; i < kNB / 2; ++i) {
-        bv[i] = reinterpret_cast<const double2*>(pp)[i];
-        cv[i] = reinterpret_cast<const double2*>(pp + kNB)[i];
-    }
+    for (int i = 0; i < kNB; ++i) raw[i] = reinterpret_cast<const hm_i4*>(pp)[i];
+    // (every load goes out before the first is used: otherwise the compiler
+    // splits each pair and issues the C halves only after the B chain)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < kNB; ++i) asm volatile("" : "+v"(raw[i]));
     double a = 0.0, sa = 0.0, sc = 0.0;
 #pragma unroll
-    for (int i = 0; i < kNB / 2; ++i) {
-        a += bv[i].x;
+    for (int i = 0; i < kNB; ++i) {
+        const double2 bc = __builtin_bit_cast(double2, raw[i]);
+        a += bc.x;
         sa += fabs(a);
-        a += bv[i].y;
-        sa += fabs(a);
-        sc += cv[i].x;
-        sc += cv[i].y;
+        sc += bc.y;
     }
     *settled = !force_seq && block_sums_settle(a, sa, sc, hidden);
     return (float)a;
@@ -569,10 +571,16 @@ __device__ __forceinline__ float chain_logits(unsigned long long need, int lane,
 // follow on the stream stay in range.
 __device__ __forceinline__ void select_failed(int lane, int64_t t, int32_t top_k,
                                               uint32_t* __restrict__ ids,
-                                              float* __restrict__ scores) {
+                                              float* __restrict__ scores,
+                                              uint32_t* l_ids = nullptr,
+                                              float* l_scores = nullptr) {
     if (lane < top_k) {
         ids[t * top_k + lane] = (uint32_t)lane;
         scores[t * top_k + lane] = 0.0f;
+        if (l_ids) {
+            l_ids[lane] = (uint32_t)lane;
+            l_scores[lane] = 0.0f;
+        }
     }
 }
 
@@ -581,7 +589,9 @@ __device__ __forceinline__ void select_token(float (&v)[EPL], const bool (&valid
                                              int wave, int64_t t, int64_t experts, int32_t top_k,
                                              uint32_t flags, uint32_t* __restrict__ ids,
                                              float* __restrict__ scores, int32_t* status,
-                                             float* seq_lds) {
+                                             float* seq_lds, uint32_t* l_ids = nullptr,
+                                             float* l_scores = nullptr) {
+    // (l_ids, l_scores: optional LDS copies of this token's ids and scores)
     if (flags & HM_ROUTE_SOFTMAX) {
         float m = -__uint_as_float(0x7f800000u);
 #pragma unroll
@@ -611,7 +621,7 @@ __device__ __forceinline__ void select_token(float (&v)[EPL], const bool (&valid
         }
         if (!(isfinite(den) && den > 0.0)) {
             if (lane == 0) hm_status_or(status, HM_STATUS_SOFTMAX_FAILED);
-            select_failed(lane, t, top_k, ids, scores);
+            select_failed(lane, t, top_k, ids, scores, l_ids, l_scores);
             return;
         }
 #pragma unroll
@@ -645,7 +655,7 @@ __device__ __forceinline__ void select_token(float (&v)[EPL], const bool (&valid
     if (flags & HM_ROUTE_RENORM) {
         if (!(isfinite(sel_sum) && sel_sum != 0.0)) {
             if (lane == 0) hm_status_or(status, HM_STATUS_RENORM_FAILED);
-            select_failed(lane, t, top_k, ids, scores);
+            select_failed(lane, t, top_k, ids, scores, l_ids, l_scores);
             return;
         }
         my_score = (float)((double)my_score / sel_sum);
@@ -653,6 +663,10 @@ __device__ __forceinline__ void select_token(float (&v)[EPL], const bool (&valid
     if (lane < top_k) {
         ids[t * top_k + lane] = my_id;
         scores[t * top_k + lane] = my_score;
+        if (l_ids) {
+            l_ids[lane] = my_id;
+            l_scores[lane] = my_score;
+        }
     }
 }
 
@@ -765,28 +779,40 @@ __global__ __launch_bounds__(NW * HM_WAVE) void router_select_partial_kernel(
     float* __restrict__ perm_weights, int32_t* __restrict__ slots) {
     extern __shared__ float seq_lds[];  // NW * experts floats
     __shared__ double s_prod[NW][HM_WAVE];
+    // one workgroup: the grouping reads the ids and scores from LDS copies
+    __shared__ uint32_t s_sel_ids[PERMUTE ? NW * 64 : 1];
+    __shared__ float s_sel_sc[PERMUTE ? NW * 64 : 1];
+    const bool local = PERMUTE && gridDim.x == 1;
     const int lane = threadIdx.x & (HM_WAVE - 1);
     const int wave = threadIdx.x / HM_WAVE;
     const int64_t t = (int64_t)blockIdx.x * NW + wave;
     const bool force_seq = (flags & HM_EXEC_ROUTE_SEQUENTIAL) != 0;
     if (t < tokens) {
         float v[EPL];
-        bool valid[EPL];
+        bool valid[EPL], settled[EPL];
+        // every logit's block sums first (lanes past the experts read the
+        // last expert's: no branch around the loads)
 #pragma unroll
         for (int j = 0; j < EPL; ++j) {
             const int64_t e = lane + (int64_t)HM_WAVE * j;
             valid[j] = e < experts;
-            v[j] = 0.0f;
-            bool settled = true;
-            if (valid[j]) v[j] = block_logit(part + (t * experts + e) * 2 * kNB, hidden, force_seq, &settled);
-            // the logits the bound leaves open: the reference's chain
-            v[j] = chain_logits(__ballot(valid[j] && !settled), lane, v[j], (int64_t)HM_WAVE * j,
-                                h + t * hidden, w,
-                                hidden, experts, s_prod[wave], status);
-            if (valid[j]) logits[t * experts + e] = v[j];
+            const int64_t ec = valid[j] ? e : experts - 1;
+            v[j] = block_logit(part + (t * experts + ec) * 2 * kNB, hidden, force_seq, &settled[j]);
+            if (!valid[j]) {
+                v[j] = 0.0f;
+                settled[j] = true;
+            }
+        }
+        // then the logits the bound leaves open: the reference's chain
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            v[j] = chain_logits(__ballot(valid[j] && !settled[j]), lane, v[j], (int64_t)HM_WAVE * j,
+                                h + t * hidden, w, hidden, experts, s_prod[wave], status);
+            if (valid[j]) logits[t * experts + lane + (int64_t)HM_WAVE * j] = v[j];
         }
         select_token<EPL>(v, valid, lane, wave, t, experts, top_k, flags, ids, scores, status,
-                          seq_lds);
+                          seq_lds, local ? s_sel_ids + wave * top_k : nullptr,
+                          local ? s_sel_sc + wave * top_k : nullptr);
     }
     if constexpr (PERMUTE) {
         if (gridDim.x > 1) {
@@ -804,8 +830,9 @@ __global__ __launch_bounds__(NW * HM_WAVE) void router_select_partial_kernel(
         } else {
             __syncthreads();  // one workgroup: its own ids and scores
         }
-        permute_small<NW * HM_WAVE>(ids, scores, (int)(tokens * top_k), top_k, (int)experts,
-                                    counts, offsets, perm_tokens, perm_weights, slots);
+        permute_small<NW * HM_WAVE>(local ? s_sel_ids : ids, local ? s_sel_sc : scores,
+                                    (int)(tokens * top_k), top_k, (int)experts, counts, offsets,
+                                    perm_tokens, perm_weights, slots);
     }
 }
 

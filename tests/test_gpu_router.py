@@ -150,8 +150,10 @@ def test_router_sequential_flag_same_bits(dev):
     batches FP64 matrix-core sums; forcing the reference's sequential chain
     for every logit gives the same bits."""
     from hmoe import capi
+    # (H = 96, 160: the chains' last 64-product piece is a half one)
     for T, H, E in ((1, 2048, 128), (16, 2048, 128), (5, 512, 64), (40, 2048, 128),
-                    (300, 2048, 128), (100, 512, 64), (70, 64, 192)):
+                    (300, 2048, 128), (100, 512, 64), (70, 64, 192), (5, 96, 64),
+                    (1, 160, 128)):
         print(f"[gpu] router sequential flag T={T} H={H} E={E}", flush=True)
         rng = np.random.default_rng(T + H)
         h = O.rmsnorm(rng.standard_normal((T, H)).astype(np.float32), np.ones(H, np.float32))
