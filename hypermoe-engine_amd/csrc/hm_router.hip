@@ -762,14 +762,15 @@ __device__ void permute_small(const uint32_t* __restrict__ ids, const float* __r
 }
 
 // Select over logits formed from the decode partials (and written to
-// `logits` too), NW waves (tokens) per workgroup.  With PERMUTE the
-// workgroup that finishes last (a device counter, zeroed by
-// router_partial_kernel) also sorts the pairs into expert groups, which is
-// hm_permute's result: one launch fewer per decode step.  Each token reads
-// 2 kNB doubles per logit (64 KB at E = 128) that other CUs wrote, at the
-// few tens of GB/s one CU draws: the fused step gives every token a
-// workgroup (a CU) of its own once there are several.
-template <int EPL, bool PERMUTE, int NW>
+// `logits` too).  !SPLIT: NW tokens per workgroup, one per wave.  SPLIT: one
+// token per workgroup, its rows of 64 logits shared out over the NW waves
+// so that all their loads are in flight together (each token reads 2 kNB
+// doubles per logit, 64 KB at E = 128, that other CUs wrote), wave 0
+// selecting.  With PERMUTE the workgroup that finishes last (a device
+// counter, zeroed by router_partial_kernel) also sorts the pairs into
+// expert groups, which is hm_permute's result: one launch fewer per decode
+// step; a single workgroup hands its ids and scores over in LDS.
+template <int EPL, bool PERMUTE, int NW, bool SPLIT>
 __global__ __launch_bounds__(NW * HM_WAVE) void router_select_partial_kernel(
     const float* __restrict__ h, const float* __restrict__ w, const double* __restrict__ part,
     int64_t tokens, int64_t hidden, int64_t experts, int32_t top_k, uint32_t flags,
@@ -782,37 +783,62 @@ __global__ __launch_bounds__(NW * HM_WAVE) void router_select_partial_kernel(
     // one workgroup: the grouping reads the ids and scores from LDS copies
     __shared__ uint32_t s_sel_ids[PERMUTE ? NW * 64 : 1];
     __shared__ float s_sel_sc[PERMUTE ? NW * 64 : 1];
+    // SPLIT: the token's logits, rows of 64 experts shared out over the waves
+    __shared__ float s_lg[SPLIT ? EPL : 1][HM_WAVE];
     const bool local = PERMUTE && gridDim.x == 1;
     const int lane = threadIdx.x & (HM_WAVE - 1);
     const int wave = threadIdx.x / HM_WAVE;
-    const int64_t t = (int64_t)blockIdx.x * NW + wave;
     const bool force_seq = (flags & HM_EXEC_ROUTE_SEQUENTIAL) != 0;
-    if (t < tokens) {
-        float v[EPL];
-        bool valid[EPL], settled[EPL];
-        // every logit's block sums first (lanes past the experts read the
-        // last expert's: no branch around the loads)
+    // one logit row j (experts 64 j + lane) of token t: its block sums, and
+    // the reference's chain where the bound leaves it open
+    auto logit_row = [&](int64_t t, int j, bool& valid) __attribute__((always_inline)) -> float {
+        const int64_t e = lane + (int64_t)HM_WAVE * j;
+        valid = e < experts;
+        bool settled;
+        // (lanes past the experts read the last expert's: no branch around the loads)
+        float v = block_logit(part + (t * experts + (valid ? e : experts - 1)) * 2 * kNB, hidden,
+                              force_seq, &settled);
+        if (!valid) {
+            v = 0.0f;
+            settled = true;
+        }
+        v = chain_logits(__ballot(valid && !settled), lane, v, (int64_t)HM_WAVE * j,
+                         h + t * hidden, w, hidden, experts, s_prod[wave], status);
+        if (valid) logits[t * experts + e] = v;
+        return v;
+    };
+    if constexpr (SPLIT) {
+        // one token per workgroup: wave w forms rows w, w + NW, .., so that
+        // every row's loads are in flight at once; wave 0 selects
+        const int64_t t = blockIdx.x;
+        for (int j = wave; j < EPL; j += NW) {
+            bool valid;
+            s_lg[j][lane] = logit_row(t, j, valid);
+        }
+        __syncthreads();
+        if (wave == 0) {
+            float v[EPL];
+            bool valid[EPL];
 #pragma unroll
-        for (int j = 0; j < EPL; ++j) {
-            const int64_t e = lane + (int64_t)HM_WAVE * j;
-            valid[j] = e < experts;
-            const int64_t ec = valid[j] ? e : experts - 1;
-            v[j] = block_logit(part + (t * experts + ec) * 2 * kNB, hidden, force_seq, &settled[j]);
-            if (!valid[j]) {
-                v[j] = 0.0f;
-                settled[j] = true;
+            for (int j = 0; j < EPL; ++j) {
+                v[j] = s_lg[j][lane];
+                valid[j] = lane + (int64_t)HM_WAVE * j < experts;
             }
+            select_token<EPL>(v, valid, lane, 0, t, experts, top_k, flags, ids, scores, status,
+                              seq_lds, local ? s_sel_ids : nullptr, local ? s_sel_sc : nullptr);
         }
-        // then the logits the bound leaves open: the reference's chain
+    } else {
+        // one token per wave
+        const int64_t t = (int64_t)blockIdx.x * NW + wave;
+        if (t < tokens) {
+            float v[EPL];
+            bool valid[EPL];
 #pragma unroll
-        for (int j = 0; j < EPL; ++j) {
-            v[j] = chain_logits(__ballot(valid[j] && !settled[j]), lane, v[j], (int64_t)HM_WAVE * j,
-                                h + t * hidden, w, hidden, experts, s_prod[wave], status);
-            if (valid[j]) logits[t * experts + lane + (int64_t)HM_WAVE * j] = v[j];
+            for (int j = 0; j < EPL; ++j) v[j] = logit_row(t, j, valid[j]);
+            select_token<EPL>(v, valid, lane, wave, t, experts, top_k, flags, ids, scores, status,
+                              seq_lds, local ? s_sel_ids + wave * top_k : nullptr,
+                              local ? s_sel_sc + wave * top_k : nullptr);
         }
-        select_token<EPL>(v, valid, lane, wave, t, experts, top_k, flags, ids, scores, status,
-                          seq_lds, local ? s_sel_ids + wave * top_k : nullptr,
-                          local ? s_sel_sc + wave * top_k : nullptr);
     }
     if constexpr (PERMUTE) {
         if (gridDim.x > 1) {
@@ -1584,9 +1610,10 @@ static int launch_decode_router(const float* h, const float* w, int64_t tokens, 
                                 const hm_decode_fusion* fused, const hm_norm_fold* norm,
                                 void* stream) {
     const int epl = (int)((experts + HM_WAVE - 1) / HM_WAVE);
-    // fused with several tokens: one wave (token) per workgroup; else four
-    const int nw = fused && tokens > 1 ? 1 : 4;
-    const dim3 sgrid((unsigned)((tokens + nw - 1) / nw));
+    // fused: one token per workgroup, its logit rows shared out over up to
+    // four waves; else four tokens (waves) per workgroup
+    const int nw = !fused ? 4 : epl <= 1 ? 1 : epl <= 2 ? 2 : 4;
+    const dim3 sgrid((unsigned)(fused ? tokens : (tokens + 3) / 4));
     const size_t seq_bytes = (size_t)nw * experts * sizeof(float);
     double* part = reinterpret_cast<double*>(static_cast<char*>(route_ws) +
                                              route_logits_bytes(tokens, experts));
@@ -1601,7 +1628,7 @@ static int launch_decode_router(const float* h, const float* w, int64_t tokens, 
     // the select kernel's fallback chains read the normalised rows
     if (norm) h = norm->x_out;
 #define HM_SELECTP(N, F, W)                                                                \
-    hipLaunchKernelGGL((router_select_partial_kernel<N, F, W>), sgrid, dim3(W * HM_WAVE),    \
+    hipLaunchKernelGGL((router_select_partial_kernel<N, F, W, F>), sgrid, dim3(W * HM_WAVE), \
                        seq_bytes, hm_stream(stream), h, w, part, tokens, hidden, experts,    \
                        top_k, flags, logits, ids, scores, status,                            \
                        F ? fused->counters : nullptr, F ? fused->counts : nullptr,           \
@@ -1611,6 +1638,7 @@ static int launch_decode_router(const float* h, const float* w, int64_t tokens, 
     do {                                                \
         if (!fused) HM_SELECTP(N, false, 4);            \
         else if (nw == 1) HM_SELECTP(N, true, 1);       \
+        else if (nw == 2) HM_SELECTP(N, true, 2);       \
         else HM_SELECTP(N, true, 4);                    \
     } while (0)
     if (epl <= 1) HM_SELECTP2(1);
