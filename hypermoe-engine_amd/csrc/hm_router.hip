@@ -632,26 +632,28 @@ __device__ __forceinline__ void select_token(float (&v)[EPL], const bool (&valid
     for (int j = 0; j < EPL; ++j) {
         key[j] = valid[j] ? hm_rank_key(v[j], (unsigned)(lane + HM_WAVE * j)) : 0ull;
     }
+    // k rounds of the wave maximum (keys are unique: the winner's own key
+    // is the one that equals it); lane r keeps the r-th id, and after the
+    // rounds fetches its score from the lane that holds it
     uint32_t my_id = 0;
-    float my_score = 0.0f;
-    double sel_sum = 0.0;
     for (int r = 0; r < top_k; ++r) {
         unsigned long long best = 0ull;
 #pragma unroll
         for (int j = 0; j < EPL; ++j) best = key[j] > best ? key[j] : best;
         best = hm_wave_max_u64_dpp(best);
-        const uint32_t id = 0xffffffffu - (uint32_t)(best & 0xffffffffull);
-        const int owner = (int)(id % HM_WAVE);
-        const int slot = (int)(id / HM_WAVE);
-        float sv = 0.0f;
 #pragma unroll
-        for (int j = 0; j < EPL; ++j) {
-            if (j == slot && lane == owner) { sv = v[j]; key[j] = 0ull; }
-        }
-        sv = __shfl(sv, owner, HM_WAVE);
-        sel_sum += (double)sv;  // rank order, uniform across lanes
-        if (lane == r) { my_id = id; my_score = sv; }
+        for (int j = 0; j < EPL; ++j) key[j] = key[j] == best ? 0ull : key[j];
+        if (lane == r) my_id = 0xffffffffu - (uint32_t)(best & 0xffffffffull);
     }
+    float my_score = 0.0f;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        const float c = __shfl(v[j], (int)(my_id % HM_WAVE), HM_WAVE);
+        if ((int)(my_id / HM_WAVE) == j) my_score = c;
+    }
+    double sel_sum = 0.0;  // rank order, uniform across lanes
+    for (int r = 0; r < top_k; ++r)
+        sel_sum += (double)__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_score), r));
     if (flags & HM_ROUTE_RENORM) {
         if (!(isfinite(sel_sum) && sel_sum != 0.0)) {
             if (lane == 0) hm_status_or(status, HM_STATUS_RENORM_FAILED);
@@ -761,6 +763,54 @@ __device__ void permute_small(const uint32_t* __restrict__ ids, const float* __r
     }
 }
 
+// The grouping of permute_small for P <= 64 pairs by one wave, in
+// registers: lane p holds pair p (its id, clamped to the expert count as
+// permute_small does, and score); its position is the number of pairs with
+// a smaller expert plus the earlier pairs of its own expert (the stable
+// counting sort), the lanes' experts lane + 64 j count their pairs and
+// those of smaller experts (counts, offsets), each pair's id read in turn
+// across the wave.
+template <int EPL>
+__device__ __forceinline__ void permute_wave(uint32_t id, float score, int pairs, int top_k,
+                                             int experts, int32_t* __restrict__ counts,
+                                             int32_t* __restrict__ offsets,
+                                             int32_t* __restrict__ perm_tokens,
+                                             float* __restrict__ perm_weights,
+                                             int32_t* __restrict__ slots) {
+    const int lane = threadIdx.x & (HM_WAVE - 1);
+    const int ep = lane < pairs ? (int)min(id, (uint32_t)(experts - 1)) : INT_MAX;
+    int less = 0, same = 0;
+    int cnt[EPL], off[EPL];
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) cnt[j] = off[j] = 0;
+    for (int q = 0; q < pairs; ++q) {
+        const int eq = __builtin_amdgcn_readlane(ep, q);
+        less += eq < ep;
+        same += (eq == ep) & (q < lane);
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            const int e = lane + HM_WAVE * j;
+            cnt[j] += eq == e;
+            off[j] += eq < e;
+        }
+    }
+    if (lane < pairs) {
+        const int pos = less + same;
+        perm_tokens[pos] = lane / top_k;
+        perm_weights[pos] = score;
+        slots[lane] = pos;
+    }
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+        const int e = lane + HM_WAVE * j;
+        if (e < experts) {
+            counts[e] = cnt[j];
+            offsets[e] = off[j];
+            if (e == experts - 1) offsets[experts] = off[j] + cnt[j];
+        }
+    }
+}
+
 // Select over logits formed from the decode partials (and written to
 // `logits` too).  !SPLIT: NW tokens per workgroup, one per wave.  SPLIT: one
 // token per workgroup, its rows of 64 logits shared out over the NW waves
@@ -826,7 +876,16 @@ __global__ __launch_bounds__(NW * HM_WAVE) void router_select_partial_kernel(
             }
             select_token<EPL>(v, valid, lane, 0, t, experts, top_k, flags, ids, scores, status,
                               seq_lds, local ? s_sel_ids : nullptr, local ? s_sel_sc : nullptr);
+            if (local && top_k <= HM_WAVE) {
+                // one token: its grouping by this wave, from the LDS copies
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                const int ln = lane < top_k ? lane : 0;
+                permute_wave<EPL>(s_sel_ids[ln], s_sel_sc[ln], top_k, top_k, (int)experts,
+                                  counts, offsets, perm_tokens, perm_weights, slots);
+            }
         }
+        if (local && top_k <= HM_WAVE) return;
     } else {
         // one token per wave
         const int64_t t = (int64_t)blockIdx.x * NW + wave;
