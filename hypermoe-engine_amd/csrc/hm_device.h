@@ -168,6 +168,32 @@ __device__ __forceinline__ unsigned long long hm_wave_max_u64_dpp(unsigned long 
     }
     return m;
 }
+// The same maximum kept in the vector unit to the end: after the row
+// steps, row_bcast:15 hands rows 0 and 2 on to rows 1 and 3 and
+// row_bcast:31 row 1 on to rows 2 and 3 (rows outside the row mask keep
+// their own value), so lane 63 holds the wave's maximum.
+__device__ __forceinline__ unsigned long long hm_wave_max_u64_bcast(unsigned long long v) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const unsigned long long o = hm_dpp_u64(v, c);
+        v = o > v ? o : v;
+    }
+    {
+        const int lo = (int)(unsigned)(v & 0xffffffffull), hi = (int)(unsigned)(v >> 32);
+        const unsigned olo = (unsigned)__builtin_amdgcn_update_dpp(lo, lo, 0x142, 0xa, 0xf, false);
+        const unsigned ohi = (unsigned)__builtin_amdgcn_update_dpp(hi, hi, 0x142, 0xa, 0xf, false);
+        const unsigned long long o = ((unsigned long long)ohi << 32) | olo;
+        v = o > v ? o : v;
+    }
+    {
+        const int lo = (int)(unsigned)(v & 0xffffffffull), hi = (int)(unsigned)(v >> 32);
+        const unsigned olo = (unsigned)__builtin_amdgcn_update_dpp(lo, lo, 0x143, 0xc, 0xf, false);
+        const unsigned ohi = (unsigned)__builtin_amdgcn_update_dpp(hi, hi, 0x143, 0xc, 0xf, false);
+        const unsigned long long o = ((unsigned long long)ohi << 32) | olo;
+        v = o > v ? o : v;
+    }
+    return hm_readlane_u64(v, HM_WAVE - 1);
+}
 // Sum of doubles over the wave (row DPP, then the four rows in ascending
 // row order); callers use it only where any summation order gives the
 // same result.

@@ -640,7 +640,7 @@ __device__ __forceinline__ void select_token(float (&v)[EPL], const bool (&valid
         unsigned long long best = 0ull;
 #pragma unroll
         for (int j = 0; j < EPL; ++j) best = key[j] > best ? key[j] : best;
-        best = hm_wave_max_u64_dpp(best);
+        best = hm_wave_max_u64_bcast(best);
 #pragma unroll
         for (int j = 0; j < EPL; ++j) key[j] = key[j] == best ? 0ull : key[j];
         if (lane == r) my_id = 0xffffffffu - (uint32_t)(best & 0xffffffffull);
