@@ -36,6 +36,12 @@ int hm_launch_gateup_gemv(const hm_layer* L, const float* hidden, const int32_t*
 int hm_launch_down_gemv(const hm_layer* L, const float* z, const int32_t* counts,
                         const int32_t* offsets, int64_t pairs, float* y, hipStream_t s);
 bool hm_gemv_combine_ok(int64_t tokens, int32_t top_k, int64_t H, int64_t I);
+bool hm_gemv_f32_ok(const hm_layer* L, const void* x);
+int hm_launch_gateup_gemv_f32(const hm_layer* L, const float* hidden, const int32_t* counts,
+                              const int32_t* offsets, const int32_t* perm_tokens,
+                              int64_t pairs, float* z, hipStream_t s);
+int hm_launch_down_gemv_f32(const hm_layer* L, const float* z, const int32_t* counts,
+                            const int32_t* offsets, int64_t pairs, float* y, hipStream_t s);
 int hm_launch_down_combine_gemv(const hm_layer* L, const float* z, const int32_t* counts,
                                 const uint32_t* ids, const int32_t* slots, const float* scores,
                                 const float* residual, int64_t tokens, int32_t top_k,
@@ -327,12 +333,19 @@ int block_forward(const hm_layer* layer, const float* hidden, const float* route
         rc = hm_launch_down_i8(layer, limbs_x, limbs_z, counts, p.offsets, P, p.zdig,
                                p.zscale, p.zdsum, p.y, generic, split_k, s);
     } else {
+        // FP32 experts: decode-size batches stream each selected expert's
+        // rows once (GEMV); others take the matrix-core tiles
+        const bool gv32 = tokens <= HM_GEMV_MAX_TOKENS && hm_gemv_f32_ok(layer, hidden) &&
+                          hm_gemv_f32_ok(layer, p.zf);
         rc = gate_up([&] {
-            return hm_launch_gateup_f32(layer, hidden, counts, p.offsets, p.perm_tokens, P,
-                                        p.zf, s);
+            return gv32 ? hm_launch_gateup_gemv_f32(layer, hidden, counts, p.offsets,
+                                                    p.perm_tokens, P, p.zf, s)
+                        : hm_launch_gateup_f32(layer, hidden, counts, p.offsets, p.perm_tokens,
+                                               P, p.zf, s);
         });
         if (rc) return rc;
-        rc = hm_launch_down_f32(layer, counts, p.offsets, P, p.zf, p.y, s);
+        rc = gv32 ? hm_launch_down_gemv_f32(layer, p.zf, counts, p.offsets, P, p.y, s)
+                  : hm_launch_down_f32(layer, counts, p.offsets, P, p.zf, p.y, s);
     }
     if (rc || (rc = mark(5))) return rc;
     rc = hm_combine(p.y, p.ids, p.slots, p.scores, tokens, top_k, H, io->residual, io->out,

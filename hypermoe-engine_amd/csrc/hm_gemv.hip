@@ -267,6 +267,103 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(
 
 
 // ---------------------------------------------------------------------------
+// FP32-weight experts at decode (A5' for a few tokens; CpuTensorBackend::
+// matmul, CpuTensorBackend.cpp:87-131, on each expert's rows):
+//   GATEUP: z[g, n] = silu(x_g . Wg[n]) * (x_g . Wu[n]),  x_g = hidden[perm_tokens[g]]
+//   DOWN:   y[g, n] = z_g . Wd[n]
+// FP32 projections are stored [N][K] (hm_pack_layer), so each output
+// column's weights are one contiguous row of K floats.  Workgroup: one
+// active expert (the blockIdx.y-th) x NC columns; wave w takes projection
+// w / (8 / NP) and CW columns, and holds their rows in registers (lane l:
+// floats 4 l + 256 j .. +3 of each, K / 256 <= MJ float4); the expert's
+// rows are staged in LDS kGvRows at a time.  Each (row, column) sum: per
+// lane in j order, then a fixed butterfly over the wave.  The sums' order
+// differs from the reference's sequential one: within the FP32 path's
+// 1e-3, as the matrix-core kernels.  SiLU and the product as
+// Activation.cpp:44 then the multiply.
+// ---------------------------------------------------------------------------
+constexpr int kF32Mj = 8;      // float4 per lane per column: K <= 2048
+
+template <bool GATEUP, int CW, int MJ>
+__global__ __launch_bounds__(kGvThreads) void gemv_f32_kernel(
+    const float* __restrict__ x_src, const int32_t* __restrict__ perm_tokens, int64_t K,
+    int64_t N, int64_t experts, const float* __restrict__ packed, int64_t hidden,
+    int64_t inter, const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
+    float* __restrict__ out) {
+    constexpr int NP = GATEUP ? 2 : 1;
+    constexpr int WPP = kGvWaves / NP;        // waves per projection
+    constexpr int NC = WPP * CW;              // columns per workgroup
+    extern __shared__ __attribute__((aligned(16))) float s_x[];  // [kGvRows][K]
+    __shared__ float s_acc[NP][NC][kGvRows];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int p = wave / WPP, cw = wave % WPP;
+    const int e = hm_active_expert_scan(counts, experts, (int)blockIdx.y);
+    if (e < 0) return;  // uniform: every wave computes the same e
+    const int nj = (int)(K / 256);
+    const float* proj = packed + ((int64_t)e * 3 + (GATEUP ? p : 2)) * hidden * inter;
+    const int64_t nb = (int64_t)NC * blockIdx.x + CW * cw;
+    // the wave's column rows, all loads in flight together (columns past N
+    // repeat the last one and are not stored)
+    float4 w[CW][MJ];
+#pragma unroll
+    for (int c = 0; c < CW; ++c) {
+        const float* wr = proj + min(nb + c, N - 1) * K + 4 * lane;
+#pragma unroll
+        for (int j = 0; j < MJ; ++j)
+            if (j < nj) w[c][j] = *reinterpret_cast<const float4*>(wr + 256 * j);
+    }
+    const int64_t g0 = offsets[e];
+    const int rows = counts[e];
+    for (int r0 = 0; r0 < rows; r0 += kGvRows) {
+        const int nr = min(kGvRows, rows - r0);
+        const int64_t k4 = K / 4;
+        for (int64_t i = tid; i < (int64_t)nr * k4; i += kGvThreads) {
+            const int r = (int)(i / k4);
+            const int64_t k = 4 * (i % k4);
+            const int64_t g = g0 + r0 + r;
+            const float* xr = x_src + (GATEUP ? (int64_t)perm_tokens[g] : g) * K;
+            *reinterpret_cast<float4*>(&s_x[r * K + k]) = *reinterpret_cast<const float4*>(xr + k);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < kGvRows; ++r) {
+            if (r < nr) {
+#pragma unroll
+                for (int c = 0; c < CW; ++c) {
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < MJ; ++j) {
+                        if (j < nj) {
+                            const float4 xv = *reinterpret_cast<const float4*>(&s_x[r * K + 4 * lane + 256 * j]);
+                            acc = __builtin_fmaf(xv.x, w[c][j].x, acc);
+                            acc = __builtin_fmaf(xv.y, w[c][j].y, acc);
+                            acc = __builtin_fmaf(xv.z, w[c][j].z, acc);
+                            acc = __builtin_fmaf(xv.w, w[c][j].w, acc);
+                        }
+                    }
+#pragma unroll
+                    for (int d = 32; d >= 1; d >>= 1) acc += __shfl_xor(acc, d, HM_WAVE);
+                    if (lane == 0) s_acc[p][CW * cw + c][r] = acc;
+                }
+            }
+        }
+        __syncthreads();
+        if (tid < nr * NC) {
+            const int r = tid / NC, c = tid % NC;
+            const int64_t n = (int64_t)NC * blockIdx.x + c;
+            if (n < N) {
+                const float v = GATEUP ? __fmul_rn(hm_silu(s_acc[0][c][r]), s_acc[NP - 1][c][r])
+                                       : s_acc[0][c][r];
+                out[(g0 + r0 + r) * N + n] = v;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+
+// ---------------------------------------------------------------------------
 // Gate/up of a few tokens (T * K32 <= kGvAllFloats) on 8-column slices:
 //   z[g, n] = silu(x_g . Wg[n]) * (x_g . Wu[n]),  x_g = hidden[perm_tokens[g]]
 // Workgroup: one active expert (the blockIdx.y-th) x 8 columns (slice
@@ -752,4 +849,53 @@ int hm_launch_down_gemv(const hm_layer* L, const float* z, const int32_t* counts
                                      slots, y, s);
     return launch_gemv<false, 1>(z, nullptr, L->intermediate, L->hidden, L, counts, offsets, slots,
                                  y, s);
+}
+
+// FP32 experts at decode: the shapes gemv_f32_kernel takes (K a multiple
+// of 256 up to 2048 for both projections, 16-byte aligned operands).
+bool hm_gemv_f32_ok(const hm_layer* L, const void* x) {
+    const int64_t H = L->hidden, I = L->intermediate;
+    return L->dtype == HM_DTYPE_FP32 && L->experts <= 1024 && H % 256 == 0 && I % 256 == 0 &&
+           H <= 256 * kF32Mj && I <= 256 * kF32Mj && ((uintptr_t)L->packed & 15) == 0 &&
+           ((uintptr_t)x & 15) == 0;
+}
+
+int hm_launch_gateup_gemv_f32(const hm_layer* L, const float* hidden, const int32_t* counts,
+                              const int32_t* offsets, const int32_t* perm_tokens,
+                              int64_t pairs, float* z, hipStream_t s) {
+    if (!hm_gemv_f32_ok(L, hidden)) return HM_ERR_UNSUPPORTED;
+    const int64_t slots = pairs < L->experts ? pairs : L->experts;
+    const size_t lds = (size_t)kGvRows * L->hidden * sizeof(float);
+    // K <= 1024: four columns per wave (the same registers as two at 2048)
+#define HM_GF(CW, MJ)                                                                          \
+    HM_STAGE_LAUNCH(true, true, (gemv_f32_kernel<true, CW, MJ>),                               \
+                    dim3((unsigned)((L->intermediate + kGvWaves / 2 * CW - 1) / (kGvWaves / 2 * CW)), \
+                         (unsigned)slots),                                                     \
+                    dim3(kGvThreads), lds, s, hidden, perm_tokens, L->hidden, L->intermediate, \
+                    L->experts, static_cast<const float*>(L->packed), L->hidden,               \
+                    L->intermediate, counts, offsets, z)
+    if (L->hidden <= 1024) HM_GF(4, 4);
+    else HM_GF(2, 8);
+#undef HM_GF
+    HM_LAUNCHED();
+    return HM_OK;
+}
+
+int hm_launch_down_gemv_f32(const hm_layer* L, const float* z, const int32_t* counts,
+                            const int32_t* offsets, int64_t pairs, float* y, hipStream_t s) {
+    if (!hm_gemv_f32_ok(L, z)) return HM_ERR_UNSUPPORTED;
+    const int64_t slots = pairs < L->experts ? pairs : L->experts;
+    const size_t lds = (size_t)kGvRows * L->intermediate * sizeof(float);
+#define HM_GF(CW, MJ)                                                                          \
+    hipLaunchKernelGGL((gemv_f32_kernel<false, CW, MJ>),                                       \
+                       dim3((unsigned)((L->hidden + kGvWaves * CW - 1) / (kGvWaves * CW)),     \
+                            (unsigned)slots),                                                  \
+                       dim3(kGvThreads), lds, s, z, nullptr, L->intermediate, L->hidden,       \
+                       L->experts, static_cast<const float*>(L->packed), L->hidden,            \
+                       L->intermediate, counts, offsets, y)
+    if (L->intermediate <= 1024) HM_GF(4, 4);
+    else HM_GF(2, 8);
+#undef HM_GF
+    HM_LAUNCHED();
+    return HM_OK;
 }

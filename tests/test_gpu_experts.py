@@ -271,11 +271,13 @@ def test_block_gemv_decode(dev, T, H, E, I, k, skew):
         assert_compare(y[lo:lo + len(b.token_indices)], ref, 1e-4, 1e-4, "expert rows")
 
 
-@pytest.mark.parametrize("T,E", [(16, 64), (40, 8), (300, 4)])
+@pytest.mark.parametrize("T,E", [(16, 64), (1, 64), (5, 8), (40, 8), (300, 4)])
 def test_block_fp32_vs_reference(dev, T, E):
     """FP32 experts (C1 shape): within 1e-3 of the reference (north star).
-    T=300 with E=4, k=2 puts about 150 rows on each expert: several 64-row
-    matrix-core tiles per expert with a ragged last tile."""
+    T <= 16 takes the FP32 GEMV (T = 5, E = 8: five rows on most experts,
+    two LDS passes); T=300 with E=4, k=2 puts about 150 rows on each
+    expert: several 64-row matrix-core tiles per expert with a ragged last
+    tile."""
     H, I, k = 2048, 768, 8 if E >= 8 else 2
     print(f"[gpu] fp32 block T={T} E={E} k={k}", flush=True)
     payload, scale, zp, h, w = _layer_inputs(3, T, H, E, I, False)
