@@ -155,6 +155,8 @@ size_t plan_block(const hm_layer* L, int64_t T, int32_t k, int32_t lx, int32_t l
         return c.used;
     } else {
         q.zf = c.take<float>((size_t)P * I);
+        // FP32 decode batches: the fused router's completion counter too
+        if (T <= HM_GEMV_MAX_TOKENS) q.counters = c.take<int32_t>(1);
     }
     q.y = c.take<float>((size_t)P * H);
     if (p) *p = q;
@@ -253,7 +255,10 @@ int block_forward(const hm_layer* layer, const float* hidden, const float* route
         route_flags & (HM_ROUTE_SOFTMAX | HM_ROUTE_RENORM | HM_EXEC_ROUTE_SEQUENTIAL);
     // decode: the grouping is fused into the router's select (one launch
     // fewer)
-    const bool fuse = gemv && H % 32 == 0 && E <= 1024 && top_k <= 64 && P <= 1024;
+    // FP32 experts of a decode batch take the FP32 GEMV
+    const bool gv32 = layer->dtype == HM_DTYPE_FP32 && tokens <= HM_GEMV_MAX_TOKENS &&
+                      p.counters && hm_gemv_f32_ok(layer, hidden) && hm_gemv_f32_ok(layer, p.zf);
+    const bool fuse = (gemv || gv32) && H % 32 == 0 && E <= 1024 && top_k <= 64 && P <= 1024;
     bool x_quantized = false;
     if (fuse) {
         const hm_decode_fusion f = {p.counters, 1, p.counts, p.offsets, p.perm_tokens,
@@ -335,8 +340,6 @@ int block_forward(const hm_layer* layer, const float* hidden, const float* route
     } else {
         // FP32 experts: decode-size batches stream each selected expert's
         // rows once (GEMV); others take the matrix-core tiles
-        const bool gv32 = tokens <= HM_GEMV_MAX_TOKENS && hm_gemv_f32_ok(layer, hidden) &&
-                          hm_gemv_f32_ok(layer, p.zf);
         rc = gate_up([&] {
             return gv32 ? hm_launch_gateup_gemv_f32(layer, hidden, counts, p.offsets,
                                                     p.perm_tokens, P, p.zf, s)
