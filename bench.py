@@ -360,6 +360,7 @@ def main():
                            "or gemv_kernel<true, 1> (more than two tokens)" if gemv else
                            "gate/up stage: ring_gemm_kernel<Lx, false> + "
                            "limb_swiglu_quantize_vec_kernel<Lz, I/256>" if cfg.int8
+                           else "gate/up GEMV: gemv_f32_kernel<true, CW, MJ>" if T <= 16
                            else "expert_f32_mfma_kernel<true>"),
                 "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
@@ -371,7 +372,7 @@ def main():
             kre, prim = ("ring_gemm_kernel<[0-9], false>|limb_swiglu_quantize",
                          "ring_gemm_kernel<[0-9], false>")
         else:
-            kre = prim = "expert_f32_mfma_kernel<true>"
+            kre = prim = "gemv_f32_kernel<true|expert_f32_mfma_kernel<true>"
         tr = pmc_traffic(cfg.name, kre, prim, (args.limbs_x, args.limbs_z), q)
         if tr is not None:
             roof["traffic"] = tr.pop("bytes")
