@@ -202,9 +202,21 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(
             *reinterpret_cast<float4*>(&s_x[r * K32 + k]) = v;
         }
         __syncthreads();
-        float acc[kGvRows], xs[kGvRows];
+        // the rows' sums over this wave's K range, once per row (the waves
+        // of projection 0, column tile 0), not in the weight loop below
+        if (p == 0 && c == 0) {
+            for (int r = 0; r < nr; ++r) {
+                float xs = 0.0f;
+                for (int64_t k = 32 * (int64_t)kb0 + lane; k < 32 * (int64_t)(kb0 + nkb); k += 64)
+                    xs += s_x[r * K32 + k];
 #pragma unroll
-        for (int r = 0; r < kGvRows; ++r) acc[r] = xs[r] = 0.0f;
+                for (int d = 32; d >= 1; d >>= 1) xs += __shfl_xor(xs, d, 64);
+                if (lane == 0) s_xs[q][r] = xs;
+            }
+        }
+        float acc[kGvRows];
+#pragma unroll
+        for (int r = 0; r < kGvRows; ++r) acc[r] = 0.0f;
 #pragma unroll
         for (int t = 0; t < kGvMaxTiles; ++t) {
             if (t < nkb) {
@@ -222,7 +234,6 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(
                             acc[r] = __builtin_fmaf(v.y, f[4 * i + 1], acc[r]);
                             acc[r] = __builtin_fmaf(v.z, f[4 * i + 2], acc[r]);
                             acc[r] = __builtin_fmaf(v.w, f[4 * i + 3], acc[r]);
-                            xs[r] += (v.x + v.y) + (v.z + v.w);
                         }
                     }
                 }
@@ -232,9 +243,7 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(
 #pragma unroll
         for (int r = 0; r < kGvRows; ++r) {
             const float a = acc[r] + __shfl_xor(acc[r], 32, 64);
-            const float x = xs[r] + __shfl_xor(xs[r], 32, 64);
             if (lane < 32) s_red[p][c][q][r][lane] = a;
-            if (p == 0 && c == 0 && lane == 0) s_xs[q][r] = x;
         }
         __syncthreads();
         // one half-wave per (row, column tile) finishes its 32 columns
