@@ -190,7 +190,8 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: every box in this build has one MI355X and the "
-              "block runs on one GPU's share (see DESIGN.md for how it would shard). "
+              "block runs on one GPU's share (across GPUs the experts would shard by "
+              "expert, with an all-to-all of the grouped rows and outputs over RCCL). "
               "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
