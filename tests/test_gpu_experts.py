@@ -241,7 +241,8 @@ def test_block_int8_nonzero_zero_points(dev):
     (1, 2048, 128, 768, 8, False), (4, 2048, 128, 768, 8, False), (16, 2048, 128, 768, 8, True),
     (16, 512, 4, 256, 2, False), (13, 1024, 3, 512, 3, False), (9, 256, 2, 1024, 1, False),
     (16, 256, 64, 1024, 4, False), (5, 528, 6, 400, 2, False), (2, 2048, 128, 768, 8, False),
-    (3, 256, 8, 96, 5, False), (1, 1024, 16, 512, 1, False), (1, 128, 4, 32, 1, False)])
+    (3, 256, 8, 96, 5, False), (1, 1024, 16, 512, 1, False), (1, 128, 4, 32, 1, False),
+    (3, 1024, 16, 512, 8, False)])
 def test_block_gemv_decode(dev, T, H, E, I, k, skew):
     """Decode-size blocks take the W8A32 GEMV (FP32): ids bit-exact, output
     within 1e-4 of the reference; several rows per expert (the register
@@ -251,7 +252,9 @@ def test_block_gemv_decode(dev, T, H, E, I, k, skew):
     column tile).  With T*k <= 16 the down projection and the combine run as
     one kernel: one active expert (sixteen waves on its K range; with I=32
     fifteen of them have no K tile), eight, and sixteen (one wave per
-    expert, K in two register chunks)."""
+    expert, K in two register chunks).  Three tokens at top-8 over sixteen
+    experts (24 pairs) take the separate down GEMV and combine with twelve
+    to sixteen active experts."""
     print(f"[gpu] gemv T={T} H={H} E={E} I={I} k={k} skew={skew}", flush=True)
     payload, scale, zp, h, w = _layer_inputs(7 + T, T, H, E, I, True, skew=skew)
     block = MoEBlock(DeviceExpertLayer(payload, scale, zp, H, I), k)
