@@ -812,6 +812,10 @@ int launch_l(const hm_layer* layer, const int8_t* adig, const float* ascale,
 //   B  the 8 weight fragments (4 gate, 4 up column blocks of 32), each the
 //      two 1 KB operand-order tiles (hm_tile_offset) of the stage's K steps,
 //      one contiguous DMA each and read back at 16 lane.
+// The stage's loads are spread over the waves, LPW per wave (the last
+// round only on the waves it reaches); a step refills the slot read two
+// steps earlier, so its barrier leaves the previous step's fragment reads
+// in flight (the K loop below).
 // Epilogue: the dequantised g and u values (z = silu(g) * u and the Z digits
 // follow in one pass over the rows at full occupancy, hm_gemm.hip).
 // ===========================================================================
@@ -932,7 +936,13 @@ __global__ __launch_bounds__(kGuThreads) void ring_gemm_kernel(
             for (int l = 0; l < L; ++l) dma4(xdsum + (int64_t)l * tokens + tok, &s_xd[m][l][HM_WAVE * wave]);
         }
     };
-    // this wave's load units: unit u = fragment u/2, half (K step) u%2
+    // this wave's load units: unit u = fragment u/2, half (K step) u%2.
+    // Unit c of wave w is u = w + 8c; when the stage's NL units do not fill
+    // every wave's LPW slots, the waves below NFULL issue LPW loads per stage
+    // and the others LPW-1.
+    constexpr int NFULL = NL - kGuWaves * (LPW - 1);
+    static_assert(NFULL >= 1 && NFULL <= kGuWaves, "load units");
+    const bool full = wave < NFULL;
     int dst[LPW];
 #pragma unroll
     for (int c = 0; c < LPW; ++c) {
@@ -962,79 +972,85 @@ __global__ __launch_bounds__(kGuThreads) void ring_gemm_kernel(
             }
         }
     };
+    // load c of a stage exists on this wave
+    auto has_unit = [&](int c) __attribute__((always_inline)) { return c < LPW - 1 || full; };
     auto issue = [&](int slot, const int8_t* const (&src)[LPW], int ks) {
         int8_t* st = ring + slot * STAGE;
 #pragma unroll
-        for (int c = 0; c < LPW; ++c) dma16(src[c] + (int64_t)ks * sstep[c], st + dst[c]);
+        for (int c = 0; c < LPW; ++c)
+            if (has_unit(c)) dma16(src[c] + (int64_t)ks * sstep[c], st + dst[c]);
+    };
+    // wait until at most n stages of this wave's loads are in flight
+    auto vm_wait_stages = [&](auto nst) __attribute__((always_inline)) {
+        constexpr int n = decltype(nst)::value;
+        if (full) vm_wait<n * LPW>();
+        else vm_wait<n * (LPW - 1)>();
     };
 
     int rd[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) rd[h] = gu_frag_read_offset(lane, h);
     v4i fa[2][WR][L], fb[2][2 * WCP];
-    auto read_frags = [&](int slot, int h) __attribute__((always_inline)) {
-        const int8_t* st = ring + slot * STAGE;
-#pragma unroll
-        for (int ii = 0; ii < WR; ++ii)
-#pragma unroll
-            for (int l = 0; l < L; ++l)
-                fa[h][ii][l] = lds16(st + (l * (BM / 32) + wr * WR + ii) * kGuFrag + rd[h]);
-#pragma unroll
-        for (int j = 0; j < 2 * WCP; ++j) {
-            const int fbi = j < WCP ? wc * WCP + j : 4 + wc * WCP + (j - WCP);
-            fb[h][j] = lds16(st + (NA + fbi) * kGuFrag + 1024 * h + 16 * lane);
-        }
-    };
     v16i acc[WR][L][2 * WCP];
-    auto mfma_step = [&](int h, auto first) __attribute__((always_inline)) {
-#pragma unroll
-        for (int ii = 0; ii < WR; ++ii)
-#pragma unroll
-            for (int l = 0; l < L; ++l)
-#pragma unroll
-                for (int j = 0; j < 2 * WCP; ++j) {
-                    if constexpr (decltype(first)::value)
-                        acc[ii][l][j] = mfma32(fa[h][ii][l], fb[h][j], v16i{});
-                    else
-                        acc[ii][l][j] = mfma32(fa[h][ii][l], fb[h][j], acc[ii][l][j]);
-                }
+    const int8_t* src[LPW];  // per-lane sources of this wave's loads
+
+    // ---- the K loop.  Stream stage s (the tiles' stages back to back) lives
+    // in ring slot s % kS.  Step s: wait until this wave's loads of stage s+1
+    // have landed, workgroup barrier, refill the slot of stage s-1 with stage
+    // s+kS-1, then the MFMAs of stage s (fragments in registers) while the
+    // fragments of stage s+1 are read: register set h as soon as the last
+    // MFMA of K step h that uses it has issued.  The slot refilled at step s
+    // was read during step s-2, so the barrier needs only this wave's older
+    // LDS reads complete: the reads of step s-1 stay in flight across it
+    // (a barrier that drained them left all eight waves waiting on the
+    // LDS together once per stage, the matrix pipes idle).
+    constexpr int NJ = 2 * WCP;                 // B fragments per K step
+    constexpr int NM = WR * L * NJ;             // MFMAs per K step
+    constexpr int RPS = 2 * (WR * L + NJ);      // LDS fragment reads per step
+    static_assert(RPS <= 15, "lgkmcnt range");
+    auto read_a = [&](int slot, int h, int ii, int l) __attribute__((always_inline)) {
+        fa[h][ii][l] = lds16(ring + slot * STAGE + (l * (BM / 32) + wr * WR + ii) * kGuFrag + rd[h]);
     };
-    // K step h = 0 with the refill of `slot` (stage ksrc of the stream)
-    // spread between its MFMAs: a wave that issues all its loads before its
-    // MFMAs stalls on the load queue while the matrix pipe idles.
-    auto mfma_step_dma = [&](auto first, const int8_t* const (&sp)[LPW], bool do_issue, int slot,
-                             int ksrc, bool act) __attribute__((always_inline)) {
-        int8_t* st = ring + slot * STAGE;
-        if (!act) {
-            // no rows of this wave in the tile: only the loads
-            if (do_issue)
+    auto read_b = [&](int slot, int h, int j) __attribute__((always_inline)) {
+        const int fbi = j < WCP ? wc * WCP + j : kGuN / 32 + wc * WCP + (j - WCP);
+        fb[h][j] = lds16(ring + slot * STAGE + (NA + fbi) * kGuFrag + 1024 * h + 16 * lane);
+    };
+    // K step h of the current stage; rslot: slot of the stage whose set-h
+    // fragments are read meanwhile (-1: none); (h = 0) the step's refill
+    // loads into dslot from source stage dks go out after the first MFMAs.
+    // The sched_barriers keep this order.
+    auto kstep_h = [&](auto hc, auto first, int rslot, int dslot, int dks) __attribute__((always_inline)) {
+        constexpr int h = decltype(hc)::value;
 #pragma unroll
-                for (int c = 0; c < LPW; ++c) dma16(sp[c] + (int64_t)ksrc * sstep[c], st + dst[c]);
-            return;
+        for (int mi = 0; mi < NM; ++mi) {
+            const int ii = mi / (L * NJ), l = (mi / NJ) % L, j = mi % NJ;
+            if constexpr (decltype(first)::value)
+                acc[ii][l][j] = mfma32(fa[h][ii][l], fb[h][j], v16i{});
+            else
+                acc[ii][l][j] = mfma32(fa[h][ii][l], fb[h][j], acc[ii][l][j]);
+            if (h == 0 && mi < LPW && dslot >= 0 && has_unit(mi))
+                dma16(src[mi] + (int64_t)dks * sstep[mi], ring + dslot * STAGE + dst[mi]);
+            if (rslot >= 0) {
+                if (j == NJ - 1) read_a(rslot, h, ii, l);
+                if (ii == WR - 1 && l == L - 1) read_b(rslot, h, j);
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        constexpr int NM = WR * L * 2 * WCP;
-        constexpr int PER = NM / LPW > 0 ? NM / LPW : 1;
+        if (h == 0 && dslot >= 0)
 #pragma unroll
-        for (int ii = 0; ii < WR; ++ii)
+            for (int c = NM; c < LPW; ++c)
+                if (has_unit(c)) dma16(src[c] + (int64_t)dks * sstep[c], ring + dslot * STAGE + dst[c]);
+    };
+    auto read_all = [&](int slot) __attribute__((always_inline)) {
 #pragma unroll
-            for (int l = 0; l < L; ++l)
+        for (int h = 0; h < 2; ++h) {
 #pragma unroll
-                for (int j = 0; j < (2 * WCP); ++j) {
-                    if constexpr (decltype(first)::value)
-                        acc[ii][l][j] = mfma32(fa[0][ii][l], fb[0][j], v16i{});
-                    else
-                        acc[ii][l][j] = mfma32(fa[0][ii][l], fb[0][j], acc[ii][l][j]);
-                    const int idx = (ii * L + l) * (2 * WCP) + j + 1;
-                    if (idx % PER == 0 && idx / PER <= LPW) {
-                        __builtin_amdgcn_sched_barrier(0);
-                        if (do_issue)
-                            dma16(sp[idx / PER - 1] + (int64_t)ksrc * sstep[idx / PER - 1], st + dst[idx / PER - 1]);
-                        __builtin_amdgcn_sched_barrier(0);
-                    }
-                }
+            for (int ii = 0; ii < WR; ++ii)
 #pragma unroll
-        for (int c = NM / PER; c < LPW; ++c)
-            if (do_issue) dma16(sp[c] + (int64_t)ksrc * sstep[c], st + dst[c]);
+                for (int l = 0; l < L; ++l) read_a(slot, h, ii, l);
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) read_b(slot, h, j);
+        }
     };
 
     // ---- stream prologue: tile 0's rows, metadata and first kS-1 stages
@@ -1044,81 +1060,68 @@ __global__ __launch_bounds__(kGuThreads) void ring_gemm_kernel(
     vm_wait<0>();
     lds_barrier();
     fetch_row_meta(0);
-    // per-lane sources of this wave's loads; from step nk-kS on (when this
-    // tile has issued its last stage) they hold the next tile's
-    const int8_t* src[LPW];
     make_src(cur, 0, src);
     int slot0 = 0;  // ring slot of the current tile's stage 0
 #pragma unroll
     for (int s = 0; s < kS - 1; ++s) issue(s, src, s);
+    vm_wait_stages(std::integral_constant<int, kS - 2>{});
+    lds_barrier();
 
     for (int i = 0; i < tr.ntiles; ++i) {
         const bool has_next = i + 1 < tr.ntiles;
         const int mn = m ^ 1;
         TileInfo nxt = cur;
         if (has_next) nxt = info(i + 1);
-        // stage 0 has landed once at most the kS-2 later stages are in flight
-        vm_wait<(kS - 2) * LPW>();
-        lds_barrier();
-        issue((slot0 + kS - 1) % kS, src, kS - 1);
-        if (has_next) fetch_rows(nxt, mn);
         // a wave whose rows all lie past the tile's last row (an expert's
         // partial last tile) skips its fragment reads and MFMAs
         const bool act = 32 * WR * wr < cur.nrows;
-        if (act) {
-            read_frags(slot0, 0);
-            read_frags(slot0, 1);
-        }
-        // One K step: wait for stage ks+1, publish it, refill the slot of
-        // stage ks (its fragments are in registers) with stage ks+kS of the
-        // stream, and run stage ks while reading stage ks+1's fragments.
-        // Phase A (`next` false) refills with this tile's stages; phase B
-        // (the last kS steps) with the next tile's first kS-1 stages.
-        auto kstep = [&](int ks, auto first, auto next) __attribute__((always_inline)) {
-            const int slot = (slot0 + ks) % kS;
-            if (ks + 1 < nk) {
-                // the stages after ks+1 still in flight are ks+2 .. ks+kS-1
-                // of the stream (fewer at the stream's end)
-                if (has_next || ks + kS - 1 < nk) vm_wait<(kS - 2) * LPW>();
-                else vm_wait<0>();
-            }
-            lds_barrier();
-            const int nslot = (slot + 1) % kS;
-            if constexpr (!decltype(next)::value) {
-                mfma_step_dma(first, src, true, slot, ks + kS, act);
-            } else {
-                mfma_step_dma(first, src, has_next && ks + kS - nk <= kS - 2, slot, ks + kS - nk, act);
-            }
-            if (act) {
-                if (ks + 1 < nk) read_frags(nslot, 0);
-                mfma_step(1, std::false_type{});
-                if (ks + 1 < nk) read_frags(nslot, 1);
+        // Step ks.  Phase A (ks <= nk-kS): refill with this tile's stage
+        // ks+kS-1; phase B: with the next tile's stage ks+kS-1-nk.
+        auto step = [&](int ks, auto first, auto phase_b, auto active) __attribute__((always_inline)) {
+            constexpr bool B = decltype(phase_b)::value, ACT = decltype(active)::value;
+            // stage ks+1 of the stream has landed once at most the stages
+            // after it that are already issued (ks+2 .. ks+kS-2) are in flight
+            if (!B || has_next) vm_wait_stages(std::integral_constant<int, kS - 3>{});
+            else if (ks + 1 < nk) vm_wait<0>();
+            if constexpr (ACT) lds_barrier_keep<RPS>();
+            else lds_barrier();
+            const int dslot = !B || has_next ? (slot0 + ks + kS - 1) % kS : -1;
+            const int dks = B ? ks + kS - 1 - nk : ks + kS - 1;
+            if (decltype(first)::value && has_next) fetch_rows(nxt, mn);
+            if constexpr (ACT) {
+                const int rslot = ks + 1 < nk ? (slot0 + ks + 1) % kS : -1;
+                kstep_h(std::integral_constant<int, 0>{}, first, rslot, dslot, dks);
+                kstep_h(std::integral_constant<int, 1>{}, std::false_type{}, rslot, -1, 0);
+            } else if (dslot >= 0) {
+                issue(dslot, src, dks);
             }
         };
-        int ks = 0;
-        if (nk > kS) {
-            kstep(0, std::true_type{}, std::false_type{});
+        auto tile_k = [&](auto active) __attribute__((always_inline)) {
+            // stage 0's fragments (landed and published by the previous
+            // step's barrier)
+            if constexpr (decltype(active)::value) read_all(slot0);
+            step(0, std::true_type{}, std::false_type{}, active);
+            int ks = 1;
 #pragma clang loop unroll(disable)
-            for (ks = 1; ks < nk - kS; ++ks) kstep(ks, std::false_type{}, std::false_type{});
-        }
-        if (has_next) {
-            // the next tile's row tokens (fetched at this tile's start) have
-            // landed once a stage issued after them has
-            if (nk < 2 * kS) {
-                vm_wait<0>();
-                lds_barrier();
+            for (; ks <= nk - kS; ++ks) step(ks, std::false_type{}, std::false_type{}, active);
+            if (has_next) {
+                // the next tile's loads start now: their sources (its row
+                // tokens have landed, a stage issued after them has) and its
+                // row metadata
+                if (nk < 2 * kS) {
+                    vm_wait<0>();
+                    lds_barrier();
+                }
+                make_src(nxt, mn, src);
+                fetch_row_meta(mn);
             }
-            make_src(nxt, mn, src);
-            fetch_row_meta(mn);
-        }
-        if (ks == 0) {
-            kstep(0, std::true_type{}, std::true_type{});
-            ks = 1;
-        }
 #pragma clang loop unroll(disable)
-        for (; ks < nk; ++ks) kstep(ks, std::false_type{}, std::true_type{});
+            for (; ks < nk; ++ks) step(ks, std::false_type{}, std::true_type{}, active);
+        };
+        if (act) tile_k(std::true_type{});
+        else tile_k(std::false_type{});
 
-        // ---- epilogue (the next tile's first kS-1 stages are in flight):
+        // ---- epilogue (the next tile's first kS-2 stages are in flight):
         // g and u into the row's two halves of gu.  The zero-point
         // correction is chosen once per tile (zg, zu are uniform), so no
         // per-element test drags its integer multiplies into the common case.

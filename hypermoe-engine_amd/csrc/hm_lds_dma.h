@@ -25,6 +25,16 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// The same barrier, leaving this wave's N most recent LDS operations in
+// flight (LDS operations complete in issue order; the caller keeps scalar
+// memory loads out of the window so that the count holds LDS operations
+// only).
+template <int N>
+__device__ __forceinline__ void lds_barrier_keep() {
+    static_assert(N >= 0 && N <= 15, "lgkmcnt range");
+    asm volatile("s_waitcnt lgkmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
 // One wave-wide 16-byte global -> LDS load: lane l's 16 bytes from its own
 // gsrc land at lds_base + 16*l (M0 holds the wave-uniform LDS base).
 //
