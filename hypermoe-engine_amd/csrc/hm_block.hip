@@ -255,9 +255,12 @@ int block_forward(const hm_layer* layer, const float* hidden, const float* route
         route_flags & (HM_ROUTE_SOFTMAX | HM_ROUTE_RENORM | HM_EXEC_ROUTE_SEQUENTIAL);
     // decode: the grouping is fused into the router's select (one launch
     // fewer)
-    // FP32 experts of a decode batch take the FP32 GEMV
+    // FP32 experts of a decode batch take the FP32 GEMV (its rows are the
+    // normalised ones when the layer's RMSNorm runs first, so their
+    // alignment is the one that decides)
+    const void* gemv_rows = ln ? static_cast<const void*>(ln->normed) : static_cast<const void*>(hidden);
     const bool gv32 = layer->dtype == HM_DTYPE_FP32 && tokens <= HM_GEMV_MAX_TOKENS &&
-                      p.counters && hm_gemv_f32_ok(layer, hidden) && hm_gemv_f32_ok(layer, p.zf);
+                      p.counters && hm_gemv_f32_ok(layer, gemv_rows) && hm_gemv_f32_ok(layer, p.zf);
     const bool fuse = (gemv || gv32) && H % 32 == 0 && E <= 1024 && top_k <= 64 && P <= 1024;
     bool x_quantized = false;
     if (fuse) {

@@ -107,6 +107,80 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(
     }
 }
 
+// The same RMSNorm for rows of 256 V floats (16-byte aligned), one wave per
+// row and four rows per workgroup: a lane's V 16-byte loads are issued
+// together and the row stays in registers (rmsnorm_kernel's strided loop
+// waits for each load before the next).  Same bracket, same fallback: a row
+// with an ambiguous element is copied to the wave's LDS and lane 0 forms the
+// sequential sum.
+template <int V>
+__global__ __launch_bounds__(kBlock) void rmsnorm_wave_kernel(
+    const float* __restrict__ x, const float* __restrict__ gamma,
+    float* __restrict__ y, int64_t rows, float eps) {
+    constexpr int W = 256 * V;
+    extern __shared__ float row_lds[];  // [4][W]
+    const int lane = threadIdx.x & (HM_WAVE - 1), wv = threadIdx.x / HM_WAVE;
+    const int64_t r = (int64_t)blockIdx.x * (kBlock / HM_WAVE) + wv;
+    if (r >= rows) return;
+    const float4* xr = reinterpret_cast<const float4*>(x + r * W);
+    const float4* g4 = reinterpret_cast<const float4*>(gamma);
+    float4* yr = reinterpret_cast<float4*>(y + r * W);
+    float4 v[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) v[j] = xr[HM_WAVE * j + lane];
+    double local = 0.0;
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        local += (double)v[j].x * v[j].x;
+        local += (double)v[j].y * v[j].y;
+        local += (double)v[j].z * v[j].z;
+        local += (double)v[j].w * v[j].w;
+    }
+    const double s_fast = hm_wave_sum_f64(local);  // equal on every lane
+    const double d = hm_rms_sum_slack(W);
+    const double wd = (double)W, ed = (double)eps;
+    const double inv_lo = hm_inv_rms(s_fast * (1.0 + d), wd, ed);
+    const double inv_hi = hm_inv_rms(s_fast * (1.0 - d), wd, ed);
+    float4 out[V];
+    bool amb = false;
+    auto one = [&](float xv, float gv, float& o) __attribute__((always_inline)) {
+        const float a = (float)((double)xv * inv_lo * (double)gv);
+        const float b = (float)((double)xv * inv_hi * (double)gv);
+        o = a;
+        amb |= __float_as_uint(a) != __float_as_uint(b);
+    };
+#pragma unroll
+    for (int j = 0; j < V; ++j) {
+        const float4 g = g4[HM_WAVE * j + lane];
+        one(v[j].x, g.x, out[j].x);
+        one(v[j].y, g.y, out[j].y);
+        one(v[j].z, g.z, out[j].z);
+        one(v[j].w, g.w, out[j].w);
+    }
+    if (__ballot(amb) != 0) {
+        // the reference's sequential sum over an LDS copy of the row
+        float4* lrow = reinterpret_cast<float4*>(row_lds + (int64_t)wv * W);
+#pragma unroll
+        for (int j = 0; j < V; ++j) lrow[HM_WAVE * j + lane] = v[j];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        double inv = 0.0;
+        if (lane == 0) inv = hm_inv_rms(hm_rms_sum_seq(row_lds + (int64_t)wv * W, W), wd, ed);
+        inv = __shfl(inv, 0, HM_WAVE);
+#pragma unroll
+        for (int j = 0; j < V; ++j) {
+            const float4 g = g4[HM_WAVE * j + lane];
+            out[j].x = (float)((double)v[j].x * inv * (double)g.x);
+            out[j].y = (float)((double)v[j].y * inv * (double)g.y);
+            out[j].z = (float)((double)v[j].z * inv * (double)g.z);
+            out[j].w = (float)((double)v[j].w * inv * (double)g.w);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < V; ++j) yr[HM_WAVE * j + lane] = out[j];
+}
+
 // ---------------------------------------------------------------------------
 // A2 router logits (src/router/CpuRouterBackend.cpp:41-49):
 //   logit[t,e] = float(sum_k double(h[t,k]) * double(w[k,e])), k ascending.
@@ -1613,6 +1687,22 @@ int hm_rmsnorm(const float* x, const float* gamma, float* y, int64_t rows,
     HM_REQUIRE(width <= 16384);                     // row staged in LDS
     if (rows == 0) return HM_OK;
     HM_REQUIRE(rows <= INT_MAX);
+    const bool aligned = ((uintptr_t)x | (uintptr_t)gamma | (uintptr_t)y) % 16 == 0;
+    if (aligned && width % 256 == 0 && width / 256 <= 16) {
+        const unsigned grid = (unsigned)((rows + kBlock / HM_WAVE - 1) / (kBlock / HM_WAVE));
+        const size_t lds = (size_t)(kBlock / HM_WAVE) * width * sizeof(float);
+        const hipStream_t s = hm_stream(stream);
+        switch (width / 256) {
+#define HM_RMS_CASE(v) \
+    case v: hipLaunchKernelGGL(rmsnorm_wave_kernel<v>, dim3(grid), dim3(kBlock), lds, s, x, gamma, y, rows, eps); break;
+            HM_RMS_CASE(1) HM_RMS_CASE(2) HM_RMS_CASE(3) HM_RMS_CASE(4) HM_RMS_CASE(5) HM_RMS_CASE(6)
+            HM_RMS_CASE(7) HM_RMS_CASE(8) HM_RMS_CASE(9) HM_RMS_CASE(10) HM_RMS_CASE(11)
+            HM_RMS_CASE(12) HM_RMS_CASE(13) HM_RMS_CASE(14) HM_RMS_CASE(15) HM_RMS_CASE(16)
+#undef HM_RMS_CASE
+        }
+        HM_LAUNCHED();
+        return HM_OK;
+    }
     hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(kBlock),
                        (size_t)width * sizeof(float), hm_stream(stream), x, gamma,
                        y, width, eps);

@@ -66,11 +66,15 @@ def layer():
     return DeviceExpertLayer(payload, scale, zp, H, I)
 
 
-def _layer_forward(block, h, gamma, w, flags):
+def _layer_forward(block, h, gamma, w, flags, normed_offset=0):
+    """normed_offset: the normalised rows start that many floats into their
+    buffer (an offset of 1 leaves them 4-byte but not 16-byte aligned)."""
     import torch
     T = h.shape[0]
     P = T * block.top_k
-    normed = torch.full((T, H), float("nan"), dtype=torch.float32, device="cuda")
+    normed_buf = torch.full((T * H + normed_offset,), float("nan"), dtype=torch.float32,
+                            device="cuda")
+    normed = normed_buf[normed_offset:].view(T, H)
     out = torch.full((T, H), float("nan"), dtype=torch.float32, device="cuda")
     ids = torch.full((T, block.top_k), -1, dtype=torch.int32, device="cuda")
     scores = torch.empty((T, block.top_k), dtype=torch.float32, device="cuda")
@@ -89,6 +93,49 @@ def _layer_forward(block, h, gamma, w, flags):
     assert int(status.item()) == 0
     assert P == ids.numel()
     return normed.cpu().numpy(), ids.cpu().numpy().view(np.uint32), out.cpu().numpy()
+
+
+@pytest.fixture(scope="module")
+def layer_f32():
+    payload, scale, zp = synth.expert_layer(93, 0, E, H, I, False)
+    return DeviceExpertLayer(payload, scale, zp, H, I), payload
+
+
+@pytest.mark.parametrize("T", [1, 5])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_layer_forward_fp32(dev, layer_f32, T, offset):
+    """FP32-weight layers through hm_moe_layer_forward.  With the normalised
+    rows 16-byte aligned, decode batches take the FP32 GEMV and the result
+    equals hm_rmsnorm followed by hm_moe_block_forward bit for bit; with
+    them 4 bytes off, the call takes the FP32 tiles instead (the GEMV needs
+    16-byte rows) rather than refusing.  Either way: the norm bit-exact, the
+    routing bit-exact, the output within 1e-3 of the reference arithmetic."""
+    import torch
+    print(f"[gpu] FP32 layer forward T={T} normed offset={offset}", flush=True)
+    dl, payload = layer_f32
+    rng = np.random.default_rng(3000 + T)
+    h = rng.standard_normal((T, H)).astype(np.float32)
+    gamma = (0.5 + rng.random(H)).astype(np.float32)
+    w = synth.router_weights(93, 0, H, E)
+    dh, dg, dw = (torch.from_numpy(a).cuda() for a in (h, gamma, w))
+    block = MoEBlock(dl, K)
+    normed, ids, out = _layer_forward(block, dh, dg, dw, 0, normed_offset=offset)
+    ref_norm = O.rmsnorm(h, gamma, EPS)
+    assert_bitexact(normed, ref_norm, f"T={T} RMSNorm")
+    ones = np.ones((E, 3), np.float32)
+    zeros = np.zeros((E, 3), np.int32)
+    rout, rids, _ = O.moe_block(payload, ones, zeros, ref_norm, w, K, I)
+    assert_bitexact(ids, rids, f"T={T} routing vs oracle")
+    moe = out - h  # the residual is added last, exactly
+    err = float(np.abs(moe - rout).max() / np.abs(rout).max())
+    assert err < 1e-3, f"T={T} offset={offset}: normwise error {err}"
+    if offset == 0:
+        dn = torch.empty_like(dh)
+        capi.call("hm_rmsnorm", dh.data_ptr(), dg.data_ptr(), dn.data_ptr(), T, H, EPS,
+                  torch.cuda.current_stream().cuda_stream)
+        ref = block.execute_batch(dn, dw, residual=dh)
+        assert_bitexact(ids, ref.ids, f"T={T} routing")
+        assert_bitexact(out, ref.output.cpu().numpy(), f"T={T} output")
 
 
 @pytest.mark.parametrize("T", [1, 2, 5, 16, 40])
@@ -118,6 +165,31 @@ def test_layer_forward_matches_norm_then_block(dev, layer, T, seq):
     assert_bitexact(dn.cpu().numpy(), ref_norm, f"T={T} hm_rmsnorm")
     assert_bitexact(ids, ref.ids, f"T={T} routing")
     assert_bitexact(out, ref.output.cpu().numpy(), f"T={T} output")
+
+
+@pytest.mark.parametrize("T", [9, 13])
+def test_rmsnorm_rows_unsettled_in_other_waves(dev, T):
+    """hm_rmsnorm at H = 2048 runs one wave per row, four rows per
+    workgroup: unsettled rows in wave slots 1 and 2 of different workgroups
+    take the sequential sum on their own, the settled rows beside them do
+    not, and the last workgroup's waves past the final row do nothing."""
+    import torch
+    print(f"[gpu] rmsnorm unsettled rows T={T}", flush=True)
+    rng = np.random.default_rng(2000 + T)
+    row0, gamma, picked = _unsettled_row(rng, EPS)
+    h = rng.standard_normal((T, H)).astype(np.float32)
+    h[1] = row0
+    h[6] = row0
+    dh, dg = torch.from_numpy(h).cuda(), torch.from_numpy(gamma).cuda()
+    dn = torch.full_like(dh, float("nan"))
+    capi.call("hm_rmsnorm", dh.data_ptr(), dg.data_ptr(), dn.data_ptr(), T, H, EPS,
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    ref = O.rmsnorm(h, gamma, EPS)
+    got = dn.cpu().numpy()
+    assert_bitexact(got, ref, f"T={T} hm_rmsnorm")
+    for r in (1, 6):
+        assert_bitexact(got[r, picked], ref[r, picked], f"T={T} row {r} unsettled elements")
 
 
 def test_layer_forward_rejects_overlap(dev, layer):
