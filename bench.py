@@ -22,6 +22,10 @@ steps themselves carry no events).
   decode (C3):  gate/up GEMV, bytes = U*2*H*I + activations, bound = HBM 8 TB/s
 The CPU baseline is the oracle's restatement of the reference CPU path
 (single thread, reference loop order) timed on a bounded token sample.
+The default C4 run also times the decode shapes C3-1 and C3-16 of the same
+layer in child benches and reports them under "decode" (step time, the
+layer's HBM fraction, the gate/up GEMV's roofline and, for C3-16, its HBM
+bytes per launch); --no-decode skips them.
 """
 from __future__ import annotations
 
@@ -65,6 +69,9 @@ def parse():
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 --pmc child runs that measure the dominant "
                          "kernel's HBM bytes per launch (roofline.traffic = null)")
+    ap.add_argument("--no-decode", action="store_true",
+                    help="C4: skip the decode legs (C3-1 and C3-16 child benches whose step "
+                         "times and HBM fractions the line reports under \"decode\")")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="also run a plain device-to-device copy of this many MiB (3x) "
                          "before the timed region: the known-size kernel that calibrates "
@@ -100,7 +107,8 @@ def pmc_traffic(workload: str, kernel_re: str, primary_re: str, limbs: tuple, qu
             cmd = [exe, "--pmc", counter, "--kernel-include-regex", f"{kernel_re}|copyBuffer",
                    "--output-format", "csv", "-d", d, "-o", "pmc", "--", sys.executable,
                    str(REPO / "bench.py"), "--workload", workload, "--steps", "2", "--warmup",
-                   "1", "--cpu-sample", "0", "--quiet", "--no-traffic", "--limbs-x", str(limbs[0]),
+                   "1", "--cpu-sample", "0", "--quiet", "--no-traffic", "--no-decode",
+                   "--limbs-x", str(limbs[0]),
                    "--limbs-z", str(limbs[1]),
                    "--copy-mb", str(copy_mib)]
             env = dict(os.environ, TMPDIR="/tmp")
@@ -157,7 +165,8 @@ def pmc_mfma(workload: str, kernels: dict, limbs: tuple, quiet: bool):
         cmd = [exe, "--pmc", *counters, "--kernel-include-regex", "|".join(kernels.values()),
                "--output-format", "csv", "-d", d, "-o", "pmc", "--", sys.executable,
                str(REPO / "bench.py"), "--workload", workload, "--steps", "2", "--warmup", "1",
-               "--cpu-sample", "0", "--quiet", "--no-traffic", "--limbs-x", str(limbs[0]),
+               "--cpu-sample", "0", "--quiet", "--no-traffic", "--no-decode",
+               "--limbs-x", str(limbs[0]),
                "--limbs-z", str(limbs[1])]
         log("[bench] counters: rocprofv3 --pmc " + " ".join(counters), quiet)
         try:
@@ -184,6 +193,40 @@ def pmc_mfma(workload: str, kernels: dict, limbs: tuple, quiet: bool):
                      "mfma_busy_cycles": busy, "busy_cu_cycles": cu,
                      "mfma_insts": sum(v["SQ_INSTS_MFMA"]) / max(1, len(v["SQ_INSTS_MFMA"]))}
     return out
+
+
+def decode_legs(quiet: bool):
+    """The decode shapes of the same layer (C3-1, C3-16: one and sixteen
+    tokens, 128 experts, top-8, INT8), each timed by a child bench in this
+    run: step time, tokens/s, the whole layer's algorithmic bytes over the
+    step against HBM peak, and the gate/up GEMV's own roofline line (C3-16
+    with its HBM bytes per launch from the rocprofv3 --pmc child runs).
+    None for a leg whose child fails."""
+    import subprocess
+    legs = {}
+    for wl, steps, traffic in (("C3-1", 400, False), ("C3-16", 200, True)):
+        cmd = [sys.executable, str(REPO / "bench.py"), "--workload", wl, "--steps", str(steps),
+               "--warmup", str(steps // 10), "--cpu-sample", "0", "--quiet", "--no-decode"]
+        if not traffic:
+            cmd.append("--no-traffic")
+        log(f"[bench] decode leg {wl}", quiet)
+        try:
+            res = subprocess.run(cmd, cwd=str(REPO), stdout=subprocess.PIPE,
+                                 stderr=subprocess.DEVNULL, text=True, timeout=420)
+            d = json.loads(res.stdout.strip().splitlines()[-1])
+        except Exception as ex:  # noqa: BLE001 -- the leg is reported as missing
+            log(f"[bench] decode leg {wl} failed: {ex}", quiet)
+            legs[wl] = None
+            continue
+        r = d["roofline"]
+        legs[wl] = {"tokens": d["config"]["tokens"], "ms_per_step": d["ms_per_step"],
+                    "tokens_per_s": d["value"], "unique_experts": d["config"]["unique_experts"],
+                    "layer_hbm_frac": d["layer_roofline"]["hbm_frac"],
+                    "layer_algorithmic_bytes": d["layer_roofline"]["algorithmic_bytes"],
+                    "gate_up_gemv": {k: r.get(k) for k in ("kernel", "achieved", "peak", "unit",
+                                                           "frac", "traffic", "launch_ms")},
+                    "stages_ms": d["stages_ms"]}
+    return legs
 
 
 def main():
@@ -422,6 +465,10 @@ def main():
                   "compare_1e-4": bool(np.all(d <= 1e-4 + 1e-4 * np.abs(rout)))}
         log(f"[bench] cpu baseline {cpu['value']} tokens/s; parity {parity}", q)
 
+    decode = None
+    if cfg.name == "C4" and not args.no_decode:
+        decode = decode_legs(q)
+
     line = {
         "metric": METRIC, "value": round(tokens_per_s, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
@@ -438,6 +485,8 @@ def main():
         "stages_ms": {n: round(v, 5) for n, v in stage.items()},
         "cpu_baseline": cpu, "parity": parity,
     }
+    if decode is not None:
+        line["decode"] = decode
     print(json.dumps(line), flush=True)
 
 
