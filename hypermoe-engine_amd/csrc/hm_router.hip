@@ -110,15 +110,16 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(
 // The same RMSNorm for rows of 256 V floats (16-byte aligned), one wave per
 // row and four rows per workgroup: a lane's V 16-byte loads are issued
 // together and the row stays in registers (rmsnorm_kernel's strided loop
-// waits for each load before the next).  Same bracket, same fallback: a row
-// with an ambiguous element is copied to the wave's LDS and lane 0 forms the
-// sequential sum.
+// waits for each load before the next).  Same bracket, same fallback (a row
+// with an ambiguous element takes the sequential sum), with the exact
+// products formed by the whole wave so that lane 0's chain is only the
+// additions.
 template <int V>
 __global__ __launch_bounds__(kBlock) void rmsnorm_wave_kernel(
     const float* __restrict__ x, const float* __restrict__ gamma,
     float* __restrict__ y, int64_t rows, float eps) {
     constexpr int W = 256 * V;
-    extern __shared__ float row_lds[];  // [4][W]
+    extern __shared__ float row_lds[];  // [4][512] doubles: a chunk of products per wave
     const int lane = threadIdx.x & (HM_WAVE - 1), wv = threadIdx.x / HM_WAVE;
     const int64_t r = (int64_t)blockIdx.x * (kBlock / HM_WAVE) + wv;
     if (r >= rows) return;
@@ -158,15 +159,52 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_wave_kernel(
         one(v[j].w, g.w, out[j].w);
     }
     if (__ballot(amb) != 0) {
-        // the reference's sequential sum over an LDS copy of the row
-        float4* lrow = reinterpret_cast<float4*>(row_lds + (int64_t)wv * W);
+        // The reference's sequential sum: s = fl(s + p_k) with the exact
+        // products p_k = double(x_k)^2.  The wave forms the products of 512
+        // consecutive elements (its registers j = 2q, 2q+1) into LDS, then
+        // lane 0 adds them in order, 16 loaded ahead; the chain is one
+        // dependent add per element.
+        double* lp = reinterpret_cast<double*>(row_lds) + (int64_t)wv * 512;
+        double s = 0.0;
 #pragma unroll
-        for (int j = 0; j < V; ++j) lrow[HM_WAVE * j + lane] = v[j];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        for (int q = 0; q < (V + 1) / 2; ++q) {
+            const int nj = 2 * q + 1 < V ? 2 : 1;
+#pragma unroll
+            for (int jj = 0; jj < nj; ++jj) {
+                const float4 x4 = v[2 * q + jj];
+                double* d = lp + 256 * jj + 4 * lane;
+                d[0] = (double)x4.x * x4.x;
+                d[1] = (double)x4.y * x4.y;
+                d[2] = (double)x4.z * x4.z;
+                d[3] = (double)x4.w * x4.w;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            if (lane == 0) {
+                const double2* p2 = reinterpret_cast<const double2*>(lp);
+                const int n2 = 128 * nj;  // pairs of products in this chunk
+                double2 cur[8], nxt[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) cur[i] = p2[i];
+                for (int b = 0; b < n2; b += 8) {
+                    if (b + 8 < n2) {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) nxt[i] = p2[b + 8 + i];
+                    }
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        s += cur[i].x;
+                        s += cur[i].y;
+                    }
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+        }
         double inv = 0.0;
-        if (lane == 0) inv = hm_inv_rms(hm_rms_sum_seq(row_lds + (int64_t)wv * W, W), wd, ed);
+        if (lane == 0) inv = hm_inv_rms(s, wd, ed);
         inv = __shfl(inv, 0, HM_WAVE);
 #pragma unroll
         for (int j = 0; j < V; ++j) {
@@ -1690,7 +1728,7 @@ int hm_rmsnorm(const float* x, const float* gamma, float* y, int64_t rows,
     const bool aligned = ((uintptr_t)x | (uintptr_t)gamma | (uintptr_t)y) % 16 == 0;
     if (aligned && width % 256 == 0 && width / 256 <= 16) {
         const unsigned grid = (unsigned)((rows + kBlock / HM_WAVE - 1) / (kBlock / HM_WAVE));
-        const size_t lds = (size_t)(kBlock / HM_WAVE) * width * sizeof(float);
+        const size_t lds = (size_t)(kBlock / HM_WAVE) * 512 * sizeof(double);
         const hipStream_t s = hm_stream(stream);
         switch (width / 256) {
 #define HM_RMS_CASE(v) \
