@@ -8,6 +8,7 @@
 // the reference's ComputeBackend interface (src/backend/Backend.hpp:36-71).
 #include "HipMoEAdapter.hpp"
 
+#include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <memory>
@@ -108,6 +109,51 @@ int main() {
     CHECK(hv.device() == hm::tensor::Device::cpu());
     CHECK(hv.data() == store->data());
     CHECK(hv.lockOwner() == rt.view().lockOwner());
+
+#ifdef HM_ADAPTER_HIP_ENUMS
+    // ---- device tensors (the reference built with the HIP enumerators of
+    // integration/reference_enums.py): a result whose tensors live on HIP
+    // device 1 converts into reference tensors the reference's own
+    // Tensor::fromStorage accepts (src/tensor/Tensor.cpp:14-26), with the
+    // device, storage and shape kept.  The device pointer is never
+    // dereferenced on the host.
+    {
+        void* devp = reinterpret_cast<void*>(std::uintptr_t{1} << 40);
+        std::shared_ptr<void> dev_owner(devp, [](void*) {});
+        auto dev_tensor = [&](std::size_t rows, std::size_t cols, std::size_t off) {
+            return hm::tensor::Tensor::fromStorage(
+                hm::tensor::Shape({rows, cols}), hm::tensor::DType::FP32, hm::tensor::Device::hip(1),
+                static_cast<char*>(devp) + off, rows * cols * sizeof(float), dev_owner);
+        };
+        hm::BatchLayerExecutionResult d = keep;
+        d.expertOutputs.clear();
+        for (std::size_t b = 0; b < 3; ++b)
+            d.expertOutputs.push_back(dev_tensor(d.expertBatches[b].size(), 4, 4096 * (b + 1)));
+        d.output = dev_tensor(2, 4, 0);
+        const hm::BatchLayerExecutionResult dkeep = d;
+        const hypermoe::runtime::BatchLayerExecutionResult rd = hypermoe::integration::toReference(std::move(d));
+        auto same_dev = [&](const hypermoe::tensor::Tensor& t, const hm::tensor::Tensor& ht) {
+            CHECK(t.valid());
+            CHECK(t.device().type == hypermoe::tensor::DeviceType::HIP);
+            CHECK(t.device().type == hypermoe::backend::hip::kHipDeviceType);
+            CHECK(t.device().ordinal == 1);
+            CHECK(hypermoe::tensor::toString(t.device().type) == "HIP");
+            CHECK(t.data() == ht.data());
+            CHECK(t.storageBytes() == ht.storageBytes());
+            CHECK(t.shape().dimensions() == ht.shape().dimensions());
+        };
+        CHECK(rd.expertOutputs.size() == 3);
+        for (std::size_t i = 0; i < 3; ++i) same_dev(rd.expertOutputs[i], dkeep.expertOutputs[i]);
+        same_dev(rd.output, dkeep.output);
+        CHECK(rd.routing.valid() && rd.routing.expertGroups.size() == 3);
+        // and a reference HIP view back into an hm view of the same storage
+        const hm::tensor::TensorView dv = hypermoe::integration::toHm(hypermoe::tensor::TensorView(rd.output));
+        CHECK(dv.device() == hm::tensor::Device::hip(1));
+        CHECK(dv.data() == rd.output.data());
+        CHECK(hypermoe::backend::hip::kHipBackendKind == hypermoe::backend::BackendKind::Hip);
+        std::printf("adapter device tensors ok\n");
+    }
+#endif
 
     // ---- the backend through the reference's interface
     auto hip = std::make_shared<hm::backend::HipBackend>(0);
