@@ -146,18 +146,34 @@ std::shared_ptr<DeviceExpertLayer> DeviceExpertLayer::fromPayload(
 
 // Pinned host copies of the routing metadata and the device buffers they
 // come from, sized for the largest batch seen.
+// One call in flight: the routing arrays the kernels write on the device,
+// their pinned host copy, the call's stage events and its completion event.
+// A slot is owned by one pending result at a time; `inFlight` marks copies
+// that nobody has waited for yet (a result dropped without get()), so the
+// next owner waits before it reuses the pinned memory.
 struct HipMoEBlock::Staging {
     std::shared_ptr<backend::HipBackend> backend;
     std::size_t pairs{}, experts{};
     std::unique_ptr<DeviceBuffer> device;
     void* host{};
-    // byte offsets inside both buffers
-    std::size_t ids{}, scores{}, counts{}, offsets{}, ptok{}, pw{}, status{}, total{};
+    // byte offsets inside both buffers; `zero` is a host word that stays 0
+    // (the source of the status reset, never written after allocation)
+    std::size_t ids{}, scores{}, counts{}, offsets{}, ptok{}, pw{}, status{}, zero{}, total{};
+    std::array<backend::EventHandle, HM_BLOCK_EVENTS> events{};
+    backend::EventHandle done{};
+    bool busy{};
+    bool inFlight{};
 
     ~Staging() {
+        for (auto e : events) backend->destroyEvent(e);
+        backend->destroyEvent(done);
         if (host) backend->freePinned(host);
     }
     void ensure(std::size_t p, std::size_t e) {
+        if (done == nullptr) {
+            for (auto& ev : events) ev = backend->createEvent();
+            done = backend->createEvent();
+        }
         if (p <= pairs && e <= experts && device) return;
         pairs = std::max(p, pairs);
         experts = std::max(e, experts);
@@ -174,14 +190,15 @@ struct HipMoEBlock::Staging {
         ptok = take(pairs * 4);
         pw = take(pairs * 4);
         status = take(4);
+        zero = take(4);
         total = at;
         if (host) {
-            backend->synchronize(backend->computeStream());
             backend->freePinned(host);
             host = nullptr;
         }
         device = std::make_unique<DeviceBuffer>(backend, total);
         host = backend->allocatePinned(total);
+        *hostAt<int32_t>(zero) = 0;
     }
     template <class T>
     T* dev(std::size_t off) const {
@@ -201,8 +218,6 @@ HipMoEBlock::HipMoEBlock(std::shared_ptr<backend::HipBackend> backend,
     if (options_.limbsX < 1 || options_.limbsX > 3 || options_.limbsZ < 1 || options_.limbsZ > 3) {
         throw std::invalid_argument("activation digit planes must be 1, 2 or 3");
     }
-    staging_ = std::make_unique<Staging>();
-    staging_->backend = backend_;
 }
 
 HipMoEBlock::~HipMoEBlock() {
@@ -210,7 +225,6 @@ HipMoEBlock::~HipMoEBlock() {
         if (backend_->isAvailable()) backend_->synchronize(backend_->computeStream());
     } catch (...) {
     }
-    for (auto e : events_) backend_->destroyEvent(e);
 }
 
 void HipMoEBlock::addLayer(LayerId layerId, std::shared_ptr<const DeviceExpertLayer> layer) {
@@ -224,18 +238,104 @@ void HipMoEBlock::addLayer(LayerId layerId, std::shared_ptr<const DeviceExpertLa
 
 BatchLayerExecutionResult HipMoEBlock::executeBatch(LayerId layerId, TensorView hiddenStates,
                                                     TensorView routerWeights) {
-    return run(layerId, hiddenStates, routerWeights, TensorView{});
+    return launchBatch(layerId, hiddenStates, routerWeights).get();
 }
 
 BatchLayerExecutionResult HipMoEBlock::executeBatch(LayerId layerId, TensorView hiddenStates,
                                                     TensorView routerWeights,
                                                     TensorView residual) {
     if (!residual) throw std::invalid_argument("MoE block residual is empty");
-    return run(layerId, hiddenStates, routerWeights, residual);
+    return launchBatch(layerId, hiddenStates, routerWeights, residual).get();
 }
 
-BatchLayerExecutionResult HipMoEBlock::run(LayerId layerId, TensorView hidden,
-                                           TensorView routerWeights, TensorView residual) {
+HipMoEBlock::Staging* HipMoEBlock::acquireSlot(std::size_t pairs, std::size_t experts) {
+    Staging* slot = nullptr;
+    {
+        std::scoped_lock lock(poolMutex_);
+        for (auto& s : slots_) {
+            if (!s->busy) {
+                slot = s.get();
+                break;
+            }
+        }
+        if (slot == nullptr) {
+            slots_.push_back(std::make_unique<Staging>());
+            slot = slots_.back().get();
+            slot->backend = backend_;
+        }
+        slot->busy = true;
+    }
+    try {
+        // copies of a result dropped without get() may still be landing
+        if (slot->inFlight) {
+            backend_->waitEvent(slot->done);
+            slot->inFlight = false;
+        }
+        slot->ensure(pairs, experts);
+    } catch (...) {
+        releaseSlot(slot);
+        throw;
+    }
+    return slot;
+}
+
+void HipMoEBlock::releaseSlot(Staging* slot) noexcept {
+    std::scoped_lock lock(poolMutex_);
+    slot->busy = false;
+}
+
+// A released output buffer of this size (only the pool still owns it; the
+// call's kernels are ordered after every earlier use on the compute stream),
+// else a new one, kept for reuse while the pool has room.
+std::shared_ptr<DeviceBuffer> HipMoEBlock::outputBuffer(
+    std::vector<std::shared_ptr<DeviceBuffer>>& pool, std::size_t bytes) {
+    constexpr std::size_t kKeep = 4;
+    std::scoped_lock lock(poolMutex_);
+    for (auto& b : pool) {
+        if (b.use_count() == 1 && b->size() == bytes) return b;
+    }
+    auto b = std::make_shared<DeviceBuffer>(backend_, bytes);
+    if (pool.size() < kKeep) {
+        pool.push_back(b);
+    } else {
+        for (auto& old : pool) {
+            if (old.use_count() == 1) {
+                old = b;
+                break;
+            }
+        }
+    }
+    return b;
+}
+
+PendingBatchResult::PendingBatchResult(PendingBatchResult&& o) noexcept
+    : block_(o.block_), slot_(o.slot_), layerId_(o.layerId_), tokens_(o.tokens_),
+      hidden_(o.hidden_), topK_(o.topK_), experts_(o.experts_), expertBytes_(o.expertBytes_),
+      output_(std::move(o.output_)), expertOut_(std::move(o.expertOut_)) {
+    o.block_ = nullptr;
+    o.slot_ = nullptr;
+}
+
+PendingBatchResult::~PendingBatchResult() {
+    if (block_ && slot_) block_->releaseSlot(static_cast<HipMoEBlock::Staging*>(slot_));
+}
+
+BatchLayerExecutionResult PendingBatchResult::get() {
+    if (!block_ || !slot_) throw std::logic_error("MoE block result was already taken");
+    // the slot goes back to the block whether or not the result builds
+    struct Release {
+        PendingBatchResult* p;
+        ~Release() {
+            p->block_->releaseSlot(static_cast<HipMoEBlock::Staging*>(p->slot_));
+            p->block_ = nullptr;
+            p->slot_ = nullptr;
+        }
+    } release{this};
+    return block_->materialize(*this);
+}
+
+PendingBatchResult HipMoEBlock::launchBatch(LayerId layerId, TensorView hidden,
+                                            TensorView routerWeights, TensorView residual) {
     std::scoped_lock executionLock(executionMutex_);
     const auto dev = tensor::Device::hip(backend_->deviceOrdinal());
     if (!hidden || hidden.shape().rank() != 2 || hidden.dtype() != DType::FP32 ||
@@ -279,25 +379,27 @@ BatchLayerExecutionResult HipMoEBlock::run(LayerId layerId, TensorView hidden,
                                      options_.limbsX, options_.limbsZ, execFlags);
     if (wsBytes == 0) throw std::invalid_argument("MoE block configuration is invalid");
     if (!workspace_ || workspace_->size() < wsBytes) {
+        // queued calls may still use the smaller workspace
         if (workspace_) backend_->synchronize(stream);
         workspace_ = std::make_unique<DeviceBuffer>(backend_, wsBytes);
     }
     const std::size_t P = T * k;
-    staging_->ensure(P, E);
-    if (events_[0] == nullptr) {
-        for (auto& e : events_) e = backend_->createEvent();
-    }
 
-    // callee-allocated outputs (MoERuntime.cpp:134)
-    auto out = std::make_shared<DeviceBuffer>(backend_, T * H * sizeof(float));
-    std::shared_ptr<DeviceBuffer> expertOut;
-    if (options_.keepExpertOutputs) {
-        expertOut = std::make_shared<DeviceBuffer>(backend_, P * H * sizeof(float));
-    }
+    PendingBatchResult pending;
+    pending.block_ = this;
+    Staging* slot = acquireSlot(P, E);
+    pending.slot_ = slot;
+    pending.layerId_ = layerId;
+    pending.tokens_ = T;
+    pending.hidden_ = H;
+    pending.topK_ = k;
+    pending.experts_ = E;
+    pending.expertBytes_ = layer.expertBytes();
+    // callee-allocated outputs (MoERuntime.cpp:134), reused once released
+    auto out = outputBuffer(outPool_, T * H * sizeof(float));
+    if (options_.keepExpertOutputs) pending.expertOut_ = outputBuffer(expertOutPool_, P * H * sizeof(float));
 
-    auto& st = *staging_;
-    *st.hostAt<int32_t>(st.status) = 0;
-    backend_->copyToDevice(st.dev<int32_t>(st.status), st.hostAt<int32_t>(st.status), 4, stream);
+    auto& st = *slot;
     hm_block_io io{};
     io.out = static_cast<float*>(out->data());
     io.ids = st.dev<uint32_t>(st.ids);
@@ -306,11 +408,12 @@ BatchLayerExecutionResult HipMoEBlock::run(LayerId layerId, TensorView hidden,
     io.offsets = st.dev<int32_t>(st.offsets);
     io.perm_tokens = st.dev<int32_t>(st.ptok);
     io.perm_weights = st.dev<float>(st.pw);
-    io.expert_out = expertOut ? static_cast<float*>(expertOut->data()) : nullptr;
+    io.expert_out = pending.expertOut_ ? static_cast<float*>(pending.expertOut_->data()) : nullptr;
     io.status = st.dev<int32_t>(st.status);
     io.residual = residual ? static_cast<const float*>(residual.data()) : nullptr;
-    io.events = events_.data();
+    io.events = st.events.data();
     try {
+        backend_->copyToDevice(io.status, st.hostAt<int32_t>(st.zero), 4, stream);
         throwOnStatus(hm_moe_block_forward(&layer.descriptor(),
                                            static_cast<const float*>(hidden.data()),
                                            static_cast<const float*>(routerWeights.data()),
@@ -318,7 +421,8 @@ BatchLayerExecutionResult HipMoEBlock::run(LayerId layerId, TensorView hidden,
                                            options_.limbsX, options_.limbsZ, &io,
                                            workspace_->data(), workspace_->size(), stream),
                       "MoE block forward");
-        // routing metadata back through pinned memory, then one stream sync
+        // routing metadata to pinned memory behind the kernels, then the
+        // call's completion event; nothing here waits for the device
         backend_->copyFromDevice(st.hostAt<void>(st.ids), io.ids, P * 4, stream);
         backend_->copyFromDevice(st.hostAt<void>(st.scores), io.scores, P * 4, stream);
         backend_->copyFromDevice(st.hostAt<void>(st.counts), io.counts, E * 4, stream);
@@ -326,15 +430,28 @@ BatchLayerExecutionResult HipMoEBlock::run(LayerId layerId, TensorView hidden,
         backend_->copyFromDevice(st.hostAt<void>(st.ptok), io.perm_tokens, P * 4, stream);
         backend_->copyFromDevice(st.hostAt<void>(st.pw), io.perm_weights, P * 4, stream);
         backend_->copyFromDevice(st.hostAt<void>(st.status), io.status, 4, stream);
-        backend_->synchronize(stream);
+        backend_->recordEvent(st.done, stream);
+        st.inFlight = true;
     } catch (...) {
         // the launched work may still read the inputs: drain before unwinding
         try {
             backend_->synchronize(stream);
         } catch (...) {
         }
-        throw;
+        throw;  // `pending` releases the slot
     }
+    pending.output_ = Tensor::fromDeviceBuffer(tensor::Shape{T, H}, DType::FP32, dev, std::move(out));
+    return pending;
+}
+
+BatchLayerExecutionResult HipMoEBlock::materialize(PendingBatchResult& pending) {
+    auto& st = *static_cast<Staging*>(pending.slot_);
+    backend_->waitEvent(st.done);
+    st.inFlight = false;
+    const std::size_t T = pending.tokens_, H = pending.hidden_, k = pending.topK_;
+    const std::size_t E = pending.experts_, P = T * k;
+    const LayerId layerId = pending.layerId_;
+    const auto dev = tensor::Device::hip(backend_->deviceOrdinal());
 
     const auto status = *st.hostAt<int32_t>(st.status);
     if (status & HM_STATUS_NONFINITE_SCORE) {
@@ -363,6 +480,7 @@ BatchLayerExecutionResult HipMoEBlock::run(LayerId layerId, TensorView hidden,
     const auto* offsets = st.hostAt<const int32_t>(st.offsets);
     const auto* ptok = st.hostAt<const int32_t>(st.ptok);
     const auto* pw = st.hostAt<const float>(st.pw);
+    const auto& expertOut = pending.expertOut_;
     auto& meta = result.execution;
     meta.tensorBackend = "HIP tensor backend";
     for (std::size_t e = 0; e < E; ++e) {
@@ -391,17 +509,17 @@ BatchLayerExecutionResult HipMoEBlock::run(LayerId layerId, TensorView hidden,
     if (!routing.valid()) throw std::runtime_error("router returned an invalid batch decision");
     meta.uniqueExperts = result.expertBatches.size();
     meta.expertCacheHits = meta.uniqueExperts;
-    meta.expertPayloadBytes = meta.uniqueExperts * layer.expertBytes();
+    meta.expertPayloadBytes = meta.uniqueExperts * pending.expertBytes_;
     auto span = [&](int a, int b) {
         float ms = 0.0F;
-        throwOnStatus(hm_event_elapsed_ms(&ms, events_[a], events_[b]), "block stage timing");
+        throwOnStatus(hm_event_elapsed_ms(&ms, st.events[a], st.events[b]), "block stage timing");
         return std::chrono::nanoseconds((long long)std::llround(ms * 1e6));
     };
     meta.routingTime = span(0, 1);
     meta.schedulingTime = span(1, 3);
     meta.expertExecutionTime = span(3, 5);
     meta.expertCombinationTime = span(5, 6);
-    result.output = Tensor::fromDeviceBuffer(tensor::Shape{T, H}, DType::FP32, dev, std::move(out));
+    result.output = std::move(pending.output_);
     return result;
 }
 

@@ -9,7 +9,8 @@
 // src/runtime/InferenceContext.hpp:13-25.  One call is one launch sequence
 // on the backend's compute stream (hm_moe_block_forward: route -> permute ->
 // grouped SwiGLU experts -> combine); the routing metadata comes back through
-// pinned memory once the stream reaches it.  All experts of a layer stay
+// pinned memory once the stream reaches it (launchBatch returns before that,
+// executeBatch waits for it).  All experts of a layer stay
 // resident in HBM (DeviceExpertLayer), so the reference's scheduler, leases
 // and residency tiers have no counterpart here.
 #pragma once
@@ -168,6 +169,40 @@ struct BlockOptions {
     bool keepExpertOutputs{true};
 };
 
+class HipMoEBlock;
+
+// The result of HipMoEBlock::launchBatch while its work is queued: the
+// combined output is a device tensor that work on the backend's compute
+// stream may use at once; get() waits for the call's routing metadata
+// (copied to pinned host memory behind the kernels) and builds the
+// reference-shaped result.  The block must outlive its pending results.
+// Movable, not copyable; dropping one without get() is allowed.
+class PendingBatchResult {
+public:
+    PendingBatchResult(PendingBatchResult&& other) noexcept;
+    PendingBatchResult& operator=(PendingBatchResult&&) = delete;
+    PendingBatchResult(const PendingBatchResult&) = delete;
+    ~PendingBatchResult();
+
+    // [T x H] FP32 on the device (ordered after the call on the compute stream).
+    [[nodiscard]] const tensor::Tensor& output() const noexcept { return output_; }
+    // Waits for the call and returns the result executeBatch returns (the
+    // output tensor moves into it); the routing checks and exceptions are
+    // executeBatch's.  Once only.
+    [[nodiscard]] BatchLayerExecutionResult get();
+
+private:
+    friend class HipMoEBlock;
+    PendingBatchResult() = default;
+    HipMoEBlock* block_{};
+    void* slot_{};  // the block's staging slot of this call
+    LayerId layerId_{};
+    std::size_t tokens_{}, hidden_{}, topK_{}, experts_{};
+    std::uint64_t expertBytes_{};
+    tensor::Tensor output_;
+    std::shared_ptr<backend::DeviceBuffer> expertOut_;
+};
+
 class HipMoEBlock {
 public:
     HipMoEBlock(std::shared_ptr<backend::HipBackend> backend, router::RouterConfig config,
@@ -180,7 +215,7 @@ public:
 
     // MoERuntime::executeBatch: hiddenStates [T x H] and routerWeights
     // [H x E], FP32 tensors on this backend's device.  Serialised per block
-    // (the reference's executionMutex_).
+    // (the reference's executionMutex_).  Equal to launchBatch(...).get().
     [[nodiscard]] BatchLayerExecutionResult executeBatch(LayerId layerId,
                                                          tensor::TensorView hiddenStates,
                                                          tensor::TensorView routerWeights);
@@ -191,12 +226,27 @@ public:
                                                          tensor::TensorView routerWeights,
                                                          tensor::TensorView residual);
 
+    // The same call without waiting for it: the kernels and the routing
+    // metadata's copies to pinned memory are queued on the compute stream
+    // and nothing here synchronises with the device.  The reference's block
+    // entry blocks on its routing read-back (CudaTensorBackend.cpp:636-640);
+    // a caller that needs the routing only later (or never) keeps the
+    // stream full instead.  Output buffers of calls whose results were
+    // released are reused by later calls of the same shape.
+    [[nodiscard]] PendingBatchResult launchBatch(LayerId layerId, tensor::TensorView hiddenStates,
+                                                 tensor::TensorView routerWeights,
+                                                 tensor::TensorView residual = {});
+
     [[nodiscard]] const router::RouterConfig& config() const noexcept { return config_; }
 
 private:
+    friend class PendingBatchResult;
     struct Staging;
-    BatchLayerExecutionResult run(LayerId layerId, tensor::TensorView hidden,
-                                  tensor::TensorView routerWeights, tensor::TensorView residual);
+    Staging* acquireSlot(std::size_t pairs, std::size_t experts);
+    void releaseSlot(Staging* slot) noexcept;
+    std::shared_ptr<backend::DeviceBuffer> outputBuffer(
+        std::vector<std::shared_ptr<backend::DeviceBuffer>>& pool, std::size_t bytes);
+    BatchLayerExecutionResult materialize(PendingBatchResult& pending);
 
     std::shared_ptr<backend::HipBackend> backend_;
     router::RouterConfig config_;
@@ -204,8 +254,11 @@ private:
     std::map<LayerId, std::shared_ptr<const DeviceExpertLayer>> layers_;
     std::mutex executionMutex_;
     std::unique_ptr<backend::DeviceBuffer> workspace_;
-    std::unique_ptr<Staging> staging_;
-    std::array<backend::EventHandle, 7> events_{};
+    // staging slots (device routing arrays, pinned copies, events), one per
+    // call in flight, and the released output buffers kept for reuse
+    std::mutex poolMutex_;
+    std::vector<std::unique_ptr<Staging>> slots_;
+    std::vector<std::shared_ptr<backend::DeviceBuffer>> outPool_, expertOutPool_;
 };
 
 }  // namespace hm

@@ -474,6 +474,58 @@ void blockTests(const std::shared_ptr<backend::HipBackend>& hip) {
             ok &= bits(s) == bits(out2[i]);
         }
         expect(ok, "residual variant adds the residual last");
+
+        // launchBatch: two calls queued with no synchronisation inside,
+        // their results taken in reverse order, each equal to the
+        // executeBatch result of the same inputs
+        const auto syncs0 = hip->stats().synchronizationCount;
+        auto p1 = block.launchBatch(7, dh.view(), dw.view());
+        auto p2 = block.launchBatch(7, dh.view(), dw.view(), dr.view());
+        expect(hip->stats().synchronizationCount == syncs0,
+               "launchBatch queues the call without a stream synchronisation");
+        const void* out1 = p1.output().data();
+        auto sameRouting = [&](const BatchLayerExecutionResult& a, const BatchLayerExecutionResult& b) {
+            bool same = a.routing.tokens.size() == b.routing.tokens.size() &&
+                        a.expertBatches.size() == b.expertBatches.size();
+            for (std::size_t t = 0; t < a.routing.tokens.size() && same; ++t) {
+                same &= a.routing.tokens[t].selectedExpertIds == b.routing.tokens[t].selectedExpertIds;
+                for (std::size_t r = 0; r < k && same; ++r)
+                    same &= bits(a.routing.tokens[t].routingScores[r]) ==
+                            bits(b.routing.tokens[t].routingScores[r]);
+            }
+            for (std::size_t g = 0; g < a.expertBatches.size() && same; ++g) {
+                same &= a.expertBatches[g].expertId == b.expertBatches[g].expertId &&
+                        a.expertBatches[g].tokenIndices == b.expertBatches[g].tokenIndices;
+                for (std::size_t i = 0; i < a.expertBatches[g].size() && same; ++i)
+                    same &= bits(a.expertBatches[g].routingWeights[i]) ==
+                            bits(b.expertBatches[g].routingWeights[i]);
+            }
+            return same;
+        };
+        auto r2 = p2.get();
+        auto r1 = p1.get();
+        expect(sameRouting(r1, res) && sameRouting(r2, res2),
+               "launched results' routing equals executeBatch's");
+        std::vector<float> o1(T * H), o2(T * H);
+        hip->copyFromDevice(o1.data(), r1.output.data(), o1.size() * 4);
+        hip->copyFromDevice(o2.data(), r2.output.data(), o2.size() * 4);
+        expect(bitexact(o1.data(), out.data(), o1.size()) && bitexact(o2.data(), out2.data(), o2.size()),
+               "launched results' outputs equal executeBatch's");
+        expect(r1.output.data() == out1, "the pending output is the result's output");
+        expectThrows<std::logic_error>([&] { (void)p1.get(); }, "a pending result is taken once");
+
+        // a released output buffer is reused by the next call of the same
+        // shape; a pending result dropped without get() leaves the block usable
+        r1 = BatchLayerExecutionResult{};
+        {
+            auto p3 = block.launchBatch(7, dh.view(), dw.view());
+            expect(p3.output().data() == out1, "released output buffer reused");
+        }
+        auto r4 = block.executeBatch(7, dh.view(), dw.view());
+        std::vector<float> o4(T * H);
+        hip->copyFromDevice(o4.data(), r4.output.data(), o4.size() * 4);
+        expect(sameRouting(r4, res) && bitexact(o4.data(), out.data(), o4.size()),
+               "a call after a dropped pending result is unchanged");
     }
 
     // argument errors
