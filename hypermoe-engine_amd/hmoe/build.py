@@ -41,7 +41,7 @@ HIP_FLAGS = [
     f"-I{INCLUDE}", f"-I{CSRC}",
 ]
 KERNEL_SOURCES = ["hm_runtime.hip", "hm_router.hip", "hm_gemm.hip", "hm_gemm_mfma.hip",
-                  "hm_gemm_f32_mfma.hip", "hm_gemv.hip", "hm_block.hip"]
+                  "hm_gemm_f32_mfma.hip", "hm_gemv.hip", "hm_block.hip", "hm_noalloc.hip"]
 # Per-source flags.  The FP64 router MFMAs keep their accumulators in VGPRs
 # (otherwise the compiler copies them to AGPRs and back on every K chunk).
 SOURCE_FLAGS = {"hm_router.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
