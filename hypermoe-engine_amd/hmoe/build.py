@@ -10,9 +10,12 @@ tree is mounted) oracle/_ref/libhm_ref.so.
 
 Every HIP translation unit is built with -ffp-contract=off (FMAs only where a
 kernel asks for one explicitly) and with packed FP32 instructions disabled.
-Sources with loads the compiler does not track (UNTRACKED_LOAD_SOURCES) are
-assembled from a saved listing that hmoe.isa_check verifies first: no
-register of such a load may be touched before a wait completes it.
+Sources with hand-written memory statements (CHECKED_SOURCES: loads the
+compiler does not track, LDS-DMA loads that set M0) are assembled from a
+saved listing that hmoe.isa_check verifies first: no register of an
+untracked load is touched before a wait completes it, the compiler's own
+code leaves M0 alone, and the hand-written blocks hold only the memory
+forms the check understands.
 """
 from __future__ import annotations
 
@@ -46,8 +49,9 @@ KERNEL_SOURCES = ["hm_runtime.hip", "hm_router.hip", "hm_gemm.hip", "hm_gemm_mfm
 # (otherwise the compiler copies them to AGPRs and back on every K chunk).
 SOURCE_FLAGS = {"hm_router.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
                 "hm_gemm_f32_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
-# Sources whose kernels issue register loads the compiler does not track.
-UNTRACKED_LOAD_SOURCES = {"hm_gemm_mfma.hip"}
+# Sources with hand-written memory statements: register loads the compiler
+# does not track (hm_gemm_mfma.hip) and LDS-DMA loads that set M0 (all three).
+CHECKED_SOURCES = {"hm_gemm_mfma.hip", "hm_router.hip", "hm_gemm_f32_mfma.hip"}
 HOST_SOURCES = ["hip_backend.cpp", "hip_tensor_backend.cpp", "moe_block.cpp", "artefact.cpp"]
 
 KERNELS_SO = LIB / "libhm_kernels.so"
@@ -65,7 +69,8 @@ def _run(cmd: list[str], cwd: Path | None = None) -> None:
 
 def _quiet_filter(text: str) -> str:
     # the feature warning of the host pass, and the note on the M0 clobber of
-    # the LDS-DMA statements (the kernels keep nothing else in M0)
+    # the LDS-DMA statements (isa_check verifies that the compiled code keeps
+    # nothing else in M0)
     return "\n".join(l for l in text.splitlines()
                      if "packed-fp32-ops" not in l and "Reserved registers on the clobber list" not in l
                      and "clobber list contains reserved registers" not in l
@@ -77,7 +82,7 @@ def _device_listing(obj: Path) -> Path:
 
 
 def _compile_hip(src: Path, obj: Path) -> str:
-    checked = src.name in UNTRACKED_LOAD_SOURCES
+    checked = src.name in CHECKED_SOURCES
     # -save-temps=obj: the object is assembled from the listing that is checked
     extra = ["-save-temps=obj"] if checked else []
     cmd = [HIPCC, *HIP_FLAGS, *SOURCE_FLAGS.get(src.name, []), *extra, "-c", str(src), "-o", str(obj)]
@@ -95,7 +100,8 @@ def _compile_hip(src: Path, obj: Path) -> str:
         problems = isa_check.check_file(listing)
         if problems:
             obj.unlink(missing_ok=True)
-            raise RuntimeError(f"{src.name}: untracked load registers used before their wait:\n"
+            raise RuntimeError(f"{src.name}: the compiled code breaks the rules of its "
+                               "hand-written memory statements (hmoe.isa_check):\n"
                                + "\n".join(problems[:20]))
     return _quiet_filter(res.stdout)
 

@@ -19,6 +19,22 @@ operands) is a violation, and so is a path that reaches the end of the
 kernel.  Loads the compiler itself tracks pass trivially (the compiler waits
 before every use, and its counts never exceed the true count of younger
 instructions), so the check covers every kernel of the file.
+
+Two further rules guard the hand-written blocks (between the compiler's
+;;#ASMSTART and ;;#ASMEND markers):
+
+- M0.  The LDS-DMA statements set M0 themselves and name it as clobbered,
+  but the compiler treats M0 as a reserved register and ignores that
+  clobber, so a value of its own kept in M0 across such a statement would
+  be lost.  No instruction outside the blocks may therefore name M0 or use
+  it implicitly (relative-index moves, messages, GWS and ordered-count LDS
+  operations, the LDS forms of the memory loads).
+- Vector memory inside the blocks.  Only the forms this check understands
+  may appear there: the 16-byte VGPR buffer load (the untracked load above)
+  and the LDS-DMA loads (buffer/global ... lds, which write no registers).
+  Any other vector memory instruction (another width, an AGPR destination,
+  a flat or global register load, a store) is refused, since its registers
+  would escape the first rule.
 """
 from __future__ import annotations
 
@@ -40,12 +56,23 @@ def _vregs(op: str) -> set[int]:
     return {int(m.group(1))} if m else set()
 
 
-def _functions(text: str) -> list[tuple[str, list[list[str]], dict[str, int]]]:
+def _functions(text: str, asm_flags: list | None = None
+               ) -> list[tuple[str, list[list[str]], dict[str, int]]]:
     """Splits an assembly listing into functions: (name, instructions as
-    operand lists, label -> instruction index)."""
+    operand lists, label -> instruction index).  With asm_flags, appends per
+    function a list saying which instructions lie in a hand-written block."""
     out = []
     name, ins, labels = None, [], {}
+    flags: list[bool] = []
+    in_asm = False
     for raw in text.split("\n"):
+        stripped = raw.strip()
+        if stripped.startswith(";;#ASMSTART"):
+            in_asm = True
+            continue
+        if stripped.startswith(";;#ASMEND"):
+            in_asm = False
+            continue
         line = raw.split(";")[0].strip()
         if not line:
             continue
@@ -53,7 +80,9 @@ def _functions(text: str) -> list[tuple[str, list[list[str]], dict[str, int]]]:
         if m and line.endswith(":") and not line.startswith("."):
             if name is not None:
                 out.append((name, ins, labels))
-            name, ins, labels = m.group(1), [], {}
+                if asm_flags is not None:
+                    asm_flags.append(flags)
+            name, ins, labels, flags = m.group(1), [], {}, []
             continue
         if line.endswith(":"):
             if name is not None:
@@ -62,12 +91,50 @@ def _functions(text: str) -> list[tuple[str, list[list[str]], dict[str, int]]]:
         if line.startswith(".") or name is None:
             continue
         ins.append(line.replace(",", " ").split())
+        flags.append(in_asm)
         if ins[-1][0] == "s_endpgm":
             out.append((name, ins, labels))
-            name, ins, labels = None, [], {}
+            if asm_flags is not None:
+                asm_flags.append(flags)
+            name, ins, labels, flags = None, [], {}, []
     if name is not None and ins:
         out.append((name, ins, labels))
+        if asm_flags is not None:
+            asm_flags.append(flags)
     return out
+
+
+# instructions that read or write M0 without naming it
+_IMPLICIT_M0 = re.compile(r"^(s_movrel|v_movrel|s_sendmsg|ds_gws_|ds_append|ds_consume|"
+                          r"ds_ordered_count|s_set_gpr_idx|v_interp_|s_ttracedata)")
+
+
+def _uses_m0(u: list[str]) -> bool:
+    if _IMPLICIT_M0.match(u[0]):
+        return True
+    if _VMEM.match(u[0]) and ("lds" in u[1:] or "_lds_" in u[0]):
+        return True  # LDS-DMA loads address the LDS through M0
+    return any(o == "m0" for o in u[1:])
+
+
+def _asm_vmem_ok(u: list[str]) -> bool:
+    """The vector memory forms allowed inside the hand-written blocks."""
+    op, ops = u[0], u[1:]
+    if op in ("global_load_lds_dwordx4", "global_load_lds_dword"):
+        return True
+    if op == "buffer_load_dwordx4" and "lds" in ops:
+        return True
+    return op == "buffer_load_dwordx4" and "offen" in ops and bool(ops) and ops[0].startswith("v")
+
+
+def _check_blocks(ins: list[list[str]], flags: list[bool]) -> list[tuple[int, str]]:
+    bad = []
+    for i, (u, in_asm) in enumerate(zip(ins, flags)):
+        if not in_asm and _uses_m0(u):
+            bad.append((i, "M0 used outside a hand-written block"))
+        if in_asm and _VMEM.match(u[0]) and not _asm_vmem_ok(u):
+            bad.append((i, "unrecognised vector memory instruction in a hand-written block"))
+    return bad
 
 
 def _decode(ins: list[list[str]], labels: dict[str, int]):
@@ -133,9 +200,12 @@ def _check_function(ins: list[list[str]], labels: dict[str, int]) -> list[tuple[
 def check_text(text: str) -> list[str]:
     """Violations in an assembly listing, one line each (empty: clean)."""
     problems = []
-    for name, ins, labels in _functions(text):
+    flags: list[list[bool]] = []
+    for (name, ins, labels), fl in zip(_functions(text, flags), flags):
         for p, i, what in _check_function(ins, labels):
             problems.append(f"{name}: load #{p} ({' '.join(ins[p])}) -> instruction #{i}: {what}")
+        for i, what in _check_blocks(ins, fl):
+            problems.append(f"{name}: instruction #{i} ({' '.join(ins[i])}): {what}")
     return problems
 
 
