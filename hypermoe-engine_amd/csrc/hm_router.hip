@@ -1039,19 +1039,27 @@ __global__ __launch_bounds__(NW * HM_WAVE) void router_select_partial_kernel(
 // router_mfma_kernel sums the exact products p_k = h_k w_k (double) with
 // v_mfma_f64_16x16x4_f64 in an order of its own: K is cut into `splits`
 // ranges (one per workgroup layer of the grid) and each range into chunks
-// of 16, of which MFMA step j takes k = 4g + j for the four k-slots g.  Any
-// summation tree of n terms whose additions round to nearest errs by at
-// most gamma_{n-1} SA, SA = sum |p_k| <= ||h|| ||w_e|| (Cauchy-Schwarz), and
-// so does the reference's sequential chain; the kernel therefore also
-// returns the squared norms of h's rows and W's columns per range.
-// router_select_split_kernel adds the ranges (ascending), bounds
-//   |S' - s_n| <= 3 gamma_n ||h|| ||w_e||
-// (one gamma for the reference, two for the matrix-core sums to cover an
-// internal rounding mode of up to 2u), inflated for the norms' own
-// rounding, and keeps float(S') when both ends of S' +- bound round to the
-// same float; otherwise (about 0.5% of the logits for N(0,1) rows and
-// N(0, 0.02) weights at H = 2048, and every non-finite case) the lane runs
-// the reference's chain.
+// of 16, of which MFMA step j takes k = 4g + j for the four k-slots g; the
+// kernel also returns the squared norms of h's rows and W's columns per
+// range.  router_select_split_kernel adds the S ranges' partials P'_r in
+// order (S'_r after range r, S' = S'_{S-1}) and bounds |S' - s_n| from
+// these, with m = n / S terms per range, A_r = sum_{k in r} |p_k| <=
+// ||h_r|| ||w_e,r|| (Cauchy-Schwarz per range) and u = 2^-53:
+//   - each range partial: any summation tree of m terms errs by at most
+//     gamma_m A_r, doubled to cover an internal rounding mode of the
+//     matrix cores of up to 2u (g2 = 2mu / (1 - 2mu));
+//   - the additions of the partials: u |S'_r| each; with the above
+//     D = g2 sum_r A_r + u sum_r |S'_r| bounds |S' - S_n| and every prefix
+//     |S'_{r-1} - S_{rm}| (S_k: the exact partial sums);
+//   - the reference's chain: its step k errs by at most u' |s_k| (u' =
+//     u / (1 - u)), |s_k| <= |S_k| + B and, for k in range r, |S_k| <=
+//     |S'_{r-1}| + D + A_r, so B <= u' m (sum_r |S'_{r-1}| + S D + sum_r
+//     A_r) / (1 - n u');
+// the bound is B + D, inflated by 2^-20 for the norms' and the bound's own
+// rounding (relative errors below 2^-40 here).  float(S') is kept when both
+// ends of S' +- bound round to the same float; otherwise (about 0.05 % of
+// the logits for N(0,1) rows and N(0, 0.02) weights at H = 2048 in four
+// ranges, and every non-finite case) the logit takes the fallbacks below.
 //
 // Workgroup: 4 waves x 16 tokens, 64 experts as 4 interleaved MFMA chains
 // (chain q holds experts e0 + 4n + q, n = 0..15), so that each W load is a
@@ -1186,11 +1194,14 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(
 // acc + p_k == fma(h_k, w_k, acc), with no conversions on its path.
 constexpr int kFK = 128;                        // k per staged piece
 constexpr int kFN = 2;                          // chains per round
+constexpr int kFS = 3;                          // pieces in the staging ring (LDS: four
+                                                // workgroups per CU)
 constexpr int kFBuf = 4 * kFK * 4;              // one buffer: 2 columns, h, pad (2 KB)
 constexpr int kFProd = kFN * kFK * 8;           // products of one piece (2 KB)
-constexpr int kFWave = 2 * kFBuf + kFProd;      // fallback LDS per wave
+constexpr int kFWave = kFS * kFBuf + kFProd;    // fallback LDS per wave
 constexpr int kFDma = 2;                        // 16-byte DMA instructions per piece
 static_assert(kFK == 2 * HM_WAVE && kFN == 2, "half a wave per staged row piece");
+static_assert(kFS == 3, "the staging waits below count three pieces");
 
 __device__ __forceinline__ void fallback_issue(char* buf, const float* __restrict__ hrow,
                                                const float* __restrict__ wt, int64_t hidden,
@@ -1240,24 +1251,19 @@ __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
     const int64_t seq_stride = ((experts * 4 + 15) / 16) * 16;
     float* seq_lds = reinterpret_cast<float*>(dyn_lds);  // indexed by wave * experts
     char* fb = dyn_lds + (kBlock / HM_WAVE) * seq_stride + (int64_t)wave * kFWave;
-    double* fprod = reinterpret_cast<double*>(fb + 2 * kFBuf);
+    double* fprod = reinterpret_cast<double*>(fb + kFS * kFBuf);
     const double u = 0x1p-53;
-    const double n = (double)hidden;
-    const double gam = n * u / (1.0 - n * u);
-    // 3 gamma_n, times (1 + 4 gamma_n) for the norms' own rounding
-    const double cb = 3.0 * gam * (1.0 + 4.0 * gam) * (1.0 + 0x1p-30);
+    const double n = (double)hidden, m = (double)(hidden / splits);
+    // the range form's bound (derived above router_mfma_kernel)
+    const double g2 = 2.0 * m * u / (1.0 - 2.0 * m * u);
+    const double cu = u / (1.0 - u) / (1.0 - n * u / (1.0 - u)) * m;
     // (all loads of the range sums go out before the additions:
     // unconditional loads from clamped ranges, so that no branch splits
     // them from their uses)
-    double hv[kMaxSplits];
+    double hr[kMaxSplits];
 #pragma unroll
     for (int sp = 0; sp < kMaxSplits; ++sp)
-        hv[sp] = hn2[(int64_t)min(sp, splits - 1) * tokens + t];
-    double hh = 0.0;
-#pragma unroll
-    for (int sp = 0; sp < kMaxSplits; ++sp)
-        if (sp < splits) hh += hv[sp];
-    const double hnorm = sqrt(hh);
+        hr[sp] = sqrt(hn2[(int64_t)min(sp, splits - 1) * tokens + t]);
     float v[EPL];
     bool valid[EPL];
     unsigned long long need[EPL];
@@ -1276,15 +1282,24 @@ __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
                 pa[sp] = part[(sc * tokens + t) * experts + e];
                 pw[sp] = wn2[sc * experts + e];
             }
-            double a = 0.0, ww = 0.0;
+            // S' (the ranges' partials added in order), the sums of |S'|
+            // before (pre) and after (post) each addition, and of the
+            // ranges' norm products
+            double a = 0.0, pre = 0.0, post = 0.0, nsum = 0.0;
 #pragma unroll
             for (int sp = 0; sp < kMaxSplits; ++sp) {
                 if (sp < splits) {
+                    pre += fabs(a);
                     a += pa[sp];
-                    ww += pw[sp];
+                    post += fabs(a);
+                    nsum += hr[sp] * sqrt(pw[sp]);
                 }
             }
-            const double bc = (cb * hnorm * sqrt(ww) + u * fabs(a)) * (1.0 + 0x1p-50);
+            // nsum bounds sum_r sum_{k in r} |p_k| (Cauchy-Schwarz per range;
+            // the computed norms err by at most gamma_m relative, covered by
+            // the final inflation)
+            const double d = g2 * nsum + u * post;
+            const double bc = (cu * (pre + (double)splits * d + nsum) + d) * (1.0 + 0x1p-20);
             const double lo = a - bc, hi = a + bc;
             nd = !(isfinite(lo) && isfinite(hi) &&
                    __float_as_uint((float)lo) == __float_as_uint((float)hi));
@@ -1346,6 +1361,7 @@ __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
             }
             const double cj = block_c_term(rs, qs, hidden);
             double a = 0.0, sa = 0.0, sc = 0.0;
+#pragma unroll
             for (int j = 0; j < kNB; ++j) {
                 a += __shfl(acc, 32 * half + j, HM_WAVE);
                 sa += fabs(a);
@@ -1385,16 +1401,22 @@ __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
         const int nf = min(kFN, total - done);
         double acc = 0.0;
         const int64_t pieces = (hidden + kFK - 1) / kFK;
-        fallback_issue(fb, hrow, wt, hidden, 0, fe, lane);
+#pragma unroll
+        for (int c = 0; c < kFS - 1; ++c)
+            if (c < pieces) fallback_issue(fb + c * kFBuf, hrow, wt, hidden, c * kFK, fe, lane);
         for (int64_t c = 0; c < pieces; ++c) {
-            char* cur = fb + (c & 1) * kFBuf;
-            if (c + 1 < pieces) {
-                fallback_issue(fb + ((c + 1) & 1) * kFBuf, hrow, wt, hidden, (c + 1) * kFK, fe,
-                               lane);
-                wait_vmcnt<kFDma>();
-            } else {
-                wait_vmcnt<0>();
-            }
+            char* cur = fb + (c % kFS) * kFBuf;
+            // the piece kFS - 1 ahead goes into the buffer piece c - 1 used
+            // (fallback_issue waits for its reads)
+            if (c + kFS - 1 < pieces)
+                fallback_issue(fb + ((c + kFS - 1) % kFS) * kFBuf, hrow, wt, hidden,
+                               (c + kFS - 1) * kFK, fe, lane);
+            // piece c has landed once at most the pieces issued after it are
+            // in flight (each piece is kFDma loads; nothing else is loaded here)
+            const int64_t after = min((int64_t)kFS - 1, pieces - 1 - c);
+            if (after >= 2) wait_vmcnt<2 * kFDma>();
+            else if (after == 1) wait_vmcnt<kFDma>();
+            else wait_vmcnt<0>();
             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
             const int kc = (int)min((int64_t)kFK, hidden - c * kFK);  // a multiple of 16
             {
@@ -1409,22 +1431,24 @@ __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
             // (one wave's LDS accesses complete in order: the chain lanes'
             // reads below see every lane's products)
             if (lane < nf) {
+                // 16 products per step, the next step's read out while this
+                // one's are added (kc is a multiple of 16)
                 const double2* pp = reinterpret_cast<const double2*>(fprod + lane * kFK);
-                double2 pa[4];
+                double2 pa[8];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) pa[q] = pp[q];
-                for (int kk = 0; kk < kc; kk += 8) {
-                    const int nx = kk + 8 < kc ? (kk + 8) / 2 : kk / 2;
-                    double2 pb[4];
+                for (int q = 0; q < 8; ++q) pa[q] = pp[q];
+                for (int kk = 0; kk < kc; kk += 16) {
+                    const int nx = kk + 16 < kc ? (kk + 16) / 2 : kk / 2;
+                    double2 pb[8];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) pb[q] = pp[nx + q];
+                    for (int q = 0; q < 8; ++q) pb[q] = pp[nx + q];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
+                    for (int q = 0; q < 8; ++q) {
                         acc = acc + pa[q].x;
                         acc = acc + pa[q].y;
                     }
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) pa[q] = pb[q];
+                    for (int q = 0; q < 8; ++q) pa[q] = pb[q];
                 }
             }
             // the products are rewritten for the next piece only after
