@@ -14,6 +14,13 @@ One step = one MoE-block call (route -> permute -> INT8 SwiGLU experts:
 integer-limb MFMA GEMMs at prefill, W8A32 GEMVs at decode -> combine) over a
 batch already resident in HBM.  Prints ONE JSON line.
 
+Timing: W warm-up steps; K steps timed (reported as
+settle.ms_per_step_before); untimed steps until --settle-ms of GPU time have
+passed; then the K timed steps whose time is the result.  A GPU that has
+been idle runs its first few dozen back-to-back C4 steps about 10 % slower
+than it does from then on for as long as the load lasts (its clock drops and
+recovers under the continuous load); the result is the rate it keeps.
+
 Roofline: the dominant kernel's algorithmic work per launch divided by its
 average launch duration, measured with hipEvents recorded on the launch
 stream at the block's stage boundaries over K further steps (the timed
@@ -51,6 +58,12 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--settle-ms", type=float, default=60.0,
+                    help="after the warm-up and a first timed pass of K steps, untimed steps "
+                         "until this much GPU time has passed, then the K timed steps whose "
+                         "time is the result (a GPU that has been idle runs its first few "
+                         "dozen back-to-back prefill steps while its clock drops and "
+                         "recovers; 0: no settling, the first pass is the result)")
     ap.add_argument("--workload", default="C4")
     ap.add_argument("--limbs-x", type=int, default=2, help="X (token row) digit planes")
     ap.add_argument("--limbs-z", type=int, default=3, help="Z (SiLU(G)*U row) digit planes")
@@ -107,9 +120,8 @@ def pmc_traffic(workload: str, kernel_re: str, primary_re: str, limbs: tuple, qu
             cmd = [exe, "--pmc", counter, "--kernel-include-regex", f"{kernel_re}|copyBuffer",
                    "--output-format", "csv", "-d", d, "-o", "pmc", "--", sys.executable,
                    str(REPO / "bench.py"), "--workload", workload, "--steps", "2", "--warmup",
-                   "1", "--cpu-sample", "0", "--quiet", "--no-traffic", "--no-decode",
-                   "--limbs-x", str(limbs[0]),
-                   "--limbs-z", str(limbs[1]),
+                   "1", "--settle-ms", "0", "--cpu-sample", "0", "--quiet", "--no-traffic",
+                   "--no-decode", "--limbs-x", str(limbs[0]), "--limbs-z", str(limbs[1]),
                    "--copy-mb", str(copy_mib)]
             env = dict(os.environ, TMPDIR="/tmp")
             log(f"[bench] traffic: rocprofv3 --pmc {counter}", quiet)
@@ -165,7 +177,7 @@ def pmc_mfma(workload: str, kernels: dict, limbs: tuple, quiet: bool):
         cmd = [exe, "--pmc", *counters, "--kernel-include-regex", "|".join(kernels.values()),
                "--output-format", "csv", "-d", d, "-o", "pmc", "--", sys.executable,
                str(REPO / "bench.py"), "--workload", workload, "--steps", "2", "--warmup", "1",
-               "--cpu-sample", "0", "--quiet", "--no-traffic", "--no-decode",
+               "--settle-ms", "0", "--cpu-sample", "0", "--quiet", "--no-traffic", "--no-decode",
                "--limbs-x", str(limbs[0]),
                "--limbs-z", str(limbs[1])]
         log("[bench] counters: rocprofv3 --pmc " + " ".join(counters), quiet)
@@ -329,19 +341,33 @@ def main():
             graph = None
         torch.cuda.synchronize()
 
-    # timed region: K steps, nothing else on the stream
-    torch.cuda.synchronize()
-    capi.call("hm_event_record", ev_start, stream)
-    for i in range(args.steps):
-        if graph is not None:
-            graph[i % pool].replay()
-        else:
-            block.launch(batches[i % pool], d_w)
-    capi.call("hm_event_record", ev_stop, stream)
-    torch.cuda.synchronize()
     ms = C.c_float()
-    capi.call("hm_event_elapsed_ms", C.byref(ms), ev_start, ev_stop)
-    total_ms = ms.value
+
+    def timed(n, first=0):
+        # n steps between two events, nothing else on the stream
+        torch.cuda.synchronize()
+        capi.call("hm_event_record", ev_start, stream)
+        for i in range(first, first + n):
+            if graph is not None:
+                graph[i % pool].replay()
+            else:
+                block.launch(batches[i % pool], d_w)
+        capi.call("hm_event_record", ev_stop, stream)
+        torch.cuda.synchronize()
+        capi.call("hm_event_elapsed_ms", C.byref(ms), ev_start, ev_stop)
+        return ms.value
+
+    # The first K steps after the warm-up, timed and reported; then the
+    # clock settles under the continuous load (untimed steps until
+    # --settle-ms of GPU time have passed) and the timed region proper: K
+    # steps whose time is the result.
+    first_ms = timed(args.steps)
+    settle_steps, settle_ms = 0, 0.0
+    while settle_ms < args.settle_ms:
+        n = max(1, min(200, int((args.settle_ms - settle_ms) / max(first_ms / args.steps, 1e-3)) + 1))
+        settle_ms += timed(n, settle_steps)
+        settle_steps += n
+    total_ms = timed(args.steps) if settle_steps else first_ms
     ms_per_step = total_ms / args.steps
     # a second pass with the stage events recorded inside every step: the
     # per-stage times and the dominant kernel's launch duration
@@ -472,6 +498,8 @@ def main():
     line = {
         "metric": METRIC, "value": round(tokens_per_s, 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
+        "settle": {"steps": settle_steps, "gpu_ms": round(settle_ms, 2),
+                   "ms_per_step_before": round(first_ms / args.steps, 5)},
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "int8" if cfg.int8 else "fp32", "data": "synthetic",
         "config": {"workload": cfg.name, "tokens": T, "hidden": H, "experts": E,
