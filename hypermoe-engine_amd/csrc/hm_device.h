@@ -212,6 +212,14 @@ __device__ __forceinline__ double hm_wave_sum_f64_dpp(double v) {
 // libm expf on every float input (exhaustive check, tests/test_expf_parity.py).
 #include "hm_expf.h"
 
+// A 16-byte load that the caches stream past (a value read once: the
+// nontemporal hint keeps it from displacing operands that are read again).
+__device__ __forceinline__ float4 hm_load_stream(const float4* p) {
+    typedef float hm_v4f __attribute__((ext_vector_type(4)));
+    const hm_v4f v = __builtin_nontemporal_load(reinterpret_cast<const hm_v4f*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 // SiLU exactly as src/tensor/activation/Activation.cpp:44 computes it:
 // value / (1 + expf(-value)) in float.
 __device__ __forceinline__ float hm_silu(float v) {

@@ -1169,8 +1169,16 @@ __global__ __launch_bounds__(kGuThreads) void ring_gemm_kernel(
                             const float g = __fmul_rn(hm_recombine(pg, L), fg);
                             const float u = __fmul_rn(hm_recombine(pu, L), fu);
                             if (live) {
-                                grow[32 * j] = g;
-                                grow[half + 32 * j] = u;
+                                if constexpr (DN) {
+                                    grow[32 * j] = g;
+                                    grow[half + 32 * j] = u;
+                                } else {
+                                    // g | u is read once, by the SwiGLU pass:
+                                    // streamed, so that it does not evict the
+                                    // operands the other tiles read again
+                                    __builtin_nontemporal_store(g, &grow[32 * j]);
+                                    __builtin_nontemporal_store(u, &grow[half + 32 * j]);
+                                }
                             }
                         }
                     }

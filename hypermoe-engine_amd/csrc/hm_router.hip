@@ -1653,7 +1653,8 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(
     if ((width & 3) == 0) {
         const int64_t w4 = width >> 2;
         // two column groups per thread per pass: sixteen rows' float4 loads
-        // in flight before the adds (ascending order per column)
+        // in flight before the adds (ascending order per column); y is read
+        // once, with the streaming hint
         for (int64_t i0 = tid; i0 < w4; i0 += 2 * kBlock) {
           float4 res[2];
 #pragma unroll
@@ -1666,7 +1667,8 @@ __global__ __launch_bounds__(kBlock) void combine_kernel(
 #pragma unroll
                 for (int q = 0; q < 8; ++q)
                     v[h][q] = r0 + q < top_k && i < w4
-                                  ? reinterpret_cast<const float4*>(y + srow[r0 + q] * width)[i]
+                                  ? hm_load_stream(
+                                        reinterpret_cast<const float4*>(y + srow[r0 + q] * width) + i)
                                   : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             }
 #pragma unroll
