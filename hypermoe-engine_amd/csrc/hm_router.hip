@@ -6,6 +6,8 @@
 
 #include <limits.h>
 
+#include <type_traits>
+
 namespace {
 
 constexpr int kBlock = 256;
@@ -1117,41 +1119,54 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(
 #pragma unroll
     for (int c = 0; c < kMS - 1; ++c)
         if (c < nk) issue(c, c);
-    for (int c = 0; c < nk; ++c) {
-        const int slot = c % kMS;
-        if (c + kMS - 2 < nk) wait_vmcnt<(kMS - 2) * 2>();
-        else wait_vmcnt<0>();
-        lds_barrier();  // chunk c landed for every wave; chunk c-1 fully read
-        if (c + kMS - 1 < nk) issue((c + kMS - 1) % kMS, c + kMS - 1);
-        const char* st = ring[slot];
-        if (tb == 0) {
-            // the first token block also writes the chunk of W transposed:
-            // lane l -> expert e0 + 16*wave + l/4, k 4*(l%4) .. +3
-            const int ex = 16 * wave + (lane >> 2), kq = 4 * (lane & 3);
-            const float* sw = reinterpret_cast<const float*>(st) + kq * kME + ex;
-            *reinterpret_cast<float4*>(wt + (int64_t)(e0 + ex) * hidden + kb + 16 * c + kq) =
-                make_float4(sw[0], sw[kME], sw[2 * kME], sw[3 * kME]);
+    // The K loop, in four copies: with or without h's squares (the waves of
+    // expert block 0 write them) and W's squares (wnorm); the choice is made
+    // once per wave, outside the loop (every copy takes the same barriers).
+    auto kloop = [&](auto hs, auto ws) __attribute__((always_inline)) {
+        constexpr bool HS = decltype(hs)::value, WS = decltype(ws)::value;
+        for (int c = 0; c < nk; ++c) {
+            const int slot = c % kMS;
+            if (c + kMS - 2 < nk) wait_vmcnt<(kMS - 2) * 2>();
+            else wait_vmcnt<0>();
+            lds_barrier();  // chunk c landed for every wave; chunk c-1 fully read
+            if (c + kMS - 1 < nk) issue((c + kMS - 1) % kMS, c + kMS - 1);
+            const char* st = ring[slot];
+            if (tb == 0) {
+                // the first token block also writes the chunk of W transposed:
+                // lane l -> expert e0 + 16*wave + l/4, k 4*(l%4) .. +3
+                const int ex = 16 * wave + (lane >> 2), kq = 4 * (lane & 3);
+                const float* sw = reinterpret_cast<const float*>(st) + kq * kME + ex;
+                *reinterpret_cast<float4*>(wt + (int64_t)(e0 + ex) * hidden + kb + 16 * c + kq) =
+                    make_float4(sw[0], sw[kME], sw[2 * kME], sw[3 * kME]);
+            }
+            const float4 a = *reinterpret_cast<const float4*>(st + kMW + (16 * wave + i) * 64 + 16 * g);
+            float4 wv[4];
+    #pragma unroll
+            for (int j = 0; j < 4; ++j)
+                wv[j] = *reinterpret_cast<const float4*>(st + (4 * g + j) * 256 + 16 * i);
+            const double ad[4] = {live ? (double)a.x : 0.0, live ? (double)a.y : 0.0,
+                                  live ? (double)a.z : 0.0, live ? (double)a.w : 0.0};
+    #pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if constexpr (HS) hsq = __builtin_fma(ad[j], ad[j], hsq);
+                const double bd[4] = {(double)wv[j].x, (double)wv[j].y, (double)wv[j].z,
+                                      (double)wv[j].w};
+    #pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(ad[j], bd[q], acc[q], 0, 0, 0);
+                if constexpr (WS) {
+    #pragma unroll
+                    for (int q = 0; q < 4; ++q) wsq[q] = __builtin_fma(bd[q], bd[q], wsq[q]);
+                }
+            }
         }
-        const float4 a = *reinterpret_cast<const float4*>(st + kMW + (16 * wave + i) * 64 + 16 * g);
-        float4 wv[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            wv[j] = *reinterpret_cast<const float4*>(st + (4 * g + j) * 256 + 16 * i);
-        const double ad[4] = {live ? (double)a.x : 0.0, live ? (double)a.y : 0.0,
-                              live ? (double)a.z : 0.0, live ? (double)a.w : 0.0};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            hsq = __builtin_fma(ad[j], ad[j], hsq);
-            const double bd[4] = {(double)wv[j].x, (double)wv[j].y, (double)wv[j].z,
-                                  (double)wv[j].w};
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                acc[q] = __builtin_amdgcn_mfma_f64_16x16x4f64(ad[j], bd[q], acc[q], 0, 0, 0);
-            // (every wave sums the squares, one writes them: a branch here
-            // splits the loop and costs more than the 16 FMAs)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) wsq[q] = __builtin_fma(bd[q], bd[q], wsq[q]);
-        }
+    };
+    if (eb == 0) {
+        if (wnorm) kloop(std::true_type{}, std::true_type{});
+        else kloop(std::true_type{}, std::false_type{});
+    } else {
+        if (wnorm) kloop(std::false_type{}, std::true_type{});
+        else kloop(std::false_type{}, std::false_type{});
     }
     // partial logits: register r of lane (g, i) holds D[g + 4r][i], i.e.
     // token t0 + g + 4r, experts e0 + 4i .. +3
