@@ -211,7 +211,7 @@ def decode_legs(quiet: bool):
     """The decode shapes of the same layer (C3-1, C3-16: one and sixteen
     tokens, 128 experts, top-8, INT8), each timed by a child bench in this
     run: step time, tokens/s, the whole layer's algorithmic bytes over the
-    step against HBM peak, and the gate/up GEMV's own roofline line (C3-16
+    step against HBM peak, and the gate/up stage's own roofline line (C3-16
     with its HBM bytes per launch from the rocprofv3 --pmc child runs).
     None for a leg whose child fails."""
     import subprocess
@@ -235,7 +235,7 @@ def decode_legs(quiet: bool):
                     "tokens_per_s": d["value"], "unique_experts": d["config"]["unique_experts"],
                     "layer_hbm_frac": d["layer_roofline"]["hbm_frac"],
                     "layer_algorithmic_bytes": d["layer_roofline"]["algorithmic_bytes"],
-                    "gate_up_gemv": {k: r.get(k) for k in ("kernel", "achieved", "peak", "unit",
+                    "gate_up": {k: r.get(k) for k in ("kernel", "achieved", "peak", "unit",
                                                            "frac", "traffic", "launch_ms")},
                     "stages_ms": d["stages_ms"]}
     return legs
@@ -393,7 +393,7 @@ def main():
     out = res.output.cpu().numpy()
     tokens_per_s = T / (ms_per_step / 1e3)
 
-    gemv = cfg.int8 and T <= capi.HM_GEMV_MAX_TOKENS
+    gemv = cfg.int8 and T <= capi.HM_GEMV_MAX_TOKENS and T * k <= capi.HM_GEMV_MAX_PAIRS
     if gemv:
         # W8A32 GEMV: gate+up weights of the selected experts, gathered FP32
         # activation rows in, FP32 Z rows out

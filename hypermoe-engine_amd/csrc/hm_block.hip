@@ -58,7 +58,7 @@ int hm_route_permute_decode(const float* h, const float* w, int64_t tokens, int6
                             int64_t experts, int32_t top_k, uint32_t flags, uint32_t* ids,
                             float* scores, int32_t* status, void* route_ws,
                             const hm_decode_fusion* fused, const hm_norm_fold* norm,
-                            void* stream);
+                            const hm_row_quant* xq, bool* quantized, void* stream);
 
 namespace {
 
@@ -106,10 +106,14 @@ struct BlockPlan {
     int32_t* counters;  // decode: the fused select's completion counter
 };
 
-// Decode-size INT8 blocks take the W8A32 GEMV kernels.
-bool use_gemv(const hm_layer* L, int64_t T, uint32_t flags) {
+// Decode-size INT8 blocks of at most HM_GEMV_MAX_PAIRS (token, expert) pairs
+// take the W8A32 GEMV kernels; larger decode blocks the limb GEMMs (their
+// weight streams run faster through the ring kernels' LDS stages once most
+// experts see a row or two: C3-16 gate/up 54.5 against 60.5 us).
+bool use_gemv(const hm_layer* L, int64_t T, int32_t k, uint32_t flags) {
     return L->dtype == HM_DTYPE_INT8 && (flags & (HM_EXEC_GENERIC | HM_EXEC_LIMBS)) == 0 &&
-           T <= HM_GEMV_MAX_TOKENS && hm_gemv_shape_ok(L->hidden, L->intermediate);
+           T <= HM_GEMV_MAX_TOKENS && T * k <= HM_GEMV_MAX_PAIRS &&
+           hm_gemv_shape_ok(L->hidden, L->intermediate);
 }
 
 bool layer_valid(const hm_layer* L) {
@@ -136,7 +140,7 @@ size_t plan_block(const hm_layer* L, int64_t T, int32_t k, int32_t lx, int32_t l
     q.perm_weights = c.take<float>((size_t)P);
     q.slots = c.take<int32_t>((size_t)P);
     q.status = c.take<int32_t>(1);
-    if (use_gemv(L, T, flags)) {
+    if (use_gemv(L, T, k, flags)) {
         q.zf = c.take<float>((size_t)P * I);
         q.counters = c.take<int32_t>(1);
     } else if (L->dtype == HM_DTYPE_INT8) {
@@ -150,6 +154,8 @@ size_t plan_block(const hm_layer* L, int64_t T, int32_t k, int32_t lx, int32_t l
         // before the down projection writes y: one region serves both
         q.y = c.take<float>((size_t)P * (H > 2 * I ? H : 2 * I));
         q.gu = q.y;
+        // decode batches: the fused router's completion counter
+        if (T <= HM_GEMV_MAX_TOKENS) q.counters = c.take<int32_t>(1);
         if (p) *p = q;
         return c.used;
     } else {
@@ -224,7 +230,7 @@ int block_forward(const hm_layer* layer, const float* hidden, const float* route
     HM_REQUIRE(workspace_bytes >= need + (size_t)(static_cast<char*>(base) - static_cast<char*>(workspace)));
     BlockPlan p;
     plan_block(layer, tokens, top_k, limbs_x, limbs_z, route_flags, base, &p);
-    const bool gemv = use_gemv(layer, tokens, route_flags);
+    const bool gemv = use_gemv(layer, tokens, top_k, route_flags);
     if (io->ids) p.ids = io->ids;
     if (io->scores) p.scores = io->scores;
     if (io->counts) p.counts = io->counts;
@@ -260,7 +266,12 @@ int block_forward(const hm_layer* layer, const float* hidden, const float* route
     const void* gemv_rows = ln ? static_cast<const void*>(ln->normed) : static_cast<const void*>(hidden);
     const bool gv32 = layer->dtype == HM_DTYPE_FP32 && tokens <= HM_GEMV_MAX_TOKENS &&
                       p.counters && hm_gemv_f32_ok(layer, gemv_rows) && hm_gemv_f32_ok(layer, p.zf);
-    const bool fuse = (gemv || gv32) && H % 32 == 0 && E <= 1024 && top_k <= 64 && P <= 1024;
+    // INT8 decode batches on the limb GEMMs: the fused router also cuts the
+    // activation digits
+    const bool limb_decode = layer->dtype == HM_DTYPE_INT8 && !gemv &&
+                             tokens <= HM_GEMV_MAX_TOKENS && p.counters && p.xdig;
+    const bool fuse = (gemv || gv32 || limb_decode) && H % 32 == 0 && E <= 1024 && top_k <= 64 &&
+                      P <= 1024;
     bool x_quantized = false;
     if (fuse) {
         const hm_decode_fusion f = {p.counters, 1, p.counts, p.offsets, p.perm_tokens,
@@ -268,9 +279,10 @@ int block_forward(const hm_layer* layer, const float* hidden, const float* route
         const hm_norm_fold nf = {ln ? ln->gamma : nullptr, ln ? ln->normed : nullptr,
                                  ln ? ln->eps : 0.0f,
                                  (route_flags & HM_EXEC_ROUTE_SEQUENTIAL) ? 1 : 0};
+        const hm_row_quant xq = {p.xdig, p.xscale, p.xdsum, limbs_x};
         rc = hm_route_permute_decode(hidden, router_w, tokens, H, E, top_k, route_bits, p.ids,
                                      p.scores, status, p.route_ws, &f, ln ? &nf : nullptr,
-                                     stream);
+                                     limb_decode ? &xq : nullptr, &x_quantized, stream);
         if (ln) hidden = ln->normed;
         if (rc || (rc = mark(1)) || (rc = mark(2))) return rc;
     } else {

@@ -941,7 +941,7 @@ __global__ __launch_bounds__(NW * HM_WAVE) void router_select_partial_kernel(
     float* __restrict__ logits, uint32_t* __restrict__ ids, float* __restrict__ scores,
     int32_t* status, int32_t* __restrict__ done_ctr, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ perm_tokens,
-    float* __restrict__ perm_weights, int32_t* __restrict__ slots) {
+    float* __restrict__ perm_weights, int32_t* __restrict__ slots, hm_row_quant xq) {
     extern __shared__ float seq_lds[];  // NW * experts floats
     __shared__ double s_prod[NW][HM_WAVE];
     // one workgroup: the grouping reads the ids and scores from LDS copies
@@ -997,6 +997,18 @@ __global__ __launch_bounds__(NW * HM_WAVE) void router_select_partial_kernel(
                 const int ln = lane < top_k ? lane : 0;
                 permute_wave<EPL>(s_sel_ids[ln], s_sel_sc[ln], top_k, top_k, (int)experts,
                                   counts, offsets, perm_tokens, perm_weights, slots);
+            }
+        }
+        // the token's row in fixed-point digits for the INT8 expert GEMMs,
+        // by the last wave (beside wave 0's selection when there are two)
+        if (xq.digits && wave == NW - 1) {
+            const int nv = (int)(hidden / 256);
+            int8_t* d = xq.digits + t * hidden;
+            int32_t* ds = xq.dsum ? xq.dsum + t : nullptr;
+            switch (xq.limbs) {
+            case 1: hm_quantize_row_wave<1>(h + t * hidden, nv, d, tokens * hidden, xq.scales + t, ds, tokens); break;
+            case 2: hm_quantize_row_wave<2>(h + t * hidden, nv, d, tokens * hidden, xq.scales + t, ds, tokens); break;
+            default: hm_quantize_row_wave<3>(h + t * hidden, nv, d, tokens * hidden, xq.scales + t, ds, tokens); break;
             }
         }
         if (local && top_k <= HM_WAVE) return;
@@ -1836,7 +1848,8 @@ static int launch_decode_router(const float* h, const float* w, int64_t tokens, 
                                 int64_t experts, int32_t top_k, uint32_t flags, float* logits,
                                 uint32_t* ids, float* scores, int32_t* status, void* route_ws,
                                 const hm_decode_fusion* fused, const hm_norm_fold* norm,
-                                void* stream) {
+                                const hm_row_quant* xq, void* stream) {
+    const hm_row_quant q = xq && fused ? *xq : hm_row_quant{nullptr, nullptr, nullptr, 0};
     const int epl = (int)((experts + HM_WAVE - 1) / HM_WAVE);
     // fused: one token per workgroup, its logit rows shared out over up to
     // four waves; else four tokens (waves) per workgroup
@@ -1861,7 +1874,7 @@ static int launch_decode_router(const float* h, const float* w, int64_t tokens, 
                        top_k, flags, logits, ids, scores, status,                            \
                        F ? fused->counters : nullptr, F ? fused->counts : nullptr,           \
                        F ? fused->offsets : nullptr, F ? fused->perm_tokens : nullptr,       \
-                       F ? fused->perm_weights : nullptr, F ? fused->slots : nullptr)
+                       F ? fused->perm_weights : nullptr, F ? fused->slots : nullptr, q)
 #define HM_SELECTP2(N)                                  \
     do {                                                \
         if (!fused) HM_SELECTP(N, false, 4);            \
@@ -1889,7 +1902,8 @@ int hm_route_permute_decode(const float* h, const float* w, int64_t tokens, int6
                             int64_t experts, int32_t top_k, uint32_t flags, uint32_t* ids,
                             float* scores, int32_t* status, void* route_ws,
                             const hm_decode_fusion* fused, const hm_norm_fold* norm,
-                            void* stream) {
+                            const hm_row_quant* xq, bool* quantized, void* stream) {
+    if (quantized) *quantized = false;
     HM_REQUIRE(experts > 0 && top_k > 0 && top_k <= experts && fused && fused->counters);
     HM_REQUIRE(h && w && ids && scores && route_ws && tokens > 0 && hidden > 0);
     // (the norm's row copy is hidden floats of LDS, as in hm_rmsnorm)
@@ -1898,9 +1912,20 @@ int hm_route_permute_decode(const float* h, const float* w, int64_t tokens, int6
     if (experts > 1024 || top_k > kMaxTopK || tokens > kDecodeTokens || hidden % kNB != 0 ||
         tokens * top_k > kSmallPairs || hidden > INT_MAX)
         return HM_ERR_UNSUPPORTED;
-    return launch_decode_router(h, w, tokens, hidden, experts, top_k, flags,
-                                static_cast<float*>(route_ws), ids, scores, status, route_ws,
-                                fused, norm, stream);
+    // the select kernel also cuts the rows' activation digits when asked
+    // (widths the one-wave row quantisation takes; the rows it reads are the
+    // normalised ones when the norm is folded in)
+    const hm_row_quant* q =
+        xq && xq->digits && xq->scales && xq->limbs >= 1 && xq->limbs <= 3 &&
+                hidden % 256 == 0 && hidden / 256 <= kHmQuantMaxV &&
+                (uintptr_t)xq->digits % 4 == 0 && (uintptr_t)(norm ? norm->x_out : h) % 16 == 0
+            ? xq
+            : nullptr;
+    const int rc = launch_decode_router(h, w, tokens, hidden, experts, top_k, flags,
+                                        static_cast<float*>(route_ws), ids, scores, status,
+                                        route_ws, fused, norm, q, stream);
+    if (rc == HM_OK && q && quantized) *quantized = true;
+    return rc;
 }
 
 extern "C" {
@@ -1951,7 +1976,7 @@ __attribute__((visibility("hidden"))) int hm_router_topk_quant(const float* h, c
         // decode: certified block partials, then select over the logits
         // formed from them
         return launch_decode_router(h, w, tokens, hidden, experts, top_k, flags, logits, ids,
-                                    scores, status, route_ws, nullptr, nullptr, stream);
+                                    scores, status, route_ws, nullptr, nullptr, nullptr, stream);
     }
     const bool aligned = ((uintptr_t)h % 16 == 0) && ((uintptr_t)w % 16 == 0);
     if (route_ws && !(flags & HM_EXEC_ROUTE_SEQUENTIAL) && aligned && experts % kME == 0 &&

@@ -18,6 +18,7 @@ HM_STATUS_NONFINITE_SCORE, HM_STATUS_SOFTMAX_FAILED, HM_STATUS_RENORM_FAILED = 1
 HM_ROUTE_SOFTMAX, HM_ROUTE_RENORM, HM_EXEC_GENERIC, HM_EXEC_LIMBS = 1, 2, 0x100, 0x200
 HM_EXEC_SPLIT_K = 0x800
 HM_GEMV_MAX_TOKENS = 16
+HM_GEMV_MAX_PAIRS = 64
 HM_EXEC_ROUTE_SEQUENTIAL = 0x400
 HM_DTYPE_FP32, HM_DTYPE_INT8 = 0, 3
 

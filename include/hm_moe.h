@@ -65,11 +65,14 @@ typedef enum hm_status {
 #define HM_EXEC_GENERIC 0x100u
 /* Execution flag for hm_moe_block_forward: INT8 experts always take the
  * integer-limb GEMMs.  Without it a block of at most HM_GEMV_MAX_TOKENS
- * tokens (decode) takes the W8A32 GEMV kernels instead, which stream each
- * selected expert's weights once and compute in FP32 (within 1e-4 of the
- * reference, not bit-identical to the limb arithmetic). */
+ * tokens and HM_GEMV_MAX_PAIRS (token, expert) pairs (decode) takes the
+ * W8A32 GEMV kernels instead, which stream each selected expert's weights
+ * once and compute in FP32 (within 1e-4 of the reference, not bit-identical
+ * to the limb arithmetic); larger blocks, decode ones included, take the
+ * limb GEMMs. */
 #define HM_EXEC_LIMBS 0x200u
 #define HM_GEMV_MAX_TOKENS 16
+#define HM_GEMV_MAX_PAIRS 64
 /* Execution flag for hm_router_topk / hm_moe_block_forward: every router
  * logit is computed with the reference's sequential FP64 chain instead of
  * certifying the parallel sums (the results are identical; the flag

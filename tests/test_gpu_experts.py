@@ -166,11 +166,17 @@ def test_block_int8_bitexact_vs_limb_oracle(dev, T, H, E, I, k, LX, LZ):
     res2 = block.execute_batch(dev.to(h), dev.to(w), exec_flags=capi.HM_EXEC_GENERIC)
     assert_bitexact(dev.host(res2.output), out, "MFMA vs generic kernels")
     if T <= capi.HM_GEMV_MAX_TOKENS:
-        # the default decode path (W8A32 GEMV in FP32) against the reference
+        # the default decode path: the W8A32 GEMV in FP32 up to
+        # HM_GEMV_MAX_PAIRS pairs (against the reference), the limb GEMMs
+        # beyond (the same bits as above)
         rout_, _, _ = O.moe_block(payload, scale, zp, h, w, k, I)
         gres = block.execute_batch(dev.to(h), dev.to(w))
-        assert_bitexact(gres.ids, res.ids, "GEMV path routing")
-        assert_compare(dev.host(gres.output), rout_, 1e-4, 1e-4, "GEMV block vs reference (1e-4)")
+        assert_bitexact(gres.ids, res.ids, "default decode path routing")
+        if T * k <= capi.HM_GEMV_MAX_PAIRS:
+            assert_compare(dev.host(gres.output), rout_, 1e-4, 1e-4,
+                           "GEMV block vs reference (1e-4)")
+        else:
+            assert_bitexact(dev.host(gres.output), out, "default decode path vs limb GEMMs")
     # reference W8A32 numerics
     rout, rids, rsc = O.moe_block(payload, scale, zp, h, w, k, I)
     assert_bitexact(res.ids, rids, "ids vs reference path")
@@ -238,13 +244,14 @@ def test_block_int8_nonzero_zero_points(dev):
 
 
 @pytest.mark.parametrize("T,H,E,I,k,skew", [
-    (1, 2048, 128, 768, 8, False), (4, 2048, 128, 768, 8, False), (16, 2048, 128, 768, 8, True),
+    (1, 2048, 128, 768, 8, False), (4, 2048, 128, 768, 8, False), (8, 2048, 128, 768, 8, True),
     (16, 512, 4, 256, 2, False), (13, 1024, 3, 512, 3, False), (9, 256, 2, 1024, 1, False),
     (16, 256, 64, 1024, 4, False), (5, 528, 6, 400, 2, False), (2, 2048, 128, 768, 8, False),
     (3, 256, 8, 96, 5, False), (1, 1024, 16, 512, 1, False), (1, 128, 4, 32, 1, False),
     (3, 1024, 16, 512, 8, False)])
 def test_block_gemv_decode(dev, T, H, E, I, k, skew):
-    """Decode-size blocks take the W8A32 GEMV (FP32): ids bit-exact, output
+    """Decode-size blocks of at most HM_GEMV_MAX_PAIRS pairs take the W8A32
+    GEMV (FP32): ids bit-exact, output
     within 1e-4 of the reference; several rows per expert (the register
     row blocks), skewed groups, every supported K length, the four-column-
     tile down workgroups (32 or more active experts) at their largest K, and
@@ -272,6 +279,31 @@ def test_block_gemv_decode(dev, T, H, E, I, k, skew):
         xe = np.ascontiguousarray(h[b.token_indices])
         ref = O.expert_mlp(payload, scale, zp, b.expert_id, xe, I)
         assert_compare(y[lo:lo + len(b.token_indices)], ref, 1e-4, 1e-4, "expert rows")
+
+
+@pytest.mark.parametrize("T,skew", [(16, True), (9, False)])
+def test_block_limb_decode(dev, T, skew):
+    """Decode-size blocks of more than HM_GEMV_MAX_PAIRS pairs (C3-16: 128
+    pairs over about 80 experts) take the limb GEMMs, their activation digits
+    cut by the fused decode router's select kernel: output bit-exact against
+    the limb oracle and within 1e-4 of the reference, routing and grouping
+    bit-exact."""
+    H, E, I, k = 2048, 128, 768, 8
+    assert T * k > capi.HM_GEMV_MAX_PAIRS
+    print(f"[gpu] limb decode T={T} skew={skew}", flush=True)
+    payload, scale, zp, h, w = _layer_inputs(29 + T, T, H, E, I, True, skew=skew)
+    block = MoEBlock(DeviceExpertLayer(payload, scale, zp, H, I), k)
+    res = block.execute_batch(dev.to(h), dev.to(w))
+    lout, lids, lsc = O.moe_block_limbs(payload, scale, zp, h, w, k, I, block.limbs_x,
+                                        block.limbs_z)
+    assert_bitexact(res.ids, lids, "ids")
+    assert_bitexact(res.scores, lsc, "scores")
+    out = dev.host(res.output)
+    assert_bitexact(out, lout, "block output vs limb oracle")
+    _, _, ptok, _, _ = O.group(lids, lsc, E)
+    assert_bitexact(res.perm_tokens, ptok, "grouping")
+    rout, _, _ = O.moe_block(payload, scale, zp, h, w, k, I)
+    assert_compare(out, rout, 1e-4, 1e-4, "limb decode block vs reference W8A32 (1e-4)")
 
 
 @pytest.mark.parametrize("T,E", [(16, 64), (1, 64), (5, 8), (40, 8), (300, 4)])

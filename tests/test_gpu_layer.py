@@ -167,6 +167,33 @@ def test_layer_forward_matches_norm_then_block(dev, layer, T, seq):
     assert_bitexact(out, ref.output.cpu().numpy(), f"T={T} output")
 
 
+@pytest.mark.parametrize("T", [9, 16])
+def test_layer_forward_limb_decode(dev, layer, T):
+    """A decode batch of more than HM_GEMV_MAX_PAIRS pairs (top-8 here) takes
+    the limb GEMMs; with the layer's RMSNorm folded into the router, the
+    select kernel cuts the activation digits from the normalised rows: the
+    same bits as hm_rmsnorm followed by the block."""
+    import torch
+    k = 8
+    assert T * k > capi.HM_GEMV_MAX_PAIRS
+    print(f"[gpu] layer forward limb decode T={T}", flush=True)
+    rng = np.random.default_rng(2000 + T)
+    row0, gamma, _ = _unsettled_row(rng, EPS)
+    h = rng.standard_normal((T, H)).astype(np.float32)
+    h[0] = row0
+    w = synth.router_weights(91, 0, H, E)
+    dh, dg, dw = (torch.from_numpy(a).cuda() for a in (h, gamma, w))
+    block = MoEBlock(layer, k)
+    normed, ids, out = _layer_forward(block, dh, dg, dw, 0)
+    assert_bitexact(normed, O.rmsnorm(h, gamma, EPS), f"T={T} RMSNorm")
+    dn = torch.empty_like(dh)
+    capi.call("hm_rmsnorm", dh.data_ptr(), dg.data_ptr(), dn.data_ptr(), T, H, EPS,
+              torch.cuda.current_stream().cuda_stream)
+    ref = block.execute_batch(dn, dw, residual=dh)
+    assert_bitexact(ids, ref.ids, f"T={T} routing")
+    assert_bitexact(out, ref.output.cpu().numpy(), f"T={T} output")
+
+
 @pytest.mark.parametrize("T", [9, 13])
 def test_rmsnorm_rows_unsettled_in_other_waves(dev, T):
     """hm_rmsnorm at H = 2048 runs one wave per row, four rows per
