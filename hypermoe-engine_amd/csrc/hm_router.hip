@@ -1268,8 +1268,8 @@ __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
     int64_t hidden, int64_t experts, int splits, int32_t top_k, uint32_t flags,
     float* __restrict__ logits, uint32_t* __restrict__ ids, float* __restrict__ scores,
     int32_t* status, hm_row_quant xq, int32_t* __restrict__ hist) {
-    // per wave: experts floats for the sequential softmax sum, then two
-    // fallback buffers (kFBuf each, 16-byte aligned)
+    // per wave: experts floats for the sequential softmax sum, then the
+    // fallback chains' staging ring and products (kFWave, 16-byte aligned)
     extern __shared__ __attribute__((aligned(16))) char dyn_lds[];
     const int lane = threadIdx.x & (HM_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / HM_WAVE);

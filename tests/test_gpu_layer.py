@@ -167,16 +167,17 @@ def test_layer_forward_matches_norm_then_block(dev, layer, T, seq):
     assert_bitexact(out, ref.output.cpu().numpy(), f"T={T} output")
 
 
-@pytest.mark.parametrize("T", [9, 16])
-def test_layer_forward_limb_decode(dev, layer, T):
+@pytest.mark.parametrize("T,offset", [(9, 0), (16, 0), (16, 1)])
+def test_layer_forward_limb_decode(dev, layer, T, offset):
     """A decode batch of more than HM_GEMV_MAX_PAIRS pairs (top-8 here) takes
     the limb GEMMs; with the layer's RMSNorm folded into the router, the
-    select kernel cuts the activation digits from the normalised rows: the
-    same bits as hm_rmsnorm followed by the block."""
+    select kernel cuts the activation digits from the normalised rows (rows
+    4 bytes off 16-byte alignment: the separate quantisation launch does):
+    the same bits as hm_rmsnorm followed by the block."""
     import torch
     k = 8
     assert T * k > capi.HM_GEMV_MAX_PAIRS
-    print(f"[gpu] layer forward limb decode T={T}", flush=True)
+    print(f"[gpu] layer forward limb decode T={T} offset={offset}", flush=True)
     rng = np.random.default_rng(2000 + T)
     row0, gamma, _ = _unsettled_row(rng, EPS)
     h = rng.standard_normal((T, H)).astype(np.float32)
@@ -184,7 +185,7 @@ def test_layer_forward_limb_decode(dev, layer, T):
     w = synth.router_weights(91, 0, H, E)
     dh, dg, dw = (torch.from_numpy(a).cuda() for a in (h, gamma, w))
     block = MoEBlock(layer, k)
-    normed, ids, out = _layer_forward(block, dh, dg, dw, 0)
+    normed, ids, out = _layer_forward(block, dh, dg, dw, 0, normed_offset=offset)
     assert_bitexact(normed, O.rmsnorm(h, gamma, EPS), f"T={T} RMSNorm")
     dn = torch.empty_like(dh)
     capi.call("hm_rmsnorm", dh.data_ptr(), dg.data_ptr(), dn.data_ptr(), T, H, EPS,
