@@ -1054,7 +1054,7 @@ __global__ __launch_bounds__(NW * HM_WAVE) void router_select_partial_kernel(
 // v_mfma_f64_16x16x4_f64 in an order of its own: K is cut into `splits`
 // ranges (one per workgroup layer of the grid) and each range into chunks
 // of 16, of which MFMA step j takes k = 4g + j for the four k-slots g; the
-// kernel also returns the squared norms of h's rows and W's columns per
+// kernel also returns the norms of h's rows and W's columns per
 // range.  router_select_split_kernel adds the S ranges' partials P'_r in
 // order (S'_r after range r, S' = S'_{S-1}) and bounds |S' - s_n| from
 // these, with m = n / S terms per range, A_r = sum_{k in r} |p_k| <=
@@ -1094,7 +1094,7 @@ typedef double hm_double4 __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(256) void router_mfma_kernel(
     const float* __restrict__ h, const float* __restrict__ w, int tokens, int hidden,
     int experts, int ksplit, double* __restrict__ part, float* __restrict__ wt,
-    double* __restrict__ hn2, double* __restrict__ wn2, int32_t* __restrict__ hist, int hist_n) {
+    double* __restrict__ hnorm_r, double* __restrict__ wnorm_r, int32_t* __restrict__ hist, int hist_n) {
     __shared__ __attribute__((aligned(1024))) char ring[kMS][kMW + kMH];
     // the permutation's chunk histograms, counted by the select kernel
     for (int i = blockIdx.x * 256 + threadIdx.x; i < hist_n; i += gridDim.x * 256) hist[i] = 0;
@@ -1195,7 +1195,9 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(
     // lanes i, i + 16, i + 32, i + 48
     hsq += __shfl_xor(hsq, 16, HM_WAVE);
     hsq += __shfl_xor(hsq, 32, HM_WAVE);
-    if (eb == 0 && g == 0 && live) hn2[(int64_t)sp * tokens + tok] = hsq;
+    // (the norms themselves: their square roots, once here rather than for
+    // every logit in the select kernel)
+    if (eb == 0 && g == 0 && live) hnorm_r[(int64_t)sp * tokens + tok] = sqrt(hsq);
     if (wnorm) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -1203,9 +1205,9 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(
             wsq[q] += __shfl_xor(wsq[q], 32, HM_WAVE);
         }
         if (g == 0) {
-            double* o = wn2 + (int64_t)sp * experts + e0 + 4 * i;
-            *reinterpret_cast<double2*>(o) = double2{wsq[0], wsq[1]};
-            *reinterpret_cast<double2*>(o + 2) = double2{wsq[2], wsq[3]};
+            double* o = wnorm_r + (int64_t)sp * experts + e0 + 4 * i;
+            *reinterpret_cast<double2*>(o) = double2{sqrt(wsq[0]), sqrt(wsq[1])};
+            *reinterpret_cast<double2*>(o + 2) = double2{sqrt(wsq[2]), sqrt(wsq[3])};
         }
     }
 }
@@ -1264,7 +1266,7 @@ __device__ __forceinline__ void locate_fallback(const unsigned long long (&need)
 template <int EPL>
 __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
     const float* __restrict__ h, const float* __restrict__ wt, const double* __restrict__ part,
-    const double* __restrict__ hn2, const double* __restrict__ wn2, int64_t tokens,
+    const double* __restrict__ hnorm_r, const double* __restrict__ wnorm_r, int64_t tokens,
     int64_t hidden, int64_t experts, int splits, int32_t top_k, uint32_t flags,
     float* __restrict__ logits, uint32_t* __restrict__ ids, float* __restrict__ scores,
     int32_t* status, hm_row_quant xq, int32_t* __restrict__ hist) {
@@ -1290,7 +1292,7 @@ __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
     double hr[kMaxSplits];
 #pragma unroll
     for (int sp = 0; sp < kMaxSplits; ++sp)
-        hr[sp] = sqrt(hn2[(int64_t)min(sp, splits - 1) * tokens + t]);
+        hr[sp] = hnorm_r[(int64_t)min(sp, splits - 1) * tokens + t];
     float v[EPL];
     bool valid[EPL];
     unsigned long long need[EPL];
@@ -1307,7 +1309,7 @@ __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
             for (int sp = 0; sp < kMaxSplits; ++sp) {
                 const int64_t sc = min(sp, splits - 1);
                 pa[sp] = part[(sc * tokens + t) * experts + e];
-                pw[sp] = wn2[sc * experts + e];
+                pw[sp] = wnorm_r[sc * experts + e];
             }
             // S' (the ranges' partials added in order), the sums of |S'|
             // before (pre) and after (post) each addition, and of the
@@ -1319,7 +1321,7 @@ __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
                     pre += fabs(a);
                     a += pa[sp];
                     post += fabs(a);
-                    nsum += hr[sp] * sqrt(pw[sp]);
+                    nsum += hr[sp] * pw[sp];
                 }
             }
             // nsum bounds sum_r sum_{k in r} |p_k| (Cauchy-Schwarz per range;
@@ -1988,8 +1990,8 @@ __attribute__((visibility("hidden"))) int hm_router_topk_quant(const float* h, c
         double* part = reinterpret_cast<double*>(static_cast<char*>(route_ws) +
                                                  route_logits_bytes(tokens, experts));
         float* wt = reinterpret_cast<float*>(part + (int64_t)sp * tokens * experts);
-        double* hn2 = reinterpret_cast<double*>(wt + experts * hidden);
-        double* wn2 = hn2 + (int64_t)sp * tokens;
+        double* hnorm_r = reinterpret_cast<double*>(wt + experts * hidden);
+        double* wnorm_r = hnorm_r + (int64_t)sp * tokens;
         const int64_t grid = ((tokens + kMT - 1) / kMT) * (experts / kME) * sp;
         // the chunk histograms of hm_permute, when the caller passes them
         const int64_t chunks = (tokens * top_k + kPermChunk - 1) / kPermChunk;
@@ -1997,7 +1999,7 @@ __attribute__((visibility("hidden"))) int hm_router_topk_quant(const float* h, c
         if (hc && counted) *counted = true;
         hipLaunchKernelGGL(router_mfma_kernel, dim3((unsigned)grid), dim3(256), 0,
                            hm_stream(stream), h, w, (int)tokens, (int)hidden, (int)experts,
-                           (int)(hidden / sp), part, wt, hn2, wn2, hc,
+                           (int)(hidden / sp), part, wt, hnorm_r, wnorm_r, hc,
                            hc ? (int)(chunks * experts) : 0);
         HM_LAUNCHED();
         const size_t split_bytes =
@@ -2011,7 +2013,7 @@ __attribute__((visibility("hidden"))) int hm_router_topk_quant(const float* h, c
         }
 #define HM_SELECTS(N)                                                                     \
         hipLaunchKernelGGL(router_select_split_kernel<N>, sgrid, dim3(kBlock), split_bytes, \
-                           hm_stream(stream), h, wt, part, hn2, wn2, tokens, hidden, experts, \
+                           hm_stream(stream), h, wt, part, hnorm_r, wnorm_r, tokens, hidden, experts, \
                            sp, top_k, flags, logits, ids, scores, status, q, hc)
         if (epl <= 1) HM_SELECTS(1);
         else if (epl <= 2) HM_SELECTS(2);
