@@ -466,9 +466,9 @@ __device__ __forceinline__ bool block_sums_settle(double a, double sa, double sc
     return isfinite(lo) && isfinite(hi) && __float_as_uint((float)lo) == __float_as_uint((float)hi);
 }
 
-// part[t][e][j][c], c = 0, 1: B_j, C_j (block-minor, so that the select
-// kernel's lane reads its logit's blocks as contiguous 16-byte vectors,
-// one block's pair in each);
+// part[t][j][e][c], c = 0, 1: B_j, C_j (block-major: a wave's 64 experts of
+// one block are 1 KB in a row, written by one store and read by one load of
+// the select kernel, each lane's block pair a 16-byte vector);
 // grid (kNB, ceil(E/64), T), one wave, lane = expert.  The block's W rows
 // (64 experts wide) go to LDS in one burst of 16-byte DMA loads
 // (E % 64 == 0, b % 4 == 0, w 16-byte aligned), else per lane.
@@ -588,23 +588,23 @@ __global__ __launch_bounds__(64) void router_partial_kernel(
         }
     }
     if (live) {
-        double2* o = reinterpret_cast<double2*>(part + ((int64_t)t * experts + e) * 2 * kNB) + j;
+        double2* o = reinterpret_cast<double2*>(part + (((int64_t)t * kNB + j) * experts + e) * 2);
         *o = make_double2(acc, block_c_term(rs, qs, hidden));
     }
 }
 
 // One logit from its block partials (see above); *settled is false when
 // the bound does not settle the float (the caller then runs the sequential
-// chain).  pp: this logit's [B_0, C_0, B_1, C_1 .. B_31, C_31] (part + (t*E + e) *
-// 2 * kNB).
-__device__ __forceinline__ float block_logit(const double* __restrict__ pp, int64_t hidden,
-                                             bool force_seq, bool* settled) {
+// chain).  pp: this logit's B_0, C_0 (part + (t*kNB*E + e) * 2); block j's
+// pair sits 2 E doubles further on per block.
+__device__ __forceinline__ float block_logit(const double* __restrict__ pp, int64_t experts,
+                                             int64_t hidden, bool force_seq, bool* settled) {
     // all 64 values in 32 vector loads (each block's B_j and C_j in one,
     // so that both sums need every load), then the dependent chain
     typedef int hm_i4 __attribute__((ext_vector_type(4)));
     hm_i4 raw[kNB];
 #pragma unroll
-    for (int i = 0; i < kNB; ++i) raw[i] = reinterpret_cast<const hm_i4*>(pp)[i];
+    for (int i = 0; i < kNB; ++i) raw[i] = *reinterpret_cast<const hm_i4*>(pp + (int64_t)i * 2 * experts);
     // (every load goes out before the first is used: otherwise the compiler
     // splits each pair and issues the C halves only after the B chain)
     __builtin_amdgcn_sched_barrier(0);
@@ -960,8 +960,8 @@ __global__ __launch_bounds__(NW * HM_WAVE) void router_select_partial_kernel(
         valid = e < experts;
         bool settled;
         // (lanes past the experts read the last expert's: no branch around the loads)
-        float v = block_logit(part + (t * experts + (valid ? e : experts - 1)) * 2 * kNB, hidden,
-                              force_seq, &settled);
+        float v = block_logit(part + (t * kNB * experts + (valid ? e : experts - 1)) * 2, experts,
+                              hidden, force_seq, &settled);
         if (!valid) {
             v = 0.0f;
             settled = true;
