@@ -683,14 +683,29 @@ __device__ __forceinline__ float chain_logits(unsigned long long need, int lane,
 // A token whose selection failed (the status word says so): placeholder ids
 // 0..top_k-1 with zero scores, so that the permutation and expert stages that
 // follow on the stream stay in range.
+// A token's id and score stores; `coherent`: device-scope stores (sc1,
+// written through to the device's coherence point), for a workgroup of
+// another XCD that reads them once this one has arrived at the completion
+// counter (no L2 write-back needed).
+template <typename V>
+__device__ __forceinline__ void hm_store_pair(V* p, V v, bool coherent) {
+    if (coherent) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else *p = v;
+}
+template <typename V>
+__device__ __forceinline__ V hm_load_pair(const V* p, bool coherent) {
+    return coherent ? __hip_atomic_load(const_cast<V*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                    : *p;
+}
+
 __device__ __forceinline__ void select_failed(int lane, int64_t t, int32_t top_k,
                                               uint32_t* __restrict__ ids,
                                               float* __restrict__ scores,
                                               uint32_t* l_ids = nullptr,
-                                              float* l_scores = nullptr) {
+                                              float* l_scores = nullptr, bool coherent = false) {
     if (lane < top_k) {
-        ids[t * top_k + lane] = (uint32_t)lane;
-        scores[t * top_k + lane] = 0.0f;
+        hm_store_pair(&ids[t * top_k + lane], (uint32_t)lane, coherent);
+        hm_store_pair(&scores[t * top_k + lane], 0.0f, coherent);
         if (l_ids) {
             l_ids[lane] = (uint32_t)lane;
             l_scores[lane] = 0.0f;
@@ -704,8 +719,9 @@ __device__ __forceinline__ void select_token(float (&v)[EPL], const bool (&valid
                                              uint32_t flags, uint32_t* __restrict__ ids,
                                              float* __restrict__ scores, int32_t* status,
                                              float* seq_lds, uint32_t* l_ids = nullptr,
-                                             float* l_scores = nullptr) {
-    // (l_ids, l_scores: optional LDS copies of this token's ids and scores)
+                                             float* l_scores = nullptr, bool coherent = false) {
+    // (l_ids, l_scores: optional LDS copies of this token's ids and scores;
+    // coherent: device-scope stores, hm_store_pair)
     if (flags & HM_ROUTE_SOFTMAX) {
         float m = -__uint_as_float(0x7f800000u);
 #pragma unroll
@@ -735,7 +751,7 @@ __device__ __forceinline__ void select_token(float (&v)[EPL], const bool (&valid
         }
         if (!(isfinite(den) && den > 0.0)) {
             if (lane == 0) hm_status_or(status, HM_STATUS_SOFTMAX_FAILED);
-            select_failed(lane, t, top_k, ids, scores, l_ids, l_scores);
+            select_failed(lane, t, top_k, ids, scores, l_ids, l_scores, coherent);
             return;
         }
 #pragma unroll
@@ -771,14 +787,14 @@ __device__ __forceinline__ void select_token(float (&v)[EPL], const bool (&valid
     if (flags & HM_ROUTE_RENORM) {
         if (!(isfinite(sel_sum) && sel_sum != 0.0)) {
             if (lane == 0) hm_status_or(status, HM_STATUS_RENORM_FAILED);
-            select_failed(lane, t, top_k, ids, scores, l_ids, l_scores);
+            select_failed(lane, t, top_k, ids, scores, l_ids, l_scores, coherent);
             return;
         }
         my_score = (float)((double)my_score / sel_sum);
     }
     if (lane < top_k) {
-        ids[t * top_k + lane] = my_id;
-        scores[t * top_k + lane] = my_score;
+        hm_store_pair(&ids[t * top_k + lane], my_id, coherent);
+        hm_store_pair(&scores[t * top_k + lane], my_score, coherent);
         if (l_ids) {
             l_ids[lane] = my_id;
             l_scores[lane] = my_score;
@@ -820,7 +836,9 @@ template <int NT>
 __device__ void permute_small(const uint32_t* __restrict__ ids, const float* __restrict__ scores,
                               int pairs, int top_k, int experts, int32_t* __restrict__ counts,
                               int32_t* __restrict__ offsets, int32_t* __restrict__ perm_tokens,
-                              float* __restrict__ perm_weights, int32_t* __restrict__ slots) {
+                              float* __restrict__ perm_weights, int32_t* __restrict__ slots,
+                              bool coherent = false) {
+    // (coherent: ids and scores read device-scope, hm_load_pair)
     constexpr int EPT = 1024 / NT;  // experts per thread in the scan (E <= 1024)
     __shared__ int s_cnt[1024];
     __shared__ int s_off[1024];
@@ -830,7 +848,7 @@ __device__ void permute_small(const uint32_t* __restrict__ ids, const float* __r
     for (int i = tid; i < experts; i += NT) s_cnt[i] = 0;
     __syncthreads();
     for (int p = tid; p < pairs; p += NT) {
-        const uint32_t e = ids[p];
+        const uint32_t e = hm_load_pair(&ids[p], coherent);
         const int ec = e < (uint32_t)experts ? (int)e : experts - 1;
         s_ids[p] = ec;
         atomicAdd(&s_cnt[ec], 1);
@@ -872,7 +890,7 @@ __device__ void permute_small(const uint32_t* __restrict__ ids, const float* __r
         for (int q = 0; q < p; ++q) rank += s_ids[q] == e;
         const int pos = s_off[e] + rank;
         perm_tokens[pos] = p / top_k;
-        perm_weights[pos] = scores[p];
+        perm_weights[pos] = hm_load_pair(&scores[p], coherent);
         slots[p] = pos;
     }
 }
@@ -950,6 +968,9 @@ __global__ __launch_bounds__(NW * HM_WAVE) void router_select_partial_kernel(
     // SPLIT: the token's logits, rows of 64 experts shared out over the waves
     __shared__ float s_lg[SPLIT ? EPL : 1][HM_WAVE];
     const bool local = PERMUTE && gridDim.x == 1;
+    // several workgroups: the last to arrive groups every token's pairs, so
+    // the ids and scores go out device-coherent
+    const bool shared = PERMUTE && gridDim.x > 1;
     const int lane = threadIdx.x & (HM_WAVE - 1);
     const int wave = threadIdx.x / HM_WAVE;
     const bool force_seq = (flags & HM_EXEC_ROUTE_SEQUENTIAL) != 0;
@@ -989,7 +1010,8 @@ __global__ __launch_bounds__(NW * HM_WAVE) void router_select_partial_kernel(
                 valid[j] = lane + (int64_t)HM_WAVE * j < experts;
             }
             select_token<EPL>(v, valid, lane, 0, t, experts, top_k, flags, ids, scores, status,
-                              seq_lds, local ? s_sel_ids : nullptr, local ? s_sel_sc : nullptr);
+                              seq_lds, local ? s_sel_ids : nullptr, local ? s_sel_sc : nullptr,
+                              shared);
             if (local && top_k <= HM_WAVE) {
                 // one token: its grouping by this wave, from the LDS copies
                 __builtin_amdgcn_wave_barrier();
@@ -1022,28 +1044,29 @@ __global__ __launch_bounds__(NW * HM_WAVE) void router_select_partial_kernel(
             for (int j = 0; j < EPL; ++j) v[j] = logit_row(t, j, valid[j]);
             select_token<EPL>(v, valid, lane, wave, t, experts, top_k, flags, ids, scores, status,
                               seq_lds, local ? s_sel_ids + wave * top_k : nullptr,
-                              local ? s_sel_sc + wave * top_k : nullptr);
+                              local ? s_sel_sc + wave * top_k : nullptr, shared);
         }
     }
     if constexpr (PERMUTE) {
         if (gridDim.x > 1) {
-            // (the device-scope fences write back and invalidate this XCD's
-            // L2: only taken when several workgroups share the batch)
+            // Arrival without a write-back of this XCD's L2: the ids and
+            // scores were stored device-coherent (sc1); once this wave's
+            // stores are complete (vmcnt 0, every wave) the workgroup counts
+            // in, and the last one reads them device-coherent too.
             __shared__ int s_last;
-            __threadfence();  // this workgroup's ids and scores, before its arrival
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
             if (threadIdx.x == 0)
-                s_last = __hip_atomic_fetch_add(done_ctr, 1, __ATOMIC_ACQ_REL,
+                s_last = __hip_atomic_fetch_add(done_ctr, 1, __ATOMIC_RELAXED,
                                                 __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1;
             __syncthreads();
             if (!s_last) return;
-            __threadfence();  // every workgroup's ids and scores are visible
         } else {
             __syncthreads();  // one workgroup: its own ids and scores
         }
         permute_small<NW * HM_WAVE>(local ? s_sel_ids : ids, local ? s_sel_sc : scores,
                                     (int)(tokens * top_k), top_k, (int)experts, counts, offsets,
-                                    perm_tokens, perm_weights, slots);
+                                    perm_tokens, perm_weights, slots, shared);
     }
 }
 
