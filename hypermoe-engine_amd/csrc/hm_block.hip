@@ -144,10 +144,10 @@ size_t plan_block(const hm_layer* L, int64_t T, int32_t k, int32_t lx, int32_t l
         q.zf = c.take<float>((size_t)P * I);
         q.counters = c.take<int32_t>(1);
     } else if (L->dtype == HM_DTYPE_INT8) {
-        q.xdig = c.take<int8_t>((size_t)lx * T * H);
+        q.xdig = c.take<int8_t>((size_t)lx * T * hm_pad64(H));  // X layout (hm_dlay_x)
         q.xscale = c.take<float>((size_t)T);
         q.xdsum = c.take<int32_t>((size_t)lx * T);
-        q.zdig = c.take<int8_t>((size_t)lz * P * I);
+        q.zdig = c.take<int8_t>((size_t)lz * P * hm_pad64(I));  // Z layout (hm_dlay_z)
         q.zscale = c.take<float>((size_t)P);
         q.zdsum = c.take<int32_t>((size_t)lz * P);
         // the gate/up values [P x 2I] are dead once the Z digits are cut,

@@ -286,19 +286,49 @@ __device__ __forceinline__ float hm_recombine(const int* p, int limbs) {
     return c;
 }
 
+// Digit-plane layouts.  Digit (plane l, row r, k) of a block of digit rows
+// sits at r * row + l * plane + (k >> 6) * chunk + (k & 63): K is cut into
+// 64-byte chunks (the ring GEMMs' K stage), K64 = K rounded up to 64.
+//   planes  [L][rows][K]          the op-level layout (hm_limb_quantize_rows)
+//   X       [T][K64/64][L][64]    token rows: a row's L planes of one chunk
+//                                 are L * 64 contiguous bytes (one 128-byte
+//                                 line at L = 2), read gathered by token
+//   Z       [K64/64][L][R][64]    grouped rows: one plane's chunk of
+//                                 consecutive rows is contiguous (a 16-row
+//                                 load unit is one kilobyte)
+// Pad digits (K <= k < K64) are never read.
+struct hm_dlay {
+    int64_t row, plane, chunk;
+};
+__host__ __device__ __forceinline__ int64_t hm_pad64(int64_t v) { return (v + 63) & ~(int64_t)63; }
+__host__ __device__ __forceinline__ hm_dlay hm_dlay_planes(int64_t rows, int64_t K) {
+    return hm_dlay{K, rows * K, 64};
+}
+__host__ __device__ __forceinline__ hm_dlay hm_dlay_x(int L, int64_t K) {
+    return hm_dlay{L * hm_pad64(K), 64, 64 * (int64_t)L};
+}
+__host__ __device__ __forceinline__ hm_dlay hm_dlay_z(int L, int64_t rows) {
+    return hm_dlay{64, 64 * rows, 64 * rows * (int64_t)L};
+}
+__host__ __device__ __forceinline__ int64_t hm_dlay_off(const hm_dlay& d, int l, int64_t r,
+                                                        int64_t k) {
+    return r * d.row + l * d.plane + (k >> 6) * d.chunk + (k & 63);
+}
+
 // One wave quantises one FP32 row of n = 256*nv floats to L fixed-point
 // digit planes: the row max gives the step (inv = range / max|x|), every
 // element becomes rint(x * inv) split into L digits.  The row is in
-// registers, lane: floats 4*(lane + 64 i) .. +3 in v[i].  Plane l of the row
-// goes to digits + l * plane_stride (4 bytes per lane and float4), its digit
-// sum to dsum[l * dsum_stride] (when dsum is set), the scale max|x| / range
-// to *scale.  Shared by the row-quantisation kernels and the prefill
-// router's select kernel, so all of them write the same bytes.
+// registers, lane: floats 4*(lane + 64 i) .. +3 in v[i].  Digit (l, k) of
+// the row goes to digits + l * plane + (k >> 6) * chunk + (k & 63) (lay's
+// plane and chunk strides, digits at the row's start; 4 bytes per lane and
+// float4), its digit sum to dsum[l * dsum_stride] (when dsum is set), the
+// scale max|x| / range to *scale.  Shared by the row-quantisation kernels
+// and the routers' select kernels, so all of them write the same bytes.
 constexpr int kHmQuantMaxV = 16;  // n <= 4096
 template <int L>
 __device__ __forceinline__ void hm_quantize_row_values(const float4* v, int nv,
                                                        int8_t* __restrict__ digits,
-                                                       int64_t plane_stride, float* scale,
+                                                       const hm_dlay& lay, float* scale,
                                                        int32_t* __restrict__ dsum,
                                                        int64_t dsum_stride) {
     const int lane = threadIdx.x & (HM_WAVE - 1);
@@ -327,7 +357,8 @@ __device__ __forceinline__ void hm_quantize_row_values(const float4* v, int nv,
             for (int l = 0; l < L; ++l) {
                 const uint32_t word = (uint32_t)(d0[l] & 255) | ((uint32_t)(d1[l] & 255) << 8) |
                                       ((uint32_t)(d2[l] & 255) << 16) | ((uint32_t)(d3[l] & 255) << 24);
-                reinterpret_cast<uint32_t*>(digits + (int64_t)l * plane_stride)[lane + HM_WAVE * i] = word;
+                const int64_t k = 4 * (int64_t)(lane + HM_WAVE * i);
+                *reinterpret_cast<uint32_t*>(digits + hm_dlay_off(lay, l, 0, k)) = word;
                 dl[l] += d0[l] + d1[l] + d2[l] + d3[l];
             }
         }
@@ -344,7 +375,7 @@ __device__ __forceinline__ void hm_quantize_row_values(const float4* v, int nv,
 template <int L>
 __device__ __forceinline__ void hm_quantize_row_wave(const float* __restrict__ xrow, int nv,
                                                      int8_t* __restrict__ digits,
-                                                     int64_t plane_stride, float* scale,
+                                                     const hm_dlay& lay, float* scale,
                                                      int32_t* __restrict__ dsum,
                                                      int64_t dsum_stride) {
     const int lane = threadIdx.x & (HM_WAVE - 1);
@@ -353,12 +384,12 @@ __device__ __forceinline__ void hm_quantize_row_wave(const float* __restrict__ x
 #pragma unroll
     for (int i = 0; i < kHmQuantMaxV; ++i)
         if (i < nv) v[i] = xr[lane + HM_WAVE * i];
-    hm_quantize_row_values<L>(v, nv, digits, plane_stride, scale, dsum, dsum_stride);
+    hm_quantize_row_values<L>(v, nv, digits, lay, scale, dsum, dsum_stride);
 }
 
 // Where a fused row quantisation writes (digits == nullptr: none).
 struct hm_row_quant {
-    int8_t* digits;    // [limbs][rows][n]
+    int8_t* digits;    // the X layout (hm_dlay_x): [rows][n64 / 64][limbs][64]
     float* scales;     // [rows]
     int32_t* dsum;     // [limbs][rows] or nullptr
     int32_t limbs;

@@ -23,12 +23,13 @@ constexpr int kBlock = 256;
 
 // ---------------------------------------------------------------------------
 // Activation rows -> digit planes (one wave per row segment).
-// digits [L][rows][n] (row stride n), scales [rows], dsum [L][rows].
+// digits in layout lay (hm_dlay: the op-level [L][rows][n] or the block's
+// X rows), scales [rows], dsum [L][rows].
 // ---------------------------------------------------------------------------
 template <int L>
 __global__ __launch_bounds__(kBlock) void limb_quantize_rows_kernel(
     const float* __restrict__ x, int64_t rows, int64_t n,
-    int8_t* __restrict__ digits, float* __restrict__ scales,
+    int8_t* __restrict__ digits, hm_dlay lay, float* __restrict__ scales,
     int32_t* __restrict__ dsum) {
     const int lane = threadIdx.x & (HM_WAVE - 1);
     const int64_t r = (int64_t)blockIdx.x * (kBlock / HM_WAVE) + threadIdx.x / HM_WAVE;
@@ -47,7 +48,7 @@ __global__ __launch_bounds__(kBlock) void limb_quantize_rows_kernel(
 #pragma unroll
         for (int l = 0; l < L; ++l) {
             const int d = hm_digit(v, l);
-            digits[((int64_t)l * rows + r) * n + k] = (int8_t)d;
+            digits[hm_dlay_off(lay, l, r, k)] = (int8_t)d;
             dl[l] += d;
         }
     }
@@ -68,11 +69,12 @@ constexpr int kQMaxV = kHmQuantMaxV;
 template <int L>
 __global__ __launch_bounds__(kBlock) void limb_quantize_rows_vec_kernel(
     const float* __restrict__ x, int64_t rows, int64_t n, int nv,
-    int8_t* __restrict__ digits, float* __restrict__ scales, int32_t* __restrict__ dsum) {
+    int8_t* __restrict__ digits, hm_dlay lay, float* __restrict__ scales,
+    int32_t* __restrict__ dsum) {
     const int lane = threadIdx.x & (HM_WAVE - 1);
     const int64_t r = (int64_t)blockIdx.x * (kBlock / HM_WAVE) + threadIdx.x / HM_WAVE;
     if (r >= rows) return;
-    hm_quantize_row_wave<L>(x + r * n, nv, digits + r * n, rows * n, scales + r,
+    hm_quantize_row_wave<L>(x + r * n, nv, digits + r * lay.row, lay, scales + r,
                             dsum ? dsum + r : nullptr, rows);
 }
 
@@ -80,7 +82,8 @@ __global__ __launch_bounds__(kBlock) void limb_quantize_rows_vec_kernel(
 // SwiGLU then the Z rows' digit planes: row r of gu [rows x 2n] holds the
 // gate values g (columns 0..n-1) and the up values u (n..2n-1) of one grouped
 // row; z = silu(g) * u (Activation.cpp:44, then the multiply) is quantised
-// like any activation row (one scale per row).  One wave per row.
+// like any activation row (one scale per row).  One wave per row.  Digits
+// in the Z layout (hm_dlay_z(L, rows)).
 // ---------------------------------------------------------------------------
 // rows of n = 256 * NV, 16-byte aligned: the row in registers (NV a
 // template argument, so a wave holds only its own row's values)
@@ -127,7 +130,8 @@ __global__ __launch_bounds__(kBlock) void limb_swiglu_quantize_vec_kernel(
             z[i].w = __fmul_rn(hm_silu_t(g[i].w, s_exp2), u[i].w);
         }
     }
-    hm_quantize_row_values<L>(z, NV, digits + r * n, rows * n, scales + r,
+    const hm_dlay lay = hm_dlay_z(L, rows);
+    hm_quantize_row_values<L>(z, NV, digits + r * lay.row, lay, scales + r,
                               dsum ? dsum + r : nullptr, rows);
 }
 
@@ -155,10 +159,11 @@ __global__ __launch_bounds__(kBlock) void limb_swiglu_quantize_kernel(
     for (int l = 0; l < L; ++l) dl[l] = 0;
     for (int64_t k = lane; k < n; k += HM_WAVE) {
         const int v = hm_fixed_point(__fmul_rn(hm_silu_t(g[k], s_exp2), u[k]), inv, range);
+        const hm_dlay lay = hm_dlay_z(L, rows);
 #pragma unroll
         for (int l = 0; l < L; ++l) {
             const int d = hm_digit(v, l);
-            digits[((int64_t)l * rows + r) * n + k] = (int8_t)d;
+            digits[hm_dlay_off(lay, l, r, k)] = (int8_t)d;
             dl[l] += d;
         }
     }
@@ -218,15 +223,16 @@ __global__ void gateup_generic_kernel(
     const int8_t* qu = packed + hm_proj_offset(e, 1, H, I);
     const int64_t H32 = hm_pad32(H);
     const int zg = zp[e * 3 + 0], zu = zp[e * 3 + 1];
+    const hm_dlay lay = hm_dlay_x(L, H);
     int pg[L], pu[L];
 #pragma unroll
     for (int l = 0; l < L; ++l) {
-        const int8_t* d = xdig + ((int64_t)l * tokens + t) * H;
         int ag = 0, au = 0;
         for (int64_t k = 0; k < H; ++k) {
             const int64_t o = hm_tile_offset(col, k, H32);
-            ag += (int)d[k] * ((int)qg[o] - zg);
-            au += (int)d[k] * ((int)qu[o] - zu);
+            const int d = xdig[hm_dlay_off(lay, l, t, k)];
+            ag += d * ((int)qg[o] - zg);
+            au += d * ((int)qu[o] - zu);
         }
         pg[l] = ag;
         pu[l] = au;
@@ -252,12 +258,13 @@ __global__ void down_generic_kernel(
     const int8_t* qd = packed + hm_proj_offset(e, 2, H, I);
     const int64_t I32 = hm_pad32(I);
     const int zd = zp[e * 3 + 2];
+    const hm_dlay lay = hm_dlay_z(L, R);
     int p[L];
 #pragma unroll
     for (int l = 0; l < L; ++l) {
-        const int8_t* d = zdig + ((int64_t)l * R + row) * I;
         int a = 0;
-        for (int64_t k = 0; k < I; ++k) a += (int)d[k] * ((int)qd[hm_tile_offset(col, k, I32)] - zd);
+        for (int64_t k = 0; k < I; ++k)
+            a += (int)zdig[hm_dlay_off(lay, l, row, k)] * ((int)qd[hm_tile_offset(col, k, I32)] - zd);
         p[l] = a;
     }
     y[idx] = __fmul_rn(hm_recombine(p, L), __fmul_rn(zscale[row], scale[e * 3 + 2]));
@@ -550,13 +557,14 @@ __global__ __launch_bounds__(256) void pack_tiles_i8_kernel(const int8_t* __rest
 // ===========================================================================
 // Rows -> digit planes.
 static int quantize_rows(const float* x, int64_t rows, int64_t n, int32_t limbs,
-                         int8_t* digits, float* scales, int32_t* dsum, hipStream_t stream) {
+                         int8_t* digits, const hm_dlay& lay, float* scales, int32_t* dsum,
+                         hipStream_t stream) {
     if (rows == 0) return HM_OK;
     const dim3 grid((unsigned)((rows + 3) / 4));
     const int64_t nv = n / 256;
     if (n % 256 == 0 && nv >= 1 && nv <= kQMaxV && (uintptr_t)x % 16 == 0 && (uintptr_t)digits % 4 == 0) {
 #define HM_QV(LV) HM_STAGE_LAUNCH(false, false, limb_quantize_rows_vec_kernel<LV>, grid, dim3(kBlock), 0, stream, \
-                                  x, rows, n, (int)nv, digits, scales, dsum)
+                                  x, rows, n, (int)nv, digits, lay, scales, dsum)
         switch (limbs) {
         case 1: HM_QV(1); break;
         case 2: HM_QV(2); break;
@@ -568,7 +576,7 @@ static int quantize_rows(const float* x, int64_t rows, int64_t n, int32_t limbs,
         return HM_OK;
     }
 #define HM_QS(LV) HM_STAGE_LAUNCH(false, false, limb_quantize_rows_kernel<LV>, grid, dim3(kBlock), 0, stream, \
-                                  x, rows, n, digits, scales, dsum)
+                                  x, rows, n, digits, lay, scales, dsum)
     switch (limbs) {
     case 1: HM_QS(1); break;
     case 2: HM_QS(2); break;
@@ -580,14 +588,16 @@ static int quantize_rows(const float* x, int64_t rows, int64_t n, int32_t limbs,
     return HM_OK;
 }
 
+// The block's token rows in the X digit layout (hm_dlay_x).
 int hm_launch_quantize_rows(const float* x, int64_t rows, int64_t n, int32_t limbs,
                             int8_t* digits, float* scales, int32_t* dsum,
                             hipStream_t stream) {
-    return quantize_rows(x, rows, n, limbs, digits, scales, dsum, stream);
+    return quantize_rows(x, rows, n, limbs, digits, hm_dlay_x(limbs, n), scales, dsum, stream);
 }
 
-// gu [rows x 2n] (g | u per row) -> z = silu(g) * u -> digit planes; the
-// last launch of the gate/up stage (its end closes an armed stage timer).
+// gu [rows x 2n] (g | u per row) -> z = silu(g) * u -> digit planes in the
+// Z layout (hm_dlay_z); the last launch of the gate/up stage (its end closes
+// an armed stage timer).
 static int swiglu_quantize_rows(const float* gu, int64_t rows, int64_t n, int32_t limbs,
                                 int8_t* digits, float* scales, int32_t* dsum,
                                 hipStream_t stream) {
@@ -767,8 +777,8 @@ int hm_limb_quantize_rows(const float* x, int64_t rows, int64_t inner, int32_t l
                           int8_t* digits, float* scales, void* stream) {
     HM_REQUIRE(x && digits && scales && rows >= 0 && inner > 0);
     HM_REQUIRE(limbs >= 1 && limbs <= 3);
-    return hm_launch_quantize_rows(x, rows, inner, limbs, digits, scales, nullptr,
-                                   hm_stream(stream));
+    return quantize_rows(x, rows, inner, limbs, digits, hm_dlay_planes(rows, inner), scales,
+                         nullptr, hm_stream(stream));
 }
 
 int hm_limb_partials(const int8_t* digits, int64_t rows, int64_t inner, int32_t limbs,

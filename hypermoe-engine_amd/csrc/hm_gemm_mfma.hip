@@ -226,8 +226,9 @@ struct TileInfo {
 
 // ---------------------------------------------------------------------------
 // The down projection: K = I, N = H, out = y [R x H].  A rows: the Z digit
-// planes adig [L][R][K] by grouped row; ascale/adsum: their fixed-point
-// scales [arows] and digit sums [L][arows] (for non-zero zero points).
+// planes adig (the Z layout hm_dlay_z: [K/64][L][R][64]) by grouped row;
+// ascale/adsum: their fixed-point scales [arows] and digit sums [L][arows]
+// (for non-zero zero points).
 // ---------------------------------------------------------------------------
 template <int L, int DB>
 __global__ __launch_bounds__(kThreads) void limb_gemm_kernel(
@@ -294,8 +295,11 @@ __global__ __launch_bounds__(kThreads) void limb_gemm_kernel(
     // 32-bit per-lane offsets)
     // A: load unit u = wave + kWaves i covers ring rows 8u .. 8u+7 (limb-major
     // [L][BM], 128 bytes a row); lane: row 8u + lane/8, ring position lane%8,
-    // which holds chunk a_chunk_pos(row, lane%8) of the row.
+    // which holds chunk a_chunk_pos(row, lane%8) of the row's stage: in the Z
+    // layout, 16-byte piece c of stage ks lies in 64-byte chunk 2 ks + c/4
+    // (the stage's uniform offset ks * astep, astep = 2 L arows 64).
     const __amdgpu_buffer_rsrc_t arsrc = buffer_rsrc(adig, (uint32_t)((int64_t)L * arows * K));
+    const uint32_t astep = (uint32_t)(2 * 64 * (int64_t)L * arows);
     uint32_t aoff[APW];
     auto make_asrc = [&](const TileInfo& t) __attribute__((always_inline)) {
         const int ln = fresh_lane();
@@ -305,7 +309,7 @@ __global__ __launch_bounds__(kThreads) void limb_gemm_kernel(
             const int l = q / BM, r = q % BM;
             const int c = a_chunk_pos(r, ln & 7);
             const int row = t.g0 + min(r, t.nrows - 1);
-            aoff[i] = (uint32_t)(((int64_t)l * arows + row) * K + 16 * c);
+            aoff[i] = (uint32_t)((((int64_t)(c >> 2) * L + l) * arows + row) * 64 + 16 * (c & 3));
         }
     };
     // B: the tile's expert as one buffer; fragment f's K tiles are
@@ -322,7 +326,7 @@ __global__ __launch_bounds__(kThreads) void limb_gemm_kernel(
         }
     };
     auto issue_a = [&](int i, int stage, int ks) __attribute__((always_inline)) {
-        dma16_buf(arsrc, aoff[i], (uint32_t)(ks * kKS),
+        dma16_buf(arsrc, aoff[i], (uint32_t)ks * astep,
                   ring + (stage % kSA) * ASTAGE + (wave + kWaves * i) * 1024);
     };
     v4i bq[DB][NCF][kKT];
@@ -551,8 +555,9 @@ __global__ __launch_bounds__(kThreads) void limb_gemm_kernel(
 // split-K does (P = min(8, ceil(K/512)), Int8GemmPlan.cpp:29-53, reduced in
 // a fixed order, CudaKernels.cu:53-107), here kSkP = 2 within a workgroup.
 //   GU    gate and up (NP = 2): A = the X digit planes of the rows' tokens
-//         (perm_tokens), out = gu [R x 2I];
-//   down  (NP = 1): A = the Z digit planes of the grouped rows, out = y.
+//         (perm_tokens; hm_dlay_x), out = gu [R x 2I];
+//   down  (NP = 1): A = the Z digit planes of the grouped rows (hm_dlay_z),
+//         out = y.
 // LDS: the A rows, L x 32 x K bytes, reused for the partials (skinny_lds).
 // ===========================================================================
 constexpr int kSkinnyRows = 32;   // one 32-row fragment
@@ -590,10 +595,10 @@ __global__ __launch_bounds__(kSkThreads) void skinny_split_kernel(
     // lane -> row lane/2, half lane%2 (32 rows x 32 bytes, MFMA order)
     {
         const int arow = s_arow[lane >> 1];
+        const hm_dlay lay = GU ? hm_dlay_x(L, K) : hm_dlay_z(L, arows);
         for (int q = wave; q < L * KT; q += kSkWaves) {
             const int l = q / KT, kt = q - l * KT;
-            dma16(adig + ((int64_t)l * arows + arow) * K + 32 * kt + 16 * (lane & 1),
-                  s_a + 1024 * q);
+            dma16(adig + hm_dlay_off(lay, l, arow, 32 * kt + 16 * (lane & 1)), s_a + 1024 * q);
         }
     }
     // this wave's column block and K part
@@ -808,7 +813,10 @@ int launch_l(const hm_layer* layer, const int8_t* adig, const float* ascale,
 //   A  the L digit planes of the tile rows (gathered by perm_tokens), in
 //      fragments of 32 rows x 64 bytes, two wave-wide 16-byte DMAs each
 //      (lane: row 16 h + lane/4, chunk (lane%4) ^ ((lane/16)%4)), read back
-//      bank-conflict free with the swizzle of gu_frag_read_offset;
+//      bank-conflict free with the swizzle of gu_frag_read_offset; at two
+//      planes (gate/up) each DMA instead moves 8 rows' whole 128-byte lines
+//      (both planes of the stage, adjacent in the X layout) and the reads
+//      follow gu_pair_read_offset;
 //   B  the 8 weight fragments (4 gate, 4 up column blocks of 32), each the
 //      two 1 KB operand-order tiles (hm_tile_offset) of the stage's K steps,
 //      one contiguous DMA each and read back at 16 lane.
@@ -835,6 +843,14 @@ __device__ __forceinline__ int gu_frag_read_offset(int lane, int h) {
     const int r = lane & 31, c = 2 * h + (lane >> 5);
     return 1024 * (r >> 4) + 16 * (4 * (r & 15) + (c ^ ((r >> 2) & 3)));
 }
+// The paired (L = 2, gate/up) fragment reader: plane l, K step h, lane m
+// (row r = m%32, 16-byte piece c = 4 l + 2 h + m/32 of the row's 128 bytes)
+// at 128 r + 16 (c ^ ((r/2)%8)) in the 32-row block; over any 16
+// consecutive lanes these are 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int gu_pair_read_offset(int lane, int h, int l) {
+    const int r = lane & 31, c = 4 * l + 2 * h + (lane >> 5);
+    return 128 * r + 16 * (c ^ ((r >> 1) & 7));
+}
 __device__ __forceinline__ v4i lds16(const int8_t* p) { return *reinterpret_cast<const v4i*>(p); }
 
 template <int L>
@@ -852,11 +868,17 @@ struct GateUpTile {
     static constexpr int STAGE = NF * kGuFrag;
 };
 
-// DN = false: gate/up, A = X digit planes [L][arows = T][K = H] gathered
-// by perm_tokens, out = gu [R x 2I] (tile: 128 gate + 128 up columns).
-// DN = true: down, A = Z digit planes [L][arows = R][K = I] of the grouped
-// rows themselves, out = y [R x H] (tile: 256 down columns; the "gate" half
-// of the gate/up tile is its first 128 columns, the "up" half the next).
+// DN = false: gate/up, A = X digit planes (hm_dlay_x: [T][H/64][L][64])
+// gathered by perm_tokens, out = gu [R x 2I] (tile: 128 gate + 128 up
+// columns).  At L = 2 the A load units are whole 128-byte lines (a row's two
+// planes of the stage), 8 rows a unit, stored at row r's 128 bytes with the
+// 16-byte pieces rotated by (r / 2) % 8 (the paired fragment order, read
+// conflict-free at gu_pair_read_offset); otherwise 16 rows of one plane's
+// 64 bytes a unit (gu_frag_load_row/chunk).
+// DN = true: down, A = Z digit planes (hm_dlay_z: [I/64][L][R][64]) of the
+// grouped rows themselves (a 16-row load unit is one contiguous kilobyte),
+// out = y [R x H] (tile: 256 down columns; the "gate" half of the gate/up
+// tile is its first 128 columns, the "up" half the next).
 template <int L, bool DN>
 __global__ __launch_bounds__(kGuThreads) void ring_gemm_kernel(
     const int8_t* __restrict__ xdig, const float* __restrict__ xscale,
@@ -949,11 +971,13 @@ __global__ __launch_bounds__(kGuThreads) void ring_gemm_kernel(
         const int u = (wave + kGuWaves * c) % NL;
         dst[c] = (u >> 1) * kGuFrag + 1024 * (u & 1);
     }
-    // per-lane sources at stage 0 and their advance per stage (A: 64 bytes
-    // of the row; B: two 1 KB tiles)
+    // per-lane sources at stage 0 and their advance per stage (A: the next
+    // 64-byte chunk of the digit layout; B: two 1 KB tiles)
+    constexpr bool PAIRED = !DN && L == 2;
+    const int astep = DN ? L * tokens * kGuKB : L * kGuKB;
     int sstep[LPW];
 #pragma unroll
-    for (int c = 0; c < LPW; ++c) sstep[c] = ((wave + kGuWaves * c) % NL) / 2 < NA ? kGuKB : 2048;
+    for (int c = 0; c < LPW; ++c) sstep[c] = ((wave + kGuWaves * c) % NL) / 2 < NA ? astep : 2048;
     auto make_src = [&](const TileInfo& t, int m, const int8_t* (&src)[LPW]) {
         const int ch = gu_frag_load_chunk(lane);
 #pragma unroll
@@ -961,9 +985,17 @@ __global__ __launch_bounds__(kGuThreads) void ring_gemm_kernel(
             const int u = (wave + kGuWaves * c) % NL;
             const int f = u >> 1, h = u & 1;
             if (f < NA) {
-                const int l = f / (BM / 32), i = f % (BM / 32);
-                const int tok = s_rt[m][32 * i + gu_frag_load_row(lane, h)];
-                src[c] = xdig + ((int64_t)l * tokens + tok) * K + 16 * ch;
+                if constexpr (PAIRED) {
+                    // unit u: rows 8 (u % 4) .. +7 of 32-row block u / 4
+                    const int r = 8 * (u & 3) + (lane >> 3);
+                    const int tok = s_rt[m][32 * (u >> 2) + r];
+                    src[c] = xdig + (int64_t)tok * (L * K) + 16 * ((lane & 7) ^ ((r >> 1) & 7));
+                } else {
+                    const int l = f / (BM / 32), i = f % (BM / 32);
+                    const int tok = s_rt[m][32 * i + gu_frag_load_row(lane, h)];
+                    src[c] = DN ? xdig + ((int64_t)l * tokens + tok) * kGuKB + 16 * ch
+                                : xdig + (int64_t)tok * (L * K) + l * kGuKB + 16 * ch;
+                }
             } else {
                 const int fb = f - NA;
                 const int64_t cb = t.n0 / 32 + (DN ? fb : (fb & 3));
@@ -987,9 +1019,13 @@ __global__ __launch_bounds__(kGuThreads) void ring_gemm_kernel(
         else vm_wait<n * (LPW - 1)>();
     };
 
-    int rd[2];
+    int rd[2], rdp[2][2];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) rd[h] = gu_frag_read_offset(lane, h);
+    for (int h = 0; h < 2; ++h) {
+        rd[h] = gu_frag_read_offset(lane, h);
+#pragma unroll
+        for (int l = 0; l < 2; ++l) rdp[h][l] = gu_pair_read_offset(lane, h, l);
+    }
     v4i fa[2][WR][L], fb[2][2 * WCP];
     v16i acc[WR][L][2 * WCP];
     const int8_t* src[LPW];  // per-lane sources of this wave's loads
@@ -1009,7 +1045,10 @@ __global__ __launch_bounds__(kGuThreads) void ring_gemm_kernel(
     constexpr int RPS = 2 * (WR * L + NJ);      // LDS fragment reads per step
     static_assert(RPS <= 15, "lgkmcnt range");
     auto read_a = [&](int slot, int h, int ii, int l) __attribute__((always_inline)) {
-        fa[h][ii][l] = lds16(ring + slot * STAGE + (l * (BM / 32) + wr * WR + ii) * kGuFrag + rd[h]);
+        if constexpr (PAIRED)
+            fa[h][ii][l] = lds16(ring + slot * STAGE + (wr * WR + ii) * 2 * kGuFrag + rdp[h][l]);
+        else
+            fa[h][ii][l] = lds16(ring + slot * STAGE + (l * (BM / 32) + wr * WR + ii) * kGuFrag + rd[h]);
     };
     auto read_b = [&](int slot, int h, int j) __attribute__((always_inline)) {
         const int fbi = j < WCP ? wc * WCP + j : kGuN / 32 + wc * WCP + (j - WCP);
@@ -1268,8 +1307,9 @@ bool hm_mfma_down_ok(int64_t H, int64_t I, int64_t E, int32_t limbs) {
     return down_ring_ok(H, I, E, limbs) || shape_ok(I, H, E, limbs);
 }
 
-// gu [R x 2I]: the gate and up values of every grouped row.  The first kernel of the
-// gate/up stage (its start opens an armed stage timer).
+// gu [R x 2I]: the gate and up values of every grouped row (X digits in the
+// hm_dlay_x layout).  The first kernel of the gate/up stage (its start opens
+// an armed stage timer).
 int hm_launch_gateup_i8_mfma(const hm_layer* layer, int32_t limbs, const int8_t* xdig,
                              const float* xscale, const int32_t* xdsum, int64_t tokens,
                              const int32_t* counts, const int32_t* offsets,
@@ -1284,7 +1324,7 @@ int hm_launch_gateup_i8_mfma(const hm_layer* layer, int32_t limbs, const int8_t*
     }
 }
 
-// y [R x H] from the Z digit planes [L][R][I] (one scale per row).
+// y [R x H] from the Z digit planes (hm_dlay_z; one scale per row).
 int hm_launch_down_i8_mfma(const hm_layer* layer, int32_t limbs, const int32_t* counts,
                            const int32_t* offsets, int64_t R, const int8_t* zdig,
                            const float* zscale, const int32_t* zdsum, float* y, bool split_k,

@@ -1025,12 +1025,13 @@ __global__ __launch_bounds__(NW * HM_WAVE) void router_select_partial_kernel(
         // by the last wave (beside wave 0's selection when there are two)
         if (xq.digits && wave == NW - 1) {
             const int nv = (int)(hidden / 256);
-            int8_t* d = xq.digits + t * hidden;
+            const hm_dlay lay = hm_dlay_x(xq.limbs, hidden);
+            int8_t* d = xq.digits + t * lay.row;
             int32_t* ds = xq.dsum ? xq.dsum + t : nullptr;
             switch (xq.limbs) {
-            case 1: hm_quantize_row_wave<1>(h + t * hidden, nv, d, tokens * hidden, xq.scales + t, ds, tokens); break;
-            case 2: hm_quantize_row_wave<2>(h + t * hidden, nv, d, tokens * hidden, xq.scales + t, ds, tokens); break;
-            default: hm_quantize_row_wave<3>(h + t * hidden, nv, d, tokens * hidden, xq.scales + t, ds, tokens); break;
+            case 1: hm_quantize_row_wave<1>(h + t * hidden, nv, d, lay, xq.scales + t, ds, tokens); break;
+            case 2: hm_quantize_row_wave<2>(h + t * hidden, nv, d, lay, xq.scales + t, ds, tokens); break;
+            default: hm_quantize_row_wave<3>(h + t * hidden, nv, d, lay, xq.scales + t, ds, tokens); break;
             }
         }
         if (local && top_k <= HM_WAVE) return;
@@ -1534,12 +1535,13 @@ __global__ __launch_bounds__(kBlock) void router_select_split_kernel(
     // by a few waves' sequential chains, the rest of the machine is idle).
     if (xq.digits) {
         const int nv = (int)(hidden / 256);
-        int8_t* d = xq.digits + t * hidden;
+        const hm_dlay lay = hm_dlay_x(xq.limbs, hidden);
+        int8_t* d = xq.digits + t * lay.row;
         int32_t* ds = xq.dsum ? xq.dsum + t : nullptr;
         switch (xq.limbs) {
-        case 1: hm_quantize_row_wave<1>(hrow, nv, d, tokens * hidden, xq.scales + t, ds, tokens); break;
-        case 2: hm_quantize_row_wave<2>(hrow, nv, d, tokens * hidden, xq.scales + t, ds, tokens); break;
-        default: hm_quantize_row_wave<3>(hrow, nv, d, tokens * hidden, xq.scales + t, ds, tokens); break;
+        case 1: hm_quantize_row_wave<1>(hrow, nv, d, lay, xq.scales + t, ds, tokens); break;
+        case 2: hm_quantize_row_wave<2>(hrow, nv, d, lay, xq.scales + t, ds, tokens); break;
+        default: hm_quantize_row_wave<3>(hrow, nv, d, lay, xq.scales + t, ds, tokens); break;
         }
     }
 }
