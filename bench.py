@@ -426,8 +426,9 @@ def main():
     else:
         achieved = gu_bytes / gu_s / 1e9
         roof = {"bound": "hbm",
-                "kernel": ("gate/up GEMV: gateup_slice_kernel<NG, LJ> (every token row in LDS) "
-                           "or gemv_kernel<true, 1> (more than two tokens)" if gemv else
+                "kernel": ("gate/up GEMV: select_gateup_kernel<EPL, LJ> (one token: the select "
+                           "and the 8-column slices in one launch), gateup_slice_kernel<NG, LJ> "
+                           "(two tokens) or gemv_kernel<true, 1> (more)" if gemv else
                            "gate/up stage: ring_gemm_kernel<Lx, false> + "
                            "limb_swiglu_quantize_vec_kernel<Lz, I/256>" if cfg.int8
                            else "gate/up GEMV: gemv_f32_kernel<true, CW, MJ>" if T <= 16
@@ -437,7 +438,7 @@ def main():
                 "work_per_launch": gu_bytes, "launch_ms": round(stage["gate_up"], 5)}
     if not args.no_traffic:
         if gemv:
-            kre = prim = "gateup_slice_kernel|gemv_kernel<true"
+            kre = prim = "select_gateup_kernel|gateup_slice_kernel|gemv_kernel<true"
         elif cfg.int8:
             kre, prim = ("ring_gemm_kernel<[0-9], false>|limb_swiglu_quantize",
                          "ring_gemm_kernel<[0-9], false>")

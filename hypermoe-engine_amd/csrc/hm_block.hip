@@ -54,6 +54,16 @@ extern "C" __attribute__((visibility("hidden"))) int hm_permute_counted(const ui
                        int32_t top_k, int64_t experts, int32_t* counts, int32_t* offsets,
                        int32_t* perm_tokens, float* perm_weights, int32_t* slots,
                        void* workspace, bool counted, void* stream);
+bool hm_select_gateup_ok(const hm_layer* L, int32_t top_k);
+int hm_route_partials_decode(const float* h, const float* w, int64_t hidden, int64_t experts,
+                             int32_t top_k, uint32_t flags, int32_t* status, void* route_ws,
+                             const hm_decode_fusion* fused, const hm_norm_fold* norm,
+                             void* stream);
+int hm_launch_select_gateup(const float* x, const float* w, int32_t top_k, uint32_t flags,
+                            uint32_t* ids, float* scores, int32_t* status, void* route_ws,
+                            int32_t* counts, int32_t* offsets, int32_t* perm_tokens,
+                            float* perm_weights, int32_t* slots, const hm_layer* L, float* z,
+                            hipStream_t stream);
 int hm_route_permute_decode(const float* h, const float* w, int64_t tokens, int64_t hidden,
                             int64_t experts, int32_t top_k, uint32_t flags, uint32_t* ids,
                             float* scores, int32_t* status, void* route_ws,
@@ -273,6 +283,9 @@ int block_forward(const hm_layer* layer, const float* hidden, const float* route
     const bool fuse = (gemv || gv32 || limb_decode) && H % 32 == 0 && E <= 1024 && top_k <= 64 &&
                       P <= 1024;
     bool x_quantized = false;
+    // one token on the GEMV path: the select runs inside the gate/up launch
+    // (select_gateup_kernel), after the router partials
+    const bool sel_gu = gemv && fuse && tokens == 1 && hm_select_gateup_ok(layer, top_k);
     if (fuse) {
         const hm_decode_fusion f = {p.counters, 1, p.counts, p.offsets, p.perm_tokens,
                                     p.perm_weights, p.slots};
@@ -280,9 +293,12 @@ int block_forward(const hm_layer* layer, const float* hidden, const float* route
                                  ln ? ln->eps : 0.0f,
                                  (route_flags & HM_EXEC_ROUTE_SEQUENTIAL) ? 1 : 0};
         const hm_row_quant xq = {p.xdig, p.xscale, p.xdsum, limbs_x};
-        rc = hm_route_permute_decode(hidden, router_w, tokens, H, E, top_k, route_bits, p.ids,
-                                     p.scores, status, p.route_ws, &f, ln ? &nf : nullptr,
-                                     limb_decode ? &xq : nullptr, &x_quantized, stream);
+        rc = sel_gu ? hm_route_partials_decode(hidden, router_w, H, E, top_k, route_bits, status,
+                                               p.route_ws, &f, ln ? &nf : nullptr, stream)
+                    : hm_route_permute_decode(hidden, router_w, tokens, H, E, top_k, route_bits,
+                                              p.ids, p.scores, status, p.route_ws, &f,
+                                              ln ? &nf : nullptr, limb_decode ? &xq : nullptr,
+                                              &x_quantized, stream);
         if (ln) hidden = ln->normed;
         if (rc || (rc = mark(1)) || (rc = mark(2))) return rc;
     } else {
@@ -324,8 +340,12 @@ int block_forward(const hm_layer* layer, const float* hidden, const float* route
     };
     if (gemv) {
         rc = gate_up([&] {
-            return hm_launch_gateup_gemv(layer, hidden, counts, p.offsets, p.perm_tokens, tokens, P,
-                                         p.zf, s);
+            return sel_gu ? hm_launch_select_gateup(hidden, router_w, top_k, route_bits, p.ids,
+                                                    p.scores, status, p.route_ws, p.counts,
+                                                    p.offsets, p.perm_tokens, p.perm_weights,
+                                                    p.slots, layer, p.zf, s)
+                          : hm_launch_gateup_gemv(layer, hidden, counts, p.offsets, p.perm_tokens,
+                                                  tokens, P, p.zf, s);
         });
         if (rc) return rc;
         // one or two tokens: the down projection and the combine in one

@@ -2,6 +2,7 @@
 // elementwise kernels for gfx950 (wave64).  Every kernel here reproduces the
 // reference CPU arithmetic bit for bit; the comments say how.
 #include "hm_device.h"
+#include "hm_gemv_slice.h"
 #include "hm_lds_dma.h"
 
 #include <limits.h>
@@ -1072,6 +1073,137 @@ __global__ __launch_bounds__(NW * HM_WAVE) void router_select_partial_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// One-token decode step: router_select_partial_kernel's select, redone by
+// every workgroup of the gate/up slice launch, then that workgroup's slice
+// (hm_gemv_slice.h).  One token's select reads 2 kNB doubles per logit
+// (32 KB at E = 128) that every XCD's L2 serves to its workgroups, and
+// costs a few hundred cycles of FP64 arithmetic: less than the launch it
+// replaces.  Workgroup (bx, by): columns 8 bx .. +7 of the by-th selected
+// expert in ascending id (its grouped row is by: one token, distinct
+// experts).  Workgroup (0, 0) also writes the routing results (logits, ids,
+// scores, the groups, the status word) for the down kernel and the caller;
+// the others keep theirs in LDS.  Same results as the two kernels it
+// replaces: the same functions on the same partials.
+// ---------------------------------------------------------------------------
+// Workgroup phases: (1) the token row's loads, then every wave loads a
+// quarter (E <= 64: an eighth) of one logit row's block partials, all in
+// flight at once, and puts the blocks' B_j and its share of sum C_j in LDS;
+// (2) wave j forms row j's block-sum chain and bound from LDS (as
+// block_logit; the C_j summed in another order, which the bound's
+// inflation covers), the reference's chain where the bound leaves a logit
+// open; (3) wave 0: softmax, top-k, renormalisation (select_token), the lead
+// workgroup writes the results and the groups; (4) the slice.
+template <int EPL, int LJ>
+__global__ __launch_bounds__(kGvThreads) void select_gateup_kernel(
+    const float* __restrict__ h, const float* __restrict__ w, const double* __restrict__ part,
+    int64_t hidden, int64_t experts, int32_t top_k, uint32_t flags, float* __restrict__ logits,
+    uint32_t* __restrict__ ids, float* __restrict__ scores, int32_t* status,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ perm_tokens, float* __restrict__ perm_weights,
+    int32_t* __restrict__ slots, int64_t inter, const int8_t* __restrict__ packed,
+    const float* __restrict__ scale, const int32_t* __restrict__ zp, float* __restrict__ z) {
+    static_assert(EPL == 1 || EPL == 2, "at most two rows of 64 logits (LDS)");
+    constexpr int WPR = kGvWaves / EPL;  // waves per logit row
+    constexpr int BPW = kNB / WPR;       // blocks per wave
+    typedef int hm_i4 __attribute__((ext_vector_type(4)));
+    extern __shared__ __attribute__((aligned(16))) float s_x[];  // the token row (K32 floats)
+    __shared__ double s_b[EPL][kNB][HM_WAVE];
+    __shared__ double s_c[EPL][WPR][HM_WAVE];
+    __shared__ double s_prod[EPL][HM_WAVE];
+    __shared__ float s_seq[EPL * HM_WAVE];
+    __shared__ float s_lg[EPL][HM_WAVE];
+    __shared__ uint32_t s_sel_ids[HM_WAVE], s_own_ids[HM_WAVE];
+    __shared__ float s_sel_sc[HM_WAVE], s_own_sc[HM_WAVE];
+    const int tid = threadIdx.x, lane = tid & (HM_WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool lead = blockIdx.x == 0 && blockIdx.y == 0;
+    int32_t* st = lead ? status : nullptr;
+    // (1) the token row (K = hidden, a multiple of 32: no padding), then the
+    // partials of row j, blocks q BPW .. +BPW-1
+    const int k4 = (int)(hidden / 4);
+    float4 xa[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+        xa[u] = reinterpret_cast<const float4*>(h)[min(tid + u * kGvThreads, k4 - 1)];
+    {
+        const int j = wave / WPR, q = wave % WPR;
+        const int64_t e = lane + (int64_t)HM_WAVE * j;
+        const double* pp = part + (e < experts ? e : experts - 1) * 2 +
+                           (int64_t)q * BPW * 2 * experts;
+        hm_i4 raw[BPW];
+#pragma unroll
+        for (int i = 0; i < BPW; ++i) raw[i] = *reinterpret_cast<const hm_i4*>(pp + (int64_t)i * 2 * experts);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < BPW; ++i) asm volatile("" : "+v"(raw[i]));
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+            if (tid + u * kGvThreads < k4) reinterpret_cast<float4*>(s_x)[tid + u * kGvThreads] = xa[u];
+        double cs = 0.0;
+#pragma unroll
+        for (int i = 0; i < BPW; ++i) {
+            const double2 bc = __builtin_bit_cast(double2, raw[i]);
+            s_b[j][q * BPW + i][lane] = bc.x;
+            cs += bc.y;
+        }
+        s_c[j][q][lane] = cs;
+    }
+    __syncthreads();
+    // (2) the logits, row j by wave j
+    if (wave < EPL) {
+        const int64_t e = lane + (int64_t)HM_WAVE * wave;
+        const bool valid = e < experts;
+        double a = 0.0, sa = 0.0, sc = 0.0;
+#pragma unroll
+        for (int i = 0; i < kNB; ++i) {
+            a += s_b[wave][i][lane];
+            sa += fabs(a);
+        }
+#pragma unroll
+        for (int q = 0; q < WPR; ++q) sc += s_c[wave][q][lane];
+        const bool settled = !valid || ((flags & HM_EXEC_ROUTE_SEQUENTIAL) == 0 &&
+                                        block_sums_settle(a, sa, sc, hidden));
+        float v = valid ? (float)a : 0.0f;
+        v = chain_logits(__ballot(valid && !settled), lane, v, (int64_t)HM_WAVE * wave, h, w,
+                         hidden, experts, s_prod[wave], st);
+        if (lead && valid) logits[e] = v;
+        s_lg[wave][lane] = v;
+    }
+    __syncthreads();
+    // (3) softmax, top-k, renormalisation (wave 0); the lead workgroup
+    // writes the results and the groups
+    if (wave == 0) {
+        float v[EPL];
+        bool valid[EPL];
+#pragma unroll
+        for (int j = 0; j < EPL; ++j) {
+            v[j] = s_lg[j][lane];
+            valid[j] = lane + (int64_t)HM_WAVE * j < experts;
+        }
+        select_token<EPL>(v, valid, lane, 0, 0, experts, top_k, flags, lead ? ids : s_own_ids,
+                          lead ? scores : s_own_sc, st, s_seq, s_sel_ids, s_sel_sc);
+        if (lead) {
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            const int ln = lane < top_k ? lane : 0;
+            permute_wave<EPL>(s_sel_ids[ln], s_sel_sc[ln], top_k, top_k, (int)experts, counts,
+                              offsets, perm_tokens, perm_weights, slots);
+        }
+    }
+    __syncthreads();
+    // (4) this workgroup's expert: the selected id of rank by (ids clamped to
+    // the expert count, as the grouping does), and its slice
+    const uint32_t my = lane < top_k ? min(s_sel_ids[lane], (uint32_t)(experts - 1)) : 0xffffffffu;
+    int rank = 0;
+    for (int q = 0; q < top_k; ++q) rank += (uint32_t)__shfl((int)my, q, HM_WAVE) < my;
+    const unsigned long long hit = __ballot(lane < top_k && rank == (int)blockIdx.y);
+    const int e = hit ? __builtin_amdgcn_readlane((int)my, __ffsll((long long)hit) - 1) : -1;
+    gateup_slice_body<1, LJ, true>(blockIdx.x, blockIdx.y, hm_slice_pre{e, (int)blockIdx.y, 1, 0},
+                                   h, nullptr, hidden, inter, experts, packed, scale, zp, nullptr,
+                                   1, z);
+}
+
+// ---------------------------------------------------------------------------
 // A2 logits for prefill batches on the FP64 matrix cores, certified.
 //
 // router_mfma_kernel sums the exact products p_k = h_k w_k (double) with
@@ -1875,7 +2007,7 @@ static int launch_decode_router(const float* h, const float* w, int64_t tokens, 
                                 int64_t experts, int32_t top_k, uint32_t flags, float* logits,
                                 uint32_t* ids, float* scores, int32_t* status, void* route_ws,
                                 const hm_decode_fusion* fused, const hm_norm_fold* norm,
-                                const hm_row_quant* xq, void* stream) {
+                                const hm_row_quant* xq, void* stream, bool select = true) {
     const hm_row_quant q = xq && fused ? *xq : hm_row_quant{nullptr, nullptr, nullptr, 0};
     const int epl = (int)((experts + HM_WAVE - 1) / HM_WAVE);
     // fused: one token per workgroup, its logit rows shared out over up to
@@ -1893,6 +2025,7 @@ static int launch_decode_router(const float* h, const float* w, int64_t tokens, 
                        (int)hidden, (int)experts, part, fused ? fused->counters : nullptr,
                        fused ? fused->n_counters : 0, nf);
     HM_LAUNCHED();
+    if (!select) return HM_OK;
     // the select kernel's fallback chains read the normalised rows
     if (norm) h = norm->x_out;
 #define HM_SELECTP(N, F, W)                                                                \
@@ -1916,6 +2049,76 @@ static int launch_decode_router(const float* h, const float* w, int64_t tokens, 
     else HM_SELECTP2(16);
 #undef HM_SELECTP2
 #undef HM_SELECTP
+    HM_LAUNCHED();
+    return HM_OK;
+}
+
+// One-token decode with the select inside the gate/up launch
+// (select_gateup_kernel): the shapes it takes -- an INT8 layer whose
+// gate/up the slice kernel covers (the token row in LDS, K tiles within four
+// loads per wave), at most 8 rows of 64 logits, the partial kernel's H.
+bool hm_select_gateup_ok(const hm_layer* L, int32_t top_k) {
+    const int64_t KT = hm_pad32(L->hidden) / 32;
+    // (E <= 128: the kernel's LDS holds two rows of block partials; H <= 2 x
+    // 4 x 512 floats: the token row in two float4 per thread)
+    return L->dtype == HM_DTYPE_INT8 && L->experts <= 2 * HM_WAVE && top_k >= 1 &&
+           top_k <= L->experts && top_k <= kMaxTopK && L->hidden % kNB == 0 &&
+           L->hidden <= 8 * kGvThreads && KT <= 16 * kGsQ && L->intermediate % 8 == 0;
+}
+
+// The first launch of such a step: the router partials (router_partial_kernel,
+// which also zeroes the step's counters and, with `norm`, folds the RMSNorm
+// in and writes norm->x_out).
+int hm_route_partials_decode(const float* h, const float* w, int64_t hidden, int64_t experts,
+                             int32_t top_k, uint32_t flags, int32_t* status, void* route_ws,
+                             const hm_decode_fusion* fused, const hm_norm_fold* norm,
+                             void* stream) {
+    HM_REQUIRE(h && w && route_ws && fused && fused->counters && experts > 0 && hidden > 0);
+    HM_REQUIRE(!norm || (norm->gamma && norm->x_out && std::isfinite(norm->eps) &&
+                         norm->eps > 0.0f && hidden <= 16384));
+    if (experts > 1024 || hidden % kNB != 0 || hidden > INT_MAX) return HM_ERR_UNSUPPORTED;
+    return launch_decode_router(h, w, 1, hidden, experts, top_k, flags,
+                                static_cast<float*>(route_ws), nullptr, nullptr, status, route_ws,
+                                fused, norm, nullptr, stream, false);
+}
+
+// The second: select_gateup_kernel.  x: the token row the router read (the
+// normalised one when the norm is folded); z [k x I]: SiLU(G) * U of the k
+// selected experts' rows in ascending id; ids ... slots: the routing results
+// and the groups (hm_route_permute_decode's).  The first kernel of the
+// gate/up stage and its last (an armed stage timer brackets it).
+int hm_launch_select_gateup(const float* x, const float* w, int32_t top_k, uint32_t flags,
+                            uint32_t* ids, float* scores, int32_t* status, void* route_ws,
+                            int32_t* counts, int32_t* offsets, int32_t* perm_tokens,
+                            float* perm_weights, int32_t* slots, const hm_layer* L, float* z,
+                            hipStream_t stream) {
+    HM_REQUIRE(x && w && ids && scores && route_ws && counts && offsets && perm_tokens &&
+               perm_weights && slots && z);
+    if (!hm_select_gateup_ok(L, top_k)) return HM_ERR_UNSUPPORTED;
+    const int64_t H = L->hidden, E = L->experts, I = L->intermediate;
+    const int64_t KT = hm_pad32(H) / 32;
+    float* logits = static_cast<float*>(route_ws);
+    const double* part = reinterpret_cast<const double*>(static_cast<char*>(route_ws) +
+                                                         route_logits_bytes(1, E));
+    const dim3 grid((unsigned)(I / 8), (unsigned)top_k);
+    const size_t lds = (size_t)H * sizeof(float);
+    const int epl = (int)((E + HM_WAVE - 1) / HM_WAVE);
+    const int lj = (int)((KT + kGsQ - 1) / kGsQ + 3) / 4;
+#define HM_SG(EPL, LJ)                                                                          \
+    HM_STAGE_LAUNCH(true, true, (select_gateup_kernel<EPL, LJ>), grid, dim3(kGvThreads), lds,   \
+                    stream, x, w, part, H, E, top_k, flags, logits, ids, scores, status, counts, \
+                    offsets, perm_tokens, perm_weights, slots, I,                                \
+                    static_cast<const int8_t*>(L->packed), L->scale, L->zero_point, z)
+#define HM_SG2(EPL)                                                                             \
+    do {                                                                                        \
+        if (lj <= 1) HM_SG(EPL, 1);                                                             \
+        else if (lj <= 2) HM_SG(EPL, 2);                                                        \
+        else HM_SG(EPL, 4);                                                                     \
+    } while (0)
+    if (epl <= 1) HM_SG2(1);
+    else HM_SG2(2);
+#undef HM_SG2
+#undef HM_SG
     HM_LAUNCHED();
     return HM_OK;
 }
