@@ -367,6 +367,55 @@ def test_block_c4_prefill_properties(dev):
     assert nw < 1e-4
 
 
+def test_block_one_token_select_at_rounding_boundaries(dev):
+    """One token on the GEMV path: every workgroup of the gate/up launch
+    redoes the select (select_gateup_kernel).  Logits the bound cannot
+    settle (experts 0-3: 1 + 2^-24, an exact tie that rounds to 1.0) take
+    the reference's chain inside that kernel; ids and scores bit-exact
+    against the reference, the output within 1e-4, and the sequential-chain
+    flag gives the same bits."""
+    from hmoe import capi
+    H, E, I, k = 256, 64, 64, 2
+    rng = np.random.default_rng(5)
+    payload, scale, zp = synth.expert_layer(21, 0, E, H, I, True)
+    h = np.zeros((1, H), np.float32)
+    w = np.zeros((H, E), np.float32)
+    h[0, 0], h[0, 1] = 1.0, 2.0 ** -24
+    h[0, 2:] = rng.standard_normal(H - 2).astype(np.float32)
+    w[0, :], w[1, :] = 1.0, 1.0
+    w[2:, 4:] = (0.02 * rng.standard_normal((H - 2, E - 4))).astype(np.float32)
+    block = MoEBlock(DeviceExpertLayer(payload, scale, zp, H, I), k)
+    res = block.execute_batch(dev.to(h), dev.to(w))
+    rout, rids, rsc = O.moe_block(payload, scale, zp, h, w, k, I)
+    assert_bitexact(res.ids, rids, "ids")
+    assert_bitexact(res.scores, rsc, "scores")
+    out = dev.host(res.output)
+    assert_compare(out, rout, 1e-4, 1e-4, "one-token block vs reference (1e-4)")
+    seq = block.execute_batch(dev.to(h), dev.to(w), exec_flags=capi.HM_EXEC_ROUTE_SEQUENTIAL)
+    assert_bitexact(seq.ids, res.ids, "ids, sequential chains")
+    assert_bitexact(dev.host(seq.output), out, "output, sequential chains")
+
+
+def test_block_one_token_nonfinite_score(dev):
+    """A non-finite router score at one token (the select inside the gate/up
+    launch) sets HM_STATUS_NONFINITE_SCORE, as CpuRouterBackend.cpp:47
+    throws; the block raises, and the next call on clean weights is right."""
+    H, E, I, k = 256, 64, 64, 2
+    payload, scale, zp, h, w = _layer_inputs(23, 1, H, E, I, True)
+    block = MoEBlock(DeviceExpertLayer(payload, scale, zp, H, I), k)
+    bad = w.copy()
+    bad[3, 5] = np.inf
+    from hmoe import capi
+    with pytest.raises(RuntimeError, match="status bits") as err:
+        block.execute_batch(dev.to(h), dev.to(bad))
+    bits = int(str(err.value).split("status bits ")[1].rstrip(")"), 16)
+    assert bits & capi.HM_STATUS_NONFINITE_SCORE
+    res = block.execute_batch(dev.to(h), dev.to(w))
+    rout, rids, _ = O.moe_block(payload, scale, zp, h, w, k, I)
+    assert_bitexact(res.ids, rids, "ids after the failed call")
+    assert_compare(dev.host(res.output), rout, 1e-4, 1e-4, "output after the failed call")
+
+
 @pytest.mark.parametrize("T", [1, 16, 300])
 def test_block_graph_replay(dev, T):
     """The block's launch sequence captured as one HIP graph (kernels only:
