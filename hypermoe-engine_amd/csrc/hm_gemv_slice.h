@@ -122,12 +122,13 @@ constexpr int kGsQ = 4;  // K quarters (waves per projection)
 // tok >= 0, the one token every row reads; counts and perm_tokens are not
 // read) and the caller has staged the token rows in s_x (the dynamic LDS)
 // and synchronised the workgroup: the one-token select + gate/up kernel,
-// whose workgroups select the experts themselves.
+// whose workgroups select the experts themselves.  R: rows per pass (the
+// weights stay in registers across the passes; one token: R = 1).
 struct hm_slice_pre {
     int e, g0, rows, tok;
 };
 
-template <int NG, int LJ, bool PRE>
+template <int NG, int LJ, bool PRE, int R = kGvRows>
 __device__ __forceinline__ void gateup_slice_body(
     unsigned bx, unsigned by, hm_slice_pre pre, const float* __restrict__ x_src,
     const int32_t* __restrict__ perm_tokens, int64_t K, int64_t N, int64_t experts,
@@ -135,8 +136,9 @@ __device__ __forceinline__ void gateup_slice_body(
     const int32_t* __restrict__ zp, const int32_t* __restrict__ counts, int n_tokens,
     float* __restrict__ out) {
     extern __shared__ __attribute__((aligned(16))) float s_x[];      // [T][K32]
-    __shared__ float s_red[2][kGsQ][kGvRows][8];
-    __shared__ float s_xs[kGsQ][kGvRows];
+    static_assert(R >= 1 && R <= kGvRows, "rows per pass");
+    __shared__ float s_red[2][kGsQ][R][8];
+    __shared__ float s_xs[kGsQ][R];
     __shared__ unsigned long long s_exp2[32];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -193,22 +195,22 @@ __device__ __forceinline__ void gateup_slice_body(
     __syncthreads();
     const int64_t g0 = act.g0;
     const int rows = act.rows;
-    for (int r0 = 0; r0 < rows; r0 += kGvRows) {
-        const int nr = min(kGvRows, rows - r0);
-        int64_t xoff[kGvRows];
+    for (int r0 = 0; r0 < rows; r0 += R) {
+        const int nr = min(R, rows - r0);
+        int64_t xoff[R];
 #pragma unroll
-        for (int r = 0; r < kGvRows; ++r)
+        for (int r = 0; r < R; ++r)
             xoff[r] = (r < nr ? row_token(g0 + r0 + r) : 0) * K32 + 32 * (kb0 + tq) + 16 * kh;
-        float acc[kGvRows];
+        float acc[R];
 #pragma unroll
-        for (int r = 0; r < kGvRows; ++r) acc[r] = 0.0f;
+        for (int r = 0; r < R; ++r) acc[r] = 0.0f;
 #pragma unroll
         for (int j = 0; j < LJ; ++j) {
             if (4 * j + tq < nkb) {
                 float f[16];
                 tile_to_float(w[j], f);
 #pragma unroll
-                for (int r = 0; r < kGvRows; ++r) {
+                for (int r = 0; r < R; ++r) {
                     if (r < nr) {
                         const float4* xv = reinterpret_cast<const float4*>(&s_x[xoff[r] + 128 * j]);
 #pragma unroll
@@ -225,7 +227,7 @@ __device__ __forceinline__ void gateup_slice_body(
         }
         // the eight lanes of each column: K halves, then the four tiles
 #pragma unroll
-        for (int r = 0; r < kGvRows; ++r) {
+        for (int r = 0; r < R; ++r) {
             float a = acc[r];
             a += __shfl_xor(a, 8, 64);
             a += __shfl_xor(a, 16, 64);
@@ -235,7 +237,7 @@ __device__ __forceinline__ void gateup_slice_body(
         // the rows' sums over this K quarter (the gate waves)
         if (p == 0) {
 #pragma unroll
-            for (int r = 0; r < kGvRows; ++r) {
+            for (int r = 0; r < R; ++r) {
                 if (r >= nr) break;
                 const int64_t xr0 = row_token(g0 + r0 + r) * K32;
                 float xs = 0.0f;

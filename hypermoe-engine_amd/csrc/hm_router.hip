@@ -1198,9 +1198,9 @@ __global__ __launch_bounds__(kGvThreads) void select_gateup_kernel(
     for (int q = 0; q < top_k; ++q) rank += (uint32_t)__shfl((int)my, q, HM_WAVE) < my;
     const unsigned long long hit = __ballot(lane < top_k && rank == (int)blockIdx.y);
     const int e = hit ? __builtin_amdgcn_readlane((int)my, __ffsll((long long)hit) - 1) : -1;
-    gateup_slice_body<1, LJ, true>(blockIdx.x, blockIdx.y, hm_slice_pre{e, (int)blockIdx.y, 1, 0},
-                                   h, nullptr, hidden, inter, experts, packed, scale, zp, nullptr,
-                                   1, z);
+    gateup_slice_body<1, LJ, true, 1>(blockIdx.x, blockIdx.y,
+                                      hm_slice_pre{e, (int)blockIdx.y, 1, 0}, h, nullptr, hidden,
+                                      inter, experts, packed, scale, zp, nullptr, 1, z);
 }
 
 // ---------------------------------------------------------------------------
