@@ -580,12 +580,34 @@ __global__ __launch_bounds__(64) void router_partial_kernel(
         }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        for (int i = 0; i < kc; ++i) {
-            const double hk = s_h[i];
-            const double wd = (double)s_w[i][lane];
+        auto step = [&](double hk, double wd) __attribute__((always_inline)) {
             acc = __builtin_fma(hk, wd, acc);  // == acc + hk * wd (the product is exact)
             rs += fabs(acc);
             qs = __builtin_fma(fabs(hk), fabs(wd), qs);
+        };
+        if (kc == kPK) {
+            // a whole chunk: the LDS values of the next kRSub steps are read
+            // while the current ones are chained, so the chain does not wait
+            // for an LDS read every other step (same steps, same order)
+            constexpr int kRSub = 16;
+            double hb[2][kRSub];
+            float wb[2][kRSub];
+            auto fetch = [&](int buf, int i0) __attribute__((always_inline)) {
+#pragma unroll
+                for (int i = 0; i < kRSub; ++i) {
+                    hb[buf][i] = s_h[i0 + i];
+                    wb[buf][i] = s_w[i0 + i][lane];
+                }
+            };
+            fetch(0, 0);
+#pragma unroll
+            for (int c = 0; c < kPK / kRSub; ++c) {
+                if (c + 1 < kPK / kRSub) fetch((c + 1) & 1, (c + 1) * kRSub);
+#pragma unroll
+                for (int i = 0; i < kRSub; ++i) step(hb[c & 1][i], (double)wb[c & 1][i]);
+            }
+        } else {
+            for (int i = 0; i < kc; ++i) step(s_h[i], (double)s_w[i][lane]);
         }
     }
     if (live) {
