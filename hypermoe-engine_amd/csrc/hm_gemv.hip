@@ -462,21 +462,35 @@ __global__ __launch_bounds__(kDcThreads) void gemv_down_combine_kernel(
         for (int r = 0; r < rows; ++r) {
             float acc = 0.0f, xs = 0.0f;
             const float* zr = &s_z[(int64_t)(g0 + r) * I32 + 32 * (kb0 + tq) + 16 * kh];
+            // the z values of load j + 1 are read while load j's are chained
+            // (reads past the lane's K range repeat its last load's, unused)
+            const int jl = max((nkb - 1 - tq) >> 2, 0);
+            float4 zc[4], zn[4];
+            auto read_z = [&](int j, float4 (&d)[4]) __attribute__((always_inline)) {
+                const float4* xv = reinterpret_cast<const float4*>(zr + 128 * min(j, jl));
+#pragma unroll
+                for (int i = 0; i < 4; ++i) d[i] = xv[i];
+            };
+            read_z(0, zc);
 #pragma unroll
             for (int j = 0; j < kDcLoads; ++j) {
+                if (j + 1 < kDcLoads) read_z(j + 1, zn);
                 if (4 * j + tq < nkb) {
                     float f[16];
                     tile_to_float(w[s][j], f);
-                    const float4* xv = reinterpret_cast<const float4*>(zr + 128 * j);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const float4 v = xv[i];
+                        const float4 v = zc[i];
                         acc = __builtin_fmaf(v.x, f[4 * i], acc);
                         acc = __builtin_fmaf(v.y, f[4 * i + 1], acc);
                         acc = __builtin_fmaf(v.z, f[4 * i + 2], acc);
                         acc = __builtin_fmaf(v.w, f[4 * i + 3], acc);
                         xs += (v.x + v.y) + (v.z + v.w);
                     }
+                }
+                if (j + 1 < kDcLoads) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) zc[i] = zn[i];
                 }
             }
             // the eight lanes of each column: K halves, then the four tiles
