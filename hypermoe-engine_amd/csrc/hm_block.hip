@@ -9,6 +9,8 @@
 #include <cmath>
 
 
+int hm_launch_rmsnorm(const float* x, const float* gamma, float* y, int64_t rows,
+                      int64_t width, float eps, bool force_seq, void* stream);
 int hm_launch_quantize_rows(const float* x, int64_t rows, int64_t n, int32_t limbs,
                             int8_t* digits, float* scales, int32_t* dsum,
                             hipStream_t stream);
@@ -303,7 +305,8 @@ int block_forward(const hm_layer* layer, const float* hidden, const float* route
         if (rc || (rc = mark(1)) || (rc = mark(2))) return rc;
     } else {
         if (ln) {
-            rc = hm_rmsnorm(hidden, ln->gamma, ln->normed, tokens, H, ln->eps, stream);
+            rc = hm_launch_rmsnorm(hidden, ln->gamma, ln->normed, tokens, H, ln->eps,
+                                   (route_flags & HM_EXEC_ROUTE_SEQUENTIAL) != 0, stream);
             if (rc) return rc;
             hidden = ln->normed;
         }

@@ -65,7 +65,7 @@ __device__ __forceinline__ double hm_rms_sum_seq(const float* __restrict__ xr, i
 
 __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(
     const float* __restrict__ x, const float* __restrict__ gamma,
-    float* __restrict__ y, int64_t width, float eps) {
+    float* __restrict__ y, int64_t width, float eps, int force_seq) {
     extern __shared__ float row_lds[];  // width floats
     __shared__ double red[kBlock / HM_WAVE];
     __shared__ int ambiguous;
@@ -74,7 +74,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(
     const float* xr = x + r * width;
     float* yr = y + r * width;
     const int tid = threadIdx.x;
-    if (tid == 0) ambiguous = 0;
+    if (tid == 0) ambiguous = force_seq;
     double local = 0.0;
     for (int64_t i = tid; i < width; i += kBlock) {
         const float v = xr[i];
@@ -114,13 +114,14 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_kernel(
 // row and four rows per workgroup: a lane's V 16-byte loads are issued
 // together and the row stays in registers (rmsnorm_kernel's strided loop
 // waits for each load before the next).  Same bracket, same fallback (a row
-// with an ambiguous element takes the sequential sum), with the exact
+// with an ambiguous element, or every row with force_seq, takes the
+// sequential sum), with the exact
 // products formed by the whole wave so that lane 0's chain is only the
 // additions.
 template <int V>
 __global__ __launch_bounds__(kBlock) void rmsnorm_wave_kernel(
     const float* __restrict__ x, const float* __restrict__ gamma,
-    float* __restrict__ y, int64_t rows, float eps) {
+    float* __restrict__ y, int64_t rows, float eps, int force_seq) {
     constexpr int W = 256 * V;
     extern __shared__ float row_lds[];  // [4][512] doubles: a chunk of products per wave
     const int lane = threadIdx.x & (HM_WAVE - 1), wv = threadIdx.x / HM_WAVE;
@@ -161,7 +162,7 @@ __global__ __launch_bounds__(kBlock) void rmsnorm_wave_kernel(
         one(v[j].z, g.z, out[j].z);
         one(v[j].w, g.w, out[j].w);
     }
-    if (__ballot(amb) != 0) {
+    if (force_seq || __ballot(amb) != 0) {
         // The reference's sequential sum: s = fl(s + p_k) with the exact
         // products p_k = double(x_k)^2.  The wave forms the products of 512
         // consecutive elements (its registers j = 2q, 2q+1) into LDS, then
@@ -1950,10 +1951,10 @@ unsigned grid_for(int64_t n) {
 
 }  // namespace
 
-extern "C" {
-
-int hm_rmsnorm(const float* x, const float* gamma, float* y, int64_t rows,
-               int64_t width, float eps, void* stream) {
+// hm_rmsnorm's launch; force_seq: every row takes the sequential sum of
+// squares (HM_EXEC_ROUTE_SEQUENTIAL through hm_moe_layer_forward).
+int hm_launch_rmsnorm(const float* x, const float* gamma, float* y, int64_t rows,
+                      int64_t width, float eps, bool force_seq, void* stream) {
     HM_REQUIRE(x && gamma && y && rows >= 0 && width > 0);
     HM_REQUIRE(std::isfinite(eps) && eps > 0.0f);  // RMSNorm.cpp:22
     HM_REQUIRE(width <= 16384);                     // row staged in LDS
@@ -1964,9 +1965,10 @@ int hm_rmsnorm(const float* x, const float* gamma, float* y, int64_t rows,
         const unsigned grid = (unsigned)((rows + kBlock / HM_WAVE - 1) / (kBlock / HM_WAVE));
         const size_t lds = (size_t)(kBlock / HM_WAVE) * 512 * sizeof(double);
         const hipStream_t s = hm_stream(stream);
+        const int fs = force_seq ? 1 : 0;
         switch (width / 256) {
 #define HM_RMS_CASE(v) \
-    case v: hipLaunchKernelGGL(rmsnorm_wave_kernel<v>, dim3(grid), dim3(kBlock), lds, s, x, gamma, y, rows, eps); break;
+    case v: hipLaunchKernelGGL(rmsnorm_wave_kernel<v>, dim3(grid), dim3(kBlock), lds, s, x, gamma, y, rows, eps, fs); break;
             HM_RMS_CASE(1) HM_RMS_CASE(2) HM_RMS_CASE(3) HM_RMS_CASE(4) HM_RMS_CASE(5) HM_RMS_CASE(6)
             HM_RMS_CASE(7) HM_RMS_CASE(8) HM_RMS_CASE(9) HM_RMS_CASE(10) HM_RMS_CASE(11)
             HM_RMS_CASE(12) HM_RMS_CASE(13) HM_RMS_CASE(14) HM_RMS_CASE(15) HM_RMS_CASE(16)
@@ -1977,10 +1979,18 @@ int hm_rmsnorm(const float* x, const float* gamma, float* y, int64_t rows,
     }
     hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(kBlock),
                        (size_t)width * sizeof(float), hm_stream(stream), x, gamma,
-                       y, width, eps);
+                       y, width, eps, force_seq ? 1 : 0);
     HM_LAUNCHED();
     return HM_OK;
 }
+
+extern "C" {
+
+int hm_rmsnorm(const float* x, const float* gamma, float* y, int64_t rows,
+               int64_t width, float eps, void* stream) {
+    return hm_launch_rmsnorm(x, gamma, y, rows, width, eps, false, stream);
+}
+
 
 // Route workspace: the logits [T x E] floats (rounded up to 256 bytes),
 // then for decode batches (T <= kDecodeTokens) the block partials

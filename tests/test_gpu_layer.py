@@ -70,12 +70,12 @@ def _layer_forward(block, h, gamma, w, flags, normed_offset=0):
     """normed_offset: the normalised rows start that many floats into their
     buffer (an offset of 1 leaves them 4-byte but not 16-byte aligned)."""
     import torch
-    T = h.shape[0]
+    T, width = h.shape
     P = T * block.top_k
-    normed_buf = torch.full((T * H + normed_offset,), float("nan"), dtype=torch.float32,
+    normed_buf = torch.full((T * width + normed_offset,), float("nan"), dtype=torch.float32,
                             device="cuda")
-    normed = normed_buf[normed_offset:].view(T, H)
-    out = torch.full((T, H), float("nan"), dtype=torch.float32, device="cuda")
+    normed = normed_buf[normed_offset:].view(T, width)
+    out = torch.full((T, width), float("nan"), dtype=torch.float32, device="cuda")
     ids = torch.full((T, block.top_k), -1, dtype=torch.int32, device="cuda")
     scores = torch.empty((T, block.top_k), dtype=torch.float32, device="cuda")
     status = torch.zeros(1, dtype=torch.int32, device="cuda")
@@ -165,6 +165,100 @@ def test_layer_forward_matches_norm_then_block(dev, layer, T, seq):
     assert_bitexact(dn.cpu().numpy(), ref_norm, f"T={T} hm_rmsnorm")
     assert_bitexact(ids, ref.ids, f"T={T} routing")
     assert_bitexact(out, ref.output.cpu().numpy(), f"T={T} output")
+
+
+def _sequential_sum_rows(rng, T, width):
+    """Rows whose sequential sum of squares stresses its roundings: random
+    rows, a tiny first element, leading zeros, magnitudes spread over 2^64
+    that climb in every 256-element stretch (the sum changes binade over
+    and over), odd integers after a 1.5 * 2^26 head (every step a tie,
+    rounded to even), the same after a head just under 2^54 with occasional
+    2^31-sized squares (ties next to a binade change), a log-normal row, all
+    zeros, all ones (the sum reaches each power of two exactly), sparse
+    powers of two and small odd multiples of powers of two."""
+    k = np.arange(width)
+    rows = np.empty((T, width), np.float32)
+    for t in range(T):
+        kind = t % 12
+        if kind == 0:
+            r = rng.standard_normal(width)
+        elif kind == 1:
+            r = rng.standard_normal(width)
+            r[0] = 1e-20
+        elif kind == 2:
+            r = rng.standard_normal(width)
+            r[:min(width - 1, 100 + int(rng.integers(200)))] = 0.0
+        elif kind == 3:
+            r = np.ldexp(1.0, (k % 256) // 4 - 32) * (1.0 + rng.random(width))
+        elif kind == 4:
+            r = (2 * rng.integers(0, 4, width) + 1).astype(np.float64)
+            r[0] = 1.5 * 2.0 ** 26
+        elif kind == 5:
+            r = (2 * rng.integers(0, 4, width) + 1).astype(np.float64)
+            big = rng.random(width) < 0.02
+            r[big] = 46341 + 2 * rng.integers(0, 100, int(big.sum()))
+            r[0] = 2.0 ** 27 - 8
+        elif kind == 6:
+            r = np.exp(rng.standard_normal(width) * 8.0)
+        elif kind == 7:
+            r = np.zeros(width)
+        elif kind == 8:
+            r = np.ones(width)
+        elif kind == 9:
+            r = np.where(rng.random(width) < 0.5, 0.0,
+                         np.ldexp(1.0, rng.integers(-30, 30, width)))
+        elif kind == 10:
+            r = np.ldexp(rng.integers(1, 9, width).astype(np.float64), rng.integers(0, 6, width))
+            r[:40] *= 4096.0
+        else:
+            r = np.ldexp((2 * rng.integers(0, 16, width) + 1).astype(np.float64),
+                         rng.integers(-12, 12, width))
+        rows[t] = r * np.where(rng.random(width) < 0.5, -1.0, 1.0)
+    return rows
+
+
+_WIDTH_LAYERS = {}
+
+
+def _width_layer(width):
+    if width == H:
+        return None
+    if width not in _WIDTH_LAYERS:
+        payload, scale, zp = synth.expert_layer(95, 0, E, width, I, True)
+        _WIDTH_LAYERS[width] = DeviceExpertLayer(payload, scale, zp, width, I)
+    return _WIDTH_LAYERS[width]
+
+
+@pytest.mark.parametrize("width,T,offset", [(H, 16, 0), (H, 24, 0), (H, 24, 1), (256, 24, 0),
+                                            (768, 24, 0), (4096, 24, 0), (4096, 12, 0)])
+def test_layer_forward_sequential_sum_rows(dev, layer, width, T, offset):
+    """HM_EXEC_ROUTE_SEQUENTIAL sends every row of hm_moe_layer_forward to
+    the sequential sum of squares: the decode fold in the router's first
+    kernel (T <= 16), rmsnorm_wave_kernel (prefill, rows 16-byte aligned;
+    widths of 1, 3, 8 and 16 times 256) and rmsnorm_kernel (normalised rows
+    4 bytes off).  On rows built to stress that sum's roundings the
+    normalised rows equal the oracle's RMSNorm bit for bit, and so do
+    hm_rmsnorm's without the flag (the bracket, or the same fallback)."""
+    import torch
+    print(f"[gpu] sequential sum rows width={width} T={T} offset={offset}", flush=True)
+    rng = np.random.default_rng(4000 + width + T + offset)
+    dl = _width_layer(width) or layer
+    h = _sequential_sum_rows(rng, T, width)
+    gamma = (0.5 + rng.random(width)).astype(np.float32)
+    w = synth.router_weights(95, 0, width, E)
+    dh, dg, dw = (torch.from_numpy(a).cuda() for a in (h, gamma, w))
+    block = MoEBlock(dl, K)
+    normed, _, _ = _layer_forward(block, dh, dg, dw, capi.HM_EXEC_ROUTE_SEQUENTIAL,
+                                  normed_offset=offset)
+    ref = O.rmsnorm(h, gamma, EPS)
+    assert np.isfinite(ref).all()
+    for t in range(T):
+        assert_bitexact(normed[t], ref[t], f"width={width} T={T} row {t} (kind {t % 12})")
+    dn = torch.full_like(dh, float("nan"))
+    capi.call("hm_rmsnorm", dh.data_ptr(), dg.data_ptr(), dn.data_ptr(), T, width, EPS,
+              torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert_bitexact(dn.cpu().numpy(), ref, f"width={width} T={T} hm_rmsnorm")
 
 
 @pytest.mark.parametrize("T,offset", [(9, 0), (16, 0), (16, 1)])
